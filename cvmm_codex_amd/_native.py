@@ -1,0 +1,116 @@
+"""ctypes binding of libcvmm_hip.so (declared in include/cvmm_hip.h).
+
+torch is imported before the library is opened so that the library binds to
+the HIP runtime torch already loaded (same SONAME), i.e. one runtime and one
+set of streams per process.  There is no fallback: if the library is missing
+every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must precede loading the HIP library)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcvmm_hip.so")
+
+F32, F16, BF16 = 0, 1, 2            # cvmm.py:36-44 dtype ids
+FLAG_ATOMIC_REDUCE = 1
+
+_DTYPE_ID = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_SZ = ctypes.c_size_t
+
+_SIGS = {
+    "cvmm_last_error": (ctypes.c_char_p, []),
+    "cvmm_abi_version": (ctypes.c_int, []),
+    "cvmm_sort_workspace_bytes": (_SZ, [_I64, _I32]),
+    "cvmm_sort_routes": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "cvmm_expert_offsets": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
+    "cvmm_fwd_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I32, _I32, _I32, _I32]),
+    "cvmm_fwd": (ctypes.c_int, [
+        _P, _I32, _I64, _I64,                 # x, dtype, rows, ld
+        _P, _I32, _I32, _I64, _I64,           # keys, dtype, E, d_in, d_out
+        _I64, _I64, _I64,                     # key strides
+        _P, _P, _P, _I64,                     # sorted_sel, sel_index, out_index, R
+        _P, _P, _I32, _I64,                   # offsets, rw, rw dtype, reduce_k
+        _I32, _P, _I32, _I64, _I64,           # op, out, out dtype, out rows, out ld
+        _I32, _P, _SZ, _P]),                  # flags, ws, ws bytes, stream
+    "cvmm_bwd_x_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I32, _I32, _I32, _I64, _I32, _I32, _I32, _I32]),
+    "cvmm_bwd_x": (ctypes.c_int, [
+        _P, _I32, _I64, _I64,                 # grad, dtype, rows, ld
+        _P, _I32, _I32, _I64, _I64,           # keys, dtype, E, d_in, d_out
+        _I64, _I64, _I64,                     # key strides
+        _P, _P, _P, _I64,                     # sorted_sel, sel_index, out_index, R
+        _P, _P, _I32, _I64,                   # offsets, rw, rw dtype, top_k
+        _P, _I32, _I64, _I64, _I32,           # x, x dtype, x rows, x ld, op
+        _P, _I32, _I64, _I64,                 # grad_x, dtype, rows, ld
+        _P, _I32,                             # grad_rw, dtype
+        _I32, _P, _SZ, _P]),
+    "cvmm_bwd_w_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I32, _I32]),
+    "cvmm_bwd_w": (ctypes.c_int, [
+        _P, _I32, _I64, _I64,                 # x
+        _P, _I32, _I64, _I64,                 # grad
+        _I32, _I64, _I64,                     # E, d_in, d_out
+        _P, _P, _P, _I64, _P,                 # sorted_sel, sel_index, out_index, R, offsets
+        _P, _I32, _I64, _I32,                 # rw, rw dtype, top_k, op
+        _P, _I32, _I64, _I64, _I64,           # grad_keys, dtype, strides
+        _I32, _P, _SZ, _P]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+_lib = None
+_lock = threading.Lock()
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def available() -> bool:
+    return os.path.exists(LIB_PATH)
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise NativeLibraryMissing(
+                        f"{LIB_PATH} is not built (run `python -m cvmm_codex_amd.build`); "
+                        "cvmm_codex_amd has no CPU or PyTorch fallback")
+                handle = ctypes.CDLL(LIB_PATH)
+                for name, (res, args) in _SIGS.items():
+                    fn = getattr(handle, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().cvmm_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def dtype_id(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE_ID[dt]
+    except KeyError:
+        raise TypeError(f"cvmm: unsupported dtype {dt}") from None
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

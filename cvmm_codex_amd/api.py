@@ -1,0 +1,494 @@
+"""MI355X-native drop-in for the reference's ``cvmm.py`` (RobertCsordas/cvmm_codex).
+
+Same public surface, argument meaning and error behaviour as the reference:
+``CVMMSel`` (cvmm.py:12-21), ``cvmm_prepare_sel`` (:24-27),
+``cvmm_prepare_sel2`` (:1786-1803), ``cvmm`` (:1759-1783), the autograd
+Function ``CVMM`` (:1521-1755), ``get_dtype`` / ``dtype_to_type_id`` (:30-44),
+``create_kernels`` and ``_cvmm_expert_offsets`` (:68-78), plus the module
+attributes the reference tests patch (``cvmm_expert_offsets_call``,
+``cvmm_lowmem_chunk_size``).
+
+All arithmetic runs in the HIP kernels of ``libcvmm_hip.so`` (C ABI in
+``include/cvmm_hip.h``), launched on torch's current stream; nothing here
+synchronises with the host.  There is no CPU or PyTorch fallback: CPU tensors
+and a missing library raise.
+
+Selector sorting is deferred: ``cvmm_prepare_sel2`` records the selection and
+the stable counting sort runs when ``cvmm`` first sees the selector, because the
+sort needs the expert count, which is ``keys.shape[0]`` and is not an argument
+of ``cvmm_prepare_sel2``.  Reading ``.sel`` / ``.sel_index`` / ``.out_index``
+earlier forces the sort (with the expert count taken from the largest id, one
+host sync).
+"""
+from __future__ import annotations
+
+import os
+from typing import Dict, Optional, Tuple, Union
+
+import torch
+
+from . import _native as N
+
+__all__ = [
+    "CVMMSel", "cvmm_prepare_sel", "cvmm_prepare_sel2", "cvmm", "CVMM", "get_dtype",
+    "dtype_to_type_id", "create_kernels", "cvmm_expert_offsets",
+]
+
+
+def _env_on(name: str, default: str = "0") -> bool:
+    return os.environ.get(name, default).lower() in ("1", "true", "yes", "on")
+
+
+# Test hooks with the reference's names (cvmm.py:47-64).  ``cvmm_expert_offsets_call``
+# is the native offsets function once create_kernels() ran; setting it to None makes
+# _cvmm_expert_offsets use the closed-form torch expression (what the reference's
+# test compares against, test_cvmm_correctness.py:73-86).
+cvmm_expert_offsets_call = None
+cvmm_use_triton_expert_offsets = not _env_on("CVMM_DISABLE_TRITON_EXPERT_OFFSETS")
+# Accepted for compatibility; the HIP backward never materialises more than one
+# route-ordered [R, d_in] buffer, so top-k chunking is not needed.
+cvmm_lowmem_chunk_size = int(os.environ.get("CVMM_LOWMEM_CHUNK_SIZE", "0"))
+# Sum the top-k terms (weighted forward combine, token-input grad_x) with fp32
+# atomics into token rows instead of a route-ordered buffer + ordered row sum.
+cvmm_atomic_reduce = _env_on("CVMM_ATOMIC_REDUCE")
+# Print each new (x.shape, keys.shape) like the reference (cvmm.py:1778-1781).
+cvmm_log_shapes = _env_on("CVMM_LOG_SHAPES")
+
+
+def _require_device(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"cvmm_codex_amd: {what} must be a ROCm GPU tensor (there is no CPU fallback)")
+
+
+# ----------------------------------------------------------------------------
+# dtype helpers (cvmm.py:30-44)
+# ----------------------------------------------------------------------------
+
+def get_dtype() -> torch.dtype:
+    """Op/output dtype: fp32 unless autocast is on (cvmm.py:30-33)."""
+    if not torch.is_autocast_enabled("cuda"):
+        return torch.float32
+    return torch.get_autocast_dtype("cuda")
+
+
+def dtype_to_type_id(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return 0
+    elif dtype == torch.float16:
+        return 1
+    elif dtype == torch.bfloat16:
+        return 2
+    raise ValueError("Unknown dtype")
+
+
+# ----------------------------------------------------------------------------
+# native selector preparation
+# ----------------------------------------------------------------------------
+
+def _flat_int32(sel: torch.Tensor) -> torch.Tensor:
+    f = sel.reshape(-1)
+    if f.dtype != torch.int32:
+        f = f.to(torch.int32)
+    return f.contiguous()
+
+
+def _sort_routes(raw_flat: torch.Tensor, n_experts: int, top_k: int):
+    """Stable counting sort on the device: (sorted int32, perm int64,
+    perm // top_k int64, inclusive offsets int64[E])."""
+    lib = N.lib()
+    dev = raw_flat.device
+    R = raw_flat.numel()
+    ssel = torch.empty(R, dtype=torch.int32, device=dev)
+    perm = torch.empty(R, dtype=torch.int64, device=dev)
+    tok = torch.empty(R, dtype=torch.int64, device=dev)
+    offsets = torch.empty(n_experts, dtype=torch.int64, device=dev)
+    ws_bytes = lib.cvmm_sort_workspace_bytes(R, n_experts)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    N.check(lib.cvmm_sort_routes(N.ptr(raw_flat), 0, R, n_experts, max(top_k, 1), N.ptr(ssel), N.ptr(perm),
+                                 N.ptr(tok), N.ptr(offsets), None, N.ptr(ws), ws_bytes, N.stream_of(dev)),
+            "cvmm_sort_routes")
+    return ssel, perm, tok, offsets
+
+
+def cvmm_expert_offsets(sorted_experts: torch.Tensor, n_experts: int) -> torch.Tensor:
+    """Native offsets: out[e] = #{i : sorted[i] <= e} (cvmm.py:1108-1120)."""
+    _require_device(sorted_experts, "sorted_experts")
+    s = _flat_int32(sorted_experts)
+    out = torch.empty(n_experts, dtype=torch.int64, device=s.device)
+    N.check(N.lib().cvmm_expert_offsets(N.ptr(s), s.numel(), n_experts, N.ptr(out), N.stream_of(s.device)),
+            "cvmm_expert_offsets")
+    return out
+
+
+def _cvmm_expert_offsets(sorted_experts: torch.Tensor, n_experts: int) -> torch.Tensor:
+    """cvmm.py:68-78."""
+    if cvmm_use_triton_expert_offsets and cvmm_expert_offsets_call is not None and sorted_experts.is_cuda:
+        return cvmm_expert_offsets_call(sorted_experts, n_experts)
+    unique_experts, counts = torch.unique_consecutive(sorted_experts, return_counts=True)
+    if unique_experts.numel() == n_experts:
+        return counts.cumsum(0)
+    expert_counts = torch.zeros((n_experts,), device=sorted_experts.device, dtype=counts.dtype)
+    expert_counts[unique_experts.long()] = counts
+    return expert_counts.cumsum(0)
+
+
+def _sorted_i32(sel: torch.Tensor) -> torch.Tensor:
+    if sel.dtype == torch.int32 and sel.is_contiguous():
+        return sel.reshape(-1)
+    cached = getattr(sel, "_cvmm_i32", None)
+    if cached is None:
+        cached = _flat_int32(sel)
+        try:
+            sel._cvmm_i32 = cached
+        except (AttributeError, RuntimeError):
+            pass
+    return cached
+
+
+def _offsets_for(sel: torch.Tensor, n_experts: int) -> torch.Tensor:
+    """Per-expert offsets of a sorted selector, cached on the tensor object."""
+    cache: Optional[Dict[int, torch.Tensor]] = getattr(sel, "_cvmm_offsets", None)
+    if cache is not None and n_experts in cache:
+        return cache[n_experts]
+    off = cvmm_expert_offsets(_sorted_i32(sel), n_experts)
+    try:
+        if cache is None:
+            cache = {}
+            sel._cvmm_offsets = cache
+        cache[n_experts] = off
+    except (AttributeError, RuntimeError):
+        pass
+    return off
+
+
+class _Routing:
+    """One recorded selection; sorted on the device on first use, per expert count."""
+
+    def __init__(self, raw_flat: torch.Tensor, top_k: int):
+        self.raw = raw_flat
+        self.k = top_k
+        self.by_e: Dict[int, Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]] = {}
+        self.first_e: Optional[int] = None
+
+    def get(self, n_experts: int):
+        hit = self.by_e.get(n_experts)
+        if hit is None:
+            hit = _sort_routes(self.raw, n_experts, self.k)
+            self.by_e[n_experts] = hit
+            if self.first_e is None:
+                self.first_e = n_experts
+        return hit
+
+    def default(self):
+        if self.first_e is None:
+            n = int(self.raw.max().item()) + 1 if self.raw.numel() else 1   # host sync
+            self.get(max(n, 1))
+        return self.by_e[self.first_e]
+
+
+class CVMMSel:
+    """Selector metadata (cvmm.py:12-21): same constructor, fields and clone().
+
+    Instances made by cvmm_prepare_sel2 resolve ``sel``/``sel_index``/``out_index``
+    lazily (see the module docstring); instances built directly are plain records.
+    """
+
+    def __init__(self, raw_sel: torch.Tensor, sel: torch.Tensor, sel_index: torch.Tensor,
+                 out_index: Optional[torch.Tensor] = None, reduction_weight: Optional[torch.Tensor] = None):
+        self.raw_sel = raw_sel
+        self._sel = sel
+        self._sel_index = sel_index
+        self._out_index = out_index
+        self.reduction_weight = reduction_weight
+        self._routing: Optional[_Routing] = None
+        self._route_mode = False
+
+    @classmethod
+    def _deferred(cls, raw_sel, routing: _Routing, route_mode: bool, w) -> "CVMMSel":
+        s = cls(raw_sel, None, None, None, w)
+        s._routing = routing
+        s._route_mode = route_mode
+        return s
+
+    def _pending(self) -> bool:
+        return self._routing is not None and self._sel is None
+
+    def _resolve(self, n_experts: Optional[int] = None) -> None:
+        if not self._pending():
+            return
+        r = self._routing
+        ssel, perm, tok, offsets = r.get(n_experts) if n_experts is not None else r.default()
+        sel = ssel.view(self.raw_sel.shape)
+        sel._cvmm_offsets = {e: v[3] for e, v in r.by_e.items()}
+        sel._cvmm_i32 = ssel
+        self._sel = sel
+        if self._route_mode:
+            self._sel_index, self._out_index = perm, None
+        else:
+            self._sel_index, self._out_index = tok, perm
+
+    @property
+    def sel(self):
+        self._resolve()
+        return self._sel
+
+    @sel.setter
+    def sel(self, v):
+        self._resolve()
+        self._sel = v
+
+    @property
+    def sel_index(self):
+        self._resolve()
+        return self._sel_index
+
+    @sel_index.setter
+    def sel_index(self, v):
+        self._resolve()
+        self._sel_index = v
+
+    @property
+    def out_index(self):
+        self._resolve()
+        return self._out_index
+
+    @out_index.setter
+    def out_index(self, v):
+        self._resolve()
+        self._out_index = v
+
+    def clone(self) -> "CVMMSel":
+        if self._pending():
+            return CVMMSel._deferred(self.raw_sel, self._routing, self._route_mode, self.reduction_weight)
+        return CVMMSel(self.raw_sel, self.sel, self.sel_index, self.out_index, self.reduction_weight)
+
+    def __repr__(self) -> str:
+        if self._pending():
+            return f"CVMMSel(raw_sel={tuple(self.raw_sel.shape)}, pending sort, route_input={self._route_mode})"
+        return (f"CVMMSel(raw_sel={self.raw_sel!r}, sel={self._sel!r}, sel_index={self._sel_index!r}, "
+                f"out_index={self._out_index!r}, reduction_weight={self.reduction_weight!r})")
+
+
+def cvmm_prepare_sel(sel: torch.Tensor, n_experts: int) -> CVMMSel:
+    """cvmm.py:24-27: sort the flattened ids; sel_index = sorting permutation."""
+    _require_device(sel, "sel")
+    raw = _flat_int32(sel)
+    ssel, perm, _, offsets = _Routing(raw, 1).get(n_experts)
+    s = ssel.view(sel.shape)
+    s._cvmm_offsets = {n_experts: offsets}
+    s._cvmm_i32 = ssel
+    return CVMMSel(raw.view(sel.shape), s, perm, None)
+
+
+def cvmm_prepare_sel2(sel: Union[torch.Tensor, CVMMSel], w: Optional[torch.Tensor] = None,
+                      route_input: bool = False) -> CVMMSel:
+    """cvmm.py:1786-1803.  Token input: sel_index = perm // top_k, out_index = perm.
+    Route input: sel_index = perm, out_index = None.  A CVMMSel argument is
+    re-wrapped (route input takes the up-projection's out_index, :1788-1792)."""
+    if isinstance(sel, CVMMSel):
+        if sel._pending():
+            # token-mode parent: out_index = perm; route-mode parent: sel_index = perm
+            return CVMMSel._deferred(sel.raw_sel, sel._routing, True if route_input else sel._route_mode, w)
+        if route_input:
+            route_index = sel.out_index if sel.out_index is not None else sel.sel_index
+            return CVMMSel(sel.raw_sel, sel.sel, route_index, None, w)
+        return CVMMSel(sel.raw_sel, sel.sel, sel.sel_index, sel.out_index, w)
+
+    _require_device(sel, "sel")
+    n_per_batch = sel.shape[-1]
+    raw = _flat_int32(sel)
+    return CVMMSel._deferred(raw.view(sel.shape), _Routing(raw, n_per_batch), route_input, w)
+
+
+# ----------------------------------------------------------------------------
+# launch helpers
+# ----------------------------------------------------------------------------
+
+def _storage_for(t: torch.Tensor, op: torch.dtype) -> torch.Tensor:
+    """Kernels read fp32 or op-dtype storage; other float types are widened to
+    fp32 (exact), which leaves the in-kernel rounding to the op dtype unchanged."""
+    if t.dtype == torch.float32 or (op != torch.float32 and t.dtype == op):
+        return t
+    return t.float()
+
+
+def _rows(t: torch.Tensor, width: int) -> torch.Tensor:
+    f = t.reshape(-1, width)
+    if f.stride(-1) != 1 or (f.shape[0] > 1 and f.stride(0) < width):
+        f = f.contiguous()
+    return f
+
+
+def _keys_view(keys: torch.Tensor) -> torch.Tensor:
+    if keys.stride(2) == 1 or keys.stride(1) == 1:
+        return keys
+    return keys.contiguous()
+
+
+def _i64(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    f = t.reshape(-1)
+    if f.dtype != torch.int64:
+        f = f.to(torch.int64)
+    return f.contiguous()
+
+
+def _workspace(nbytes: int, device) -> Optional[torch.Tensor]:
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+
+
+def _forward(x, sel_index, sel, keys, out_index, rw, op_dtype):
+    for t, name in ((x, "x"), (keys, "keys"), (sel, "sel"), (sel_index, "sel_index")):
+        _require_device(t, name)
+    n_experts, d_in, d_out = keys.shape
+    assert x.shape[-1] == keys.shape[1]                                   # cvmm.py:825
+    dev = x.device
+    lib = N.lib()
+    xf = _rows(_storage_for(x, op_dtype), d_in)
+    kv = _keys_view(_storage_for(keys, op_dtype))
+    s32 = _sorted_i32(sel)
+    R = s32.numel()
+    si = _i64(sel_index)
+    oi = _i64(out_index)
+    if si.numel() != R or (oi is not None and oi.numel() != R):
+        raise ValueError("cvmm: sel_index/out_index must have one entry per route")
+    off = _offsets_for(sel, n_experts)
+    rwf = None
+    if rw is None:
+        out_rows, out_shape = R, (*sel.shape, d_out)
+        k = 1
+    else:
+        _require_device(rw, "reduction_weight")
+        if rw.numel() != R:
+            raise ValueError("cvmm: reduction_weight must have one entry per route")
+        k = rw.shape[-1]
+        rwf = rw.reshape(-1).contiguous()
+        out_rows, out_shape = R // k, (*rw.shape[:-1], d_out)
+    out = torch.empty(out_rows, d_out, dtype=op_dtype, device=dev)
+    flags = N.FLAG_ATOMIC_REDUCE if cvmm_atomic_reduce else 0
+    od = N.dtype_id(op_dtype)
+    ws_bytes = lib.cvmm_fwd_workspace_bytes(R, n_experts, d_out, out_rows, od, 1, int(rw is not None), flags)
+    ws = _workspace(ws_bytes, dev)
+    N.check(lib.cvmm_fwd(
+        N.ptr(xf), N.dtype_id(xf.dtype), xf.shape[0], xf.stride(0),
+        N.ptr(kv), N.dtype_id(kv.dtype), n_experts, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2),
+        N.ptr(s32), N.ptr(si), N.ptr(oi), R,
+        N.ptr(off), N.ptr(rwf), N.dtype_id(rwf.dtype) if rwf is not None else 0, k,
+        od, N.ptr(out), od, out_rows, d_out,
+        flags, N.ptr(ws), ws_bytes, N.stream_of(dev)), "cvmm_fwd")
+    return out.view(out_shape)
+
+
+def _backward(ctx, grad_output, x, keys, raw_sel, sel, sel_index, out_index, rw,
+              need_grad_x, need_grad_keys, need_grad_rw):
+    op = ctx.op_type
+    n_experts, d_in, d_out = keys.shape
+    dev = x.device
+    lib = N.lib()
+    top_k = raw_sel.shape[-1] if raw_sel.ndim > 0 else 1
+    k = rw.shape[-1] if rw is not None else top_k
+    g = _rows(_storage_for(grad_output, op), d_out)
+    s32 = _sorted_i32(sel)
+    R = s32.numel()
+    si = _i64(sel_index)
+    oi = _i64(out_index)
+    off = _offsets_for(sel, n_experts)
+    rwf = rw.reshape(-1).contiguous() if rw is not None else None
+    rwd = N.dtype_id(rwf.dtype) if rwf is not None else 0
+    od = N.dtype_id(op)
+    flags = N.FLAG_ATOMIC_REDUCE if cvmm_atomic_reduce else 0
+    stream = N.stream_of(dev)
+    grad_x = grad_w = grad_rw = None
+
+    if need_grad_keys:
+        xs = _rows(_storage_for(x, op), d_in)
+        grad_w = torch.empty(keys.shape, dtype=keys.dtype, device=dev)
+        ws_bytes = lib.cvmm_bwd_w_workspace_bytes(R, n_experts, d_in, d_out, od, 1)
+        ws = _workspace(ws_bytes, dev)
+        N.check(lib.cvmm_bwd_w(
+            N.ptr(xs), N.dtype_id(xs.dtype), xs.shape[0], xs.stride(0),
+            N.ptr(g), N.dtype_id(g.dtype), g.shape[0], g.stride(0),
+            n_experts, d_in, d_out, N.ptr(s32), N.ptr(si), N.ptr(oi), R, N.ptr(off),
+            N.ptr(rwf), rwd, k, od,
+            N.ptr(grad_w), N.dtype_id(grad_w.dtype), grad_w.stride(0), grad_w.stride(1), grad_w.stride(2),
+            flags, N.ptr(ws), ws_bytes, stream), "cvmm_bwd_w")
+
+    if need_grad_x or need_grad_rw:
+        kv = _keys_view(_storage_for(keys, op))
+        xr = _rows(x, d_in)
+        gx = None
+        if need_grad_x:
+            gx = torch.empty(xr.shape, dtype=x.dtype, device=dev)
+        if need_grad_rw:
+            grad_rw = torch.empty(rw.shape, dtype=rw.dtype, device=dev)
+        gx_rows = gx.shape[0] if gx is not None else xr.shape[0]
+        ws_bytes = lib.cvmm_bwd_x_workspace_bytes(
+            R, n_experts, d_in, gx_rows, 1, int(rw is not None), int(oi is not None), k,
+            N.dtype_id(x.dtype), od, int(need_grad_rw), flags)
+        ws = _workspace(ws_bytes, dev)
+        N.check(lib.cvmm_bwd_x(
+            N.ptr(g), N.dtype_id(g.dtype), g.shape[0], g.stride(0),
+            N.ptr(kv), N.dtype_id(kv.dtype), n_experts, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2),
+            N.ptr(s32), N.ptr(si), N.ptr(oi), R, N.ptr(off), N.ptr(rwf), rwd, k,
+            N.ptr(xr), N.dtype_id(xr.dtype), xr.shape[0], xr.stride(0), od,
+            N.ptr(gx), N.dtype_id(x.dtype), gx_rows, d_in,
+            N.ptr(grad_rw), N.dtype_id(rw.dtype) if rw is not None else 0,
+            flags, N.ptr(ws), ws_bytes, stream), "cvmm_bwd_x")
+        if gx is not None:
+            grad_x = gx.view(x.shape)
+    return grad_x, grad_w, grad_rw
+
+
+class CVMM(torch.autograd.Function):
+    """cvmm.py:1521-1755: forward = routed GEMM (+ weighted top-k combine),
+    backward = grad x / grad keys / grad reduction weight."""
+
+    warned = False
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, raw_sel: torch.Tensor, sel_index: torch.Tensor, sel: torch.Tensor,
+                keys: torch.Tensor, out_index: Optional[torch.Tensor] = None,
+                reduction_weight: Optional[torch.Tensor] = None):
+        ctx.save_for_backward(x, keys, raw_sel, sel, sel_index, out_index, reduction_weight)
+        out_type = get_dtype()
+        res = _forward(x, sel_index, sel, keys, out_index, reduction_weight, out_type)
+        ctx.op_type = out_type
+        ctx.keys_type = keys.dtype
+        ctx.dtype = out_type
+        return res
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        x, keys, raw_sel, sel, sel_index, out_index, reduction_weight = ctx.saved_tensors
+        need_grad_x = ctx.needs_input_grad[0]
+        need_grad_keys = ctx.needs_input_grad[4]
+        need_grad_rw = ctx.needs_input_grad[6] and reduction_weight is not None
+        grad_x, grad_w, grad_rw = _backward(ctx, grad_output, x, keys, raw_sel, sel, sel_index, out_index,
+                                            reduction_weight, need_grad_x, need_grad_keys, need_grad_rw)
+        return grad_x, None, None, None, grad_w, None, grad_rw
+
+
+known_shapes = set()
+
+
+def create_kernels() -> None:
+    """Load libcvmm_hip.so (idempotent); raises if it is missing."""
+    global cvmm_expert_offsets_call
+    N.lib()
+    if cvmm_expert_offsets_call is None:
+        cvmm_expert_offsets_call = cvmm_expert_offsets
+
+
+def cvmm(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.Tensor) -> torch.Tensor:
+    """cvmm.py:1759-1783."""
+    create_kernels()
+    if not isinstance(sel, CVMMSel):
+        sel = cvmm_prepare_sel(sel, keys.shape[0])
+    sel._resolve(keys.shape[0])
+    if cvmm_log_shapes:
+        sh = (x.shape, keys.shape)
+        if sh not in known_shapes:
+            print("New shape:", sh)
+            known_shapes.add(sh)
+    return CVMM.apply(x, sel.raw_sel, sel.sel_index, sel.sel, keys, sel.out_index, sel.reduction_weight)

@@ -1,0 +1,461 @@
+// C ABI of libcvmm_hip.so: argument checking, workspace carving and the
+// per-case choice of kernels (the reference's CVMM.backward dispatcher,
+// cvmm.py:1552-1755, reduced to what the selector layout decides).
+#include <string>
+#include <cstdio>
+#include <cstdarg>
+
+#include "cvmm_common.h"
+#include "cvmm_internal.h"
+#include "../../include/cvmm_hip.h"
+
+namespace cvmm {
+hipError_t launch_routed_gemm_bf16(const GemmParams& p, hipStream_t stream);
+hipError_t launch_routed_gemm_f16(const GemmParams& p, hipStream_t stream);
+hipError_t launch_routed_gemm_f32(const GemmParams& p, hipStream_t stream);
+hipError_t launch_wgrad_bf16(const WgradParams& p, hipStream_t stream);
+hipError_t launch_wgrad_f16(const WgradParams& p, hipStream_t stream);
+hipError_t launch_wgrad_f32(const WgradParams& p, hipStream_t stream);
+
+hipError_t launch_routed_gemm(const GemmParams& p, int32_t op, hipStream_t s) {
+  if (op == kBF16) return launch_routed_gemm_bf16(p, s);
+  if (op == kF16) return launch_routed_gemm_f16(p, s);
+  if (op == kF32) return launch_routed_gemm_f32(p, s);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_wgrad(const WgradParams& p, int32_t op, hipStream_t s) {
+  if (op == kBF16) return launch_wgrad_bf16(p, s);
+  if (op == kF16) return launch_wgrad_f16(p, s);
+  if (op == kF32) return launch_wgrad_f32(p, s);
+  return hipErrorInvalidValue;
+}
+
+// m-tile height the routed GEMM uses for output width N (kept in sync with
+// launch_routed_gemm_op: 256x64 tiles for N <= 64, else 128x128).
+int routed_gemm_bm(int64_t N) { return N <= 64 ? 256 : 128; }
+
+void wgrad_geometry(int64_t M, int64_t N, int64_t n_routes, int32_t n_experts, int32_t op_dtype, int64_t* split,
+                    int64_t* grid_chunks, int64_t* max_slots, int64_t* tiles_mn) {
+  const int64_t bk = op_dtype == kF32 ? 32 : 64;
+  // chunk = max(1024, 2 * mean routes per expert): balanced loads stay one
+  // chunk per expert; an expert above twice the mean is split.
+  int64_t s = n_experts > 0 ? (2 * n_routes + n_experts - 1) / n_experts : n_routes;
+  if (s < 1024) s = 1024;
+  s = (s + bk - 1) / bk * bk;
+  *split = s;
+  *grid_chunks = (n_routes + s - 1) / s + n_experts;
+  // a multi-chunk expert has > s routes and < 2*count/s chunks
+  *max_slots = (2 * n_routes) / s + 1;
+  int bm, bn;
+  wgrad_tile(M, N, &bm, &bn);
+  *tiles_mn = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+}
+
+static int64_t wgrad_tile_elems(int64_t M, int64_t N) {
+  int bm, bn;
+  wgrad_tile(M, N, &bm, &bn);
+  return (int64_t)bm * bn;
+}
+
+}  // namespace cvmm
+
+using namespace cvmm;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int check_launch(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(CVMM_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return CVMM_OK;
+}
+
+bool valid_dtype(int32_t d) { return d == kF32 || d == kF16 || d == kBF16; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Workspace carving: fixed-order list of 256-byte aligned regions.
+struct Carver {
+  char* base;
+  size_t used = 0;
+  explicit Carver(void* b) : base(static_cast<char*>(b)) {}
+  void* take(size_t bytes) {
+    void* p = base ? base + used : nullptr;
+    used = align_up(used + bytes, 256);
+    return p;
+  }
+};
+
+// Route-major buffer dtype / reduce rules shared by the workspace query and
+// the compute entry point.
+bool reduce_needed(int32_t weighted, int32_t token_input, int64_t top_k) {
+  return token_input && (weighted || top_k > 1);
+}
+
+int64_t ntiles_of(int64_t n, int64_t bn) { return (n + bn - 1) / bn; }
+
+// n-tile width of the routed GEMM for output width n (256x64 tiles when narrow).
+int64_t gemm_bn(int64_t n) { return n <= 64 ? 64 : 128; }
+
+}  // namespace
+
+extern "C" {
+
+const char* cvmm_last_error(void) { return g_err.c_str(); }
+
+int cvmm_abi_version(void) { return 1; }
+
+// ---------------------------------------------------------------------------
+size_t cvmm_sort_workspace_bytes(int64_t n_routes, int32_t n_experts) {
+  return sort_workspace_bytes(n_routes, n_experts);
+}
+
+int cvmm_sort_routes(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts, int64_t top_k,
+                     int32_t* sorted_sel, int64_t* perm, int64_t* token_index, int64_t* offsets,
+                     int32_t* n_invalid, void* workspace, size_t workspace_bytes, void* stream) {
+  if (n_experts <= 0) return fail(CVMM_ERR_INVALID, "cvmm_sort_routes: n_experts must be > 0 (got %d)", n_experts);
+  if (n_experts > 32767) return fail(CVMM_ERR_UNSUPPORTED, "cvmm_sort_routes: at most 32767 experts (got %d)", n_experts);
+  if (n_routes < 0 || n_routes > 0x7fffffffll)
+    return fail(CVMM_ERR_INVALID, "cvmm_sort_routes: n_routes out of range (%lld)", (long long)n_routes);
+  if (top_k <= 0) return fail(CVMM_ERR_INVALID, "cvmm_sort_routes: top_k must be > 0");
+  if (offsets == nullptr) return fail(CVMM_ERR_INVALID, "cvmm_sort_routes: offsets is NULL");
+  hipStream_t s = (hipStream_t)stream;
+  if (n_routes == 0) {
+    if (n_invalid) { int r = check_launch(launch_fill_zero(n_invalid, 4, s), "fill"); if (r) return r; }
+    return check_launch(launch_fill_zero(offsets, (size_t)n_experts * 8, s), "cvmm_sort_routes(fill)");
+  }
+  if (!sel || !sorted_sel || !perm) return fail(CVMM_ERR_INVALID, "cvmm_sort_routes: NULL pointer");
+  if (workspace == nullptr || workspace_bytes < sort_workspace_bytes(n_routes, n_experts))
+    return fail(CVMM_ERR_WORKSPACE, "cvmm_sort_routes: workspace too small (%zu < %zu)", workspace_bytes,
+                sort_workspace_bytes(n_routes, n_experts));
+  return check_launch(launch_sort_routes(sel, sel_is_int64 != 0, n_routes, n_experts, top_k, sorted_sel, perm,
+                                         token_index, offsets, n_invalid, workspace, s),
+                      "cvmm_sort_routes");
+}
+
+int cvmm_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_experts, int64_t* offsets,
+                        void* stream) {
+  if (n_experts <= 0 || offsets == nullptr) return fail(CVMM_ERR_INVALID, "cvmm_expert_offsets: bad arguments");
+  if (n_routes > 0 && sorted_sel == nullptr) return fail(CVMM_ERR_INVALID, "cvmm_expert_offsets: sorted_sel NULL");
+  return check_launch(launch_expert_offsets(sorted_sel, n_routes, n_experts, offsets, (hipStream_t)stream),
+                      "cvmm_expert_offsets");
+}
+
+// ---------------------------------------------------------------------------
+size_t cvmm_fwd_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_out, int64_t out_rows,
+                                int32_t out_dtype, int32_t has_offsets, int32_t weighted, int32_t flags) {
+  Carver c(nullptr);
+  if (!has_offsets) c.take((size_t)n_experts * 8);
+  if (weighted) {
+    if (flags & CVMM_FLAG_ATOMIC_REDUCE) c.take((size_t)out_rows * d_out * 4);
+    else c.take((size_t)n_routes * d_out * dtype_size(out_dtype));
+  }
+  return c.used;
+}
+
+int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const void* keys, int32_t keys_dtype,
+             int32_t n_experts, int64_t d_in, int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj,
+             const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index, int64_t n_routes,
+             const int64_t* offsets, const void* rw, int32_t rw_dtype, int64_t reduce_k, int32_t op_dtype,
+             void* out, int32_t out_dtype, int64_t out_rows, int64_t out_ld, int32_t flags, void* workspace,
+             size_t workspace_bytes, void* stream) {
+  if (!valid_dtype(x_dtype) || !valid_dtype(keys_dtype) || !valid_dtype(op_dtype) || !valid_dtype(out_dtype) ||
+      (rw && !valid_dtype(rw_dtype)))
+    return fail(CVMM_ERR_INVALID, "cvmm_fwd: invalid dtype id");
+  if (n_experts <= 0 || d_in <= 0 || d_out <= 0 || n_routes < 0)
+    return fail(CVMM_ERR_INVALID, "cvmm_fwd: bad sizes (E=%d, d_in=%lld, d_out=%lld, R=%lld)", n_experts,
+                (long long)d_in, (long long)d_out, (long long)n_routes);
+  if (x_ld < d_in || out_ld < d_out) return fail(CVMM_ERR_INVALID, "cvmm_fwd: row stride smaller than width");
+  const bool weighted = rw != nullptr;
+  if (weighted && (reduce_k <= 0 || n_routes % reduce_k != 0 || out_rows != n_routes / reduce_k))
+    return fail(CVMM_ERR_INVALID, "cvmm_fwd: weighted output needs out_rows = R / reduce_k");
+  if (!weighted && out_rows != n_routes) return fail(CVMM_ERR_INVALID, "cvmm_fwd: out_rows must equal R");
+  const size_t need = cvmm_fwd_workspace_bytes(n_routes, n_experts, d_out, out_rows, out_dtype, offsets != nullptr,
+                                               weighted, flags);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(CVMM_ERR_WORKSPACE, "cvmm_fwd: workspace too small (%zu < %zu)", workspace_bytes, need);
+  if (n_routes == 0) return CVMM_OK;
+  if (!x || !keys || !sorted_sel || !sel_index || !out) return fail(CVMM_ERR_INVALID, "cvmm_fwd: NULL pointer");
+  if (op_dtype != kF32 && !((x_dtype == kF32 || x_dtype == op_dtype) && (keys_dtype == kF32 || keys_dtype == op_dtype)))
+    return fail(CVMM_ERR_UNSUPPORTED, "cvmm_fwd: x/keys storage must be fp32 or the op dtype");
+  if (op_dtype == kF32 && (x_dtype != kF32 || keys_dtype != kF32))
+    return fail(CVMM_ERR_UNSUPPORTED, "cvmm_fwd: fp32 op needs fp32 x and keys");
+  hipStream_t s = (hipStream_t)stream;
+  Carver c(workspace);
+  const int64_t* offs = offsets;
+  if (!offs) {
+    int64_t* o = (int64_t*)c.take((size_t)n_experts * 8);
+    int r = check_launch(launch_expert_offsets(sorted_sel, n_routes, n_experts, o, s), "cvmm_fwd(offsets)");
+    if (r) return r;
+    offs = o;
+  }
+  const int64_t* rp = out_index ? out_index : sel_index;
+
+  GemmParams p{};
+  p.a = x; p.a_dtype = x_dtype; p.a_ld = x_ld; p.a_rows = x_rows;
+  p.a_vec = aligned16(x) && (x_ld * (int64_t)dtype_size(x_dtype)) % 16 == 0;
+  p.a_idx = sel_index; p.a_div = 1;
+  p.b = keys; p.b_dtype = keys_dtype; p.b_se = k_se; p.b_sk = k_si; p.b_sn = k_sj;
+  const int64_t bsz = (int64_t)dtype_size(keys_dtype);
+  p.b_vec = aligned16(keys) && (k_se * bsz) % 16 == 0 &&
+            ((k_sj == 1 && (k_si * bsz) % 16 == 0) || (k_sj != 1 && k_si == 1 && (k_sj * bsz) % 16 == 0));
+  p.K = d_in; p.N = d_out;
+  p.offsets = offs; p.n_experts = n_experts; p.n_routes = n_routes;
+  const int64_t bm = routed_gemm_bm(d_out);
+  p.grid_tiles = (n_routes + bm - 1) / bm + (n_experts < n_routes ? n_experts : n_routes);
+  p.o_idx = rp; p.o_div = 1;
+  p.val_dtype = out_dtype;
+  p.prod_dtype = -1;
+  p.w_idx = rp;
+
+  if (!weighted) {
+    p.epi = kEpiStore; p.out = out; p.out_dtype = out_dtype; p.out_ld = out_ld; p.out_rows = out_rows;
+    return check_launch(launch_routed_gemm(p, op_dtype, s), "cvmm_fwd(gemm)");
+  }
+  if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
+    // fused combine: y rounded to the output dtype, times rnd_out(w), fp32 atomics per token row
+    float* acc = (float*)c.take((size_t)out_rows * d_out * 4);
+    int r = check_launch(launch_fill_zero(acc, (size_t)out_rows * d_out * 4, s), "cvmm_fwd(zero)");
+    if (r) return r;
+    p.epi = kEpiAtomic; p.out = acc; p.out_dtype = kF32; p.out_ld = d_out; p.out_rows = out_rows;
+    p.o_div = reduce_k;
+    p.w = rw; p.w_dtype = rw_dtype; p.w_round = out_dtype;
+    r = check_launch(launch_routed_gemm(p, op_dtype, s), "cvmm_fwd(gemm)");
+    if (r) return r;
+    return check_launch(launch_cast_rows(acc, d_out, out_rows, d_out, -1, out, out_dtype, out_ld, s),
+                        "cvmm_fwd(cast)");
+  }
+  // route-ordered y in the output dtype, then the ordered per-token combine
+  void* ybuf = c.take((size_t)n_routes * d_out * dtype_size(out_dtype));
+  p.epi = kEpiStore; p.out = ybuf; p.out_dtype = out_dtype; p.out_ld = d_out; p.out_rows = n_routes;
+  int r = check_launch(launch_routed_gemm(p, op_dtype, s), "cvmm_fwd(gemm)");
+  if (r) return r;
+  return check_launch(launch_combine_rows(ybuf, out_dtype, d_out, rw, rw_dtype, out_dtype, out_rows, reduce_k, d_out,
+                                          out_dtype, out, out_dtype, out_ld, s),
+                      "cvmm_fwd(combine)");
+}
+
+// ---------------------------------------------------------------------------
+size_t cvmm_bwd_x_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t grad_x_rows,
+                                  int32_t has_offsets, int32_t weighted, int32_t token_input, int64_t top_k,
+                                  int32_t grad_x_dtype, int32_t op_dtype, int32_t need_grad_rw, int32_t flags) {
+  Carver c(nullptr);
+  if (!has_offsets) c.take((size_t)n_experts * 8);
+  if (reduce_needed(weighted, token_input, top_k)) {
+    if (flags & CVMM_FLAG_ATOMIC_REDUCE) c.take((size_t)grad_x_rows * d_in * 4);
+    else c.take((size_t)n_routes * d_in * dtype_size(weighted ? op_dtype : grad_x_dtype));
+  }
+  if (weighted && need_grad_rw) c.take((size_t)n_routes * ntiles_of(d_in, gemm_bn(d_in)) * 4);
+  return c.used;
+}
+
+int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t grad_ld, const void* keys,
+               int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out, int64_t k_se, int64_t k_si,
+               int64_t k_sj, const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index,
+               int64_t n_routes, const int64_t* offsets, const void* rw, int32_t rw_dtype, int64_t top_k,
+               const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, int32_t op_dtype, void* grad_x,
+               int32_t grad_x_dtype, int64_t grad_x_rows, int64_t grad_x_ld, void* grad_rw, int32_t grad_rw_dtype,
+               int32_t flags, void* workspace, size_t workspace_bytes, void* stream) {
+  const bool weighted = rw != nullptr;
+  const bool token_input = out_index != nullptr;
+  if (!valid_dtype(grad_dtype) || !valid_dtype(keys_dtype) || !valid_dtype(op_dtype) ||
+      (grad_x && !valid_dtype(grad_x_dtype)) || (weighted && !valid_dtype(rw_dtype)) ||
+      (grad_rw && !valid_dtype(grad_rw_dtype)) || (x && !valid_dtype(x_dtype)))
+    return fail(CVMM_ERR_INVALID, "cvmm_bwd_x: invalid dtype id");
+  if (n_experts <= 0 || d_in <= 0 || d_out <= 0 || n_routes < 0 || top_k <= 0)
+    return fail(CVMM_ERR_INVALID, "cvmm_bwd_x: bad sizes");
+  if (grad_ld < d_out || (grad_x && grad_x_ld < d_in)) return fail(CVMM_ERR_INVALID, "cvmm_bwd_x: bad row stride");
+  if (grad_rw && !weighted) return fail(CVMM_ERR_INVALID, "cvmm_bwd_x: grad_rw needs reduction_weight");
+  if (grad_rw && (!x || x_ld < d_in)) return fail(CVMM_ERR_INVALID, "cvmm_bwd_x: grad_rw needs x");
+  if (weighted && n_routes % top_k != 0) return fail(CVMM_ERR_INVALID, "cvmm_bwd_x: R not a multiple of top_k");
+  const bool reduce = reduce_needed(weighted, token_input, top_k);
+  if (grad_x) {
+    const int64_t want = reduce ? n_routes / top_k : n_routes;
+    if (grad_x_rows != want)
+      return fail(CVMM_ERR_INVALID, "cvmm_bwd_x: grad_x has %lld rows, expected %lld", (long long)grad_x_rows,
+                  (long long)want);
+  }
+  const size_t need = cvmm_bwd_x_workspace_bytes(n_routes, n_experts, d_in, grad_x_rows, offsets != nullptr,
+                                                 weighted, token_input, top_k, grad_x_dtype, op_dtype,
+                                                 grad_rw != nullptr, flags);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(CVMM_ERR_WORKSPACE, "cvmm_bwd_x: workspace too small (%zu < %zu)", workspace_bytes, need);
+  if (n_routes == 0 || (!grad_x && !grad_rw)) return CVMM_OK;
+  if (!grad || !keys || !sorted_sel || !sel_index) return fail(CVMM_ERR_INVALID, "cvmm_bwd_x: NULL pointer");
+  if (op_dtype != kF32 && !((grad_dtype == kF32 || grad_dtype == op_dtype) && (keys_dtype == kF32 || keys_dtype == op_dtype)))
+    return fail(CVMM_ERR_UNSUPPORTED, "cvmm_bwd_x: grad/keys storage must be fp32 or the op dtype");
+  if (op_dtype == kF32 && (grad_dtype != kF32 || keys_dtype != kF32))
+    return fail(CVMM_ERR_UNSUPPORTED, "cvmm_bwd_x: fp32 op needs fp32 grad and keys");
+
+  hipStream_t s = (hipStream_t)stream;
+  Carver c(workspace);
+  const int64_t* offs = offsets;
+  if (!offs) {
+    int64_t* o = (int64_t*)c.take((size_t)n_experts * 8);
+    int r = check_launch(launch_expert_offsets(sorted_sel, n_routes, n_experts, o, s), "cvmm_bwd_x(offsets)");
+    if (r) return r;
+    offs = o;
+  }
+  const int64_t* rp = token_input ? out_index : sel_index;
+
+  // grad @ keys[e]^T: K = d_out, N = d_in, B[k][n] = keys[e][n][k]
+  GemmParams p{};
+  p.a = grad; p.a_dtype = grad_dtype; p.a_ld = grad_ld; p.a_rows = grad_rows;
+  p.a_vec = aligned16(grad) && (grad_ld * (int64_t)dtype_size(grad_dtype)) % 16 == 0;
+  p.a_idx = rp; p.a_div = weighted ? top_k : 1;
+  p.b = keys; p.b_dtype = keys_dtype; p.b_se = k_se; p.b_sk = k_sj; p.b_sn = k_si;
+  const int64_t bsz = (int64_t)dtype_size(keys_dtype);
+  p.b_vec = aligned16(keys) && (k_se * bsz) % 16 == 0 &&
+            ((k_si == 1 && (k_sj * bsz) % 16 == 0) || (k_si != 1 && k_sj == 1 && (k_si * bsz) % 16 == 0));
+  p.K = d_out; p.N = d_in;
+  p.offsets = offs; p.n_experts = n_experts; p.n_routes = n_routes;
+  const int64_t bm = routed_gemm_bm(d_in);
+  p.grid_tiles = (n_routes + bm - 1) / bm + (n_experts < n_routes ? n_experts : n_routes);
+  p.o_idx = rp; p.o_div = 1;
+  p.w_idx = rp;
+  p.prod_dtype = -1;
+
+  void* route_buf = nullptr;
+  float* acc = nullptr;
+  if (grad_x) {
+    if (!reduce) {
+      p.epi = kEpiStore; p.out = grad_x; p.out_dtype = grad_x_dtype; p.out_ld = grad_x_ld; p.out_rows = grad_x_rows;
+      if (weighted) {  // route-major weighted: rnd_op(rnd_op(g) * rnd_op(w))
+        p.val_dtype = op_dtype; p.w = rw; p.w_dtype = rw_dtype; p.w_round = op_dtype; p.prod_dtype = op_dtype;
+      } else {
+        p.val_dtype = grad_x_dtype;
+      }
+    } else if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
+      acc = (float*)c.take((size_t)grad_x_rows * d_in * 4);
+      int r = check_launch(launch_fill_zero(acc, (size_t)grad_x_rows * d_in * 4, s), "cvmm_bwd_x(zero)");
+      if (r) return r;
+      p.epi = kEpiAtomic; p.out = acc; p.out_dtype = kF32; p.out_ld = d_in; p.out_rows = grad_x_rows;
+      p.o_div = top_k;
+      if (weighted) { p.val_dtype = op_dtype; p.w = rw; p.w_dtype = rw_dtype; p.w_round = op_dtype; }
+      else p.val_dtype = grad_x_dtype;
+    } else {
+      const int32_t bdt = weighted ? op_dtype : grad_x_dtype;
+      route_buf = c.take((size_t)n_routes * d_in * dtype_size(bdt));
+      p.epi = kEpiStore; p.out = route_buf; p.out_dtype = bdt; p.out_ld = d_in; p.out_rows = n_routes;
+      p.val_dtype = bdt;
+    }
+  } else {
+    p.epi = kEpiStore; p.out = nullptr;
+  }
+
+  float* dg_part = nullptr;
+  const int64_t dg_nt = ntiles_of(d_in, gemm_bn(d_in));
+  if (weighted && grad_rw) {
+    dg_part = (float*)c.take((size_t)n_routes * dg_nt * 4);
+    int r = check_launch(launch_fill_zero(dg_part, (size_t)n_routes * dg_nt * 4, s), "cvmm_bwd_x(zero dg)");
+    if (r) return r;
+    p.dg = dg_part; p.dg_ntiles = (int32_t)dg_nt;
+    p.dg_x = x; p.dg_x_dtype = x_dtype; p.dg_x_ld = x_ld; p.dg_x_rows = x_rows; p.dg_x_idx = sel_index;
+    p.dg_val_dtype = op_dtype;
+  }
+
+  int r = check_launch(launch_routed_gemm(p, op_dtype, s), "cvmm_bwd_x(gemm)");
+  if (r) return r;
+  if (grad_x && reduce) {
+    if (acc) {
+      r = check_launch(launch_cast_rows(acc, d_in, grad_x_rows, d_in, weighted ? op_dtype : -1, grad_x,
+                                        grad_x_dtype, grad_x_ld, s),
+                       "cvmm_bwd_x(cast)");
+    } else {
+      const int32_t bdt = weighted ? op_dtype : grad_x_dtype;
+      r = check_launch(launch_combine_rows(route_buf, bdt, d_in, weighted ? rw : nullptr, rw_dtype, op_dtype,
+                                           grad_x_rows, top_k, d_in, weighted ? op_dtype : -1, grad_x, grad_x_dtype,
+                                           grad_x_ld, s),
+                       "cvmm_bwd_x(combine)");
+    }
+    if (r) return r;
+  }
+  if (dg_part) {
+    r = check_launch(launch_sum_partials(dg_part, n_routes, (int32_t)dg_nt, grad_rw, grad_rw_dtype, s),
+                     "cvmm_bwd_x(dgate)");
+    if (r) return r;
+  }
+  return CVMM_OK;
+}
+
+// ---------------------------------------------------------------------------
+size_t cvmm_bwd_w_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out,
+                                  int32_t op_dtype, int32_t has_offsets) {
+  int64_t split, grid_chunks, max_slots, tiles;
+  wgrad_geometry(d_in, d_out, n_routes, n_experts, op_dtype, &split, &grid_chunks, &max_slots, &tiles);
+  Carver c(nullptr);
+  if (!has_offsets) c.take((size_t)n_experts * 8);
+  c.take((size_t)n_experts * tiles * 4);
+  c.take((size_t)max_slots * tiles * wgrad_tile_elems(d_in, d_out) * 4);
+  return c.used;
+}
+
+int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const void* grad, int32_t grad_dtype,
+               int64_t grad_rows, int64_t grad_ld, int32_t n_experts, int64_t d_in, int64_t d_out,
+               const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index, int64_t n_routes,
+               const int64_t* offsets, const void* rw, int32_t rw_dtype, int64_t top_k, int32_t op_dtype,
+               void* grad_keys, int32_t grad_keys_dtype, int64_t gk_se, int64_t gk_si, int64_t gk_sj, int32_t flags,
+               void* workspace, size_t workspace_bytes, void* stream) {
+  (void)flags;
+  const bool weighted = rw != nullptr;
+  if (!valid_dtype(x_dtype) || !valid_dtype(grad_dtype) || !valid_dtype(op_dtype) || !valid_dtype(grad_keys_dtype) ||
+      (weighted && !valid_dtype(rw_dtype)))
+    return fail(CVMM_ERR_INVALID, "cvmm_bwd_w: invalid dtype id");
+  if (n_experts <= 0 || d_in <= 0 || d_out <= 0 || n_routes < 0 || top_k <= 0)
+    return fail(CVMM_ERR_INVALID, "cvmm_bwd_w: bad sizes");
+  if (x_ld < d_in || grad_ld < d_out) return fail(CVMM_ERR_INVALID, "cvmm_bwd_w: bad row stride");
+  if (!grad_keys) return fail(CVMM_ERR_INVALID, "cvmm_bwd_w: grad_keys NULL");
+  const size_t need = cvmm_bwd_w_workspace_bytes(n_routes, n_experts, d_in, d_out, op_dtype, offsets != nullptr);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(CVMM_ERR_WORKSPACE, "cvmm_bwd_w: workspace too small (%zu < %zu)", workspace_bytes, need);
+  if (n_routes > 0 && (!x || !grad || !sorted_sel || !sel_index))
+    return fail(CVMM_ERR_INVALID, "cvmm_bwd_w: NULL pointer");
+  if (op_dtype != kF32 && !((x_dtype == kF32 || x_dtype == op_dtype) && (grad_dtype == kF32 || grad_dtype == op_dtype)))
+    return fail(CVMM_ERR_UNSUPPORTED, "cvmm_bwd_w: x/grad storage must be fp32 or the op dtype");
+  if (op_dtype == kF32 && (x_dtype != kF32 || grad_dtype != kF32))
+    return fail(CVMM_ERR_UNSUPPORTED, "cvmm_bwd_w: fp32 op needs fp32 x and grad");
+
+  hipStream_t s = (hipStream_t)stream;
+  WgradParams p{};
+  int64_t tiles;
+  wgrad_geometry(d_in, d_out, n_routes, n_experts, op_dtype, &p.split, &p.grid_chunks, &p.max_slots, &tiles);
+  Carver c(workspace);
+  const int64_t* offs = offsets;
+  if (!offs) {
+    int64_t* o = (int64_t*)c.take((size_t)n_experts * 8);
+    int r = n_routes > 0 ? check_launch(launch_expert_offsets(sorted_sel, n_routes, n_experts, o, s), "offsets")
+                         : check_launch(launch_fill_zero(o, (size_t)n_experts * 8, s), "offsets");
+    if (r) return r;
+    offs = o;
+  }
+  p.counters = (int32_t*)c.take((size_t)n_experts * tiles * 4);
+  int r = check_launch(launch_fill_zero(p.counters, (size_t)n_experts * tiles * 4, s), "cvmm_bwd_w(zero)");
+  if (r) return r;
+  p.partial = (float*)c.take((size_t)p.max_slots * tiles * wgrad_tile_elems(d_in, d_out) * 4);
+
+  const int64_t* rp = out_index ? out_index : sel_index;
+  p.x = x; p.x_dtype = x_dtype; p.x_ld = x_ld; p.x_rows = x_rows;
+  p.x_vec = aligned16(x) && (x_ld * (int64_t)dtype_size(x_dtype)) % 16 == 0;
+  p.x_idx = sel_index;
+  p.g = grad; p.g_dtype = grad_dtype; p.g_ld = grad_ld; p.g_rows = grad_rows;
+  p.g_vec = aligned16(grad) && (grad_ld * (int64_t)dtype_size(grad_dtype)) % 16 == 0;
+  p.g_idx = rp; p.g_div = weighted ? top_k : 1;
+  p.w = rw; p.w_dtype = rw_dtype; p.w_idx = rp;
+  p.M = d_in; p.N = d_out;
+  p.offsets = offs; p.n_experts = n_experts; p.n_routes = n_routes;
+  p.dw = grad_keys; p.dw_dtype = grad_keys_dtype; p.dw_se = gk_se; p.dw_sm = gk_si; p.dw_sn = gk_sj;
+  return check_launch(launch_wgrad(p, op_dtype, s), "cvmm_bwd_w(gemm)");
+}
+
+}  // extern "C"

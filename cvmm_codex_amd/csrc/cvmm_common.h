@@ -1,0 +1,95 @@
+// Shared device/host helpers for the CVMM HIP kernels (gfx950 / CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace cvmm {
+
+// dtype ids follow the reference's dtype_to_type_id (cvmm.py:36-44).
+enum DType : int32_t { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+template <typename T> struct DTypeOf;
+template <> struct DTypeOf<float> { static constexpr int32_t value = kF32; };
+template <> struct DTypeOf<f16_t> { static constexpr int32_t value = kF16; };
+template <> struct DTypeOf<bf16_t> { static constexpr int32_t value = kBF16; };
+
+__host__ __device__ inline size_t dtype_size(int32_t dt) { return dt == kF32 ? 4 : 2; }
+
+// ---------------------------------------------------------------------------
+// conversions (RNE; gfx950 lowers float->bf16 to v_cvt_pk_bf16_f32)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16_t v) { return (float)v; }
+__device__ __forceinline__ float to_f32(f16_t v) { return (float)v; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) { return (bf16_t)v; }
+template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float v) { return (f16_t)v; }
+
+// Round a float to the storage precision of dtype `dt` (value stays a float).
+__device__ __forceinline__ float round_to(float v, int32_t dt) {
+  if (dt == kBF16) return (float)(bf16_t)v;
+  if (dt == kF16) return (float)(f16_t)v;
+  return v;
+}
+
+// Load element i of a tensor of runtime dtype `dt` as float.
+__device__ __forceinline__ float load_as_f32(const void* p, int32_t dt, int64_t i) {
+  if (dt == kBF16) return (float)((const bf16_t*)p)[i];
+  if (dt == kF16) return (float)((const f16_t*)p)[i];
+  return ((const float*)p)[i];
+}
+
+// Store float v (rounded RNE) into element i of a tensor of runtime dtype `dt`.
+__device__ __forceinline__ void store_from_f32(void* p, int32_t dt, int64_t i, float v) {
+  if (dt == kBF16) ((bf16_t*)p)[i] = (bf16_t)v;
+  else if (dt == kF16) ((f16_t*)p)[i] = (f16_t)v;
+  else ((float*)p)[i] = v;
+}
+
+// ---------------------------------------------------------------------------
+// 16-byte chunk <-> 8 (or 4) lanes of op-type values
+// ---------------------------------------------------------------------------
+union Chunk16 {
+  uint4 u;
+  float f[4];
+  bf16_t b[8];
+  f16_t h[8];
+  uint16_t s[8];
+};
+
+// Wave helpers (64-wide wavefronts).
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ int64_t wave_incl_scan(int64_t v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    int64_t o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// Map a linear workgroup id so that consecutive logical ids are dispatched to
+// the same XCD (the hardware places workgroup i on XCD i % 8).  Bijective for
+// any grid size.
+__device__ __forceinline__ int64_t xcd_remap(int64_t i, int64_t n) {
+  constexpr int kXcd = 8;
+  if (n < kXcd) return i;
+  const int64_t xcd = i % kXcd, local = i / kXcd;
+  const int64_t per = n / kXcd, rem = n % kXcd;
+  return xcd * per + (xcd < rem ? xcd : rem) + local;
+}
+
+}  // namespace cvmm

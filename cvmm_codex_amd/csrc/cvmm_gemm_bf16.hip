@@ -1,0 +1,8 @@
+// Routed GEMM instantiations for op type bf16_t (see cvmm_gemm_impl.h).
+#include "cvmm_gemm_impl.h"
+
+namespace cvmm {
+hipError_t launch_routed_gemm_bf16(const GemmParams& p, hipStream_t stream) {
+  return launch_routed_gemm_op<bf16_t>(p, stream);
+}
+}  // namespace cvmm

@@ -1,0 +1,142 @@
+// Internal launch interfaces between the C-ABI layer and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace cvmm {
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// ---------------------------------------------------------------------------
+// routed GEMM:  for every expert-sorted route p,
+//   acc[p][n] = sum_k rnd_op(A[arow(p)][k]) * rnd_op(B_e[k][n]),   e = expert of p
+// with arow(p) = a_idx[p] / a_div.  B_e[k][n] = b[e*b_se + k*b_sk + n*b_sn] with
+// either b_sn == 1 (kBNContig) or b_sk == 1 (kBKContig).
+// ---------------------------------------------------------------------------
+enum Epilogue : int32_t {
+  kEpiStore = 0,   // out[orow][n] = v            (out dtype out_dtype)
+  kEpiAtomic = 1,  // ((float*)out)[orow][n] += v (fp32 accumulation buffer)
+};
+
+struct GemmParams {
+  // A operand (gathered rows, unit column stride)
+  const void* a;
+  int32_t a_dtype;
+  int64_t a_ld, a_rows;
+  int32_t a_vec;
+  const int64_t* a_idx;
+  int64_t a_div;
+  // B operand (per-expert matrix)
+  const void* b;
+  int32_t b_dtype;
+  int64_t b_se, b_sk, b_sn;
+  int32_t b_vec;
+  int64_t K, N;
+  // route grouping
+  const int64_t* offsets;  // inclusive per-expert offsets, int64[E]
+  int32_t n_experts;
+  int64_t n_routes;
+  int64_t grid_tiles;      // m-tile slots launched (>= actual number of tiles)
+  // epilogue:  v = rnd(acc, val_dtype);  if w: v = rnd(v * rnd(w[w_idx[p]], w_round), prod_dtype)
+  int32_t epi;
+  void* out;
+  int32_t out_dtype;
+  int64_t out_ld, out_rows;
+  const int64_t* o_idx;    // orow(p) = o_idx[p] / o_div
+  int64_t o_div;
+  int32_t val_dtype;
+  const void* w;           // optional per-route scale
+  int32_t w_dtype;
+  const int64_t* w_idx;
+  int32_t w_round;
+  int32_t prod_dtype;      // -1: no rounding of the product
+  // optional routing-weight gradient: dg[w_idx[p] * dg_ntiles + n_tile] =
+  //   sum_{n in tile} rnd(acc, dg_val_dtype) * dg_x[dg_x_idx[p]][n]
+  float* dg;
+  int32_t dg_ntiles;
+  const void* dg_x;
+  int32_t dg_x_dtype;
+  int64_t dg_x_ld, dg_x_rows;
+  const int64_t* dg_x_idx;
+  int32_t dg_val_dtype;
+};
+
+// op_dtype selects the MFMA type; returns hipErrorInvalidValue on unsupported combos.
+hipError_t launch_routed_gemm(const GemmParams& p, int32_t op_dtype, hipStream_t stream);
+int routed_gemm_bm(int64_t N);
+
+// ---------------------------------------------------------------------------
+// per-expert weight gradient:
+//   dW[e][m][n] = sum_{p in e} rnd_op(X[x_idx[p]][m]) * G(p)[n]
+//   G(p)[n] = rnd_op(g[g_idx[p] / g_div][n])           (unweighted)
+//           = rnd_op(rnd_op(g[..][n]) * rnd_op(w[w_idx[p]]))  (weighted)
+// deterministic split over routes (chunks of `split` routes, fixed-order sum).
+// ---------------------------------------------------------------------------
+struct WgradParams {
+  const void* x;
+  int32_t x_dtype;
+  int64_t x_ld, x_rows;
+  int32_t x_vec;
+  const int64_t* x_idx;
+  const void* g;
+  int32_t g_dtype;
+  int64_t g_ld, g_rows;
+  int32_t g_vec;
+  const int64_t* g_idx;
+  int64_t g_div;
+  const void* w;
+  int32_t w_dtype;
+  const int64_t* w_idx;
+  int64_t M, N;
+  const int64_t* offsets;
+  int32_t n_experts;
+  int64_t n_routes;
+  int64_t split;
+  int64_t grid_chunks;
+  void* dw;
+  int32_t dw_dtype;
+  int64_t dw_se, dw_sm, dw_sn;
+  float* partial;          // [max_slots][M][N] fp32
+  int64_t max_slots;
+  int32_t* counters;       // [E][tiles_m*tiles_n], zero on entry
+};
+
+hipError_t launch_wgrad(const WgradParams& p, int32_t op_dtype, hipStream_t stream);
+
+// dW tile shape [BM x BN] for a dW of M x N: 64 wide on a narrow side.
+__host__ __device__ inline void wgrad_tile(int64_t M, int64_t N, int* bm, int* bn) {
+  if (N <= 64 && M > 64) { *bm = 256; *bn = 64; }
+  else if (M <= 64 && N > 64) { *bm = 64; *bn = 256; }
+  else { *bm = 128; *bn = 128; }
+}
+void wgrad_geometry(int64_t M, int64_t N, int64_t n_routes, int32_t n_experts, int32_t op_dtype,
+                    int64_t* split, int64_t* grid_chunks, int64_t* max_slots, int64_t* tiles_mn);
+
+// ---------------------------------------------------------------------------
+// selector preparation
+// ---------------------------------------------------------------------------
+size_t sort_workspace_bytes(int64_t n_routes, int32_t n_experts);
+hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_routes, int32_t n_experts,
+                              int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                              int64_t* offsets, int32_t* n_invalid, void* ws, hipStream_t stream);
+hipError_t launch_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_experts,
+                                 int64_t* offsets, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// small kernels
+// ---------------------------------------------------------------------------
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
+// out[t][n] = rnd(rnd(sum_j rnd(w[t*k+j], w_round) * buf[t*k+j][n], mid_dtype), out_dtype)
+hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_ld, const void* w, int32_t w_dtype,
+                               int32_t w_round, int64_t n_tokens, int64_t k, int64_t n, int32_t mid_dtype,
+                               void* out, int32_t out_dtype, int64_t out_ld, hipStream_t stream);
+// out[t][n] = rnd(rnd(acc[t][n], mid_dtype), out_dtype)
+hipError_t launch_cast_rows(const float* acc, int64_t acc_ld, int64_t rows, int64_t n, int32_t mid_dtype,
+                            void* out, int32_t out_dtype, int64_t out_ld, hipStream_t stream);
+// out[r] = rnd(sum_t part[r*ntiles + t], out_dtype)
+hipError_t launch_sum_partials(const float* part, int64_t rows, int32_t ntiles, void* out, int32_t out_dtype,
+                               hipStream_t stream);
+
+}  // namespace cvmm

@@ -1,0 +1,153 @@
+/*
+ * cvmm_hip.h -- C ABI of libcvmm_hip.so, the MI355X (gfx950) CVMM kernels.
+ *
+ * CVMM ("conditional vector-matrix multiply") is the routed grouped GEMM of
+ * MoE projections.  Every entry point takes raw device pointers, sizes,
+ * element strides, dtype ids and a hipStream_t (passed as void*), launches
+ * asynchronously on that stream and never synchronises the host.  Scratch
+ * memory is passed in by the caller; query its size with the matching
+ * *_workspace_bytes function (a NULL/short workspace is an error).
+ *
+ * Terminology (reference: RobertCsordas/cvmm_codex cvmm.py):
+ *   route            one (token, top-k slot) pair; R = tokens * top_k
+ *   sorted_sel       int32[R]  expert ids sorted ascending       (CVMMSel.sel)
+ *   sel_index        int64[R]  x row read by sorted route i      (CVMMSel.sel_index)
+ *   out_index        int64[R]  route position of sorted route i, or NULL for
+ *                              route-major input                   (CVMMSel.out_index)
+ *   route position   rp(i) = out_index ? out_index[i] : sel_index[i]
+ *   offsets          int64[E]  inclusive per-expert route counts (cumsum)
+ *   reduction_weight per-route weights indexed by route position (CVMMSel.reduction_weight)
+ *
+ * Return value: CVMM_OK (0) or an error code; cvmm_last_error() describes the
+ * last failure of the calling thread.
+ */
+#ifndef CVMM_HIP_H
+#define CVMM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype ids: the reference's dtype_to_type_id (cvmm.py:36-44) */
+#define CVMM_DTYPE_F32 0
+#define CVMM_DTYPE_F16 1
+#define CVMM_DTYPE_BF16 2
+
+#define CVMM_OK 0
+#define CVMM_ERR_INVALID 1     /* bad argument (shape, dtype, alignment, NULL) */
+#define CVMM_ERR_UNSUPPORTED 2 /* valid but not implemented (e.g. > 32767 experts) */
+#define CVMM_ERR_WORKSPACE 3   /* workspace missing or too small */
+#define CVMM_ERR_LAUNCH 4      /* HIP launch error */
+
+/* flags */
+#define CVMM_FLAG_ATOMIC_REDUCE 1 /* top-k sums (weighted combine, token grad) by fp32 atomics
+                                     instead of a route-ordered buffer + ordered row sum */
+
+/* Thread-local description of the last error. */
+const char* cvmm_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int cvmm_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Selector preparation                                                      */
+/* ------------------------------------------------------------------------ */
+
+size_t cvmm_sort_workspace_bytes(int64_t n_routes, int32_t n_experts);
+
+/* Stable counting sort of the flattened expert ids `sel` (int32 or int64).
+ * Replaces the sort in cvmm_prepare_sel (cvmm.py:24-27) and
+ * cvmm_prepare_sel2 (cvmm.py:1796-1803) plus the offsets kernel
+ * (cvmm.py:315-335).  Writes sorted_sel[R] (int32), perm[R] (int64, the
+ * stable sorting permutation), token_index[R] = perm / top_k when
+ * token_index != NULL, offsets[E] (int64 inclusive cumsum) and, when
+ * n_invalid != NULL, the number of ids outside [0, E) (those sort last and
+ * are ignored by the GEMMs). */
+int cvmm_sort_routes(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts,
+                     int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                     int64_t* offsets, int32_t* n_invalid, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* offsets[e] = #{i : sorted_sel[i] <= e}; replaces cvmm_expert_offsets
+ * (cvmm.py:1108-1120, kernel cvmm.py:315-335). */
+int cvmm_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_experts, int64_t* offsets,
+                        void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Forward: CVMM.forward (cvmm.py:1524-1550) = cvmm_triton (cvmm.py:814-867)  */
+/* + the weighted top-k combine (cvmm.py:1543-1545)                            */
+/* ------------------------------------------------------------------------ */
+
+/* y_i = rnd_out(x[sel_index[i]] @ keys[sorted_sel[i]]) for each sorted route i.
+ *  reduction_weight == NULL: out[rp(i)] = y_i            (out: [R, d_out])
+ *  otherwise:                out[t] = rnd_out(sum_j rnd_out(w[t*k+j]) * y_(t*k+j))
+ *                                                       (out: [R/reduce_k, d_out])
+ * keys element (e, i, j) is at keys[e*k_se + i*k_si + j*k_sj]; x rows are
+ * contiguous with row stride x_ld.  op_dtype is the MFMA operand type
+ * (autocast dtype or F32); x/keys are converted to it in-kernel. */
+size_t cvmm_fwd_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_out, int64_t out_rows,
+                                int32_t out_dtype, int32_t has_offsets, int32_t weighted, int32_t flags);
+int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld,
+             const void* keys, int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out,
+             int64_t k_se, int64_t k_si, int64_t k_sj,
+             const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index, int64_t n_routes,
+             const int64_t* offsets, const void* reduction_weight, int32_t rw_dtype, int64_t reduce_k,
+             int32_t op_dtype, void* out, int32_t out_dtype, int64_t out_rows, int64_t out_ld,
+             int32_t flags, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Backward, input side: grad_x and the reduction-weight gradient.          */
+/* Replaces cvmm_grouped_bwd_x_kernel (+ top-k .sum, cvmm.py:1204-1223),     */
+/* cvmm_weighted_route_bwd_x (cvmm.py:1386-1433) and the generic fallback    */
+/* (cvmm.py:1687-1753).                                                       */
+/* ------------------------------------------------------------------------ */
+
+/* g_i = grad[rp(i) / (weighted ? top_k : 1)] @ keys[e_i]^T, then
+ *  unweighted, route-major x or top_k == 1 : grad_x[rp(i)] = rnd_x(g_i)
+ *  unweighted, token x, top_k > 1          : grad_x[t] = rnd_x(sum_j rnd_x(g_(t,j)))
+ *  weighted, route-major x                 : grad_x[rp] = rnd_x(rnd_op(rnd_op(g) * rnd_op(w[rp])))
+ *  weighted, token x                       : grad_x[t] = rnd_x(rnd_op(sum_j rnd_op(w) * rnd_op(g)))
+ *  weighted (both)                          : grad_rw[rp] = <rnd_op(g_i), x[sel_index[i]]>
+ * grad_x and/or grad_rw may be NULL when not needed. */
+size_t cvmm_bwd_x_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t grad_x_rows,
+                                  int32_t has_offsets, int32_t weighted, int32_t token_input, int64_t top_k,
+                                  int32_t grad_x_dtype, int32_t op_dtype, int32_t need_grad_rw, int32_t flags);
+int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t grad_ld,
+               const void* keys, int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out,
+               int64_t k_se, int64_t k_si, int64_t k_sj,
+               const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index, int64_t n_routes,
+               const int64_t* offsets, const void* reduction_weight, int32_t rw_dtype, int64_t top_k,
+               const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, int32_t op_dtype,
+               void* grad_x, int32_t grad_x_dtype, int64_t grad_x_rows, int64_t grad_x_ld,
+               void* grad_rw, int32_t grad_rw_dtype,
+               int32_t flags, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Backward, weight side: grad_keys[e] = sum_{i in e} x_i^T G_i              */
+/* Replaces cvmm_grouped_bwd_w_gather_x_kernel (cvmm.py:481-538),            */
+/* cvmm_grouped_bwd_w_weighted_kernel (cvmm.py:541-604) and                  */
+/* cvmm_triton_backward / kernel3 (cvmm.py:1470-1518, :607-805).             */
+/* Deterministic: fixed route chunks, partials summed in chunk order.        */
+/* ------------------------------------------------------------------------ */
+
+/* x_i = rnd_op(x[sel_index[i]]), G_i = rnd_op(grad[rp(i)]) (unweighted) or
+ * rnd_op(rnd_op(grad[rp(i)/top_k]) * rnd_op(w[rp(i)])) (weighted).  Every
+ * expert's gradient is written, zeros for experts without routes. */
+size_t cvmm_bwd_w_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out,
+                                  int32_t op_dtype, int32_t has_offsets);
+int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld,
+               const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t grad_ld,
+               int32_t n_experts, int64_t d_in, int64_t d_out,
+               const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index, int64_t n_routes,
+               const int64_t* offsets, const void* reduction_weight, int32_t rw_dtype, int64_t top_k,
+               int32_t op_dtype, void* grad_keys, int32_t grad_keys_dtype, int64_t gk_se, int64_t gk_si,
+               int64_t gk_sj, int32_t flags, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CVMM_HIP_H */

@@ -1,0 +1,76 @@
+"""Host-side API semantics of cvmm_codex_amd.cvmm that need no GPU."""
+import pytest
+import torch
+
+import cvmm_codex_amd as pkg
+import cvmm_codex_amd.api as C
+
+
+def _plain_sel():
+    raw = torch.tensor([[2, 0], [1, 2]], dtype=torch.int32)
+    ssel = torch.tensor([[0, 1], [2, 2]], dtype=torch.int32)
+    perm = torch.tensor([1, 2, 0, 3])
+    return C.CVMMSel(raw, ssel, perm // 2, perm)
+
+
+def test_public_names():
+    for name in ("CVMMSel", "cvmm_prepare_sel", "cvmm_prepare_sel2", "cvmm", "CVMM", "get_dtype",
+                 "dtype_to_type_id", "create_kernels"):
+        assert hasattr(pkg, name) and hasattr(C, name)
+    for name in ("cvmm_expert_offsets_call", "cvmm_lowmem_chunk_size", "_cvmm_expert_offsets"):
+        assert hasattr(C, name)
+
+
+def test_cvmmsel_fields_and_clone():
+    s = _plain_sel()
+    c = s.clone()
+    assert c is not s
+    assert c.raw_sel is s.raw_sel and c.sel is s.sel and c.sel_index is s.sel_index
+    assert c.out_index is s.out_index and c.reduction_weight is None
+    s2 = C.CVMMSel(s.raw_sel, s.sel, s.sel_index)         # positional, defaults
+    assert s2.out_index is None and s2.reduction_weight is None
+
+
+def test_prepare_sel2_rewraps_cvmmsel():
+    """cvmm.py:1788-1792: route input takes out_index (or sel_index)."""
+    s = _plain_sel()
+    w = torch.rand(2, 2)
+    r = C.cvmm_prepare_sel2(s, w, route_input=True)
+    assert r.sel_index is s.out_index and r.out_index is None and r.reduction_weight is w
+    t = C.cvmm_prepare_sel2(s, w)
+    assert t.sel_index is s.sel_index and t.out_index is s.out_index and t.reduction_weight is w
+    rr = C.cvmm_prepare_sel2(r, None, route_input=True)  # route-major parent: sel_index
+    assert rr.sel_index is r.sel_index
+
+
+def test_cpu_tensors_are_rejected():
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        C.cvmm_prepare_sel2(torch.zeros(3, 2, dtype=torch.int64))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        C.cvmm_prepare_sel(torch.zeros(3, 2, dtype=torch.int64), 4)
+
+
+def test_dtype_ids_match_reference():
+    assert C.dtype_to_type_id(torch.float32) == 0
+    assert C.dtype_to_type_id(torch.float16) == 1
+    assert C.dtype_to_type_id(torch.bfloat16) == 2
+    with pytest.raises(ValueError):
+        C.dtype_to_type_id(torch.int8)
+
+
+def test_get_dtype_follows_autocast():
+    assert C.get_dtype() == torch.float32
+
+
+def test_storage_conversion_rules():
+    f16 = torch.zeros(2, dtype=torch.float16)
+    bf = torch.zeros(2, dtype=torch.bfloat16)
+    assert C._storage_for(bf, torch.bfloat16) is bf
+    assert C._storage_for(f16, torch.bfloat16).dtype == torch.float32
+    assert C._storage_for(bf, torch.float32).dtype == torch.float32
+    k = torch.zeros(3, 4, 5).transpose(1, 2)
+    assert C._keys_view(k) is k                      # unit stride on d_in
+    k2 = torch.zeros(3, 4, 5).permute(2, 0, 1).contiguous().permute(1, 2, 0)
+    assert C._keys_view(k2) is k2
+    k3 = torch.zeros(5, 4, 3).permute(2, 1, 0)[:, ::2, ::2]
+    assert C._keys_view(k3).is_contiguous()

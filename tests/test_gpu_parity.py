@@ -1,0 +1,340 @@
+"""GPU parity of the HIP CVMM path against the CPU oracle and the golden
+fixtures.  Tolerances: max|a-b|/max|b| <= 1e-4 in fp32 mode and <= 2e-2 in
+bf16-AMP mode, plus the reference harness's own
+elementwise (atol, rtol) table against the exact fp64 fixtures
+(benchmark_correctness_original.py:47-66)."""
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+import cvmm_codex_amd.api as C
+from oracle import cvmm_oracle as O
+from tests import golden_data as G
+from tests import gpu_util as U
+
+pytestmark = pytest.mark.gpu
+
+FIXTURES = G.fixtures()
+
+
+def _fixture_tensors(fx):
+    dt = U.TORCH_DT
+    x = torch.from_numpy(fx.x).to(dt[fx.x_dtype])
+    keys = torch.from_numpy(fx.keys).to(dt[fx.keys_dtype])
+    sel = torch.from_numpy(fx.sel)
+    w = None if fx.weights is None else torch.from_numpy(fx.weights).to(dt[fx.weights_dtype])
+    go = torch.from_numpy(fx.grad_out).to(dt[fx.grad_dtype])
+    return x, keys, sel, w, go
+
+
+@pytest.fixture(params=[False, True], ids=["ordered-reduce", "atomic-reduce"])
+def reduce_mode(request, monkeypatch):
+    monkeypatch.setattr(C, "cvmm_atomic_reduce", request.param)
+    return request.param
+
+
+@pytest.mark.parametrize("fx", FIXTURES, ids=lambda f: f.name)
+def test_golden_cases(fx, reduce_mode):
+    """The reference harness's 7 edge cases x 3 dtype modes."""
+    x, keys, sel, w, go = _fixture_tensors(fx)
+    amp = fx.mode != "float32"
+    got = U.run_hip(x, keys, sel, w, go, fx.case["route_input"], amp)
+    # 1) against the oracle with the reference's rounding points
+    exp = U.run_oracle(x, keys, sel, w, go, fx.case["route_input"], amp)
+    U.compare(got, exp, G.NORM_REL[fx.mode])
+    # 2) against the exact fp64 einsum definition with the harness tolerances
+    gold = {"out": fx.exp_out, "x_grad": fx.exp_x_grad, "keys_grad": fx.exp_keys_grad,
+            "weights_grad": fx.exp_weights_grad}
+    for name, ref in gold.items():
+        if ref is None:
+            continue
+        atol, rtol = G.TOLERANCES[fx.mode][name]
+        np.testing.assert_allclose(U.to_np(got[name]), ref, atol=atol, rtol=rtol, err_msg=name)
+
+
+# ---------------------------------------------------------------------------
+# the reference's own GPU tests (test_cvmm_correctness.py), with CPU-seeded data
+# ---------------------------------------------------------------------------
+
+def _einsum_reference(x, sel, keys, weights=None):
+    """test_cvmm_correctness.py:7-15 (fp32 there; fp64 here)."""
+    selected = keys[sel].double()
+    if x.shape[:-1] == sel.shape:
+        out = (x.double().unsqueeze(-1) * selected).sum(dim=-2)
+    else:
+        out = (x.double().unsqueeze(-2).unsqueeze(-1) * selected).sum(dim=-2)
+    if weights is not None:
+        out = (weights.unsqueeze(-1).double() * out).sum(dim=-2)
+    return out
+
+
+def _check_case(weighted, route_input=False):
+    """test_cvmm_correctness.py:18-58, same shapes and tolerances."""
+    g = torch.Generator().manual_seed(1234 + int(weighted) + 17 * int(route_input))
+    b, t, d, out_d, n_experts, top_k = 3, 5, 16, 11, 7, 3
+    x_shape = (b, t, top_k, d) if route_input else (b, t, d)
+    x = torch.randn(*x_shape, generator=g).to(torch.bfloat16)
+    keys = torch.randn(n_experts, d, out_d, generator=g)
+    sel = torch.randint(0, n_experts, (b, t, top_k), generator=g)
+    weights = torch.randn(b, t, top_k, generator=g) if weighted else None
+    out_shape = (b, t, out_d) if weighted else (b, t, top_k, out_d)
+    grad = torch.randn(*out_shape, generator=g)
+    got = U.run_hip(x, keys, sel, weights, grad.to(torch.bfloat16), route_input, True)
+
+    xr = x.double().requires_grad_(True)
+    kr = keys.double().requires_grad_(True)
+    wr = None if weights is None else weights.double().requires_grad_(True)
+    exp = _einsum_reference(xr, sel, kr, wr)
+    exp.backward(grad.to(torch.bfloat16).double())
+    rtol, atol = (5e-2, 1e-1) if route_input else (2e-2, 2e-2)
+    torch.testing.assert_close(got["out"].float().cpu(), exp.float(), rtol=rtol, atol=atol)
+    grad_rtol, grad_atol = (6e-2, 1e-1) if route_input else (3e-2, 3e-2)
+    pairs = [(got["x_grad"], xr.grad), (got["keys_grad"], kr.grad)]
+    if weighted:
+        pairs.append((got["weights_grad"], wr.grad))
+    for a, e in pairs:
+        torch.testing.assert_close(a.float().cpu(), e.float(), rtol=grad_rtol, atol=grad_atol)
+
+
+def test_unweighted():
+    _check_case(False)
+
+
+def test_weighted():
+    _check_case(True)
+
+
+def test_weighted_route_input():
+    _check_case(True, route_input=True)
+
+
+@pytest.mark.parametrize("n_experts,total_routes", list(itertools.product((1, 7, 64, 512), (1, 13, 1000))))
+def test_expert_offsets_kernel(n_experts, total_routes, monkeypatch):
+    """test_cvmm_correctness.py:73-86: native offsets == the torch closed form."""
+    C.create_kernels()
+    g = torch.Generator().manual_seed(n_experts * 7 + total_routes)
+    sel = torch.randint(0, n_experts, (total_routes,), generator=g, dtype=torch.int32).sort().values
+    fast = C._cvmm_expert_offsets(sel.cuda(), n_experts)
+    monkeypatch.setattr(C, "cvmm_expert_offsets_call", None)
+    ref = C._cvmm_expert_offsets(sel.cuda(), n_experts)
+    assert torch.equal(fast.cpu(), ref.cpu())
+    assert np.array_equal(fast.cpu().numpy(), O.expert_offsets(sel.numpy(), n_experts))
+
+
+def test_top32_lowmem_unweighted(monkeypatch):
+    """test_cvmm_correctness.py:89-118 (top-32 over 64 experts)."""
+    monkeypatch.setattr(C, "cvmm_lowmem_chunk_size", 0)
+    g = torch.Generator().manual_seed(2026)
+    b, t, d, out_d, n_experts, top_k = 2, 5, 32, 16, 64, 32
+    x = torch.randn(b, t, d, generator=g).to(torch.bfloat16)
+    keys = torch.randn(n_experts, d, out_d, generator=g)
+    sel = torch.randint(0, n_experts, (b, t, top_k), generator=g)
+    grad = torch.randn(b, t, top_k, out_d, generator=g)
+    got = U.run_hip(x, keys, sel, None, grad.to(torch.bfloat16), False, True)
+    xr = x.double().requires_grad_(True)
+    kr = keys.double().requires_grad_(True)
+    exp = _einsum_reference(xr, sel, kr)
+    exp.backward(grad.to(torch.bfloat16).double())
+    torch.testing.assert_close(got["out"].float().cpu(), exp.float(), rtol=5e-2, atol=1e-1)
+    torch.testing.assert_close(got["x_grad"].float().cpu(), xr.grad.float(), rtol=3e-1, atol=6e-1)
+    torch.testing.assert_close(got["keys_grad"].float().cpu(), kr.grad.float(), rtol=1e-1, atol=1e-1)
+    # and the tighter oracle bound
+    exp2 = U.run_oracle(x, keys, sel, None, grad.to(torch.bfloat16), False, True)
+    U.compare(got, exp2, 2e-2)
+
+
+def test_weighted_route_input_reused_selector():
+    """test_cvmm_correctness.py:121-137: bit-identical outputs."""
+    g = torch.Generator().manual_seed(1251)
+    b, t, d, out_d, n_experts, top_k = 3, 5, 16, 11, 7, 3
+    x = torch.randn(b, t, top_k, d, generator=g).to(torch.bfloat16).cuda()
+    keys = torch.randn(n_experts, d, out_d, generator=g).cuda()
+    sel = torch.randint(0, n_experts, (b, t, top_k), generator=g).cuda()
+    weights = torch.randn(b, t, top_k, generator=g).cuda()
+    base = C.cvmm_prepare_sel2(sel)
+    reused = C.cvmm_prepare_sel2(base, weights, route_input=True)
+    fresh = C.cvmm_prepare_sel2(sel, weights, route_input=True)
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        a = C.cvmm(x, reused, keys)
+        e = C.cvmm(x, fresh, keys)
+    assert torch.equal(a, e)
+    # the same with an already-resolved parent selector
+    base2 = C.cvmm_prepare_sel2(sel)
+    _ = base2.sel_index
+    reused2 = C.cvmm_prepare_sel2(base2, weights, route_input=True)
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        a2 = C.cvmm(x, reused2, keys)
+    assert torch.equal(a2, e)
+
+
+# ---------------------------------------------------------------------------
+# selector preparation: bit-exact against the stable sort
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape,E,dtype", [
+    ((1,), 1, torch.int64), ((13,), 7, torch.int64), ((3, 5, 3), 7, torch.int32),
+    ((16, 512, 8), 64, torch.int64), ((8, 1024, 64), 256, torch.int64), ((2, 7, 1), 13, torch.int32),
+    ((4, 4096, 8), 512, torch.int64), ((1, 5, 2), 32, torch.int64), ((64, 1000, 2), 2000, torch.int64),
+])
+def test_sort_routes_bit_exact(shape, E, dtype):
+    g = torch.Generator().manual_seed(sum(shape) * 31 + E)
+    sel = torch.randint(0, E, shape, generator=g, dtype=dtype)
+    k = shape[-1]
+    s = C.cvmm_prepare_sel2(sel.cuda())
+    C.create_kernels()
+    s._resolve(E)
+    m = O.prepare_sel2(sel.numpy())
+    assert s.raw_sel.dtype == torch.int32 and tuple(s.raw_sel.shape) == shape
+    assert np.array_equal(s.raw_sel.cpu().numpy(), m.raw_sel)
+    assert np.array_equal(s.sel.cpu().numpy(), m.sel)
+    assert np.array_equal(s.out_index.cpu().numpy(), m.out_index)
+    assert np.array_equal(s.sel_index.cpu().numpy(), m.sel_index)
+    off = C._offsets_for(s.sel, E)
+    assert np.array_equal(off.cpu().numpy(), O.expert_offsets(m.sel, E))
+    r = C.cvmm_prepare_sel2(sel.cuda(), route_input=True)
+    r._resolve(E)
+    assert r.out_index is None and np.array_equal(r.sel_index.cpu().numpy(), m.out_index)
+    p = C.cvmm_prepare_sel(sel.cuda(), E)
+    assert p.out_index is None and np.array_equal(p.sel_index.cpu().numpy(), m.out_index)
+    assert np.array_equal(p.sel.cpu().numpy(), m.sel)
+
+
+def test_sort_invalid_ids_go_last():
+    """Ids outside [0, E) are counted, sorted stably after all valid routes and
+    never read by the GEMMs."""
+    E = 16
+    g = torch.Generator().manual_seed(5)
+    sel = torch.randint(-3, E + 4, (4000,), generator=g)
+    raw = sel.to(torch.int32).cuda()
+    from cvmm_codex_amd import _native as N
+    lib = N.lib()
+    R = raw.numel()
+    ssel = torch.empty(R, dtype=torch.int32, device="cuda")
+    perm = torch.empty(R, dtype=torch.int64, device="cuda")
+    off = torch.empty(E, dtype=torch.int64, device="cuda")
+    nin = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws_b = lib.cvmm_sort_workspace_bytes(R, E)
+    ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
+    N.check(lib.cvmm_sort_routes(N.ptr(raw), 0, R, E, 1, N.ptr(ssel), N.ptr(perm), None, N.ptr(off), N.ptr(nin),
+                                 N.ptr(ws), ws_b, N.stream_of(raw.device)), "sort")
+    s = sel.numpy()
+    valid = (s >= 0) & (s < E)
+    key = np.where(valid, s, E)
+    exp_perm = np.argsort(key, kind="stable")
+    assert int(nin.item()) == int((~valid).sum())
+    assert np.array_equal(perm.cpu().numpy(), exp_perm)
+    assert np.array_equal(ssel.cpu().numpy(), s[exp_perm].astype(np.int32))
+    assert np.array_equal(off.cpu().numpy(), np.cumsum(np.bincount(s[valid], minlength=E)))
+
+
+# ---------------------------------------------------------------------------
+# more paths
+# ---------------------------------------------------------------------------
+
+def _rand_case(seed, B, T, D, H, E, K, weighted=False, route_input=False, x_dt=torch.bfloat16,
+               k_dt=torch.float32, skew=None):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*((B, T, K, D) if route_input else (B, T, D)), generator=g).to(x_dt)
+    keys = (torch.randn(E, D, H, generator=g) / D ** 0.5).to(k_dt)
+    if skew is None:
+        sel = torch.randint(0, E, (B, T, K), generator=g)
+    else:  # expert 0 takes `skew` of all routes
+        sel = torch.randint(1, E, (B, T, K), generator=g)
+        hot = torch.rand(B, T, K, generator=g) < skew
+        sel[hot] = 0
+    w = torch.rand(B, T, K, generator=g) if weighted else None
+    go = torch.randn(*((B, T, H) if weighted else (B, T, K, H)), generator=g).to(
+        x_dt if x_dt != torch.float32 else torch.bfloat16)
+    return x, keys, sel, w, go
+
+
+@pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True), (True, False), (False, True)])
+def test_hot_expert_split_reduction(weighted, route_input, reduce_mode):
+    """One expert holds ~70% of the routes: its weight gradient is split into
+    several route chunks reduced in a fixed order."""
+    x, keys, sel, w, go = _rand_case(11, 4, 512, 128, 96, 8, 4, weighted, route_input, skew=0.7)
+    got = U.run_hip(x, keys, sel, w, go, route_input, True)
+    exp = U.run_oracle(x, keys, sel, w, go, route_input, True)
+    U.compare(got, exp, 2e-2)
+
+
+def test_weight_grad_is_deterministic():
+    x, keys, sel, w, go = _rand_case(12, 4, 512, 128, 96, 8, 4, True, True, skew=0.7)
+    a = U.run_hip(x, keys, sel, w, go, True, True)
+    b = U.run_hip(x, keys, sel, w, go, True, True)
+    for n in ("out", "x_grad", "keys_grad", "weights_grad"):
+        assert torch.equal(a[n], b[n]), n
+
+
+def test_fp16_autocast():
+    x, keys, sel, w, go = _rand_case(13, 2, 64, 96, 80, 6, 2, x_dt=torch.float16)
+    got = U.run_hip(x, keys, sel, w, go.to(torch.float16), False, True, amp_dtype=torch.float16)
+    exp = U.run_oracle(x, keys, sel, w, go.to(torch.float16), False, True, amp_dtype="float16")
+    U.compare(got, exp, 2e-2)
+
+
+def test_fp32_x_under_autocast():
+    """fp32 activations with bf16 autocast: cast to bf16 inside the kernels."""
+    x, keys, sel, w, go = _rand_case(14, 2, 64, 96, 80, 6, 3, True, False, x_dt=torch.float32)
+    got = U.run_hip(x, keys, sel, w, go, False, True)
+    exp = U.run_oracle(x, keys, sel, w, go, False, True)
+    U.compare(got, exp, 2e-2)
+
+
+def test_transposed_keys_view():
+    """keys given as a transposed view (unit stride on d_in)."""
+    x, keys, sel, w, go = _rand_case(15, 2, 64, 64, 96, 5, 2)
+    kt = keys.transpose(1, 2).contiguous().transpose(1, 2)
+    assert kt.stride(1) == 1
+    got = U.run_hip(x, kt, sel, w, go, False, True)
+    exp = U.run_oracle(x, keys, sel, w, go, False, True)
+    U.compare(got, exp, 2e-2)
+
+
+def test_stride0_grad_output():
+    """``out.sum().backward()`` (the reference benchmark) passes an expanded grad."""
+    x, keys, sel, _, _ = _rand_case(16, 2, 64, 64, 48, 5, 3)
+    dev = torch.device("cuda")
+    xd = x.to(dev).requires_grad_(True)
+    kd = keys.to(dev).requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = C.cvmm(xd, C.cvmm_prepare_sel2(sel.to(dev)), kd)
+    y.sum().backward()
+    ones = torch.ones(y.shape, dtype=torch.bfloat16)
+    exp = U.run_oracle(x, keys, sel, None, ones, False, True)
+    U.compare({"out": y, "x_grad": xd.grad, "keys_grad": kd.grad}, exp, 2e-2,
+              names=("out", "x_grad", "keys_grad"))
+
+
+def test_empty_selection():
+    dev = torch.device("cuda")
+    x = torch.randn(0, 16, device=dev, requires_grad=True)
+    keys = torch.randn(4, 16, 8, device=dev, requires_grad=True)
+    sel = torch.zeros(0, 2, dtype=torch.int64, device=dev)
+    y = C.cvmm(x, C.cvmm_prepare_sel2(sel), keys)
+    assert y.shape == (0, 2, 8)
+    y.sum().backward()
+    assert torch.equal(keys.grad, torch.zeros_like(keys))
+
+
+# ---------------------------------------------------------------------------
+# BASELINE configs at full size
+# ---------------------------------------------------------------------------
+
+def test_config_tiny_fp32():
+    import workloads as W
+    p = W.c1_tiny()
+    got = U.run_hip(p.x, p.keys, p.sel, p.weights, p.grad_out, p.route_input, p.amp)
+    exp = U.run_oracle(p.x, p.keys, p.sel, p.weights, p.grad_out, p.route_input, p.amp)
+    U.compare(got, exp, 1e-4)
+
+
+@pytest.mark.parametrize("name", ["ff_up_1024", "ff_down_1024_weighted"])
+def test_config_ff_projections(name, reduce_mode):
+    import workloads as W
+    p = W.PROJECTIONS[name]()
+    got = U.run_hip(p.x, p.keys, p.sel, p.weights, p.grad_out, p.route_input, p.amp)
+    exp = U.run_oracle(p.x, p.keys, p.sel, p.weights, p.grad_out, p.route_input, p.amp, compute=np.float32)
+    U.compare(got, exp, 2e-2)

@@ -1,0 +1,79 @@
+"""The C-ABI library loads and exports what include/cvmm_hip.h declares.
+
+Runs without a GPU: only host-side functions are called (workspace queries,
+argument validation that fails before any launch)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from cvmm_codex_amd import _native as N
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cvmm_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cvmm_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not N.available():
+        from cvmm_codex_amd import build
+        build.build(verbose=False)
+    return N.lib()
+
+
+def test_header_declares_the_bound_symbols():
+    assert set(_declared()) == set(N.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(N.LIB_PATH)
+    for name in _declared():
+        assert hasattr(raw, name), name
+
+
+def test_abi_version(lib):
+    assert lib.cvmm_abi_version() == 1
+
+
+def test_workspace_queries(lib):
+    assert lib.cvmm_sort_workspace_bytes(65536, 64) > 0
+    # no workspace needed for an unweighted forward with offsets given
+    assert lib.cvmm_fwd_workspace_bytes(65536, 64, 128, 65536, N.BF16, 1, 0, 0) == 0
+    # weighted combine: route-ordered buffer or fp32 token accumulator
+    assert lib.cvmm_fwd_workspace_bytes(65536, 64, 1024, 8192, N.BF16, 1, 1, 0) >= 65536 * 1024 * 2
+    assert lib.cvmm_fwd_workspace_bytes(65536, 64, 1024, 8192, N.BF16, 1, 1, N.FLAG_ATOMIC_REDUCE) >= 8192 * 1024 * 4
+    # weight grad: counters + bounded partial slots
+    assert lib.cvmm_bwd_w_workspace_bytes(65536, 64, 1024, 128, N.BF16, 1) > 64 * 8 * 4
+
+
+def test_invalid_arguments_fail_before_launch(lib):
+    rc = lib.cvmm_sort_routes(None, 0, 10, 0, 1, None, None, None, None, None, None, 0, None)
+    assert rc == 1 and b"n_experts" in lib.cvmm_last_error()
+    rc = lib.cvmm_sort_routes(None, 0, 10, 100000, 1, None, None, None, None, None, None, 0, None)
+    assert rc == 2
+    args = [None, 7, 1, 16, None, 0, 4, 16, 8, 128, 8, 1, None, None, None, 1, None, None, 0, 1,
+            0, None, 0, 1, 8, 0, None, 0, None]
+    assert lib.cvmm_fwd(*args) == 1 and b"dtype" in lib.cvmm_last_error()
+    args[1] = 0
+    args[-4] = 0
+    args[2] = 1
+    args[23] = 2   # out_rows != R
+    assert lib.cvmm_fwd(*args) == 1
+    # weighted forward without workspace
+    wargs = [None, 0, 8, 16, None, 0, 4, 16, 8, 128, 8, 1, None, None, None, 8, None, ctypes.c_void_p(16), 0, 4,
+             0, None, 0, 2, 8, 0, None, 0, None]
+    assert lib.cvmm_fwd(*wargs) == 3
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    monkeypatch.setattr(N, "LIB_PATH", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(N, "_lib", None)
+    with pytest.raises(N.NativeLibraryMissing):
+        N.lib()
