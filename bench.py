@@ -1,0 +1,282 @@
+"""CVMM forward+backward benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload ff_up_1024]
+
+A step = one pass of the CVMM hot path over one batch of synthetic input:
+selector preparation (stable counting sort), forward, and backward (grad x,
+grad keys, grad reduction weight), launched by the drop-in API exactly as a
+training step would.  ``value`` is whole-job TFLOP/s = 6*R*d_in*d_out / step
+time (inputs resident in HBM).  The dominant kernel is also timed on its own
+with HIP events on the stream it runs on, giving ``roofline``; the CPU oracle
+is timed on a bounded sample of the same workload as ``cpu_baseline``.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import workloads as W  # noqa: E402
+
+METRIC = "CVMM fwd+bwd ms/iter and TFLOP/s (% of MI355X roofline), 1 GPU"
+PEAK = {"bf16": 2500.0, "fp16": 2500.0, "fp32": 157.3}     # dense MFMA TFLOP/s
+HBM_PEAK_GBS = 8000.0
+DEFAULT_WORKLOAD = "ff_up_1024"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Runner:
+    """Holds one projection's device tensors and runs steps through the API."""
+
+    def __init__(self, proj: W.Projection, device):
+        import cvmm_codex_amd.api as C
+        self.C = C
+        self.p = proj.to(device)
+        self.x = self.p.x.detach().requires_grad_(True)
+        self.keys = self.p.keys.detach().requires_grad_(True)
+        self.w = None if self.p.weights is None else self.p.weights.detach().requires_grad_(True)
+        self.E = self.keys.shape[0]
+
+    def prepare(self):
+        s = self.C.cvmm_prepare_sel2(self.p.sel, self.w, route_input=self.p.route_input)
+        s._resolve(self.E)
+        return s
+
+    def forward(self, s):
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=self.p.amp):
+            return self.C.cvmm(self.x, s, self.keys)
+
+    def backward(self, y):
+        y.backward(self.p.grad_out.to(y.dtype))
+
+    def zero(self):
+        self.x.grad = None
+        self.keys.grad = None
+        if self.w is not None:
+            self.w.grad = None
+
+    def step(self):
+        self.zero()
+        s = self.prepare()
+        y = self.forward(s)
+        self.backward(y)
+
+
+def time_steps(runner: Runner, steps: int, warmup: int):
+    for _ in range(warmup):
+        runner.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        runner.step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def time_phases(runner: Runner, iters: int):
+    """HIP events between the phases of a step (current stream)."""
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    acc = np.zeros(3)
+    for _ in range(iters):
+        runner.zero()
+        ev[0].record()
+        s = runner.prepare()
+        ev[1].record()
+        y = runner.forward(s)
+        ev[2].record()
+        runner.backward(y)
+        ev[3].record()
+        torch.cuda.synchronize()
+        acc += [ev[i].elapsed_time(ev[i + 1]) for i in range(3)]
+    return dict(zip(("sel", "fwd", "bwd"), (acc / iters).tolist()))
+
+
+def kernel_launchers(runner: Runner):
+    """One C-ABI call per hot kernel, with every input already on the device.
+
+    Each returns a callable that launches exactly that phase on the current
+    stream (routed GEMM forward / grad-input, weight gradient)."""
+    C = runner.C
+    s = runner.prepare()
+    op = torch.bfloat16 if runner.p.amp else torch.float32
+    y = None
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=runner.p.amp):
+        y = C.cvmm(runner.x, s, runner.keys)
+    go = runner.p.grad_out.to(y.dtype)
+
+    class Ctx:
+        op_type = op
+
+    args = (runner.x.detach(), runner.keys.detach(), s.raw_sel, s.sel, s.sel_index, s.out_index,
+            None if runner.w is None else runner.w.detach())
+    keys = runner.keys.detach()
+    fast = C._fast_path(op, keys.shape[1], keys.shape[2])
+    kt, kn = C._cast_keys(keys, op, True, True) if fast else (None, None)
+
+    def cast():
+        C._cast_keys(keys, op, True, True)
+
+    def fwd():
+        C._forward(runner.x.detach(), s.sel_index, s.sel, keys, s.out_index, args[6], op, kt)
+
+    def bwd_w():
+        C._backward(Ctx, go, *args, False, True, False)
+
+    def bwd_x():
+        C._backward(Ctx, go, *args, True, False, runner.w is not None, keys_n=kn)
+
+    out = {"fwd": fwd, "bwd_w": bwd_w, "bwd_x": bwd_x}
+    if fast:
+        out["cast_keys"] = cast
+    return out
+
+
+def time_launcher(fn, iters: int):
+    stream = torch.cuda.current_stream()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(iters):
+        fn()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters
+
+
+def phase_flops(proj: W.Projection, phase: str) -> float:
+    return 2.0 * proj.routes * proj.keys.shape[1] * proj.keys.shape[2]
+
+
+def cpu_baseline(proj: W.Projection, budget_s: float = 12.0):
+    """The oracle on the host cores: forward+backward of the same workload in
+    float32 (the fp32 gather + per-expert matmul CPU path; rounding points
+    off), repeated until the time budget is spent (at least once)."""
+    from oracle import cvmm_oracle as O
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    op = None
+    xn = proj.x.float().numpy()
+    kn = proj.keys.float().numpy()
+    wn = None if proj.weights is None else proj.weights.float().numpy()
+    gn = proj.grad_out.float().numpy()
+    sel = proj.sel.numpy()
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        meta = O.prepare_sel2(sel, wn, route_input=proj.route_input)
+        O.forward(xn, meta, kn, op, op, compute=np.float32)
+        O.backward(xn, meta, kn, gn, op, compute=np.float32)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 50:
+            break
+    per = el / n
+    return {"value": round(proj.flops / per / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads),
+            "kind": "port",
+            "sample": f"full {proj.name} workload, {n} oracle sel+fwd+bwd iterations in {el:.1f}s "
+                      f"(numpy float32, rounding points off), {per * 1e3:.1f} ms/iter"}
+
+
+def load_traffic(kernel: str, workload: str):
+    path = os.path.join(ROOT, "profiles", f"traffic_{kernel}_{workload}.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            return json.load(f).get("bytes_per_launch")
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(W.PROJECTIONS))
+    ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["fwd", "bwd_w", "bwd_x", "cast_keys"], default=None,
+                    help="launch only this phase --steps times (for rocprofv3 runs)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    dev = torch.device("cuda:0")
+    proj = W.PROJECTIONS[args.workload]()
+    runner = Runner(proj, dev)
+
+    if args.only:
+        fn = kernel_launchers(runner)[args.only]
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        for _ in range(args.steps):
+            fn()
+        torch.cuda.synchronize()
+        log(f"launched {args.only} {args.steps} times")
+        return
+
+    log(f"workload {proj.name}: R={proj.routes} d_in={proj.keys.shape[1]} d_out={proj.keys.shape[2]} "
+        f"E={proj.keys.shape[0]}")
+    ms = time_steps(runner, args.steps, args.warmup)
+    log(f"step {ms:.4f} ms")
+    phases = time_phases(runner, max(10, args.steps // 2))
+    log(f"phases {phases}")
+
+    launchers = kernel_launchers(runner)
+    kern = {k: time_launcher(f, args.kernel_iters) for k, f in launchers.items()}
+    log(f"per-call ms {kern}")
+    dom = max((k for k in kern if k != "cast_keys"), key=kern.get)
+    dtype = "bf16" if proj.amp else "fp32"
+    flops = phase_flops(proj, dom)
+    achieved = flops / (kern[dom] * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 3), "peak": PEAK[dtype],
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK[dtype], 5),
+                "traffic": load_traffic(dom, proj.name), "avg_launch_ms": round(kern[dom], 5)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(proj)
+
+    value = proj.flops / (ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+        "data": "synthetic (seeded CPU generator, BASELINE.json recipe)",
+        "config": {"workload": proj.name, "routes": proj.routes, "d_in": proj.keys.shape[1],
+                   "d_out": proj.keys.shape[2], "n_experts": proj.keys.shape[0],
+                   "top_k": proj.sel.shape[-1], "weighted": proj.weights is not None,
+                   "step": "sel+fwd+bwd", "gflop_per_step": round(proj.flops / 1e9, 3)},
+        "step_roofline_frac": round(value / PEAK[dtype], 5),
+        "breakdown_ms": {k: round(v, 5) for k, v in phases.items()},
+        "kernel_ms": {k: round(v, 5) for k, v in kern.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

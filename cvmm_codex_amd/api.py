@@ -338,15 +338,38 @@ def _workspace(nbytes: int, device) -> Optional[torch.Tensor]:
     return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
 
 
-def _forward(x, sel_index, sel, keys, out_index, rw, op_dtype):
+def _fast_path(op: torch.dtype, d_in: int, d_out: int) -> bool:
+    """The DMA-staged kernels need 16-bit operands and widths divisible by 8."""
+    return op in (torch.bfloat16, torch.float16) and d_in % 8 == 0 and d_out % 8 == 0
+
+
+def _cast_keys(keys: torch.Tensor, op: torch.dtype, want_t: bool, want_n: bool):
+    """keys [E, d_in, d_out] -> op-dtype copies kt [E, d_out, d_in] (forward) and
+    kn [E, d_in, d_out] (grad-input), one pass."""
+    n_experts, d_in, d_out = keys.shape
+    kt = torch.empty(n_experts, d_out, d_in, dtype=op, device=keys.device) if want_t else None
+    kn = torch.empty(n_experts, d_in, d_out, dtype=op, device=keys.device) if want_n else None
+    N.check(N.lib().cvmm_cast_keys(N.ptr(keys), N.dtype_id(keys.dtype), n_experts, d_in, d_out, keys.stride(0),
+                                   keys.stride(1), keys.stride(2), N.dtype_id(op), N.ptr(kt), N.ptr(kn),
+                                   N.stream_of(keys.device)), "cvmm_cast_keys")
+    return kt, kn
+
+
+def _forward(x, sel_index, sel, keys, out_index, rw, op_dtype, keys_t=None):
     for t, name in ((x, "x"), (keys, "keys"), (sel, "sel"), (sel_index, "sel_index")):
         _require_device(t, name)
     n_experts, d_in, d_out = keys.shape
     assert x.shape[-1] == keys.shape[1]                                   # cvmm.py:825
     dev = x.device
     lib = N.lib()
-    xf = _rows(_storage_for(x, op_dtype), d_in)
-    kv = _keys_view(_storage_for(keys, op_dtype))
+    if keys_t is not None:
+        # op-dtype activations and the [E, d_out, d_in] weight copy, seen as a
+        # [E, d_in, d_out] view with unit stride on d_in: the fast kernels' layout
+        xf = _rows(x if x.dtype == op_dtype else x.to(op_dtype), d_in)
+        kv = keys_t.transpose(1, 2)
+    else:
+        xf = _rows(_storage_for(x, op_dtype), d_in)
+        kv = _keys_view(_storage_for(keys, op_dtype))
     s32 = _sorted_i32(sel)
     R = s32.numel()
     si = _i64(sel_index)
@@ -381,14 +404,15 @@ def _forward(x, sel_index, sel, keys, out_index, rw, op_dtype):
 
 
 def _backward(ctx, grad_output, x, keys, raw_sel, sel, sel_index, out_index, rw,
-              need_grad_x, need_grad_keys, need_grad_rw):
+              need_grad_x, need_grad_keys, need_grad_rw, keys_n=None):
     op = ctx.op_type
     n_experts, d_in, d_out = keys.shape
     dev = x.device
     lib = N.lib()
     top_k = raw_sel.shape[-1] if raw_sel.ndim > 0 else 1
     k = rw.shape[-1] if rw is not None else top_k
-    g = _rows(_storage_for(grad_output, op), d_out)
+    g = _rows(grad_output.to(op) if _fast_path(op, d_in, d_out) and grad_output.dtype != op
+              else _storage_for(grad_output, op), d_out)
     s32 = _sorted_i32(sel)
     R = s32.numel()
     si = _i64(sel_index)
@@ -401,8 +425,9 @@ def _backward(ctx, grad_output, x, keys, raw_sel, sel, sel_index, out_index, rw,
     stream = N.stream_of(dev)
     grad_x = grad_w = grad_rw = None
 
+    fast = _fast_path(op, d_in, d_out)
     if need_grad_keys:
-        xs = _rows(_storage_for(x, op), d_in)
+        xs = _rows(x.to(op) if fast and x.dtype != op else _storage_for(x, op), d_in)
         grad_w = torch.empty(keys.shape, dtype=keys.dtype, device=dev)
         ws_bytes = lib.cvmm_bwd_w_workspace_bytes(R, n_experts, d_in, d_out, od, 1)
         ws = _workspace(ws_bytes, dev)
@@ -415,7 +440,7 @@ def _backward(ctx, grad_output, x, keys, raw_sel, sel, sel_index, out_index, rw,
             flags, N.ptr(ws), ws_bytes, stream), "cvmm_bwd_w")
 
     if need_grad_x or need_grad_rw:
-        kv = _keys_view(_storage_for(keys, op))
+        kv = keys_n if keys_n is not None else _keys_view(_storage_for(keys, op))
         xr = _rows(x, d_in)
         gx = None
         if need_grad_x:
@@ -452,7 +477,12 @@ class CVMM(torch.autograd.Function):
                 reduction_weight: Optional[torch.Tensor] = None):
         ctx.save_for_backward(x, keys, raw_sel, sel, sel_index, out_index, reduction_weight)
         out_type = get_dtype()
-        res = _forward(x, sel_index, sel, keys, out_index, reduction_weight, out_type)
+        keys_t = keys_n = None
+        if _fast_path(out_type, keys.shape[1], keys.shape[2]):
+            need_n = ctx.needs_input_grad[0] or ctx.needs_input_grad[6]
+            keys_t, keys_n = _cast_keys(keys, out_type, True, need_n)
+        res = _forward(x, sel_index, sel, keys, out_index, reduction_weight, out_type, keys_t)
+        ctx.keys_n = keys_n
         ctx.op_type = out_type
         ctx.keys_type = keys.dtype
         ctx.dtype = out_type
@@ -465,7 +495,9 @@ class CVMM(torch.autograd.Function):
         need_grad_keys = ctx.needs_input_grad[4]
         need_grad_rw = ctx.needs_input_grad[6] and reduction_weight is not None
         grad_x, grad_w, grad_rw = _backward(ctx, grad_output, x, keys, raw_sel, sel, sel_index, out_index,
-                                            reduction_weight, need_grad_x, need_grad_keys, need_grad_rw)
+                                            reduction_weight, need_grad_x, need_grad_keys, need_grad_rw,
+                                            keys_n=ctx.keys_n)
+        ctx.keys_n = None
         return grad_x, None, None, None, grad_w, None, grad_rw
 
 

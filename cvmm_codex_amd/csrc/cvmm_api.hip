@@ -17,14 +17,37 @@ hipError_t launch_wgrad_bf16(const WgradParams& p, hipStream_t stream);
 hipError_t launch_wgrad_f16(const WgradParams& p, hipStream_t stream);
 hipError_t launch_wgrad_f32(const WgradParams& p, hipStream_t stream);
 
+hipError_t launch_routed_gemm_nt_bf16(const GemmParams& p, hipStream_t stream);
+hipError_t launch_routed_gemm_nt_f16(const GemmParams& p, hipStream_t stream);
+
+// Fast path (DMA-staged, 16-bit k-contiguous operands) when eligible, else the
+// general kernel (any storage type / stride / width).
+static bool nt_eligible(const GemmParams& p, int32_t op) {
+  auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  return (op == kBF16 || op == kF16) && p.a_dtype == op && p.b_dtype == op && p.b_sk == 1 && p.K % 8 == 0 &&
+         p.epi == kEpiStore && al(p.a) && al(p.b) && p.a_ld % 8 == 0 && p.b_sn % 8 == 0 && p.b_se % 8 == 0;
+}
+
 hipError_t launch_routed_gemm(const GemmParams& p, int32_t op, hipStream_t s) {
+  if (nt_eligible(p, op)) return op == kBF16 ? launch_routed_gemm_nt_bf16(p, s) : launch_routed_gemm_nt_f16(p, s);
   if (op == kBF16) return launch_routed_gemm_bf16(p, s);
   if (op == kF16) return launch_routed_gemm_f16(p, s);
   if (op == kF32) return launch_routed_gemm_f32(p, s);
   return hipErrorInvalidValue;
 }
 
+hipError_t launch_wgrad_v2_bf16(const WgradParams& p, hipStream_t stream);
+hipError_t launch_wgrad_v2_f16(const WgradParams& p, hipStream_t stream);
+
+// Fast path: 16-bit x and dY in the op dtype, 16-byte aligned rows, widths % 8.
+static bool wgrad_v2_eligible(const WgradParams& p, int32_t op) {
+  auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  return (op == kBF16 || op == kF16) && p.x_dtype == op && p.g_dtype == op && p.M % 8 == 0 && p.N % 8 == 0 &&
+         al(p.x) && al(p.g) && p.x_ld % 8 == 0 && p.g_ld % 8 == 0;
+}
+
 hipError_t launch_wgrad(const WgradParams& p, int32_t op, hipStream_t s) {
+  if (wgrad_v2_eligible(p, op)) return op == kBF16 ? launch_wgrad_v2_bf16(p, s) : launch_wgrad_v2_f16(p, s);
   if (op == kBF16) return launch_wgrad_bf16(p, s);
   if (op == kF16) return launch_wgrad_f16(p, s);
   if (op == kF32) return launch_wgrad_f32(p, s);
@@ -114,7 +137,7 @@ extern "C" {
 
 const char* cvmm_last_error(void) { return g_err.c_str(); }
 
-int cvmm_abi_version(void) { return 1; }
+int cvmm_abi_version(void) { return 2; }
 
 // ---------------------------------------------------------------------------
 size_t cvmm_sort_workspace_bytes(int64_t n_routes, int32_t n_experts) {
@@ -150,6 +173,22 @@ int cvmm_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_e
   if (n_routes > 0 && sorted_sel == nullptr) return fail(CVMM_ERR_INVALID, "cvmm_expert_offsets: sorted_sel NULL");
   return check_launch(launch_expert_offsets(sorted_sel, n_routes, n_experts, offsets, (hipStream_t)stream),
                       "cvmm_expert_offsets");
+}
+
+// ---------------------------------------------------------------------------
+int cvmm_cast_keys(const void* keys, int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out,
+                   int64_t k_se, int64_t k_si, int64_t k_sj, int32_t out_dtype, void* keys_t, void* keys_n,
+                   void* stream) {
+  if (!valid_dtype(keys_dtype) || (out_dtype != kBF16 && out_dtype != kF16))
+    return fail(CVMM_ERR_INVALID, "cvmm_cast_keys: keys dtype must be float, output bf16 or f16");
+  if (n_experts <= 0 || d_in <= 0 || d_out <= 0) return fail(CVMM_ERR_INVALID, "cvmm_cast_keys: bad sizes");
+  if (n_experts > 65535 || (d_in + 63) / 64 > 65535)
+    return fail(CVMM_ERR_UNSUPPORTED, "cvmm_cast_keys: too many experts / rows");
+  if (!keys) return fail(CVMM_ERR_INVALID, "cvmm_cast_keys: keys NULL");
+  if (!keys_t && !keys_n) return CVMM_OK;
+  return check_launch(launch_cast_keys(keys, keys_dtype, k_se, k_si, k_sj, n_experts, d_in, d_out, out_dtype,
+                                       keys_t, keys_n, (hipStream_t)stream),
+                      "cvmm_cast_keys");
 }
 
 // ---------------------------------------------------------------------------
@@ -451,6 +490,7 @@ int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, con
   p.g = grad; p.g_dtype = grad_dtype; p.g_ld = grad_ld; p.g_rows = grad_rows;
   p.g_vec = aligned16(grad) && (grad_ld * (int64_t)dtype_size(grad_dtype)) % 16 == 0;
   p.g_idx = rp; p.g_div = weighted ? top_k : 1;
+  p.g_fdiv = make_fast_div(p.g_div);
   p.w = rw; p.w_dtype = rw_dtype; p.w_idx = rp;
   p.M = d_in; p.N = d_out;
   p.offsets = offs; p.n_experts = n_experts; p.n_routes = n_routes;

@@ -68,6 +68,24 @@ union Chunk16 {
   uint16_t s[8];
 };
 
+// Exact division of 0 <= n < 2^31 by a fixed 1 <= d < 2^31 as a multiply and
+// shift (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", 1994): l = ceil(log2 d), m = ceil(2^(31+l) / d),
+// n / d = (n * m) >> (31 + l); n * m < 2^63.
+struct FastDiv {
+  uint64_t m;
+  int32_t shift;
+  __host__ __device__ __forceinline__ int64_t div(int64_t n) const { return (int64_t)(((uint64_t)n * m) >> shift); }
+};
+
+inline FastDiv make_fast_div(int64_t d) {
+  int l = 0;
+  while ((1ll << l) < d) ++l;
+  const unsigned __int128 num = (unsigned __int128)1 << (31 + l);
+  const uint64_t m = (uint64_t)((num + (unsigned __int128)(d - 1)) / (unsigned __int128)d);
+  return FastDiv{m, 31 + l};
+}
+
 // Wave helpers (64-wide wavefronts).
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 

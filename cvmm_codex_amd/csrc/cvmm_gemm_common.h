@@ -1,0 +1,190 @@
+// Pieces shared by the routed GEMM kernels: the in-kernel tile scheduler, the
+// per-row route metadata and the epilogue (all driven by GemmParams).
+#pragma once
+
+#include "cvmm_common.h"
+#include "cvmm_internal.h"
+
+namespace cvmm {
+
+constexpr int kGemmThreads = 256;
+
+template <int BM>
+struct RouteMeta {
+  int64_t arow[BM];   // A row of tile row r, -1 if none
+  int64_t orow[BM];   // output row, -1 if none
+  int64_t widx[BM];   // routing-weight / dgate index
+  int64_t dgrow[BM];  // x row for the routing-weight gradient
+  float w[BM];        // rounded routing weight (1 if unweighted)
+  int32_t expert;
+  int64_t row0;
+  int32_t rows;
+};
+
+// Find the (expert, first route, row count) of m-tile `tile`: expert e owns
+// ceil(count_e / BM) consecutive tiles.  Wave 0 scans the offsets 64 experts at
+// a time; returns false (uniformly) when `tile` is past the last tile.
+template <int BM>
+__device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& m) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  // ---- schedule: which expert / routes does m-tile `tile` cover? -----------
+  if (wave == 0) {
+    if (lane == 0) m.expert = -1;
+    int64_t carry = 0;
+    for (int32_t base = 0; base < p.n_experts; base += 64) {
+      const int32_t e = base + lane;
+      int64_t start = 0, end = 0;
+      if (e < p.n_experts) {
+        end = p.offsets[e];
+        start = e > 0 ? p.offsets[e - 1] : 0;
+        end = end < 0 ? 0 : (end > p.n_routes ? p.n_routes : end);
+        start = start < 0 ? 0 : (start > p.n_routes ? p.n_routes : start);
+        if (end < start) end = start;
+      }
+      const int64_t nt = (end - start + BM - 1) / BM;
+      const int64_t incl = wave_incl_scan(nt) + carry;
+      const int64_t excl = incl - nt;
+      if (e < p.n_experts && tile >= excl && tile < incl) {
+        m.expert = e;
+        const int64_t r0 = start + (tile - excl) * BM;
+        m.row0 = r0;
+        m.rows = (int32_t)((end - r0) < BM ? (end - r0) : BM);
+      }
+      carry = __shfl(incl, 63, 64);
+      if (tile < carry) break;
+    }
+  }
+  __syncthreads();
+  if (m.expert < 0) return false;
+  const int64_t row0 = m.row0;
+  const int32_t rows = m.rows;
+
+  // ---- per-row route metadata -------------------------------------------------
+  for (int r = tid; r < BM; r += kGemmThreads) {
+    int64_t ar = -1, orow = -1, widx = -1, dgr = -1;
+    float wv = 1.f;
+    if (r < rows) {
+      const int64_t q = row0 + r;
+      const int64_t ai = p.a_idx[q] / p.a_div;
+      if (ai >= 0 && ai < p.a_rows) ar = ai;
+      const int64_t oi = p.o_idx[q] / p.o_div;
+      if (oi >= 0 && oi < p.out_rows) orow = oi;
+      if (p.w_idx != nullptr) {
+        const int64_t wi = p.w_idx[q];
+        if (wi >= 0 && wi < p.n_routes) widx = wi;
+      }
+      if (p.w != nullptr && widx >= 0) wv = round_to(load_as_f32(p.w, p.w_dtype, widx), p.w_round);
+      if (p.dg != nullptr) {
+        const int64_t di = p.dg_x_idx[q];
+        if (di >= 0 && di < p.dg_x_rows) dgr = di;
+      }
+    }
+    m.arow[r] = ar;
+    m.orow[r] = orow;
+    m.widx[r] = widx;
+    m.w[r] = wv;
+    m.dgrow[r] = dgr;
+  }
+  __syncthreads();
+
+  return true;
+}
+
+// Epilogue over the fp32 tile of rows [0, rows) and columns
+// [n0, n0 + BN): value stores (or fp32 atomics) and the routing-weight
+// gradient partial of this n tile.
+template <int BM, int BN, int C_LD>
+__device__ void gemm_epilogue(const GemmParams& p, const float* C0, const float* C1, int half,
+                              const RouteMeta<BM>& m, int64_t n0, int64_t ntile) {
+  // fp32 tile row r lives at (r < half ? C0 : C1) + (r % half) * C_LD
+  auto crow = [&](int r) { return (r < half ? C0 : C1) + (r % half) * C_LD; };
+  const int tid = threadIdx.x;
+  const int32_t rows = m.rows;
+  const bool has_w = p.w != nullptr;
+  if (p.out == nullptr) {
+    // only the routing-weight gradient is wanted
+  } else if (p.epi == kEpiStore) {
+    constexpr int TPR = BN / 8;
+    constexpr int RPP = kGemmThreads / TPR;
+    const int cg = tid % TPR;
+    const bool ovec = p.out_dtype != kF32 && p.out_ld % 8 == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
+    for (int r = tid / TPR; r < rows; r += RPP) {
+      const int64_t orow = m.orow[r];
+      if (orow < 0) continue;
+      const float wv = m.w[r];
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float c = round_to(crow(r)[cg * 8 + j], p.val_dtype);
+        if (has_w) {
+          c = c * wv;
+          if (p.prod_dtype >= 0) c = round_to(c, p.prod_dtype);
+        }
+        v[j] = c;
+      }
+      const int64_t nb = n0 + cg * 8;
+      const int64_t off = orow * p.out_ld + nb;
+      if (ovec && nb + 8 <= p.N) {
+        Chunk16 ch;
+        if (p.out_dtype == kBF16) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) ch.b[j] = (bf16_t)v[j];
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) ch.h[j] = (f16_t)v[j];
+        }
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.out) + off) = ch.u;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (nb + j < p.N) store_from_f32(p.out, p.out_dtype, off + j, v[j]);
+      }
+    }
+  } else {  // kEpiAtomic: consecutive lanes -> consecutive columns of one row
+    float* out = reinterpret_cast<float*>(p.out);
+    const int col = tid % BN;
+    const int64_t n = n0 + col;
+    if (n < p.N) {
+      for (int r = tid / BN; r < rows; r += kGemmThreads / BN) {
+        const int64_t orow = m.orow[r];
+        if (orow < 0) continue;
+        float c = round_to(crow(r)[col], p.val_dtype);
+        if (has_w) {
+          c = c * m.w[r];
+          if (p.prod_dtype >= 0) c = round_to(c, p.prod_dtype);
+        }
+        unsafeAtomicAdd(out + orow * p.out_ld + n, c);
+      }
+    }
+  }
+
+  if (p.dg != nullptr) {  // routing-weight gradient partial over this n tile
+    constexpr int TPR = BN / 8;
+    constexpr int RPP = kGemmThreads / TPR;
+    const int cg = tid % TPR;
+    for (int r0 = 0; r0 < BM; r0 += RPP) {
+      const int r = r0 + tid / TPR;
+      float s = 0.f;
+      const int64_t xr = r < rows ? m.dgrow[r] : -1;
+      if (xr >= 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int64_t n = n0 + cg * 8 + j;
+          if (n < p.N)
+            s += round_to(crow(r)[cg * 8 + j], p.dg_val_dtype) *
+                 load_as_f32(p.dg_x, p.dg_x_dtype, xr * p.dg_x_ld + n);
+        }
+      }
+      // fixed-order butterfly over the TPR lanes of the row (deterministic)
+#pragma unroll
+      for (int d = 1; d < TPR; d <<= 1) s += __shfl_xor(s, d, 64);
+      if (cg == 0 && r < rows && xr >= 0 && m.widx[r] >= 0)
+        p.dg[m.widx[r] * p.dg_ntiles + ntile] = s;
+    }
+  }
+}
+
+
+}  // namespace cvmm

@@ -21,11 +21,11 @@
 #include "cvmm_common.h"
 #include "cvmm_internal.h"
 #include "cvmm_mfma.h"
+#include "cvmm_gemm_common.h"
 
 namespace cvmm {
 
 enum BMode : int { kBNContig = 0, kBKContig = 1 };
-constexpr int kGemmThreads = 256;
 
 template <typename OpT, typename AT, typename BT, int BM, int BN, int BMODE>
 __global__ __launch_bounds__(kGemmThreads, 2) void routed_gemm_kernel(const GemmParams p) {
@@ -40,14 +40,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void routed_gemm_kernel(const Gemm
   static_assert(UBK * kGemmThreads == BN * KCH, "B tile split");
 
   __shared__ __attribute__((aligned(16))) char smem[Cfg::SMEM];
-  __shared__ int64_t s_arow[BM];
-  __shared__ int64_t s_orow[BM];
-  __shared__ int64_t s_widx[BM];
-  __shared__ int64_t s_dgrow[BM];
-  __shared__ float s_w[BM];
-  __shared__ int32_t s_expert;
-  __shared__ int64_t s_row0;
-  __shared__ int32_t s_rows;
+  __shared__ RouteMeta<BM> meta;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -58,66 +51,8 @@ __global__ __launch_bounds__(kGemmThreads, 2) void routed_gemm_kernel(const Gemm
   const int64_t ntile = id % n_ntiles;
   const int64_t n0 = ntile * BN;
 
-  // ---- schedule: which expert / routes does m-tile `tile` cover? -----------
-  if (wave == 0) {
-    if (lane == 0) s_expert = -1;
-    int64_t carry = 0;
-    for (int32_t base = 0; base < p.n_experts; base += 64) {
-      const int32_t e = base + lane;
-      int64_t start = 0, end = 0;
-      if (e < p.n_experts) {
-        end = p.offsets[e];
-        start = e > 0 ? p.offsets[e - 1] : 0;
-        end = end < 0 ? 0 : (end > p.n_routes ? p.n_routes : end);
-        start = start < 0 ? 0 : (start > p.n_routes ? p.n_routes : start);
-        if (end < start) end = start;
-      }
-      const int64_t nt = (end - start + BM - 1) / BM;
-      const int64_t incl = wave_incl_scan(nt) + carry;
-      const int64_t excl = incl - nt;
-      if (e < p.n_experts && tile >= excl && tile < incl) {
-        s_expert = e;
-        const int64_t r0 = start + (tile - excl) * BM;
-        s_row0 = r0;
-        s_rows = (int32_t)((end - r0) < BM ? (end - r0) : BM);
-      }
-      carry = __shfl(incl, 63, 64);
-      if (tile < carry) break;
-    }
-  }
-  __syncthreads();
-  const int32_t expert = s_expert;
-  if (expert < 0) return;
-  const int64_t row0 = s_row0;
-  const int32_t rows = s_rows;
-
-  // ---- per-row route metadata -------------------------------------------------
-  for (int r = tid; r < BM; r += kGemmThreads) {
-    int64_t ar = -1, orow = -1, widx = -1, dgr = -1;
-    float wv = 1.f;
-    if (r < rows) {
-      const int64_t q = row0 + r;
-      const int64_t ai = p.a_idx[q] / p.a_div;
-      if (ai >= 0 && ai < p.a_rows) ar = ai;
-      const int64_t oi = p.o_idx[q] / p.o_div;
-      if (oi >= 0 && oi < p.out_rows) orow = oi;
-      if (p.w_idx != nullptr) {
-        const int64_t wi = p.w_idx[q];
-        if (wi >= 0 && wi < p.n_routes) widx = wi;
-      }
-      if (p.w != nullptr && widx >= 0) wv = round_to(load_as_f32(p.w, p.w_dtype, widx), p.w_round);
-      if (p.dg != nullptr) {
-        const int64_t di = p.dg_x_idx[q];
-        if (di >= 0 && di < p.dg_x_rows) dgr = di;
-      }
-    }
-    s_arow[r] = ar;
-    s_orow[r] = orow;
-    s_widx[r] = widx;
-    s_w[r] = wv;
-    s_dgrow[r] = dgr;
-  }
-  __syncthreads();
+  if (!gemm_schedule<BM>(p, tile, meta)) return;
+  const int32_t expert = meta.expert;
 
   OpT* As0 = reinterpret_cast<OpT*>(smem);
   OpT* Bs0 = As0 + Cfg::A_ELEMS;
@@ -133,7 +68,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void routed_gemm_kernel(const Gemm
     const int u = tid + j * kGemmThreads;
     a_m[j] = u / KCH;
     a_kc[j] = u % KCH;
-    const int64_t ar = s_arow[a_m[j]];
+    const int64_t ar = meta.arow[a_m[j]];
     aptr[j] = ar >= 0 ? a_base + ar * p.a_ld : nullptr;
   }
   const BT* b_e = reinterpret_cast<const BT*>(p.b) + (int64_t)expert * p.b_se;
@@ -259,88 +194,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void routed_gemm_kernel(const Gemm
   acc_to_lds<Cfg>(acc, Cs, wm, wn, lane);
   __syncthreads();
 
-  const bool has_w = p.w != nullptr;
-  if (p.out == nullptr) {
-    // only the routing-weight gradient is wanted
-  } else if (p.epi == kEpiStore) {
-    constexpr int TPR = BN / 8;
-    constexpr int RPP = kGemmThreads / TPR;
-    const int cg = tid % TPR;
-    const bool ovec = p.out_dtype != kF32 && p.out_ld % 8 == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
-    for (int r = tid / TPR; r < rows; r += RPP) {
-      const int64_t orow = s_orow[r];
-      if (orow < 0) continue;
-      const float wv = s_w[r];
-      float v[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float c = round_to(Cs[r * Cfg::C_LD + cg * 8 + j], p.val_dtype);
-        if (has_w) {
-          c = c * wv;
-          if (p.prod_dtype >= 0) c = round_to(c, p.prod_dtype);
-        }
-        v[j] = c;
-      }
-      const int64_t nb = n0 + cg * 8;
-      const int64_t off = orow * p.out_ld + nb;
-      if (ovec && nb + 8 <= p.N) {
-        Chunk16 ch;
-        if (p.out_dtype == kBF16) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) ch.b[j] = (bf16_t)v[j];
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) ch.h[j] = (f16_t)v[j];
-        }
-        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.out) + off) = ch.u;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (nb + j < p.N) store_from_f32(p.out, p.out_dtype, off + j, v[j]);
-      }
-    }
-  } else {  // kEpiAtomic: consecutive lanes -> consecutive columns of one row
-    float* out = reinterpret_cast<float*>(p.out);
-    const int col = tid % BN;
-    const int64_t n = n0 + col;
-    if (n < p.N) {
-      for (int r = tid / BN; r < rows; r += kGemmThreads / BN) {
-        const int64_t orow = s_orow[r];
-        if (orow < 0) continue;
-        float c = round_to(Cs[r * Cfg::C_LD + col], p.val_dtype);
-        if (has_w) {
-          c = c * s_w[r];
-          if (p.prod_dtype >= 0) c = round_to(c, p.prod_dtype);
-        }
-        unsafeAtomicAdd(out + orow * p.out_ld + n, c);
-      }
-    }
-  }
-
-  if (p.dg != nullptr) {  // routing-weight gradient partial over this n tile
-    constexpr int TPR = BN / 8;
-    constexpr int RPP = kGemmThreads / TPR;
-    const int cg = tid % TPR;
-    for (int r0 = 0; r0 < BM; r0 += RPP) {
-      const int r = r0 + tid / TPR;
-      float s = 0.f;
-      const int64_t xr = r < rows ? s_dgrow[r] : -1;
-      if (xr >= 0) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int64_t n = n0 + cg * 8 + j;
-          if (n < p.N)
-            s += round_to(Cs[r * Cfg::C_LD + cg * 8 + j], p.dg_val_dtype) *
-                 load_as_f32(p.dg_x, p.dg_x_dtype, xr * p.dg_x_ld + n);
-        }
-      }
-      // fixed-order butterfly over the TPR lanes of the row (deterministic)
-#pragma unroll
-      for (int d = 1; d < TPR; d <<= 1) s += __shfl_xor(s, d, 64);
-      if (cg == 0 && r < rows && xr >= 0 && s_widx[r] >= 0)
-        p.dg[s_widx[r] * p.dg_ntiles + ntile] = s;
-    }
-  }
+  gemm_epilogue<BM, BN, Cfg::C_LD>(p, Cs, Cs + (BM / 2) * Cfg::C_LD, BM / 2, meta, n0, ntile);
 }
 
 template <typename OpT, typename AT, typename BT, int BM, int BN>

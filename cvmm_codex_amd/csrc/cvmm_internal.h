@@ -5,6 +5,8 @@
 #include <stdint.h>
 #include <stddef.h>
 
+#include "cvmm_common.h"
+
 namespace cvmm {
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -86,6 +88,7 @@ struct WgradParams {
   int32_t g_vec;
   const int64_t* g_idx;
   int64_t g_div;
+  FastDiv g_fdiv;          // g_div as multiply-shift (route indices < 2^31)
   const void* w;
   int32_t w_dtype;
   const int64_t* w_idx;
@@ -123,6 +126,12 @@ hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_rout
                               int64_t* offsets, int32_t* n_invalid, void* ws, hipStream_t stream);
 hipError_t launch_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_experts,
                                  int64_t* offsets, hipStream_t stream);
+
+// keys (any float storage / strides) -> op dtype copies kt [E][d_out][d_in]
+// and/or kn [E][d_in][d_out] (either may be null)
+hipError_t launch_cast_keys(const void* keys, int32_t keys_dtype, int64_t se, int64_t si, int64_t sj,
+                            int32_t n_experts, int64_t d_in, int64_t d_out, int32_t out_dtype, void* kt,
+                            void* kn, hipStream_t stream);
 
 // ---------------------------------------------------------------------------
 // small kernels

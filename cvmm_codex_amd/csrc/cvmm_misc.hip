@@ -1,7 +1,8 @@
 // Small bandwidth kernels around the routed GEMMs: zero fill (used instead of
 // hipMemsetAsync so a captured graph holds only kernel nodes), the top-k row
 // combine of a route-ordered buffer, fp32 -> storage casts and the ordered
-// sum of per-tile routing-weight gradient partials.
+// sum of per-tile routing-weight gradient partials.  Row kernels move 8
+// columns (16 bytes of 16-bit data) per thread.
 #include "cvmm_common.h"
 #include "cvmm_internal.h"
 
@@ -32,54 +33,127 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// out[t][n] = rnd(rnd(sum_j w_j * buf[t*k + j][n], mid), out)   (j in route order)
+// 8 consecutive columns of any storage type as floats (vector when aligned).
+__device__ __forceinline__ void load8_any(const void* p, int32_t dt, int64_t off, bool vec, int64_t nvalid,
+                                          float (&v)[8]) {
+  if (vec && nvalid >= 8) {
+    if (dt == kF32) {
+      const float4 a = *reinterpret_cast<const float4*>((const float*)p + off);
+      const float4 b = *reinterpret_cast<const float4*>((const float*)p + off + 4);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+      Chunk16 c;
+      c.u = *reinterpret_cast<const uint4*>((const uint16_t*)p + off);
+      if (dt == kBF16) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (float)c.b[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (float)c.h[j];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = j < nvalid ? load_as_f32(p, dt, off + j) : 0.f;
+  }
+}
+
+__device__ __forceinline__ void store8_any(void* p, int32_t dt, int64_t off, bool vec, int64_t nvalid,
+                                           const float (&v)[8]) {
+  if (vec && nvalid >= 8) {
+    if (dt == kF32) {
+      *reinterpret_cast<float4*>((float*)p + off) = make_float4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<float4*>((float*)p + off + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+      Chunk16 c;
+      if (dt == kBF16) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c.b[j] = (bf16_t)v[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c.h[j] = (f16_t)v[j];
+      }
+      *reinterpret_cast<uint4*>((uint16_t*)p + off) = c.u;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < nvalid) store_from_f32(p, dt, off + j, v[j]);
+  }
+}
+
+__host__ __device__ inline bool vec_ok(const void* p, int32_t dt, int64_t ld) {
+  return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && (ld * (int64_t)dtype_size(dt)) % 16 == 0;
+}
+
+// out[t][n] = rnd(rnd(sum_j w_j * buf[t*k + j][n], mid), out), j in route order
+// (the top-k sum of cvmm.py:1223 and the weighted combine of cvmm.py:1545).
 __global__ void combine_rows_kernel(const void* __restrict__ buf, int32_t buf_dtype, int64_t buf_ld,
                                     const void* __restrict__ w, int32_t w_dtype, int32_t w_round, int64_t k,
                                     int64_t n, int32_t mid_dtype, void* __restrict__ out, int32_t out_dtype,
-                                    int64_t out_ld) {
+                                    int64_t out_ld, bool in_vec, bool out_vec) {
   const int64_t t = blockIdx.x;
-  const int64_t col = (int64_t)blockIdx.y * blockDim.x + threadIdx.x;
-  if (col >= n) return;
-  float s = 0.f;
+  const int64_t c = ((int64_t)blockIdx.y * blockDim.x + threadIdx.x) * 8;
+  if (c >= n) return;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int64_t j = 0; j < k; ++j) {
     const int64_t r = t * k + j;
-    float v = load_as_f32(buf, buf_dtype, r * buf_ld + col);
-    if (w != nullptr) v *= round_to(load_as_f32(w, w_dtype, r), w_round);
-    s += v;
+    const float wv = w != nullptr ? round_to(load_as_f32(w, w_dtype, r), w_round) : 1.f;
+    float v[8];
+    load8_any(buf, buf_dtype, r * buf_ld + c, in_vec, n - c, v);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] += wv * v[q];
   }
-  if (mid_dtype >= 0) s = round_to(s, mid_dtype);
-  store_from_f32(out, out_dtype, t * out_ld + col, s);
+  if (mid_dtype >= 0) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] = round_to(acc[q], mid_dtype);
+  }
+  store8_any(out, out_dtype, t * out_ld + c, out_vec, n - c, acc);
+}
+
+static void rows_grid(int64_t rows, int64_t n, dim3* grid, dim3* block) {
+  int64_t chunks = (n + 7) / 8;
+  int threads = (int)((chunks + 63) / 64 * 64);
+  if (threads > 256) threads = 256;
+  *block = dim3(threads);
+  *grid = dim3((unsigned)rows, (unsigned)((chunks + threads - 1) / threads));
 }
 
 hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_ld, const void* w, int32_t w_dtype,
                                int32_t w_round, int64_t n_tokens, int64_t k, int64_t n, int32_t mid_dtype,
                                void* out, int32_t out_dtype, int64_t out_ld, hipStream_t stream) {
   if (n_tokens <= 0 || n <= 0) return hipSuccess;
-  if (n_tokens > 0x7fffffffll) return hipErrorInvalidValue;
-  if ((n + 255) / 256 > 65535) return hipErrorInvalidValue;
-  dim3 grid((unsigned)n_tokens, (unsigned)((n + 255) / 256));
-  hipLaunchKernelGGL(combine_rows_kernel, grid, dim3(256), 0, stream, buf, buf_dtype, buf_ld, w, w_dtype, w_round,
-                     k, n, mid_dtype, out, out_dtype, out_ld);
+  if (n_tokens > 0x7fffffffll || (n + 2047) / 2048 > 65535) return hipErrorInvalidValue;
+  dim3 grid, block;
+  rows_grid(n_tokens, n, &grid, &block);
+  hipLaunchKernelGGL(combine_rows_kernel, grid, block, 0, stream, buf, buf_dtype, buf_ld, w, w_dtype, w_round, k, n,
+                     mid_dtype, out, out_dtype, out_ld, vec_ok(buf, buf_dtype, buf_ld), vec_ok(out, out_dtype, out_ld));
   return hipGetLastError();
 }
 
 __global__ void cast_rows_kernel(const float* __restrict__ acc, int64_t acc_ld, int64_t n, int32_t mid_dtype,
-                                 void* __restrict__ out, int32_t out_dtype, int64_t out_ld) {
+                                 void* __restrict__ out, int32_t out_dtype, int64_t out_ld, bool in_vec,
+                                 bool out_vec) {
   const int64_t t = blockIdx.x;
-  const int64_t col = (int64_t)blockIdx.y * blockDim.x + threadIdx.x;
-  if (col >= n) return;
-  float v = acc[t * acc_ld + col];
-  if (mid_dtype >= 0) v = round_to(v, mid_dtype);
-  store_from_f32(out, out_dtype, t * out_ld + col, v);
+  const int64_t c = ((int64_t)blockIdx.y * blockDim.x + threadIdx.x) * 8;
+  if (c >= n) return;
+  float v[8];
+  load8_any(acc, kF32, t * acc_ld + c, in_vec, n - c, v);
+  if (mid_dtype >= 0) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = round_to(v[q], mid_dtype);
+  }
+  store8_any(out, out_dtype, t * out_ld + c, out_vec, n - c, v);
 }
 
 hipError_t launch_cast_rows(const float* acc, int64_t acc_ld, int64_t rows, int64_t n, int32_t mid_dtype,
                             void* out, int32_t out_dtype, int64_t out_ld, hipStream_t stream) {
   if (rows <= 0 || n <= 0) return hipSuccess;
-  if (rows > 0x7fffffffll) return hipErrorInvalidValue;
-  if ((n + 255) / 256 > 65535) return hipErrorInvalidValue;
-  dim3 grid((unsigned)rows, (unsigned)((n + 255) / 256));
-  hipLaunchKernelGGL(cast_rows_kernel, grid, dim3(256), 0, stream, acc, acc_ld, n, mid_dtype, out, out_dtype, out_ld);
+  if (rows > 0x7fffffffll || (n + 2047) / 2048 > 65535) return hipErrorInvalidValue;
+  dim3 grid, block;
+  rows_grid(rows, n, &grid, &block);
+  hipLaunchKernelGGL(cast_rows_kernel, grid, block, 0, stream, acc, acc_ld, n, mid_dtype, out, out_dtype, out_ld,
+                     vec_ok(acc, kF32, acc_ld), vec_ok(out, out_dtype, out_ld));
   return hipGetLastError();
 }
 

@@ -76,6 +76,15 @@ int cvmm_sort_routes(const void* sel, int32_t sel_is_int64, int64_t n_routes, in
 int cvmm_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_experts, int64_t* offsets,
                         void* stream);
 
+/* Cast the expert weights once per step to the MFMA operand type (bf16/f16)
+ * in the two k-contiguous layouts the routed GEMMs read:
+ *   keys_t [E][d_out][d_in]  (forward)   keys_n [E][d_in][d_out]  (grad-input)
+ * Either output may be NULL.  Replaces the per-tile in-register weight cast
+ * of cvmm_kernel (cvmm.py:198-204) with one pass per step; RNE rounding. */
+int cvmm_cast_keys(const void* keys, int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out,
+                   int64_t k_se, int64_t k_si, int64_t k_sj, int32_t out_dtype, void* keys_t, void* keys_n,
+                   void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Forward: CVMM.forward (cvmm.py:1524-1550) = cvmm_triton (cvmm.py:814-867)  */
 /* + the weighted top-k combine (cvmm.py:1543-1545)                            */

@@ -48,8 +48,9 @@ __all__ = [
 def f32_to_bf16_bits(a: np.ndarray) -> np.ndarray:
     """fp32 -> bf16 bit pattern, round-to-nearest-even, NaN -> quiet NaN."""
     a32 = np.ascontiguousarray(a, dtype=np.float32)
-    u = a32.view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    u = a32.view(np.uint32)
+    # uint32 arithmetic: only NaN bit patterns can wrap, and those are replaced
+    r = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
     nan = np.isnan(a32)
     if nan.any():
         r = r.copy()
