@@ -164,84 +164,73 @@ __global__ __launch_bounds__(256, 2) void wgrad_v2_kernel(const WgradParams p) {
     b_col[j] = (((lane % TB::CPR) ^ TB::swz(row)) * 8);
   }
 
-  // route -> (x row, dY row); -1 when the route is past the chunk or invalid.
-  // Row indices fit int32 (the C ABI rejects > 2^31 routes).
-  auto route_rows = [&](int64_t q, int32_t& xr, int32_t& gr) {
-    xr = -1;
-    gr = -1;
+  // Route rows of a stage: lane t of every wave resolves route lo + 64*stage + t
+  // (coalesced index loads, one division per route); DMA lanes then fetch the
+  // row of the route they copy with a cross-lane shuffle.  -1 = no route.
+  // Row indices fit int32 (the C ABI rejects more than 2^31 - 1 routes).
+  struct StageRoutes {
+    int32_t xr, gr;
+    float w;
+  };
+  auto load_routes = [&](int64_t stage, StageRoutes& sr) {
+    const int64_t q = lo + stage * 64 + lane;
+    sr.xr = -1;
+    sr.gr = -1;
+    sr.w = 0.f;
     if (q < hi) {
       const int64_t xi = p.x_idx[q];
       const int64_t graw = p.g_idx[q];
       const int64_t gi = (graw >= 0 && graw < 0x7fffffffll) ? p.g_fdiv.div(graw) : -1;
       if (xi >= 0 && xi < p.x_rows && gi >= 0 && gi < p.g_rows) {
-        xr = (int32_t)xi;
-        gr = (int32_t)gi;
-      }
-    }
-  };
-
-  int32_t ax_cur[TA::PER_WAVE], ax_nxt[TA::PER_WAVE];
-  int32_t bg_cur[TB::PER_WAVE], bg_nxt[TB::PER_WAVE];
-  // weighted: dY chunks through registers
-  constexpr int GCH = WEIGHTED ? Cfg::GCH : 1;
-  int32_t gr_cur[GCH], gr_nxt[GCH];
-  float gw_cur[GCH], gw_nxt[GCH];
-  uint4 g_val[GCH];
-
-  auto load_idx = [&](int64_t stage, int32_t (&ax)[TA::PER_WAVE], int32_t (&bg)[TB::PER_WAVE],
-                      int32_t (&gr)[GCH], float (&gw)[GCH]) {
-    const int64_t q0 = lo + stage * 64;
-    int32_t dummy;
-#pragma unroll
-    for (int j = 0; j < TA::PER_WAVE; ++j) route_rows(q0 + a_row[j], ax[j], dummy);
-    if constexpr (!WEIGHTED) {
-#pragma unroll
-      for (int j = 0; j < TB::PER_WAVE; ++j) route_rows(q0 + b_row[j], dummy, bg[j]);
-    } else {
-#pragma unroll
-      for (int j = 0; j < GCH; ++j) {
-        const int64_t q = q0 + (tid + j * 256) / TB::CPR;
-        route_rows(q, dummy, gr[j]);
-        float w = 0.f;
-        if (gr[j] >= 0) {
+        sr.xr = (int32_t)xi;
+        sr.gr = (int32_t)gi;
+        if constexpr (WEIGHTED) {
           const int64_t wi = p.w_idx[q];
-          w = (wi >= 0 && wi < p.n_routes) ? round_to(load_as_f32(p.w, p.w_dtype, wi), OP) : 0.f;
+          sr.w = (wi >= 0 && wi < p.n_routes) ? round_to(load_as_f32(p.w, p.w_dtype, wi), OP) : 0.f;
         }
-        gw[j] = w;
       }
     }
   };
 
-  auto issue = [&](const int32_t (&ax)[TA::PER_WAVE], const int32_t (&bg)[TB::PER_WAVE], char* st) {
+  constexpr int GCH = WEIGHTED ? Cfg::GCH : 1;
+  uint4 g_val[GCH];
+  float g_w[GCH];
+
+  auto issue = [&](const StageRoutes& sr, char* st) {
 #pragma unroll
     for (int j = 0; j < TA::PER_WAVE; ++j) {
+      const int32_t xr = __shfl(sr.xr, a_row[j], 64);
       const int64_t col = m0 + a_col[j];
-      const char* src = (ax[j] >= 0 && col < p.M) ? xb + ((int64_t)ax[j] * p.x_ld + col) * 2 : zero;
+      const char* src = (xr >= 0 && col < p.M) ? xb + ((int64_t)xr * p.x_ld + col) * 2 : zero;
       wg_dma16(src, st + (wave * TA::PER_WAVE + j) * 1024);
     }
     if constexpr (!WEIGHTED) {
 #pragma unroll
       for (int j = 0; j < TB::PER_WAVE; ++j) {
+        const int32_t gr = __shfl(sr.gr, b_row[j], 64);
         const int64_t col = n0 + b_col[j];
-        const char* src = (bg[j] >= 0 && col < p.N) ? gb + ((int64_t)bg[j] * p.g_ld + col) * 2 : zero;
+        const char* src = (gr >= 0 && col < p.N) ? gb + ((int64_t)gr * p.g_ld + col) * 2 : zero;
         wg_dma16(src, st + TA::BYTES + (wave * TB::PER_WAVE + j) * 1024);
       }
     }
   };
 
   // weighted dY: global -> registers (issued with the DMA), scaled into LDS after the MFMAs
-  auto g_load = [&](const int32_t (&gr)[GCH]) {
+  auto g_load = [&](const StageRoutes& sr) {
     if constexpr (WEIGHTED) {
 #pragma unroll
       for (int j = 0; j < GCH; ++j) {
-        const int64_t col = n0 + ((tid + j * 256) % TB::CPR) * 8;
-        g_val[j] = (gr[j] >= 0 && col < p.N)
-                       ? *reinterpret_cast<const uint4*>(gb + ((int64_t)gr[j] * p.g_ld + col) * 2)
-                       : make_uint4(0, 0, 0, 0);
+        const int u = tid + j * 256;
+        const int row = u / TB::CPR;
+        const int32_t gr = __shfl(sr.gr, row, 64);
+        g_w[j] = __shfl(sr.w, row, 64);
+        const int64_t col = n0 + (u % TB::CPR) * 8;
+        g_val[j] = (gr >= 0 && col < p.N) ? *reinterpret_cast<const uint4*>(gb + ((int64_t)gr * p.g_ld + col) * 2)
+                                          : make_uint4(0, 0, 0, 0);
       }
     }
   };
-  auto g_store = [&](const float (&gw)[GCH], char* st) {
+  auto g_store = [&](char* st) {
     if constexpr (WEIGHTED) {
 #pragma unroll
       for (int j = 0; j < GCH; ++j) {
@@ -250,7 +239,7 @@ __global__ __launch_bounds__(256, 2) void wgrad_v2_kernel(const WgradParams p) {
         c.u = g_val[j];
         float v[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] = round_to(to_f32(reinterpret_cast<const OpT*>(&c)[q]) * gw[j], OP);
+        for (int q = 0; q < 8; ++q) v[q] = round_to(to_f32(reinterpret_cast<const OpT*>(&c)[q]) * g_w[j], OP);
         *reinterpret_cast<uint4*>(st + TA::BYTES + TB::off(u / TB::CPR, (u % TB::CPR) * 8)) = pack_chunk<OpT>(v);
       }
     }
@@ -304,41 +293,42 @@ __global__ __launch_bounds__(256, 2) void wgrad_v2_kernel(const WgradParams p) {
   };
 
   if (n_stages > 0) {
-    load_idx(0, ax_cur, bg_cur, gr_cur, gw_cur);
+    StageRoutes r_cur, r_nxt;
+    load_routes(0, r_cur);
     wg_wait_vmcnt<0>();
-    issue(ax_cur, bg_cur, stage0);
-    g_load(gr_cur);
-    if (n_stages > 1) load_idx(1, ax_nxt, bg_nxt, gr_nxt, gw_nxt);
+    issue(r_cur, stage0);
+    g_load(r_cur);
+    if (n_stages > 1) load_routes(1, r_nxt);
     wg_wait_vmcnt<0>();
-    g_store(gw_cur, stage0);
+    g_store(stage0);
     for (int64_t s = 0; s < n_stages; s += 2) {
-      // ---- even stage: read stage0, fill stage1
+      // ---- even stage: read stage0, fill stage1 (routes in r_nxt)
       wg_wait_vmcnt<0>();
       __syncthreads();
       if (s + 1 < n_stages) {
-        issue(ax_nxt, bg_nxt, stage1);
-        g_load(gr_nxt);
+        issue(r_nxt, stage1);
+        g_load(r_nxt);
       }
-      if (s + 2 < n_stages) load_idx(s + 2, ax_cur, bg_cur, gr_cur, gw_cur);
+      if (s + 2 < n_stages) load_routes(s + 2, r_cur);
       compute(stage0);
       if (s + 1 >= n_stages) break;
       if constexpr (WEIGHTED) {
         wg_wait_vmcnt<0>();
-        g_store(gw_nxt, stage1);
+        g_store(stage1);
       }
-      // ---- odd stage: read stage1, fill stage0
+      // ---- odd stage: read stage1, fill stage0 (routes in r_cur)
       wg_wait_vmcnt<0>();
       __syncthreads();
       if (s + 2 < n_stages) {
-        issue(ax_cur, bg_cur, stage0);
-        g_load(gr_cur);
+        issue(r_cur, stage0);
+        g_load(r_cur);
       }
-      if (s + 3 < n_stages) load_idx(s + 3, ax_nxt, bg_nxt, gr_nxt, gw_nxt);
+      if (s + 3 < n_stages) load_routes(s + 3, r_nxt);
       compute(stage1);
       if constexpr (WEIGHTED) {
         if (s + 2 < n_stages) {
           wg_wait_vmcnt<0>();
-          g_store(gw_cur, stage0);
+          g_store(stage0);
         }
       }
     }
