@@ -6,9 +6,11 @@ A step = one pass of the CVMM hot path over one batch of synthetic input:
 selector preparation (stable counting sort), forward, and backward (grad x,
 grad keys, grad reduction weight), launched by the drop-in API exactly as a
 training step would.  ``value`` is whole-job TFLOP/s = 6*R*d_in*d_out / step
-time (inputs resident in HBM).  The dominant kernel is also timed on its own
-with HIP events on the stream it runs on, giving ``roofline``; the CPU oracle
-is timed on a bounded sample of the same workload as ``cpu_baseline``.
+time (inputs resident in HBM).  Every kernel is also timed on its own: the
+library brackets each launch with HIP events on the stream it runs on, and the
+kernel class with the most device time per step gives ``roofline``
+(algorithmic bytes or flops of one launch / its average launch time).  The CPU
+oracle is timed on a bounded sample of the same workload as ``cpu_baseline``.
 """
 from __future__ import annotations
 
@@ -103,14 +105,12 @@ def time_phases(runner: Runner, iters: int):
 
 
 def kernel_launchers(runner: Runner):
-    """One C-ABI call per hot kernel, with every input already on the device.
-
-    Each returns a callable that launches exactly that phase on the current
-    stream (routed GEMM forward / grad-input, weight gradient)."""
+    """One C-ABI phase per entry, with every input already on the device, for
+    ``--only`` (rocprofv3 runs of a single phase): routed GEMM forward, weight
+    gradient, grad-input, bf16 weight copies."""
     C = runner.C
     s = runner.prepare()
     op = torch.bfloat16 if runner.p.amp else torch.float32
-    y = None
     with torch.autocast("cuda", dtype=torch.bfloat16, enabled=runner.p.amp):
         y = C.cvmm(runner.x, s, runner.keys)
     go = runner.p.grad_out.to(y.dtype)
@@ -142,22 +142,78 @@ def kernel_launchers(runner: Runner):
     return out
 
 
-def time_launcher(fn, iters: int):
-    stream = torch.cuda.current_stream()
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    fn()
+# kernel classes timed by the library's hooks (CVMM_KC_* in include/cvmm_hip.h)
+def _classes():
+    from cvmm_codex_amd import _native as N
+    return {"sort": N.KC_SORT, "offsets": N.KC_OFFSETS, "cast_keys": N.KC_CAST_KEYS,
+            "gemm_fwd": N.KC_GEMM_FWD, "gemm_bwd_x": N.KC_GEMM_BWDX, "wgrad": N.KC_WGRAD,
+            "combine": N.KC_COMBINE, "fill": N.KC_FILL}
+
+
+def kernel_times(runner: Runner, steps: int):
+    """Per-launch device time of every kernel class over `steps` training steps:
+    the library brackets each launch with HIP events on its own stream."""
+    import ctypes
+    from cvmm_codex_amd import _native as N
+    lib = N.lib()
+    classes = _classes()
+    runner.step()
     torch.cuda.synchronize()
-    a.record(stream)
+    lib.cvmm_timing_enable(sum(classes.values()))
+    try:
+        for _ in range(steps):
+            runner.step()
+        torch.cuda.synchronize()
+    finally:
+        lib.cvmm_timing_enable(0)
+    out = {}
+    for name, cls in classes.items():
+        ms, n = ctypes.c_double(), ctypes.c_int64()
+        N.check(lib.cvmm_timing_result(cls, ctypes.byref(ms), ctypes.byref(n)), "cvmm_timing_result")
+        if n.value:
+            out[name] = {"avg_ms": ms.value / n.value, "launches_per_step": n.value / steps,
+                         "ms_per_step": ms.value / steps}
+    return out
+
+
+def kernel_work(proj: W.Projection, name: str):
+    """Algorithmic flops and HBM bytes of ONE launch of a hot kernel class:
+    every operand byte read once and every result byte written once, at the
+    storage widths the fast path uses (16-bit operands under autocast, fp32
+    weight gradient)."""
+    R = proj.routes
+    E, d_in, d_out = proj.keys.shape
+    top_k = proj.sel.shape[-1]
+    b = 2 if proj.amp else 4
+    tokens = R // top_k
+    weighted = proj.weights is not None
+    x_rows = R if proj.route_input else tokens
+    keys_b = E * d_in * d_out * b
+    flops = 2.0 * R * d_in * d_out
+    if name == "gemm_fwd":
+        # x rows + weight copy + y (output rows, or the route-ordered buffer the combine reads)
+        return flops, x_rows * d_in * b + keys_b + R * d_out * b
+    if name == "gemm_bwd_x":
+        g_rows = tokens if weighted else R
+        by = g_rows * d_out * b + keys_b + R * d_in * b
+        if weighted:  # routing-weight gradient: x rows re-read, one fp32 partial per route and n-tile
+            by += x_rows * d_in * b + R * max(1, d_in // 128) * 4
+        return flops, by
+    if name == "wgrad":
+        g_rows = tokens if weighted else R
+        return flops, x_rows * d_in * b + g_rows * d_out * b + E * d_in * d_out * 4
+    return None, None
+
+
+def copy_calibration(nbytes: int = 256 << 20, iters: int = 5):
+    """A plain device copy of known size: the reference reading of FETCH_SIZE
+    and WRITE_SIZE (nbytes read and nbytes written per launch)."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").uniform_()
+    dst = torch.empty_like(src)
     for _ in range(iters):
-        fn()
-    b.record(stream)
+        dst.copy_(src)
     torch.cuda.synchronize()
-    return a.elapsed_time(b) / iters
-
-
-def phase_flops(proj: W.Projection, phase: str) -> float:
-    return 2.0 * proj.routes * proj.keys.shape[1] * proj.keys.shape[2]
+    log(f"copied {nbytes} bytes {iters} times")
 
 
 def cpu_baseline(proj: W.Projection, budget_s: float = 12.0):
@@ -209,19 +265,22 @@ def main():
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(W.PROJECTIONS))
     ap.add_argument("--kernel-iters", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["fwd", "bwd_w", "bwd_x", "cast_keys"], default=None,
-                    help="launch only this phase --steps times (for rocprofv3 runs)")
+    ap.add_argument("--only", choices=["fwd", "bwd_w", "bwd_x", "cast_keys", "copy"], default=None,
+                    help="launch only this phase --steps times, or the copy calibration (rocprofv3 runs)")
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path would shard over experts, which is not built here)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         sys.exit(1)
 
     dev = torch.device("cuda:0")
+    if args.only == "copy":
+        copy_calibration(iters=args.steps)
+        return
     proj = W.PROJECTIONS[args.workload]()
     runner = Runner(proj, dev)
 
@@ -243,16 +302,24 @@ def main():
     phases = time_phases(runner, max(10, args.steps // 2))
     log(f"phases {phases}")
 
-    launchers = kernel_launchers(runner)
-    kern = {k: time_launcher(f, args.kernel_iters) for k, f in launchers.items()}
-    log(f"per-call ms {kern}")
-    dom = max((k for k in kern if k != "cast_keys"), key=kern.get)
+    kt = kernel_times(runner, args.kernel_iters)
+    log("kernel ms/launch " + json.dumps({k: round(v["avg_ms"], 5) for k, v in kt.items()}))
     dtype = "bf16" if proj.amp else "fp32"
-    flops = phase_flops(proj, dom)
-    achieved = flops / (kern[dom] * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 3), "peak": PEAK[dtype],
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK[dtype], 5),
-                "traffic": load_traffic(dom, proj.name), "avg_launch_ms": round(kern[dom], 5)}
+    peak = PEAK[dtype]
+    # dominant kernel: the hot kernel class with the most device time per step
+    dom = max((k for k in kt if kernel_work(proj, k)[0] is not None), key=lambda k: kt[k]["ms_per_step"])
+    flops, nbytes = kernel_work(proj, dom)
+    sec = kt[dom]["avg_ms"] * 1e-3
+    t_mfma, t_hbm = flops / (peak * 1e12), nbytes / (HBM_PEAK_GBS * 1e9)
+    if t_hbm >= t_mfma:
+        roofline = {"bound": "hbm", "achieved": round(nbytes / sec / 1e9, 2), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 5)}
+    else:
+        roofline = {"bound": "mfma", "achieved": round(flops / sec / 1e12, 3), "peak": peak,
+                    "unit": "TFLOP/s", "frac": round(flops / sec / 1e12 / peak, 5)}
+    roofline.update({"traffic": load_traffic(dom, proj.name), "kernel": dom,
+                     "avg_launch_ms": round(kt[dom]["avg_ms"], 5), "algorithmic_bytes": int(nbytes),
+                     "algorithmic_flops": flops})
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -271,7 +338,7 @@ def main():
                    "step": "sel+fwd+bwd", "gflop_per_step": round(proj.flops / 1e9, 3)},
         "step_roofline_frac": round(value / PEAK[dtype], 5),
         "breakdown_ms": {k: round(v, 5) for k, v in phases.items()},
-        "kernel_ms": {k: round(v, 5) for k, v in kern.items()},
+        "kernel_ms_per_launch": {k: round(v["avg_ms"], 5) for k, v in kt.items()},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

@@ -17,6 +17,12 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcvmm_hip
 
 F32, F16, BF16 = 0, 1, 2            # cvmm.py:36-44 dtype ids
 FLAG_ATOMIC_REDUCE = 1
+FLAG_COUNTERS_ZEROED = 2
+TUNE_PANEL_TILES_PER_WG = 1
+
+# kernel classes of the timing hooks (include/cvmm_hip.h CVMM_KC_*)
+KC_SORT, KC_OFFSETS, KC_CAST_KEYS, KC_GEMM_FWD, KC_GEMM_BWDX, KC_WGRAD, KC_COMBINE, KC_FILL = (
+    1, 2, 4, 8, 16, 32, 64, 128)
 
 _DTYPE_ID = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -28,8 +34,12 @@ _SZ = ctypes.c_size_t
 _SIGS = {
     "cvmm_last_error": (ctypes.c_char_p, []),
     "cvmm_abi_version": (ctypes.c_int, []),
+    "cvmm_timing_enable": (ctypes.c_int, [ctypes.c_uint32]),
+    "cvmm_tuning_set": (ctypes.c_int, [_I32, _I64]),
+    "cvmm_timing_result": (ctypes.c_int, [ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
+                                          ctypes.POINTER(ctypes.c_int64)]),
     "cvmm_sort_workspace_bytes": (_SZ, [_I64, _I32]),
-    "cvmm_sort_routes": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "cvmm_sort_routes": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "cvmm_expert_offsets": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
     "cvmm_cast_keys": (ctypes.c_int, [_P, _I32, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P]),
     "cvmm_fwd_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I32, _I32, _I32, _I32]),
@@ -38,7 +48,7 @@ _SIGS = {
         _P, _I32, _I32, _I64, _I64,           # keys, dtype, E, d_in, d_out
         _I64, _I64, _I64,                     # key strides
         _P, _P, _P, _I64,                     # sorted_sel, sel_index, out_index, R
-        _P, _P, _I32, _I64,                   # offsets, rw, rw dtype, reduce_k
+        _P, _P, _P, _I32, _I64,               # offsets, route_pos, rw, rw dtype, reduce_k
         _I32, _P, _I32, _I64, _I64,           # op, out, out dtype, out rows, out ld
         _I32, _P, _SZ, _P]),                  # flags, ws, ws bytes, stream
     "cvmm_bwd_x_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I32, _I32, _I32, _I64, _I32, _I32, _I32, _I32]),
@@ -47,11 +57,12 @@ _SIGS = {
         _P, _I32, _I32, _I64, _I64,           # keys, dtype, E, d_in, d_out
         _I64, _I64, _I64,                     # key strides
         _P, _P, _P, _I64,                     # sorted_sel, sel_index, out_index, R
-        _P, _P, _I32, _I64,                   # offsets, rw, rw dtype, top_k
+        _P, _P, _P, _I32, _I64,               # offsets, route_pos, rw, rw dtype, top_k
         _P, _I32, _I64, _I64, _I32,           # x, x dtype, x rows, x ld, op
         _P, _I32, _I64, _I64,                 # grad_x, dtype, rows, ld
         _P, _I32,                             # grad_rw, dtype
         _I32, _P, _SZ, _P]),
+    "cvmm_bwd_w_counter_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I32]),
     "cvmm_bwd_w_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I32, _I32]),
     "cvmm_bwd_w": (ctypes.c_int, [
         _P, _I32, _I64, _I64,                 # x
@@ -113,5 +124,12 @@ def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """Raw handle of the current HIP stream of `device` (the kernels launch on it)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(idx)
+    return torch.cuda.current_stream(idx).cuda_stream

@@ -92,21 +92,36 @@ def _flat_int32(sel: torch.Tensor) -> torch.Tensor:
     return f.contiguous()
 
 
+_SORT_WS: Dict[Tuple[torch.device, int], torch.Tensor] = {}
+
+
 def _sort_routes(raw_flat: torch.Tensor, n_experts: int, top_k: int):
     """Stable counting sort on the device: (sorted int32, perm int64,
-    perm // top_k int64, inclusive offsets int64[E])."""
+    perm // top_k int64, inclusive offsets int64[E]).  `raw_flat` holds int32
+    or int64 ids (int64 read as their low 32 bits, like an int32 cast).  The
+    inverse permutation (int32) is attached to perm as ``_cvmm_route_pos``: the
+    forward/backward calls that receive this perm as their route index use it
+    to gather each token's routes."""
     lib = N.lib()
     dev = raw_flat.device
+    if raw_flat.dtype not in (torch.int32, torch.int64):
+        raw_flat = raw_flat.to(torch.int32)
+    raw_flat = raw_flat.contiguous()
     R = raw_flat.numel()
-    ssel = torch.empty(R, dtype=torch.int32, device=dev)
-    perm = torch.empty(R, dtype=torch.int64, device=dev)
-    tok = torch.empty(R, dtype=torch.int64, device=dev)
-    offsets = torch.empty(n_experts, dtype=torch.int64, device=dev)
+    stream = N.stream_of(dev)
+    i32 = torch.empty(2 * R, dtype=torch.int32, device=dev)
+    ssel, route_pos = i32[:R], i32[R:]
+    ints = torch.empty(2 * R + n_experts, dtype=torch.int64, device=dev)
+    perm, tok, offsets = ints[:R], ints[R:2 * R], ints[2 * R:]
     ws_bytes = lib.cvmm_sort_workspace_bytes(R, n_experts)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    N.check(lib.cvmm_sort_routes(N.ptr(raw_flat), 0, R, n_experts, max(top_k, 1), N.ptr(ssel), N.ptr(perm),
-                                 N.ptr(tok), N.ptr(offsets), None, N.ptr(ws), ws_bytes, N.stream_of(dev)),
-            "cvmm_sort_routes")
+    ws = _SORT_WS.get((dev, stream))
+    if ws is None or ws.numel() < ws_bytes:
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        _SORT_WS[(dev, stream)] = ws
+    N.check(lib.cvmm_sort_routes(N.ptr(raw_flat), int(raw_flat.dtype == torch.int64), R, n_experts, max(top_k, 1),
+                                 N.ptr(ssel), N.ptr(perm), N.ptr(tok), N.ptr(offsets), N.ptr(route_pos), None,
+                                 N.ptr(ws), ws.numel(), stream), "cvmm_sort_routes")
+    perm._cvmm_route_pos = route_pos
     return ssel, perm, tok, offsets
 
 
@@ -195,7 +210,8 @@ class CVMMSel:
 
     def __init__(self, raw_sel: torch.Tensor, sel: torch.Tensor, sel_index: torch.Tensor,
                  out_index: Optional[torch.Tensor] = None, reduction_weight: Optional[torch.Tensor] = None):
-        self.raw_sel = raw_sel
+        self._raw_sel = raw_sel
+        self._raw_src: Optional[torch.Tensor] = None
         self._sel = sel
         self._sel_index = sel_index
         self._out_index = out_index
@@ -204,11 +220,33 @@ class CVMMSel:
         self._route_mode = False
 
     @classmethod
-    def _deferred(cls, raw_sel, routing: _Routing, route_mode: bool, w) -> "CVMMSel":
-        s = cls(raw_sel, None, None, None, w)
+    def _deferred(cls, raw_src: torch.Tensor, routing: _Routing, route_mode: bool, w) -> "CVMMSel":
+        """`raw_src`: the selection as given (any integer dtype); the int32
+        copy the reference stores as raw_sel is made only if it is read."""
+        s = cls(None, None, None, None, w)
+        s._raw_src = raw_src
         s._routing = routing
         s._route_mode = route_mode
         return s
+
+    @property
+    def raw_sel(self):
+        if self._raw_sel is None and self._raw_src is not None:
+            src = self._raw_src
+            self._raw_sel = src if src.dtype == torch.int32 else src.reshape(-1).to(torch.int32).view(src.shape)
+        return self._raw_sel
+
+    @raw_sel.setter
+    def raw_sel(self, v):
+        self._raw_sel = v
+        self._raw_src = None
+
+    def _raw_shape_tensor(self) -> torch.Tensor:
+        """A tensor of raw_sel's shape without forcing the int32 copy (the
+        autograd function only reads its shape)."""
+        if self._raw_sel is None and self._raw_src is not None:
+            return self._raw_src
+        return self._raw_sel
 
     def _pending(self) -> bool:
         return self._routing is not None and self._sel is None
@@ -218,7 +256,7 @@ class CVMMSel:
             return
         r = self._routing
         ssel, perm, tok, offsets = r.get(n_experts) if n_experts is not None else r.default()
-        sel = ssel.view(self.raw_sel.shape)
+        sel = ssel.view(self._raw_shape_tensor().shape)
         sel._cvmm_offsets = {e: v[3] for e, v in r.by_e.items()}
         sel._cvmm_i32 = ssel
         self._sel = sel
@@ -259,12 +297,14 @@ class CVMMSel:
 
     def clone(self) -> "CVMMSel":
         if self._pending():
-            return CVMMSel._deferred(self.raw_sel, self._routing, self._route_mode, self.reduction_weight)
+            return CVMMSel._deferred(self._raw_shape_tensor(), self._routing, self._route_mode,
+                                     self.reduction_weight)
         return CVMMSel(self.raw_sel, self.sel, self.sel_index, self.out_index, self.reduction_weight)
 
     def __repr__(self) -> str:
         if self._pending():
-            return f"CVMMSel(raw_sel={tuple(self.raw_sel.shape)}, pending sort, route_input={self._route_mode})"
+            return (f"CVMMSel(raw_sel={tuple(self._raw_shape_tensor().shape)}, pending sort, "
+                    f"route_input={self._route_mode})")
         return (f"CVMMSel(raw_sel={self.raw_sel!r}, sel={self._sel!r}, sel_index={self._sel_index!r}, "
                 f"out_index={self._out_index!r}, reduction_weight={self.reduction_weight!r})")
 
@@ -272,12 +312,13 @@ class CVMMSel:
 def cvmm_prepare_sel(sel: torch.Tensor, n_experts: int) -> CVMMSel:
     """cvmm.py:24-27: sort the flattened ids; sel_index = sorting permutation."""
     _require_device(sel, "sel")
-    raw = _flat_int32(sel)
-    ssel, perm, _, offsets = _Routing(raw, 1).get(n_experts)
+    ssel, perm, _, offsets = _Routing(sel.reshape(-1), 1).get(n_experts)
     s = ssel.view(sel.shape)
     s._cvmm_offsets = {n_experts: offsets}
     s._cvmm_i32 = ssel
-    return CVMMSel(raw.view(sel.shape), s, perm, None)
+    out = CVMMSel(None, s, perm, None)
+    out._raw_src = sel
+    return out
 
 
 def cvmm_prepare_sel2(sel: Union[torch.Tensor, CVMMSel], w: Optional[torch.Tensor] = None,
@@ -288,7 +329,8 @@ def cvmm_prepare_sel2(sel: Union[torch.Tensor, CVMMSel], w: Optional[torch.Tenso
     if isinstance(sel, CVMMSel):
         if sel._pending():
             # token-mode parent: out_index = perm; route-mode parent: sel_index = perm
-            return CVMMSel._deferred(sel.raw_sel, sel._routing, True if route_input else sel._route_mode, w)
+            return CVMMSel._deferred(sel._raw_shape_tensor(), sel._routing, True if route_input else sel._route_mode,
+                                     w)
         if route_input:
             route_index = sel.out_index if sel.out_index is not None else sel.sel_index
             return CVMMSel(sel.raw_sel, sel.sel, route_index, None, w)
@@ -296,8 +338,7 @@ def cvmm_prepare_sel2(sel: Union[torch.Tensor, CVMMSel], w: Optional[torch.Tenso
 
     _require_device(sel, "sel")
     n_per_batch = sel.shape[-1]
-    raw = _flat_int32(sel)
-    return CVMMSel._deferred(raw.view(sel.shape), _Routing(raw, n_per_batch), route_input, w)
+    return CVMMSel._deferred(sel, _Routing(sel.reshape(-1), n_per_batch), route_input, w)
 
 
 # ----------------------------------------------------------------------------
@@ -334,8 +375,40 @@ def _i64(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
     return f.contiguous()
 
 
+def _route_pos(rp: Optional[torch.Tensor], n_routes: int) -> Optional[torch.Tensor]:
+    """The sort's inverse permutation when `rp` is the perm it returned."""
+    pos = getattr(rp, "_cvmm_route_pos", None) if rp is not None else None
+    if pos is None or pos.numel() != n_routes or pos.dtype != torch.int32 or pos.device != rp.device:
+        return None
+    return pos
+
+
 def _workspace(nbytes: int, device) -> Optional[torch.Tensor]:
     return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+
+
+class _WgradWorkspace:
+    """One weight-gradient workspace per (device, stream), kept between calls.
+
+    cvmm_bwd_w's tile counters sit at the start of its workspace and the call
+    leaves them zero, so a kept workspace only needs its counter prefix zeroed
+    once.  ``clean`` is the length of the prefix known to be zero: a call
+    writes partial tiles right after its own counter region, so after it only
+    that region is known clean.  Calls on one stream run in stream order, so
+    sharing the buffer between them is safe."""
+
+    _cache: dict = {}
+
+    @classmethod
+    def get(cls, device, stream: int, nbytes: int, counter_bytes: int):
+        key = (device, stream)
+        buf, clean = cls._cache.get(key, (None, 0))
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
+            clean = buf.numel()
+        zeroed = counter_bytes <= clean
+        cls._cache[key] = (buf, counter_bytes)
+        return buf, zeroed
 
 
 def _fast_path(op: torch.dtype, d_in: int, d_out: int) -> bool:
@@ -397,7 +470,8 @@ def _forward(x, sel_index, sel, keys, out_index, rw, op_dtype, keys_t=None):
         N.ptr(xf), N.dtype_id(xf.dtype), xf.shape[0], xf.stride(0),
         N.ptr(kv), N.dtype_id(kv.dtype), n_experts, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2),
         N.ptr(s32), N.ptr(si), N.ptr(oi), R,
-        N.ptr(off), N.ptr(rwf), N.dtype_id(rwf.dtype) if rwf is not None else 0, k,
+        N.ptr(off), N.ptr(_route_pos(out_index if out_index is not None else sel_index, R)),
+        N.ptr(rwf), N.dtype_id(rwf.dtype) if rwf is not None else 0, k,
         od, N.ptr(out), od, out_rows, d_out,
         flags, N.ptr(ws), ws_bytes, N.stream_of(dev)), "cvmm_fwd")
     return out.view(out_shape)
@@ -430,14 +504,16 @@ def _backward(ctx, grad_output, x, keys, raw_sel, sel, sel_index, out_index, rw,
         xs = _rows(x.to(op) if fast and x.dtype != op else _storage_for(x, op), d_in)
         grad_w = torch.empty(keys.shape, dtype=keys.dtype, device=dev)
         ws_bytes = lib.cvmm_bwd_w_workspace_bytes(R, n_experts, d_in, d_out, od, 1)
-        ws = _workspace(ws_bytes, dev)
+        ws, zeroed = _WgradWorkspace.get(dev, stream, ws_bytes,
+                                         lib.cvmm_bwd_w_counter_bytes(R, n_experts, d_in, d_out, od))
+        wflags = flags | (N.FLAG_COUNTERS_ZEROED if zeroed else 0)
         N.check(lib.cvmm_bwd_w(
             N.ptr(xs), N.dtype_id(xs.dtype), xs.shape[0], xs.stride(0),
             N.ptr(g), N.dtype_id(g.dtype), g.shape[0], g.stride(0),
             n_experts, d_in, d_out, N.ptr(s32), N.ptr(si), N.ptr(oi), R, N.ptr(off),
             N.ptr(rwf), rwd, k, od,
             N.ptr(grad_w), N.dtype_id(grad_w.dtype), grad_w.stride(0), grad_w.stride(1), grad_w.stride(2),
-            flags, N.ptr(ws), ws_bytes, stream), "cvmm_bwd_w")
+            wflags, N.ptr(ws), ws.numel(), stream), "cvmm_bwd_w")
 
     if need_grad_x or need_grad_rw:
         kv = keys_n if keys_n is not None else _keys_view(_storage_for(keys, op))
@@ -455,7 +531,8 @@ def _backward(ctx, grad_output, x, keys, raw_sel, sel, sel_index, out_index, rw,
         N.check(lib.cvmm_bwd_x(
             N.ptr(g), N.dtype_id(g.dtype), g.shape[0], g.stride(0),
             N.ptr(kv), N.dtype_id(kv.dtype), n_experts, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2),
-            N.ptr(s32), N.ptr(si), N.ptr(oi), R, N.ptr(off), N.ptr(rwf), rwd, k,
+            N.ptr(s32), N.ptr(si), N.ptr(oi), R, N.ptr(off),
+            N.ptr(_route_pos(out_index if out_index is not None else sel_index, R)), N.ptr(rwf), rwd, k,
             N.ptr(xr), N.dtype_id(xr.dtype), xr.shape[0], xr.stride(0), od,
             N.ptr(gx), N.dtype_id(x.dtype), gx_rows, d_in,
             N.ptr(grad_rw), N.dtype_id(rw.dtype) if rw is not None else 0,
@@ -523,4 +600,5 @@ def cvmm(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.Tensor)
         if sh not in known_shapes:
             print("New shape:", sh)
             known_shapes.add(sh)
-    return CVMM.apply(x, sel.raw_sel, sel.sel_index, sel.sel, keys, sel.out_index, sel.reduction_weight)
+    return CVMM.apply(x, sel._raw_shape_tensor(), sel.sel_index, sel.sel, keys, sel.out_index,
+                      sel.reduction_weight)

@@ -4,6 +4,9 @@
 #include <string>
 #include <cstdio>
 #include <cstdarg>
+#include <atomic>
+#include <mutex>
+#include <vector>
 
 #include "cvmm_common.h"
 #include "cvmm_internal.h"
@@ -87,6 +90,43 @@ using namespace cvmm;
 
 namespace {
 
+// ---- timing hooks -----------------------------------------------------------
+struct TimedLaunch {
+  uint32_t cls;
+  hipEvent_t start, stop;
+};
+std::atomic<int32_t> g_panel_tpw{0};
+std::mutex g_timing_mu;
+uint32_t g_timing_mask = 0;
+std::vector<TimedLaunch> g_timed;
+
+// Runs `launch()` (which enqueues on `stream`), bracketed by events when the
+// class is being timed.
+template <typename F>
+hipError_t timed(uint32_t cls, hipStream_t stream, F&& launch);
+template <typename F>
+hipError_t timed_combine(hipStream_t stream, F&& launch) { return timed(CVMM_KC_COMBINE, stream, launch); }
+template <typename F>
+hipError_t timed_fill(hipStream_t stream, F&& launch) { return timed(CVMM_KC_FILL, stream, launch); }
+
+template <typename F>
+hipError_t timed(uint32_t cls, hipStream_t stream, F&& launch) {
+  uint32_t mask;
+  {
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    mask = g_timing_mask;
+  }
+  if (!(mask & cls)) return launch();
+  TimedLaunch t{cls, nullptr, nullptr};
+  if (hipEventCreate(&t.start) != hipSuccess || hipEventCreate(&t.stop) != hipSuccess) return launch();
+  hipEventRecord(t.start, stream);
+  const hipError_t e = launch();
+  hipEventRecord(t.stop, stream);
+  std::lock_guard<std::mutex> lk(g_timing_mu);
+  g_timed.push_back(t);
+  return e;
+}
+
 thread_local std::string g_err;
 
 int fail(int code, const char* fmt, ...) {
@@ -137,7 +177,44 @@ extern "C" {
 
 const char* cvmm_last_error(void) { return g_err.c_str(); }
 
-int cvmm_abi_version(void) { return 2; }
+int cvmm_abi_version(void) { return 4; }
+
+int cvmm_timing_enable(uint32_t class_mask) {
+  std::lock_guard<std::mutex> lk(g_timing_mu);
+  g_timing_mask = class_mask;
+  return CVMM_OK;
+}
+
+int cvmm_tuning_set(int32_t knob, int64_t value) {
+  if (knob == CVMM_TUNE_PANEL_TILES_PER_WG) {
+    if (value < 0 || value > 4096) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: tiles per workgroup out of range");
+    g_panel_tpw.store((int32_t)value);
+    return CVMM_OK;
+  }
+  return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: unknown knob %d", knob);
+}
+
+int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launches) {
+  if (!total_ms || !launches) return fail(CVMM_ERR_INVALID, "cvmm_timing_result: NULL output");
+  std::vector<TimedLaunch> mine;
+  {
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    std::vector<TimedLaunch> rest;
+    for (const auto& t : g_timed) (t.cls == kernel_class ? mine : rest).push_back(t);
+    g_timed.swap(rest);
+  }
+  double sum = 0.0;
+  for (const auto& t : mine) {
+    float ms = 0.f;
+    if (hipEventSynchronize(t.stop) == hipSuccess && hipEventElapsedTime(&ms, t.start, t.stop) == hipSuccess)
+      sum += ms;
+    hipEventDestroy(t.start);
+    hipEventDestroy(t.stop);
+  }
+  *total_ms = sum;
+  *launches = (int64_t)mine.size();
+  return CVMM_OK;
+}
 
 // ---------------------------------------------------------------------------
 size_t cvmm_sort_workspace_bytes(int64_t n_routes, int32_t n_experts) {
@@ -146,7 +223,8 @@ size_t cvmm_sort_workspace_bytes(int64_t n_routes, int32_t n_experts) {
 
 int cvmm_sort_routes(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts, int64_t top_k,
                      int32_t* sorted_sel, int64_t* perm, int64_t* token_index, int64_t* offsets,
-                     int32_t* n_invalid, void* workspace, size_t workspace_bytes, void* stream) {
+                     int32_t* route_pos, int32_t* n_invalid, void* workspace, size_t workspace_bytes,
+                     void* stream) {
   if (n_experts <= 0) return fail(CVMM_ERR_INVALID, "cvmm_sort_routes: n_experts must be > 0 (got %d)", n_experts);
   if (n_experts > 32767) return fail(CVMM_ERR_UNSUPPORTED, "cvmm_sort_routes: at most 32767 experts (got %d)", n_experts);
   if (n_routes < 0 || n_routes > 0x7fffffffll)
@@ -155,15 +233,15 @@ int cvmm_sort_routes(const void* sel, int32_t sel_is_int64, int64_t n_routes, in
   if (offsets == nullptr) return fail(CVMM_ERR_INVALID, "cvmm_sort_routes: offsets is NULL");
   hipStream_t s = (hipStream_t)stream;
   if (n_routes == 0) {
-    if (n_invalid) { int r = check_launch(launch_fill_zero(n_invalid, 4, s), "fill"); if (r) return r; }
-    return check_launch(launch_fill_zero(offsets, (size_t)n_experts * 8, s), "cvmm_sort_routes(fill)");
+    if (n_invalid) { int r = check_launch(timed_fill(s, [&] { return launch_fill_zero(n_invalid, 4, s); }), "fill"); if (r) return r; }
+    return check_launch(timed_fill(s, [&] { return launch_fill_zero(offsets, (size_t)n_experts * 8, s); }), "cvmm_sort_routes(fill)");
   }
   if (!sel || !sorted_sel || !perm) return fail(CVMM_ERR_INVALID, "cvmm_sort_routes: NULL pointer");
   if (workspace == nullptr || workspace_bytes < sort_workspace_bytes(n_routes, n_experts))
     return fail(CVMM_ERR_WORKSPACE, "cvmm_sort_routes: workspace too small (%zu < %zu)", workspace_bytes,
                 sort_workspace_bytes(n_routes, n_experts));
-  return check_launch(launch_sort_routes(sel, sel_is_int64 != 0, n_routes, n_experts, top_k, sorted_sel, perm,
-                                         token_index, offsets, n_invalid, workspace, s),
+  return check_launch(timed(CVMM_KC_SORT, s, [&] { return launch_sort_routes(sel, sel_is_int64 != 0, n_routes, n_experts, top_k, sorted_sel, perm,
+                                         token_index, offsets, route_pos, n_invalid, workspace, s); }),
                       "cvmm_sort_routes");
 }
 
@@ -171,7 +249,7 @@ int cvmm_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_e
                         void* stream) {
   if (n_experts <= 0 || offsets == nullptr) return fail(CVMM_ERR_INVALID, "cvmm_expert_offsets: bad arguments");
   if (n_routes > 0 && sorted_sel == nullptr) return fail(CVMM_ERR_INVALID, "cvmm_expert_offsets: sorted_sel NULL");
-  return check_launch(launch_expert_offsets(sorted_sel, n_routes, n_experts, offsets, (hipStream_t)stream),
+  return check_launch(timed(CVMM_KC_OFFSETS, (hipStream_t)stream, [&] { return launch_expert_offsets(sorted_sel, n_routes, n_experts, offsets, (hipStream_t)stream); }),
                       "cvmm_expert_offsets");
 }
 
@@ -186,8 +264,8 @@ int cvmm_cast_keys(const void* keys, int32_t keys_dtype, int32_t n_experts, int6
     return fail(CVMM_ERR_UNSUPPORTED, "cvmm_cast_keys: too many experts / rows");
   if (!keys) return fail(CVMM_ERR_INVALID, "cvmm_cast_keys: keys NULL");
   if (!keys_t && !keys_n) return CVMM_OK;
-  return check_launch(launch_cast_keys(keys, keys_dtype, k_se, k_si, k_sj, n_experts, d_in, d_out, out_dtype,
-                                       keys_t, keys_n, (hipStream_t)stream),
+  return check_launch(timed(CVMM_KC_CAST_KEYS, (hipStream_t)stream, [&] { return launch_cast_keys(keys, keys_dtype, k_se, k_si, k_sj, n_experts, d_in, d_out, out_dtype,
+                                       keys_t, keys_n, (hipStream_t)stream); }),
                       "cvmm_cast_keys");
 }
 
@@ -197,8 +275,12 @@ size_t cvmm_fwd_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_o
   Carver c(nullptr);
   if (!has_offsets) c.take((size_t)n_experts * 8);
   if (weighted) {
-    if (flags & CVMM_FLAG_ATOMIC_REDUCE) c.take((size_t)out_rows * d_out * 4);
-    else c.take((size_t)n_routes * d_out * dtype_size(out_dtype));
+    if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
+      c.take((size_t)out_rows * d_out * 4);
+    } else {
+      c.take((size_t)n_routes * d_out * dtype_size(out_dtype));
+      c.take((size_t)n_routes * 4);
+    }
   }
   return c.used;
 }
@@ -206,7 +288,8 @@ size_t cvmm_fwd_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_o
 int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const void* keys, int32_t keys_dtype,
              int32_t n_experts, int64_t d_in, int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj,
              const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index, int64_t n_routes,
-             const int64_t* offsets, const void* rw, int32_t rw_dtype, int64_t reduce_k, int32_t op_dtype,
+             const int64_t* offsets, const int32_t* route_pos, const void* rw, int32_t rw_dtype, int64_t reduce_k,
+             int32_t op_dtype,
              void* out, int32_t out_dtype, int64_t out_rows, int64_t out_ld, int32_t flags, void* workspace,
              size_t workspace_bytes, void* stream) {
   if (!valid_dtype(x_dtype) || !valid_dtype(keys_dtype) || !valid_dtype(op_dtype) || !valid_dtype(out_dtype) ||
@@ -235,7 +318,7 @@ int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const
   const int64_t* offs = offsets;
   if (!offs) {
     int64_t* o = (int64_t*)c.take((size_t)n_experts * 8);
-    int r = check_launch(launch_expert_offsets(sorted_sel, n_routes, n_experts, o, s), "cvmm_fwd(offsets)");
+    int r = check_launch(timed(CVMM_KC_OFFSETS, s, [&] { return launch_expert_offsets(sorted_sel, n_routes, n_experts, o, s); }), "cvmm_fwd(offsets)");
     if (r) return r;
     offs = o;
   }
@@ -257,31 +340,42 @@ int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const
   p.val_dtype = out_dtype;
   p.prod_dtype = -1;
   p.w_idx = rp;
+  p.panel_tpw = g_panel_tpw.load();
 
   if (!weighted) {
     p.epi = kEpiStore; p.out = out; p.out_dtype = out_dtype; p.out_ld = out_ld; p.out_rows = out_rows;
-    return check_launch(launch_routed_gemm(p, op_dtype, s), "cvmm_fwd(gemm)");
+    return check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
   }
   if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
     // fused combine: y rounded to the output dtype, times rnd_out(w), fp32 atomics per token row
     float* acc = (float*)c.take((size_t)out_rows * d_out * 4);
-    int r = check_launch(launch_fill_zero(acc, (size_t)out_rows * d_out * 4, s), "cvmm_fwd(zero)");
+    int r = check_launch(timed_fill(s, [&] { return launch_fill_zero(acc, (size_t)out_rows * d_out * 4, s); }), "cvmm_fwd(zero)");
     if (r) return r;
     p.epi = kEpiAtomic; p.out = acc; p.out_dtype = kF32; p.out_ld = d_out; p.out_rows = out_rows;
     p.o_div = reduce_k;
     p.w = rw; p.w_dtype = rw_dtype; p.w_round = out_dtype;
-    r = check_launch(launch_routed_gemm(p, op_dtype, s), "cvmm_fwd(gemm)");
+    r = check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
     if (r) return r;
-    return check_launch(launch_cast_rows(acc, d_out, out_rows, d_out, -1, out, out_dtype, out_ld, s),
+    return check_launch(timed_combine(s, [&] { return launch_cast_rows(acc, d_out, out_rows, d_out, -1, out, out_dtype, out_ld, s); }),
                         "cvmm_fwd(cast)");
   }
-  // route-ordered y in the output dtype, then the ordered per-token combine
+  // y in the output dtype, row q = sorted route q (contiguous rows per expert
+  // tile), then the per-token combine in route order through the inverse
   void* ybuf = c.take((size_t)n_routes * d_out * dtype_size(out_dtype));
+  int32_t* inv_ws = (int32_t*)c.take((size_t)n_routes * 4);
+  const int32_t* inv = route_pos;
+  int r = 0;
+  if (!inv) {
+    r = check_launch(timed_combine(s, [&] { return launch_invert_rows(rp, n_routes, inv_ws, s); }), "cvmm_fwd(invert)");
+    if (r) return r;
+    inv = inv_ws;
+  }
   p.epi = kEpiStore; p.out = ybuf; p.out_dtype = out_dtype; p.out_ld = d_out; p.out_rows = n_routes;
-  int r = check_launch(launch_routed_gemm(p, op_dtype, s), "cvmm_fwd(gemm)");
+  p.o_idx = nullptr;
+  r = check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
   if (r) return r;
-  return check_launch(launch_combine_rows(ybuf, out_dtype, d_out, rw, rw_dtype, out_dtype, out_rows, reduce_k, d_out,
-                                          out_dtype, out, out_dtype, out_ld, s),
+  return check_launch(timed_combine(s, [&] { return launch_combine_rows(ybuf, out_dtype, d_out, inv, rp, rw, rw_dtype, out_dtype, out_rows, reduce_k, d_out,
+                                          out_dtype, out, out_dtype, out_ld, s); }),
                       "cvmm_fwd(combine)");
 }
 
@@ -292,8 +386,12 @@ size_t cvmm_bwd_x_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d
   Carver c(nullptr);
   if (!has_offsets) c.take((size_t)n_experts * 8);
   if (reduce_needed(weighted, token_input, top_k)) {
-    if (flags & CVMM_FLAG_ATOMIC_REDUCE) c.take((size_t)grad_x_rows * d_in * 4);
-    else c.take((size_t)n_routes * d_in * dtype_size(weighted ? op_dtype : grad_x_dtype));
+    if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
+      c.take((size_t)grad_x_rows * d_in * 4);
+    } else {
+      c.take((size_t)n_routes * d_in * dtype_size(weighted ? op_dtype : grad_x_dtype));
+      c.take((size_t)n_routes * 4);
+    }
   }
   if (weighted && need_grad_rw) c.take((size_t)n_routes * ntiles_of(d_in, gemm_bn(d_in)) * 4);
   return c.used;
@@ -302,7 +400,8 @@ size_t cvmm_bwd_x_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d
 int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t grad_ld, const void* keys,
                int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out, int64_t k_se, int64_t k_si,
                int64_t k_sj, const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index,
-               int64_t n_routes, const int64_t* offsets, const void* rw, int32_t rw_dtype, int64_t top_k,
+               int64_t n_routes, const int64_t* offsets, const int32_t* route_pos, const void* rw, int32_t rw_dtype,
+               int64_t top_k,
                const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, int32_t op_dtype, void* grad_x,
                int32_t grad_x_dtype, int64_t grad_x_rows, int64_t grad_x_ld, void* grad_rw, int32_t grad_rw_dtype,
                int32_t flags, void* workspace, size_t workspace_bytes, void* stream) {
@@ -342,7 +441,7 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
   const int64_t* offs = offsets;
   if (!offs) {
     int64_t* o = (int64_t*)c.take((size_t)n_experts * 8);
-    int r = check_launch(launch_expert_offsets(sorted_sel, n_routes, n_experts, o, s), "cvmm_bwd_x(offsets)");
+    int r = check_launch(timed(CVMM_KC_OFFSETS, s, [&] { return launch_expert_offsets(sorted_sel, n_routes, n_experts, o, s); }), "cvmm_bwd_x(offsets)");
     if (r) return r;
     offs = o;
   }
@@ -364,8 +463,11 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
   p.o_idx = rp; p.o_div = 1;
   p.w_idx = rp;
   p.prod_dtype = -1;
+  p.role = 1;
+  p.panel_tpw = g_panel_tpw.load();
 
   void* route_buf = nullptr;
+  const int32_t* inv = nullptr;
   float* acc = nullptr;
   if (grad_x) {
     if (!reduce) {
@@ -377,16 +479,26 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
       }
     } else if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
       acc = (float*)c.take((size_t)grad_x_rows * d_in * 4);
-      int r = check_launch(launch_fill_zero(acc, (size_t)grad_x_rows * d_in * 4, s), "cvmm_bwd_x(zero)");
+      int r = check_launch(timed_fill(s, [&] { return launch_fill_zero(acc, (size_t)grad_x_rows * d_in * 4, s); }), "cvmm_bwd_x(zero)");
       if (r) return r;
       p.epi = kEpiAtomic; p.out = acc; p.out_dtype = kF32; p.out_ld = d_in; p.out_rows = grad_x_rows;
       p.o_div = top_k;
       if (weighted) { p.val_dtype = op_dtype; p.w = rw; p.w_dtype = rw_dtype; p.w_round = op_dtype; }
       else p.val_dtype = grad_x_dtype;
     } else {
+      // row q = sorted route q; the combine gathers each token's routes
       const int32_t bdt = weighted ? op_dtype : grad_x_dtype;
       route_buf = c.take((size_t)n_routes * d_in * dtype_size(bdt));
+      int32_t* inv_ws = (int32_t*)c.take((size_t)n_routes * 4);
+      inv = route_pos;
+      if (!inv) {
+        int r = check_launch(timed_combine(s, [&] { return launch_invert_rows(rp, n_routes, inv_ws, s); }),
+                             "cvmm_bwd_x(invert)");
+        if (r) return r;
+        inv = inv_ws;
+      }
       p.epi = kEpiStore; p.out = route_buf; p.out_dtype = bdt; p.out_ld = d_in; p.out_rows = n_routes;
+      p.o_idx = nullptr;
       p.val_dtype = bdt;
     }
   } else {
@@ -397,31 +509,31 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
   const int64_t dg_nt = ntiles_of(d_in, gemm_bn(d_in));
   if (weighted && grad_rw) {
     dg_part = (float*)c.take((size_t)n_routes * dg_nt * 4);
-    int r = check_launch(launch_fill_zero(dg_part, (size_t)n_routes * dg_nt * 4, s), "cvmm_bwd_x(zero dg)");
+    int r = check_launch(timed_fill(s, [&] { return launch_fill_zero(dg_part, (size_t)n_routes * dg_nt * 4, s); }), "cvmm_bwd_x(zero dg)");
     if (r) return r;
     p.dg = dg_part; p.dg_ntiles = (int32_t)dg_nt;
     p.dg_x = x; p.dg_x_dtype = x_dtype; p.dg_x_ld = x_ld; p.dg_x_rows = x_rows; p.dg_x_idx = sel_index;
     p.dg_val_dtype = op_dtype;
   }
 
-  int r = check_launch(launch_routed_gemm(p, op_dtype, s), "cvmm_bwd_x(gemm)");
+  int r = check_launch(timed(CVMM_KC_GEMM_BWDX, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_bwd_x(gemm)");
   if (r) return r;
   if (grad_x && reduce) {
     if (acc) {
-      r = check_launch(launch_cast_rows(acc, d_in, grad_x_rows, d_in, weighted ? op_dtype : -1, grad_x,
-                                        grad_x_dtype, grad_x_ld, s),
+      r = check_launch(timed_combine(s, [&] { return launch_cast_rows(acc, d_in, grad_x_rows, d_in, weighted ? op_dtype : -1, grad_x,
+                                        grad_x_dtype, grad_x_ld, s); }),
                        "cvmm_bwd_x(cast)");
     } else {
       const int32_t bdt = weighted ? op_dtype : grad_x_dtype;
-      r = check_launch(launch_combine_rows(route_buf, bdt, d_in, weighted ? rw : nullptr, rw_dtype, op_dtype,
+      r = check_launch(timed_combine(s, [&] { return launch_combine_rows(route_buf, bdt, d_in, inv, rp, weighted ? rw : nullptr, rw_dtype, op_dtype,
                                            grad_x_rows, top_k, d_in, weighted ? op_dtype : -1, grad_x, grad_x_dtype,
-                                           grad_x_ld, s),
+                                           grad_x_ld, s); }),
                        "cvmm_bwd_x(combine)");
     }
     if (r) return r;
   }
   if (dg_part) {
-    r = check_launch(launch_sum_partials(dg_part, n_routes, (int32_t)dg_nt, grad_rw, grad_rw_dtype, s),
+    r = check_launch(timed_combine(s, [&] { return launch_sum_partials(dg_part, n_routes, (int32_t)dg_nt, grad_rw, grad_rw_dtype, s); }),
                      "cvmm_bwd_x(dgate)");
     if (r) return r;
   }
@@ -429,13 +541,22 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
 }
 
 // ---------------------------------------------------------------------------
+size_t cvmm_bwd_w_counter_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out,
+                                int32_t op_dtype) {
+  int64_t split, grid_chunks, max_slots, tiles;
+  wgrad_geometry(d_in, d_out, n_routes, n_experts, op_dtype, &split, &grid_chunks, &max_slots, &tiles);
+  Carver c(nullptr);
+  c.take((size_t)n_experts * tiles * 4);
+  return c.used;
+}
+
 size_t cvmm_bwd_w_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out,
                                   int32_t op_dtype, int32_t has_offsets) {
   int64_t split, grid_chunks, max_slots, tiles;
   wgrad_geometry(d_in, d_out, n_routes, n_experts, op_dtype, &split, &grid_chunks, &max_slots, &tiles);
   Carver c(nullptr);
+  c.take((size_t)n_experts * tiles * 4);  // counters first: see CVMM_FLAG_COUNTERS_ZEROED
   if (!has_offsets) c.take((size_t)n_experts * 8);
-  c.take((size_t)n_experts * tiles * 4);
   c.take((size_t)max_slots * tiles * wgrad_tile_elems(d_in, d_out) * 4);
   return c.used;
 }
@@ -446,7 +567,6 @@ int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, con
                const int64_t* offsets, const void* rw, int32_t rw_dtype, int64_t top_k, int32_t op_dtype,
                void* grad_keys, int32_t grad_keys_dtype, int64_t gk_se, int64_t gk_si, int64_t gk_sj, int32_t flags,
                void* workspace, size_t workspace_bytes, void* stream) {
-  (void)flags;
   const bool weighted = rw != nullptr;
   if (!valid_dtype(x_dtype) || !valid_dtype(grad_dtype) || !valid_dtype(op_dtype) || !valid_dtype(grad_keys_dtype) ||
       (weighted && !valid_dtype(rw_dtype)))
@@ -470,17 +590,23 @@ int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, con
   int64_t tiles;
   wgrad_geometry(d_in, d_out, n_routes, n_experts, op_dtype, &p.split, &p.grid_chunks, &p.max_slots, &tiles);
   Carver c(workspace);
+  // The kernel's last arriver on each tile resets its counter, so the region
+  // is zero again when the kernel ends; callers that keep the workspace can
+  // pass CVMM_FLAG_COUNTERS_ZEROED and skip the fill.
+  p.counters = (int32_t*)c.take((size_t)n_experts * tiles * 4);
+  if (!(flags & CVMM_FLAG_COUNTERS_ZEROED)) {
+    int r = check_launch(timed_fill(s, [&] { return launch_fill_zero(p.counters, (size_t)n_experts * tiles * 4, s); }),
+                         "cvmm_bwd_w(zero)");
+    if (r) return r;
+  }
   const int64_t* offs = offsets;
   if (!offs) {
     int64_t* o = (int64_t*)c.take((size_t)n_experts * 8);
-    int r = n_routes > 0 ? check_launch(launch_expert_offsets(sorted_sel, n_routes, n_experts, o, s), "offsets")
-                         : check_launch(launch_fill_zero(o, (size_t)n_experts * 8, s), "offsets");
+    int r = n_routes > 0 ? check_launch(timed(CVMM_KC_OFFSETS, s, [&] { return launch_expert_offsets(sorted_sel, n_routes, n_experts, o, s); }), "offsets")
+                         : check_launch(timed_fill(s, [&] { return launch_fill_zero(o, (size_t)n_experts * 8, s); }), "offsets");
     if (r) return r;
     offs = o;
   }
-  p.counters = (int32_t*)c.take((size_t)n_experts * tiles * 4);
-  int r = check_launch(launch_fill_zero(p.counters, (size_t)n_experts * tiles * 4, s), "cvmm_bwd_w(zero)");
-  if (r) return r;
   p.partial = (float*)c.take((size_t)p.max_slots * tiles * wgrad_tile_elems(d_in, d_out) * 4);
 
   const int64_t* rp = out_index ? out_index : sel_index;
@@ -495,7 +621,7 @@ int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, con
   p.M = d_in; p.N = d_out;
   p.offsets = offs; p.n_experts = n_experts; p.n_routes = n_routes;
   p.dw = grad_keys; p.dw_dtype = grad_keys_dtype; p.dw_se = gk_se; p.dw_sm = gk_si; p.dw_sn = gk_sj;
-  return check_launch(launch_wgrad(p, op_dtype, s), "cvmm_bwd_w(gemm)");
+  return check_launch(timed(CVMM_KC_WGRAD, s, [&] { return launch_wgrad(p, op_dtype, s); }), "cvmm_bwd_w(gemm)");
 }
 
 }  // extern "C"

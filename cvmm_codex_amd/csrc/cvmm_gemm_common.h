@@ -69,7 +69,7 @@ __device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& 
       const int64_t q = row0 + r;
       const int64_t ai = p.a_idx[q] / p.a_div;
       if (ai >= 0 && ai < p.a_rows) ar = ai;
-      const int64_t oi = p.o_idx[q] / p.o_div;
+      const int64_t oi = p.o_idx != nullptr ? p.o_idx[q] / p.o_div : q;
       if (oi >= 0 && oi < p.out_rows) orow = oi;
       if (p.w_idx != nullptr) {
         const int64_t wi = p.w_idx[q];

@@ -53,7 +53,7 @@ struct NtCfg {
   static constexpr int STAGE_BYTES = (A_BYTES + B_BYTES > C_HALF_BYTES) ? A_BYTES + B_BYTES : C_HALF_BYTES;
 };
 
-template <typename OpT, int BM, int BN>
+template <typename OpT, int BM, int BN, int Role>
 __global__ __launch_bounds__(kGemmThreads, 2) void routed_gemm_nt_kernel(const GemmParams p) {
   using Cfg = NtCfg<OpT, BM, BN>;
   // Two LDS objects (double buffer).  The loop is unrolled by two so every
@@ -197,7 +197,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void routed_gemm_nt_kernel(const G
 // consecutive output columns of one row and stores them straight from
 // registers (8 bytes), leaving LDS to the next stage's DMA.  Plain stores only
 // (no routing-weight gradient, no atomics); N % 8 == 0.
-template <typename OpT, int BM, int BN>
+template <typename OpT, int BM, int BN, int Role>
 __global__ __launch_bounds__(kGemmThreads, 2) void routed_gemm_nloop_kernel(const GemmParams p, int32_t ng) {
   using Cfg = NtCfg<OpT, BM, BN>;
   __shared__ __attribute__((aligned(1024))) char stage0[Cfg::A_BYTES + Cfg::B_BYTES];
@@ -373,8 +373,12 @@ hipError_t launch_routed_gemm_nloop_t(const GemmParams& p, int32_t ng, hipStream
   const int64_t grid = p.grid_tiles * n_groups;
   if (grid <= 0) return hipSuccess;
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((routed_gemm_nloop_kernel<OpT, BM, BN>), dim3((unsigned)grid), dim3(kGemmThreads), 0, stream,
-                     p, ng);
+  if (p.role == 0)
+    hipLaunchKernelGGL((routed_gemm_nloop_kernel<OpT, BM, BN, 0>), dim3((unsigned)grid), dim3(kGemmThreads), 0,
+                       stream, p, ng);
+  else
+    hipLaunchKernelGGL((routed_gemm_nloop_kernel<OpT, BM, BN, 1>), dim3((unsigned)grid), dim3(kGemmThreads), 0,
+                       stream, p, ng);
   return hipGetLastError();
 }
 
@@ -384,8 +388,12 @@ hipError_t launch_routed_gemm_nt_t(const GemmParams& p, hipStream_t stream) {
   const int64_t grid = p.grid_tiles * n_ntiles;
   if (grid <= 0) return hipSuccess;
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((routed_gemm_nt_kernel<OpT, BM, BN>), dim3((unsigned)grid), dim3(kGemmThreads), 0,
-                     stream, p);
+  if (p.role == 0)
+    hipLaunchKernelGGL((routed_gemm_nt_kernel<OpT, BM, BN, 0>), dim3((unsigned)grid), dim3(kGemmThreads), 0,
+                       stream, p);
+  else
+    hipLaunchKernelGGL((routed_gemm_nt_kernel<OpT, BM, BN, 1>), dim3((unsigned)grid), dim3(kGemmThreads), 0,
+                       stream, p);
   return hipGetLastError();
 }
 

@@ -1,8 +1,8 @@
-// Routed GEMM fast-path instantiations for op type bf16_t (see cvmm_gemm_nt.h).
-#include "cvmm_gemm_nt.h"
+// Routed GEMM fast-path instantiations for op type bf16_t (cvmm_gemm_panel.h, cvmm_gemm_nt.h).
+#include "cvmm_gemm_panel.h"
 
 namespace cvmm {
 hipError_t launch_routed_gemm_nt_bf16(const GemmParams& p, hipStream_t stream) {
-  return launch_routed_gemm_nt_op<bf16_t>(p, stream);
+  return launch_routed_gemm_fast_op<bf16_t>(p, stream);
 }
 }  // namespace cvmm

@@ -46,7 +46,7 @@ struct GemmParams {
   void* out;
   int32_t out_dtype;
   int64_t out_ld, out_rows;
-  const int64_t* o_idx;    // orow(p) = o_idx[p] / o_div
+  const int64_t* o_idx;    // orow(p) = o_idx[p] / o_div, or p when NULL
   int64_t o_div;
   int32_t val_dtype;
   const void* w;           // optional per-route scale
@@ -63,6 +63,11 @@ struct GemmParams {
   int64_t dg_x_ld, dg_x_rows;
   const int64_t* dg_x_idx;
   int32_t dg_val_dtype;
+  // 0 = forward, 1 = grad-input: selects separately named kernel
+  // instantiations so that profiles tell the two products apart
+  int32_t role;
+  // n-tiles per workgroup of the small-K kernel (0: built-in choice)
+  int32_t panel_tpw;
 };
 
 // op_dtype selects the MFMA type; returns hipErrorInvalidValue on unsupported combos.
@@ -123,7 +128,8 @@ void wgrad_geometry(int64_t M, int64_t N, int64_t n_routes, int32_t n_experts, i
 size_t sort_workspace_bytes(int64_t n_routes, int32_t n_experts);
 hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_routes, int32_t n_experts,
                               int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
-                              int64_t* offsets, int32_t* n_invalid, void* ws, hipStream_t stream);
+                              int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* ws,
+                              hipStream_t stream);
 hipError_t launch_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_experts,
                                  int64_t* offsets, hipStream_t stream);
 
@@ -138,9 +144,11 @@ hipError_t launch_cast_keys(const void* keys, int32_t keys_dtype, int64_t se, in
 // ---------------------------------------------------------------------------
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 // out[t][n] = rnd(rnd(sum_j rnd(w[t*k+j], w_round) * buf[t*k+j][n], mid_dtype), out_dtype)
-hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_ld, const void* w, int32_t w_dtype,
-                               int32_t w_round, int64_t n_tokens, int64_t k, int64_t n, int32_t mid_dtype,
-                               void* out, int32_t out_dtype, int64_t out_ld, hipStream_t stream);
+hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_ld, const int32_t* inv,
+                               const int64_t* rp, const void* w, int32_t w_dtype, int32_t w_round, int64_t n_tokens,
+                               int64_t k, int64_t n, int32_t mid_dtype, void* out, int32_t out_dtype, int64_t out_ld,
+                               hipStream_t stream);
+hipError_t launch_invert_rows(const int64_t* rp, int64_t n_routes, int32_t* inv, hipStream_t stream);
 // out[t][n] = rnd(rnd(acc[t][n], mid_dtype), out_dtype)
 hipError_t launch_cast_rows(const float* acc, int64_t acc_ld, int64_t rows, int64_t n, int32_t mid_dtype,
                             void* out, int32_t out_dtype, int64_t out_ld, hipStream_t stream);

@@ -86,21 +86,31 @@ __host__ __device__ inline bool vec_ok(const void* p, int32_t dt, int64_t ld) {
   return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && (ld * (int64_t)dtype_size(dt)) % 16 == 0;
 }
 
-// out[t][n] = rnd(rnd(sum_j w_j * buf[t*k + j][n], mid), out), j in route order
-// (the top-k sum of cvmm.py:1223 and the weighted combine of cvmm.py:1545).
+// out[t][n] = rnd(rnd(sum_j w_j * buf[row(t*k + j)][n], mid), out), j in route
+// order (the top-k sum of cvmm.py:1223 and the weighted combine of
+// cvmm.py:1545).  row(r) = r, or, with a route-ordered buffer (row q holds
+// route rp[q]), row(r) = inv[r] checked against rp: a route no row holds adds
+// nothing.
 __global__ void combine_rows_kernel(const void* __restrict__ buf, int32_t buf_dtype, int64_t buf_ld,
-                                    const void* __restrict__ w, int32_t w_dtype, int32_t w_round, int64_t k,
-                                    int64_t n, int32_t mid_dtype, void* __restrict__ out, int32_t out_dtype,
-                                    int64_t out_ld, bool in_vec, bool out_vec) {
+                                    const int32_t* __restrict__ inv, const int64_t* __restrict__ rp,
+                                    int64_t n_routes, const void* __restrict__ w, int32_t w_dtype,
+                                    int32_t w_round, int64_t k, int64_t n, int32_t mid_dtype,
+                                    void* __restrict__ out, int32_t out_dtype, int64_t out_ld, bool in_vec,
+                                    bool out_vec) {
   const int64_t t = blockIdx.x;
   const int64_t c = ((int64_t)blockIdx.y * blockDim.x + threadIdx.x) * 8;
   if (c >= n) return;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int64_t j = 0; j < k; ++j) {
     const int64_t r = t * k + j;
+    int64_t row = r;
+    if (inv != nullptr) {
+      row = inv[r];
+      if (row < 0 || row >= n_routes || rp[row] != r) continue;
+    }
     const float wv = w != nullptr ? round_to(load_as_f32(w, w_dtype, r), w_round) : 1.f;
     float v[8];
-    load8_any(buf, buf_dtype, r * buf_ld + c, in_vec, n - c, v);
+    load8_any(buf, buf_dtype, row * buf_ld + c, in_vec, n - c, v);
 #pragma unroll
     for (int q = 0; q < 8; ++q) acc[q] += wv * v[q];
   }
@@ -111,6 +121,23 @@ __global__ void combine_rows_kernel(const void* __restrict__ buf, int32_t buf_dt
   store8_any(out, out_dtype, t * out_ld + c, out_vec, n - c, acc);
 }
 
+// inv[rp[q]] = q for every q with rp[q] in [0, R): the sorted position of
+// each route.
+__global__ void invert_rows_kernel(const int64_t* __restrict__ rp, int64_t n_routes, int32_t* __restrict__ inv) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= n_routes) return;
+  const int64_t r = rp[q];
+  if (r >= 0 && r < n_routes) inv[r] = (int32_t)q;
+}
+
+hipError_t launch_invert_rows(const int64_t* rp, int64_t n_routes, int32_t* inv, hipStream_t stream) {
+  if (n_routes <= 0) return hipSuccess;
+  if (n_routes > 0x7fffffffll) return hipErrorInvalidValue;
+  const int64_t blocks = (n_routes + 255) / 256;
+  hipLaunchKernelGGL(invert_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, rp, n_routes, inv);
+  return hipGetLastError();
+}
+
 static void rows_grid(int64_t rows, int64_t n, dim3* grid, dim3* block) {
   int64_t chunks = (n + 7) / 8;
   int threads = (int)((chunks + 63) / 64 * 64);
@@ -119,15 +146,18 @@ static void rows_grid(int64_t rows, int64_t n, dim3* grid, dim3* block) {
   *grid = dim3((unsigned)rows, (unsigned)((chunks + threads - 1) / threads));
 }
 
-hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_ld, const void* w, int32_t w_dtype,
-                               int32_t w_round, int64_t n_tokens, int64_t k, int64_t n, int32_t mid_dtype,
-                               void* out, int32_t out_dtype, int64_t out_ld, hipStream_t stream) {
+hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_ld, const int32_t* inv,
+                               const int64_t* rp, const void* w, int32_t w_dtype, int32_t w_round, int64_t n_tokens,
+                               int64_t k, int64_t n, int32_t mid_dtype, void* out, int32_t out_dtype, int64_t out_ld,
+                               hipStream_t stream) {
   if (n_tokens <= 0 || n <= 0) return hipSuccess;
   if (n_tokens > 0x7fffffffll || (n + 2047) / 2048 > 65535) return hipErrorInvalidValue;
+  if ((inv == nullptr) != (rp == nullptr)) return hipErrorInvalidValue;
   dim3 grid, block;
   rows_grid(n_tokens, n, &grid, &block);
-  hipLaunchKernelGGL(combine_rows_kernel, grid, block, 0, stream, buf, buf_dtype, buf_ld, w, w_dtype, w_round, k, n,
-                     mid_dtype, out, out_dtype, out_ld, vec_ok(buf, buf_dtype, buf_ld), vec_ok(out, out_dtype, out_ld));
+  hipLaunchKernelGGL(combine_rows_kernel, grid, block, 0, stream, buf, buf_dtype, buf_ld, inv, rp, n_tokens * k, w,
+                     w_dtype, w_round, k, n, mid_dtype, out, out_dtype, out_ld, vec_ok(buf, buf_dtype, buf_ld),
+                     vec_ok(out, out_dtype, out_ld));
   return hipGetLastError();
 }
 

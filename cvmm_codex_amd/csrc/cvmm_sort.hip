@@ -20,8 +20,9 @@ namespace cvmm {
 constexpr int kSortThreads = 256;
 
 template <typename IdxT>
-__device__ __forceinline__ int32_t bucket_of(IdxT key, int32_t n_experts) {
-  return (key < 0 || key >= (IdxT)n_experts) ? n_experts : (int32_t)key;
+__device__ __forceinline__ int32_t bucket_of(IdxT raw, int32_t n_experts) {
+  const int32_t key = (int32_t)raw;  // int64 ids wrap like the int32 conversion of cvmm.py:1797
+  return (key < 0 || key >= n_experts) ? n_experts : key;
 }
 
 template <typename IdxT>
@@ -82,7 +83,8 @@ template <typename IdxT>
 __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     const IdxT* __restrict__ sel, int64_t n_routes, int32_t n_experts, int64_t chunk,
     int64_t n_chunks, const int32_t* __restrict__ bases, int32_t n_bits, int64_t top_k,
-    int32_t* __restrict__ sorted_sel, int64_t* __restrict__ perm, int64_t* __restrict__ token_index) {
+    int32_t* __restrict__ sorted_sel, int64_t* __restrict__ perm, int64_t* __restrict__ token_index,
+    int32_t* __restrict__ route_pos) {
   extern __shared__ int32_t pos[];  // n_experts + 1 running output positions
   const int64_t b = blockIdx.x;
   for (int e = threadIdx.x; e <= n_experts; e += kSortThreads) pos[e] = bases[(int64_t)e * n_chunks + b];
@@ -95,7 +97,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
   for (int64_t base = lo; base < hi; base += kSortThreads) {
     const int64_t i = base + threadIdx.x;
     const bool valid = i < hi;
-    IdxT key = valid ? sel[i] : (IdxT)0;
+    const IdxT key = valid ? sel[i] : (IdxT)0;
     const int32_t bucket = valid ? bucket_of(key, n_experts) : 0;
     uint64_t peers = __ballot(valid);
     for (int bit = 0; bit < n_bits; ++bit) {
@@ -110,9 +112,10 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
         const int32_t p0 = pos[bucket];
         const int64_t p = (int64_t)p0 + rank;
         if (rank == 0) pos[bucket] = p0 + cnt;
-        sorted_sel[p] = (key < (IdxT)INT32_MIN) ? INT32_MIN : (key > (IdxT)INT32_MAX ? INT32_MAX : (int32_t)key);
+        sorted_sel[p] = (int32_t)key;
         perm[p] = i;
         if (token_index != nullptr) token_index[p] = i / top_k;
+        if (route_pos != nullptr) route_pos[i] = (int32_t)p;
       }
       __syncthreads();
     }
@@ -156,7 +159,8 @@ size_t sort_workspace_bytes(int64_t n_routes, int32_t n_experts) {
 
 hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_routes, int32_t n_experts,
                               int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
-                              int64_t* offsets, int32_t* n_invalid_out, void* ws, hipStream_t stream) {
+                              int64_t* offsets, int32_t* route_pos, int32_t* n_invalid_out, void* ws,
+                              hipStream_t stream) {
   const int64_t chunk = sort_chunk_size(n_routes);
   const int64_t n_chunks = (n_routes + chunk - 1) / chunk;
   int32_t* counts = (int32_t*)ws;
@@ -177,11 +181,11 @@ hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_rout
   if (sel_is_int64) {
     hipLaunchKernelGGL(sort_scatter_kernel<int64_t>, dim3(n_chunks), dim3(kSortThreads), lds, stream,
                        (const int64_t*)sel, n_routes, n_experts, chunk, n_chunks, counts, n_bits, top_k,
-                       sorted_sel, perm, token_index);
+                       sorted_sel, perm, token_index, route_pos);
   } else {
     hipLaunchKernelGGL(sort_scatter_kernel<int32_t>, dim3(n_chunks), dim3(kSortThreads), lds, stream,
                        (const int32_t*)sel, n_routes, n_experts, chunk, n_chunks, counts, n_bits, top_k,
-                       sorted_sel, perm, token_index);
+                       sorted_sel, perm, token_index, route_pos);
   }
   return hipGetLastError();
 }

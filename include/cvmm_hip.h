@@ -45,6 +45,18 @@ extern "C" {
 /* flags */
 #define CVMM_FLAG_ATOMIC_REDUCE 1 /* top-k sums (weighted combine, token grad) by fp32 atomics
                                      instead of a route-ordered buffer + ordered row sum */
+#define CVMM_FLAG_COUNTERS_ZEROED 2 /* cvmm_bwd_w: the counter region at the start of the
+                                       workspace is already zero (see cvmm_bwd_w) */
+
+/* kernel classes for the timing hooks */
+#define CVMM_KC_SORT 1        /* histogram + scan + scatter of cvmm_sort_routes */
+#define CVMM_KC_OFFSETS 2
+#define CVMM_KC_CAST_KEYS 4
+#define CVMM_KC_GEMM_FWD 8    /* routed GEMM of cvmm_fwd */
+#define CVMM_KC_GEMM_BWDX 16  /* routed GEMM of cvmm_bwd_x */
+#define CVMM_KC_WGRAD 32      /* weight-gradient kernel of cvmm_bwd_w */
+#define CVMM_KC_COMBINE 64    /* top-k row combine / fp32 cast / gate-grad sum */
+#define CVMM_KC_FILL 128      /* zero fills */
 
 /* Thread-local description of the last error. */
 const char* cvmm_last_error(void);
@@ -52,24 +64,43 @@ const char* cvmm_last_error(void);
 /* ABI version of this library (bumped on any signature change). */
 int cvmm_abi_version(void);
 
+/* Measurement hooks (no counterpart in the reference; for benchmarks): while
+ * a kernel class is enabled, every launch of it is bracketed by HIP events
+ * recorded on the launch stream.  cvmm_timing_result synchronises on those
+ * events and returns the summed elapsed milliseconds and the launch count of
+ * one class, then forgets them.  Process-wide; not for concurrent use. */
+int cvmm_timing_enable(uint32_t class_mask);
+int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launches);
+
+/* Tuning knobs (no counterpart in the reference; for tests and tuning
+ * sweeps).  Process-wide; value 0 restores the built-in choice.
+ *   CVMM_TUNE_PANEL_TILES_PER_WG: n-tiles per workgroup of the small-K
+ *     routed GEMM (1..4096). */
+#define CVMM_TUNE_PANEL_TILES_PER_WG 1
+int cvmm_tuning_set(int32_t knob, int64_t value);
+
 /* ------------------------------------------------------------------------ */
 /* Selector preparation                                                      */
 /* ------------------------------------------------------------------------ */
 
 size_t cvmm_sort_workspace_bytes(int64_t n_routes, int32_t n_experts);
 
-/* Stable counting sort of the flattened expert ids `sel` (int32 or int64).
+/* Stable counting sort of the flattened expert ids `sel` (int32, or int64
+ * read as its low 32 bits, the value the reference's int32 conversion gives).
  * Replaces the sort in cvmm_prepare_sel (cvmm.py:24-27) and
  * cvmm_prepare_sel2 (cvmm.py:1796-1803) plus the offsets kernel
  * (cvmm.py:315-335).  Writes sorted_sel[R] (int32), perm[R] (int64, the
  * stable sorting permutation), token_index[R] = perm / top_k when
- * token_index != NULL, offsets[E] (int64 inclusive cumsum) and, when
- * n_invalid != NULL, the number of ids outside [0, E) (those sort last and
- * are ignored by the GEMMs). */
+ * token_index != NULL, offsets[E] (int64 inclusive cumsum), when
+ * route_pos != NULL the inverse permutation route_pos[perm[i]] = i (int32;
+ * no counterpart in the reference: it lets cvmm_fwd / cvmm_bwd_x gather each
+ * token's routes from route-ordered rows) and, when n_invalid != NULL, the
+ * number of ids outside [0, E) (those sort last and are ignored by the
+ * GEMMs). */
 int cvmm_sort_routes(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts,
                      int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
-                     int64_t* offsets, int32_t* n_invalid, void* workspace, size_t workspace_bytes,
-                     void* stream);
+                     int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 /* offsets[e] = #{i : sorted_sel[i] <= e}; replaces cvmm_expert_offsets
  * (cvmm.py:1108-1120, kernel cvmm.py:315-335). */
@@ -96,15 +127,17 @@ int cvmm_cast_keys(const void* keys, int32_t keys_dtype, int32_t n_experts, int6
  *                                                       (out: [R/reduce_k, d_out])
  * keys element (e, i, j) is at keys[e*k_se + i*k_si + j*k_sj]; x rows are
  * contiguous with row stride x_ld.  op_dtype is the MFMA operand type
- * (autocast dtype or F32); x/keys are converted to it in-kernel. */
+ * (autocast dtype or F32); x/keys are converted to it in-kernel.
+ * route_pos (optional): the inverse of rp = out_index or sel_index, as
+ * cvmm_sort_routes writes it; computed in the workspace when NULL. */
 size_t cvmm_fwd_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_out, int64_t out_rows,
                                 int32_t out_dtype, int32_t has_offsets, int32_t weighted, int32_t flags);
 int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld,
              const void* keys, int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out,
              int64_t k_se, int64_t k_si, int64_t k_sj,
              const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index, int64_t n_routes,
-             const int64_t* offsets, const void* reduction_weight, int32_t rw_dtype, int64_t reduce_k,
-             int32_t op_dtype, void* out, int32_t out_dtype, int64_t out_rows, int64_t out_ld,
+             const int64_t* offsets, const int32_t* route_pos, const void* reduction_weight, int32_t rw_dtype,
+             int64_t reduce_k, int32_t op_dtype, void* out, int32_t out_dtype, int64_t out_rows, int64_t out_ld,
              int32_t flags, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
@@ -120,7 +153,7 @@ int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld,
  *  weighted, route-major x                 : grad_x[rp] = rnd_x(rnd_op(rnd_op(g) * rnd_op(w[rp])))
  *  weighted, token x                       : grad_x[t] = rnd_x(rnd_op(sum_j rnd_op(w) * rnd_op(g)))
  *  weighted (both)                          : grad_rw[rp] = <rnd_op(g_i), x[sel_index[i]]>
- * grad_x and/or grad_rw may be NULL when not needed. */
+ * grad_x and/or grad_rw may be NULL when not needed; route_pos as for cvmm_fwd. */
 size_t cvmm_bwd_x_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t grad_x_rows,
                                   int32_t has_offsets, int32_t weighted, int32_t token_input, int64_t top_k,
                                   int32_t grad_x_dtype, int32_t op_dtype, int32_t need_grad_rw, int32_t flags);
@@ -128,8 +161,8 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
                const void* keys, int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out,
                int64_t k_se, int64_t k_si, int64_t k_sj,
                const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index, int64_t n_routes,
-               const int64_t* offsets, const void* reduction_weight, int32_t rw_dtype, int64_t top_k,
-               const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, int32_t op_dtype,
+               const int64_t* offsets, const int32_t* route_pos, const void* reduction_weight, int32_t rw_dtype,
+               int64_t top_k, const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, int32_t op_dtype,
                void* grad_x, int32_t grad_x_dtype, int64_t grad_x_rows, int64_t grad_x_ld,
                void* grad_rw, int32_t grad_rw_dtype,
                int32_t flags, void* workspace, size_t workspace_bytes, void* stream);
@@ -144,7 +177,13 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
 
 /* x_i = rnd_op(x[sel_index[i]]), G_i = rnd_op(grad[rp(i)]) (unweighted) or
  * rnd_op(rnd_op(grad[rp(i)/top_k]) * rnd_op(w[rp(i)])) (weighted).  Every
- * expert's gradient is written, zeros for experts without routes. */
+ * expert's gradient is written, zeros for experts without routes.
+ * The workspace starts with cvmm_bwd_w_counter_bytes() bytes of tile
+ * counters.  They must be zero on entry: the call zeroes them itself unless
+ * flags has CVMM_FLAG_COUNTERS_ZEROED, and it leaves them zero when it ends,
+ * so a caller that keeps one workspace per stream zeroes it once. */
+size_t cvmm_bwd_w_counter_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out,
+                                int32_t op_dtype);
 size_t cvmm_bwd_w_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out,
                                   int32_t op_dtype, int32_t has_offsets);
 int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld,

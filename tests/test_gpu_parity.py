@@ -217,6 +217,25 @@ def test_sort_routes_bit_exact(shape, E, dtype):
     assert np.array_equal(p.sel.cpu().numpy(), m.sel)
 
 
+def test_sort_int64_ids_wrap_like_int32_cast():
+    """int64 ids are sorted as their int32 conversion (cvmm.py:1797 casts the
+    flattened selection to int32 before sorting): 2**32 + 3 is expert 3."""
+    g = torch.Generator().manual_seed(77)
+    E = 9
+    sel = torch.randint(0, E, (5, 40, 4), generator=g, dtype=torch.int64)
+    big = sel.clone()
+    big[::2] += 2 ** 32
+    big[1::3] -= 2 ** 33
+    s = C.cvmm_prepare_sel2(big.cuda())
+    C.create_kernels()
+    s._resolve(E)
+    m = O.prepare_sel2(sel.numpy())
+    assert np.array_equal(s.raw_sel.cpu().numpy(), m.raw_sel)
+    assert np.array_equal(s.sel.cpu().numpy(), m.sel)
+    assert np.array_equal(s.out_index.cpu().numpy(), m.out_index)
+    assert np.array_equal(s.sel_index.cpu().numpy(), m.sel_index)
+
+
 def test_sort_invalid_ids_go_last():
     """Ids outside [0, E) are counted, sorted stably after all valid routes and
     never read by the GEMMs."""
@@ -231,16 +250,20 @@ def test_sort_invalid_ids_go_last():
     perm = torch.empty(R, dtype=torch.int64, device="cuda")
     off = torch.empty(E, dtype=torch.int64, device="cuda")
     nin = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pos = torch.full((R,), -1, dtype=torch.int32, device="cuda")
     ws_b = lib.cvmm_sort_workspace_bytes(R, E)
     ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
-    N.check(lib.cvmm_sort_routes(N.ptr(raw), 0, R, E, 1, N.ptr(ssel), N.ptr(perm), None, N.ptr(off), N.ptr(nin),
-                                 N.ptr(ws), ws_b, N.stream_of(raw.device)), "sort")
+    N.check(lib.cvmm_sort_routes(N.ptr(raw), 0, R, E, 1, N.ptr(ssel), N.ptr(perm), None, N.ptr(off), N.ptr(pos),
+                                 N.ptr(nin), N.ptr(ws), ws_b, N.stream_of(raw.device)), "sort")
     s = sel.numpy()
     valid = (s >= 0) & (s < E)
     key = np.where(valid, s, E)
     exp_perm = np.argsort(key, kind="stable")
     assert int(nin.item()) == int((~valid).sum())
     assert np.array_equal(perm.cpu().numpy(), exp_perm)
+    inv = np.empty_like(exp_perm)
+    inv[exp_perm] = np.arange(R)
+    assert np.array_equal(pos.cpu().numpy(), inv)
     assert np.array_equal(ssel.cpu().numpy(), s[exp_perm].astype(np.int32))
     assert np.array_equal(off.cpu().numpy(), np.cumsum(np.bincount(s[valid], minlength=E)))
 
@@ -282,6 +305,28 @@ def test_weight_grad_is_deterministic():
     b = U.run_hip(x, keys, sel, w, go, True, True)
     for n in ("out", "x_grad", "keys_grad", "weights_grad"):
         assert torch.equal(a[n], b[n]), n
+
+
+@pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True), (True, False)])
+def test_route_positions_from_sort_or_computed(weighted, route_input):
+    """The route-ordered rows are gathered per token through the sort's
+    inverse permutation; a selector built by hand (indices without it) makes
+    the call compute the inverse itself.  Both give the same bits."""
+    x, keys, sel, w, go = _rand_case(21, 3, 200, 128, 256, 7, 4, weighted, route_input)
+    a = U.run_hip(x, keys, sel, w, go, route_input, True)
+
+    def manual(sel_d, w_d, route_input):
+        s = C.cvmm_prepare_sel2(sel_d, w_d, route_input=route_input)
+        s._resolve(keys.shape[0])
+        return C.CVMMSel(s.raw_sel, s.sel, s.sel_index.clone(),
+                         None if s.out_index is None else s.out_index.clone(), s.reduction_weight)
+
+    b = U.run_hip(x, keys, sel, w, go, route_input, True, prepare=manual)
+    for n in ("out", "x_grad", "keys_grad", "weights_grad"):
+        if a[n] is None:
+            assert b[n] is None
+        else:
+            assert torch.equal(a[n], b[n]), n
 
 
 def test_fp16_autocast():

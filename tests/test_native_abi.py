@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.cvmm_abi_version() == 2
+    assert lib.cvmm_abi_version() == 4
 
 
 def test_workspace_queries(lib):
@@ -54,21 +54,21 @@ def test_workspace_queries(lib):
 
 
 def test_invalid_arguments_fail_before_launch(lib):
-    rc = lib.cvmm_sort_routes(None, 0, 10, 0, 1, None, None, None, None, None, None, 0, None)
+    rc = lib.cvmm_sort_routes(None, 0, 10, 0, 1, None, None, None, None, None, None, None, 0, None)
     assert rc == 1 and b"n_experts" in lib.cvmm_last_error()
-    rc = lib.cvmm_sort_routes(None, 0, 10, 100000, 1, None, None, None, None, None, None, 0, None)
+    rc = lib.cvmm_sort_routes(None, 0, 10, 100000, 1, None, None, None, None, None, None, None, 0, None)
     assert rc == 2
-    args = [None, 7, 1, 16, None, 0, 4, 16, 8, 128, 8, 1, None, None, None, 1, None, None, 0, 1,
+    args = [None, 7, 1, 16, None, 0, 4, 16, 8, 128, 8, 1, None, None, None, 1, None, None, None, 0, 1,
             0, None, 0, 1, 8, 0, None, 0, None]
     assert lib.cvmm_fwd(*args) == 1 and b"dtype" in lib.cvmm_last_error()
     args[1] = 0
     args[-4] = 0
     args[2] = 1
-    args[23] = 2   # out_rows != R
+    args[24] = 2   # out_rows != R
     assert lib.cvmm_fwd(*args) == 1
     # weighted forward without workspace
-    wargs = [None, 0, 8, 16, None, 0, 4, 16, 8, 128, 8, 1, None, None, None, 8, None, ctypes.c_void_p(16), 0, 4,
-             0, None, 0, 2, 8, 0, None, 0, None]
+    wargs = [None, 0, 8, 16, None, 0, 4, 16, 8, 128, 8, 1, None, None, None, 8, None, None, ctypes.c_void_p(16),
+             0, 4, 0, None, 0, 2, 8, 0, None, 0, None]
     assert lib.cvmm_fwd(*wargs) == 3
 
 
@@ -77,3 +77,10 @@ def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(N, "_lib", None)
     with pytest.raises(N.NativeLibraryMissing):
         N.lib()
+
+
+def test_tuning_knob_rejects_bad_values(lib):
+    assert lib.cvmm_tuning_set(N.TUNE_PANEL_TILES_PER_WG, -1) != 0
+    assert lib.cvmm_tuning_set(N.TUNE_PANEL_TILES_PER_WG, 5000) != 0
+    assert lib.cvmm_tuning_set(99, 1) != 0
+    assert lib.cvmm_tuning_set(N.TUNE_PANEL_TILES_PER_WG, 0) == 0
