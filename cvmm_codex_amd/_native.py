@@ -107,6 +107,24 @@ def lib():
     return _lib
 
 
+_host = None
+
+
+def host():
+    """The host glue module (``_host``, C++), loaded after the library; raises
+    if either has not been built."""
+    global _host
+    if _host is None:
+        lib()
+        try:
+            from cvmm_codex_amd import _host as h
+        except ImportError as e:
+            raise NativeLibraryMissing(
+                f"cvmm_codex_amd._host is not built ({e}); run `python -m cvmm_codex_amd.build`") from None
+        _host = h
+    return _host
+
+
 def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = lib().cvmm_last_error().decode(errors="replace")

@@ -85,16 +85,6 @@ def dtype_to_type_id(dtype: torch.dtype) -> int:
 # native selector preparation
 # ----------------------------------------------------------------------------
 
-def _flat_int32(sel: torch.Tensor) -> torch.Tensor:
-    f = sel.reshape(-1)
-    if f.dtype != torch.int32:
-        f = f.to(torch.int32)
-    return f.contiguous()
-
-
-_SORT_WS: Dict[Tuple[torch.device, int], torch.Tensor] = {}
-
-
 def _sort_routes(raw_flat: torch.Tensor, n_experts: int, top_k: int):
     """Stable counting sort on the device: (sorted int32, perm int64,
     perm // top_k int64, inclusive offsets int64[E]).  `raw_flat` holds int32
@@ -102,37 +92,15 @@ def _sort_routes(raw_flat: torch.Tensor, n_experts: int, top_k: int):
     inverse permutation (int32) is attached to perm as ``_cvmm_route_pos``: the
     forward/backward calls that receive this perm as their route index use it
     to gather each token's routes."""
-    lib = N.lib()
-    dev = raw_flat.device
-    if raw_flat.dtype not in (torch.int32, torch.int64):
-        raw_flat = raw_flat.to(torch.int32)
-    raw_flat = raw_flat.contiguous()
-    R = raw_flat.numel()
-    stream = N.stream_of(dev)
-    i32 = torch.empty(2 * R, dtype=torch.int32, device=dev)
-    ssel, route_pos = i32[:R], i32[R:]
-    ints = torch.empty(2 * R + n_experts, dtype=torch.int64, device=dev)
-    perm, tok, offsets = ints[:R], ints[R:2 * R], ints[2 * R:]
-    ws_bytes = lib.cvmm_sort_workspace_bytes(R, n_experts)
-    ws = _SORT_WS.get((dev, stream))
-    if ws is None or ws.numel() < ws_bytes:
-        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-        _SORT_WS[(dev, stream)] = ws
-    N.check(lib.cvmm_sort_routes(N.ptr(raw_flat), int(raw_flat.dtype == torch.int64), R, n_experts, max(top_k, 1),
-                                 N.ptr(ssel), N.ptr(perm), N.ptr(tok), N.ptr(offsets), N.ptr(route_pos), None,
-                                 N.ptr(ws), ws.numel(), stream), "cvmm_sort_routes")
+    ssel, perm, tok, offsets, route_pos = N.host().sort_routes(raw_flat, n_experts, top_k,
+                                                               N.stream_of(raw_flat.device))
     perm._cvmm_route_pos = route_pos
     return ssel, perm, tok, offsets
 
 
 def cvmm_expert_offsets(sorted_experts: torch.Tensor, n_experts: int) -> torch.Tensor:
     """Native offsets: out[e] = #{i : sorted[i] <= e} (cvmm.py:1108-1120)."""
-    _require_device(sorted_experts, "sorted_experts")
-    s = _flat_int32(sorted_experts)
-    out = torch.empty(n_experts, dtype=torch.int64, device=s.device)
-    N.check(N.lib().cvmm_expert_offsets(N.ptr(s), s.numel(), n_experts, N.ptr(out), N.stream_of(s.device)),
-            "cvmm_expert_offsets")
-    return out
+    return N.host().expert_offsets(sorted_experts, n_experts, N.stream_of(sorted_experts.device))
 
 
 def _cvmm_expert_offsets(sorted_experts: torch.Tensor, n_experts: int) -> torch.Tensor:
@@ -147,25 +115,12 @@ def _cvmm_expert_offsets(sorted_experts: torch.Tensor, n_experts: int) -> torch.
     return expert_counts.cumsum(0)
 
 
-def _sorted_i32(sel: torch.Tensor) -> torch.Tensor:
-    if sel.dtype == torch.int32 and sel.is_contiguous():
-        return sel.reshape(-1)
-    cached = getattr(sel, "_cvmm_i32", None)
-    if cached is None:
-        cached = _flat_int32(sel)
-        try:
-            sel._cvmm_i32 = cached
-        except (AttributeError, RuntimeError):
-            pass
-    return cached
-
-
 def _offsets_for(sel: torch.Tensor, n_experts: int) -> torch.Tensor:
     """Per-expert offsets of a sorted selector, cached on the tensor object."""
     cache: Optional[Dict[int, torch.Tensor]] = getattr(sel, "_cvmm_offsets", None)
     if cache is not None and n_experts in cache:
         return cache[n_experts]
-    off = cvmm_expert_offsets(_sorted_i32(sel), n_experts)
+    off = cvmm_expert_offsets(sel, n_experts)
     try:
         if cache is None:
             cache = {}
@@ -348,31 +303,12 @@ def cvmm_prepare_sel2(sel: Union[torch.Tensor, CVMMSel], w: Optional[torch.Tenso
 def _storage_for(t: torch.Tensor, op: torch.dtype) -> torch.Tensor:
     """Kernels read fp32 or op-dtype storage; other float types are widened to
     fp32 (exact), which leaves the in-kernel rounding to the op dtype unchanged."""
-    if t.dtype == torch.float32 or (op != torch.float32 and t.dtype == op):
-        return t
-    return t.float()
-
-
-def _rows(t: torch.Tensor, width: int) -> torch.Tensor:
-    f = t.reshape(-1, width)
-    if f.stride(-1) != 1 or (f.shape[0] > 1 and f.stride(0) < width):
-        f = f.contiguous()
-    return f
+    return N.host().storage_for(t, N.dtype_id(op))
 
 
 def _keys_view(keys: torch.Tensor) -> torch.Tensor:
-    if keys.stride(2) == 1 or keys.stride(1) == 1:
-        return keys
-    return keys.contiguous()
-
-
-def _i64(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
-    if t is None:
-        return None
-    f = t.reshape(-1)
-    if f.dtype != torch.int64:
-        f = f.to(torch.int64)
-    return f.contiguous()
+    """keys as they are when one of the two inner strides is 1, else contiguous."""
+    return N.host().keys_view(keys)
 
 
 def _route_pos(rp: Optional[torch.Tensor], n_routes: int) -> Optional[torch.Tensor]:
@@ -383,163 +319,45 @@ def _route_pos(rp: Optional[torch.Tensor], n_routes: int) -> Optional[torch.Tens
     return pos
 
 
-def _workspace(nbytes: int, device) -> Optional[torch.Tensor]:
-    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
-
-
-class _WgradWorkspace:
-    """One weight-gradient workspace per (device, stream), kept between calls.
-
-    cvmm_bwd_w's tile counters sit at the start of its workspace and the call
-    leaves them zero, so a kept workspace only needs its counter prefix zeroed
-    once.  ``clean`` is the length of the prefix known to be zero: a call
-    writes partial tiles right after its own counter region, so after it only
-    that region is known clean.  Calls on one stream run in stream order, so
-    sharing the buffer between them is safe."""
-
-    _cache: dict = {}
-
-    @classmethod
-    def get(cls, device, stream: int, nbytes: int, counter_bytes: int):
-        key = (device, stream)
-        buf, clean = cls._cache.get(key, (None, 0))
-        if buf is None or buf.numel() < nbytes:
-            buf = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
-            clean = buf.numel()
-        zeroed = counter_bytes <= clean
-        cls._cache[key] = (buf, counter_bytes)
-        return buf, zeroed
-
-
 def _fast_path(op: torch.dtype, d_in: int, d_out: int) -> bool:
     """The DMA-staged kernels need 16-bit operands and widths divisible by 8."""
     return op in (torch.bfloat16, torch.float16) and d_in % 8 == 0 and d_out % 8 == 0
 
 
+def _flags() -> int:
+    return N.FLAG_ATOMIC_REDUCE if cvmm_atomic_reduce else 0
+
+
 def _cast_keys(keys: torch.Tensor, op: torch.dtype, want_t: bool, want_n: bool):
     """keys [E, d_in, d_out] -> op-dtype copies kt [E, d_out, d_in] (forward) and
     kn [E, d_in, d_out] (grad-input), one pass."""
-    n_experts, d_in, d_out = keys.shape
-    kt = torch.empty(n_experts, d_out, d_in, dtype=op, device=keys.device) if want_t else None
-    kn = torch.empty(n_experts, d_in, d_out, dtype=op, device=keys.device) if want_n else None
-    N.check(N.lib().cvmm_cast_keys(N.ptr(keys), N.dtype_id(keys.dtype), n_experts, d_in, d_out, keys.stride(0),
-                                   keys.stride(1), keys.stride(2), N.dtype_id(op), N.ptr(kt), N.ptr(kn),
-                                   N.stream_of(keys.device)), "cvmm_cast_keys")
-    return kt, kn
+    _require_device(keys, "keys")
+    return N.host().cast_keys(keys, N.dtype_id(op), want_t, want_n, N.stream_of(keys.device))
 
 
 def _forward(x, sel_index, sel, keys, out_index, rw, op_dtype, keys_t=None):
-    for t, name in ((x, "x"), (keys, "keys"), (sel, "sel"), (sel_index, "sel_index")):
-        _require_device(t, name)
-    n_experts, d_in, d_out = keys.shape
-    assert x.shape[-1] == keys.shape[1]                                   # cvmm.py:825
-    dev = x.device
-    lib = N.lib()
-    if keys_t is not None:
-        # op-dtype activations and the [E, d_out, d_in] weight copy, seen as a
-        # [E, d_in, d_out] view with unit stride on d_in: the fast kernels' layout
-        xf = _rows(x if x.dtype == op_dtype else x.to(op_dtype), d_in)
-        kv = keys_t.transpose(1, 2)
-    else:
-        xf = _rows(_storage_for(x, op_dtype), d_in)
-        kv = _keys_view(_storage_for(keys, op_dtype))
-    s32 = _sorted_i32(sel)
-    R = s32.numel()
-    si = _i64(sel_index)
-    oi = _i64(out_index)
-    if si.numel() != R or (oi is not None and oi.numel() != R):
-        raise ValueError("cvmm: sel_index/out_index must have one entry per route")
-    off = _offsets_for(sel, n_experts)
-    rwf = None
+    """cvmm_triton (cvmm.py:814-867) + the weighted combine (:1543-1545)."""
+    _require_device(sel, "sel")
+    n_experts = keys.shape[0]
+    R = sel.numel()
+    out = N.host().forward(x, keys, keys_t, sel, sel_index, out_index, _offsets_for(sel, n_experts),
+                           _route_pos(out_index if out_index is not None else sel_index, R), rw,
+                           N.dtype_id(op_dtype), _flags(), N.stream_of(x.device))
     if rw is None:
-        out_rows, out_shape = R, (*sel.shape, d_out)
-        k = 1
-    else:
-        _require_device(rw, "reduction_weight")
-        if rw.numel() != R:
-            raise ValueError("cvmm: reduction_weight must have one entry per route")
-        k = rw.shape[-1]
-        rwf = rw.reshape(-1).contiguous()
-        out_rows, out_shape = R // k, (*rw.shape[:-1], d_out)
-    out = torch.empty(out_rows, d_out, dtype=op_dtype, device=dev)
-    flags = N.FLAG_ATOMIC_REDUCE if cvmm_atomic_reduce else 0
-    od = N.dtype_id(op_dtype)
-    ws_bytes = lib.cvmm_fwd_workspace_bytes(R, n_experts, d_out, out_rows, od, 1, int(rw is not None), flags)
-    ws = _workspace(ws_bytes, dev)
-    N.check(lib.cvmm_fwd(
-        N.ptr(xf), N.dtype_id(xf.dtype), xf.shape[0], xf.stride(0),
-        N.ptr(kv), N.dtype_id(kv.dtype), n_experts, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2),
-        N.ptr(s32), N.ptr(si), N.ptr(oi), R,
-        N.ptr(off), N.ptr(_route_pos(out_index if out_index is not None else sel_index, R)),
-        N.ptr(rwf), N.dtype_id(rwf.dtype) if rwf is not None else 0, k,
-        od, N.ptr(out), od, out_rows, d_out,
-        flags, N.ptr(ws), ws_bytes, N.stream_of(dev)), "cvmm_fwd")
-    return out.view(out_shape)
+        return out.view(*sel.shape, keys.shape[2])
+    return out.view(*rw.shape[:-1], keys.shape[2])
 
 
 def _backward(ctx, grad_output, x, keys, raw_sel, sel, sel_index, out_index, rw,
               need_grad_x, need_grad_keys, need_grad_rw, keys_n=None):
-    op = ctx.op_type
-    n_experts, d_in, d_out = keys.shape
-    dev = x.device
-    lib = N.lib()
+    """CVMM.backward's products (cvmm.py:1552-1755)."""
     top_k = raw_sel.shape[-1] if raw_sel.ndim > 0 else 1
-    k = rw.shape[-1] if rw is not None else top_k
-    g = _rows(grad_output.to(op) if _fast_path(op, d_in, d_out) and grad_output.dtype != op
-              else _storage_for(grad_output, op), d_out)
-    s32 = _sorted_i32(sel)
-    R = s32.numel()
-    si = _i64(sel_index)
-    oi = _i64(out_index)
-    off = _offsets_for(sel, n_experts)
-    rwf = rw.reshape(-1).contiguous() if rw is not None else None
-    rwd = N.dtype_id(rwf.dtype) if rwf is not None else 0
-    od = N.dtype_id(op)
-    flags = N.FLAG_ATOMIC_REDUCE if cvmm_atomic_reduce else 0
-    stream = N.stream_of(dev)
-    grad_x = grad_w = grad_rw = None
-
-    fast = _fast_path(op, d_in, d_out)
-    if need_grad_keys:
-        xs = _rows(x.to(op) if fast and x.dtype != op else _storage_for(x, op), d_in)
-        grad_w = torch.empty(keys.shape, dtype=keys.dtype, device=dev)
-        ws_bytes = lib.cvmm_bwd_w_workspace_bytes(R, n_experts, d_in, d_out, od, 1)
-        ws, zeroed = _WgradWorkspace.get(dev, stream, ws_bytes,
-                                         lib.cvmm_bwd_w_counter_bytes(R, n_experts, d_in, d_out, od))
-        wflags = flags | (N.FLAG_COUNTERS_ZEROED if zeroed else 0)
-        N.check(lib.cvmm_bwd_w(
-            N.ptr(xs), N.dtype_id(xs.dtype), xs.shape[0], xs.stride(0),
-            N.ptr(g), N.dtype_id(g.dtype), g.shape[0], g.stride(0),
-            n_experts, d_in, d_out, N.ptr(s32), N.ptr(si), N.ptr(oi), R, N.ptr(off),
-            N.ptr(rwf), rwd, k, od,
-            N.ptr(grad_w), N.dtype_id(grad_w.dtype), grad_w.stride(0), grad_w.stride(1), grad_w.stride(2),
-            wflags, N.ptr(ws), ws.numel(), stream), "cvmm_bwd_w")
-
-    if need_grad_x or need_grad_rw:
-        kv = keys_n if keys_n is not None else _keys_view(_storage_for(keys, op))
-        xr = _rows(x, d_in)
-        gx = None
-        if need_grad_x:
-            gx = torch.empty(xr.shape, dtype=x.dtype, device=dev)
-        if need_grad_rw:
-            grad_rw = torch.empty(rw.shape, dtype=rw.dtype, device=dev)
-        gx_rows = gx.shape[0] if gx is not None else xr.shape[0]
-        ws_bytes = lib.cvmm_bwd_x_workspace_bytes(
-            R, n_experts, d_in, gx_rows, 1, int(rw is not None), int(oi is not None), k,
-            N.dtype_id(x.dtype), od, int(need_grad_rw), flags)
-        ws = _workspace(ws_bytes, dev)
-        N.check(lib.cvmm_bwd_x(
-            N.ptr(g), N.dtype_id(g.dtype), g.shape[0], g.stride(0),
-            N.ptr(kv), N.dtype_id(kv.dtype), n_experts, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2),
-            N.ptr(s32), N.ptr(si), N.ptr(oi), R, N.ptr(off),
-            N.ptr(_route_pos(out_index if out_index is not None else sel_index, R)), N.ptr(rwf), rwd, k,
-            N.ptr(xr), N.dtype_id(xr.dtype), xr.shape[0], xr.stride(0), od,
-            N.ptr(gx), N.dtype_id(x.dtype), gx_rows, d_in,
-            N.ptr(grad_rw), N.dtype_id(rw.dtype) if rw is not None else 0,
-            flags, N.ptr(ws), ws_bytes, stream), "cvmm_bwd_x")
-        if gx is not None:
-            grad_x = gx.view(x.shape)
-    return grad_x, grad_w, grad_rw
+    R = sel.numel()
+    return N.host().backward(grad_output, x, keys, keys_n, sel, sel_index, out_index,
+                             _offsets_for(sel, keys.shape[0]),
+                             _route_pos(out_index if out_index is not None else sel_index, R), rw, top_k,
+                             N.dtype_id(ctx.op_type), bool(need_grad_x), bool(need_grad_keys), bool(need_grad_rw),
+                             _flags(), N.stream_of(x.device))
 
 
 class CVMM(torch.autograd.Function):
@@ -582,9 +400,9 @@ known_shapes = set()
 
 
 def create_kernels() -> None:
-    """Load libcvmm_hip.so (idempotent); raises if it is missing."""
+    """Load libcvmm_hip.so and the host glue (idempotent); raises if either is missing."""
     global cvmm_expert_offsets_call
-    N.lib()
+    N.host()
     if cvmm_expert_offsets_call is None:
         cvmm_expert_offsets_call = cvmm_expert_offsets
 

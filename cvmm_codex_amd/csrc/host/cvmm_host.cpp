@@ -1,0 +1,319 @@
+// Host glue between the Python API (cvmm_codex_amd/api.py) and the C ABI of
+// libcvmm_hip.so (include/cvmm_hip.h): output allocation, the storage and
+// layout rules for each operand, workspace sizing and the ABI calls.  One call
+// per phase replaces a few dozen Python-level tensor operations, which at the
+// sizes of an MoE projection cost as much host time as the kernels take on the
+// GPU.  Streams come from Python (the raw handle of torch's current stream);
+// every call here is asynchronous.
+//
+// Mirrors the reference's per-phase host logic: cvmm_prepare_sel2's sort
+// (cvmm.py:1796-1803), cvmm_triton (cvmm.py:814-867) with the weighted combine
+// (cvmm.py:1543-1545), and CVMM.backward's products (cvmm.py:1552-1755).
+#include <torch/extension.h>
+
+#include <map>
+#include <mutex>
+#include <optional>
+#include <string>
+#include <tuple>
+#include <utility>
+#include <vector>
+
+#include "cvmm_hip.h"
+
+namespace py = pybind11;
+
+namespace {
+
+using at::Tensor;
+using OptT = std::optional<Tensor>;
+
+int32_t dtype_id(at::ScalarType t) {
+  switch (t) {
+    case at::kFloat: return 0;
+    case at::kHalf: return 1;
+    case at::kBFloat16: return 2;
+    default: throw py::type_error(std::string("cvmm: unsupported dtype ") + c10::toString(t));
+  }
+}
+
+at::ScalarType dtype_of(int64_t id) {
+  switch (id) {
+    case 0: return at::kFloat;
+    case 1: return at::kHalf;
+    case 2: return at::kBFloat16;
+    default: throw py::value_error("cvmm: bad dtype id");
+  }
+}
+
+void check(int rc, const char* what) {
+  if (rc != 0)
+    throw std::runtime_error(std::string(what) + " failed (code " + std::to_string(rc) + "): " + cvmm_last_error());
+}
+
+void* ptr(const Tensor& t) { return t.data_ptr(); }
+void* ptr(const OptT& t) { return t.has_value() ? t->data_ptr() : nullptr; }
+template <typename T> T* tptr(const OptT& t) { return t.has_value() ? static_cast<T*>(t->data_ptr()) : nullptr; }
+template <typename T> T* tptr(const Tensor& t) { return static_cast<T*>(t.data_ptr()); }
+
+void require_device(const Tensor& t, const char* what) {
+  if (!t.is_cuda())
+    throw std::runtime_error(std::string("cvmm_codex_amd: ") + what +
+                             " must be a ROCm GPU tensor (there is no CPU fallback)");
+}
+
+// Kernels read fp32 or op-dtype storage; other float types are widened to
+// fp32 (exact), which leaves the in-kernel rounding to the op dtype unchanged.
+Tensor storage_for(const Tensor& t, at::ScalarType op) {
+  if (t.scalar_type() == at::kFloat || (op != at::kFloat && t.scalar_type() == op)) return t;
+  return t.to(at::kFloat);
+}
+
+// [rows, width] view with unit column stride and a row stride >= width.
+Tensor rows_of(const Tensor& t, int64_t width) {
+  Tensor f = t.reshape({-1, width});
+  if (f.stride(1) != 1 || (f.size(0) > 1 && f.stride(0) < width)) f = f.contiguous();
+  return f;
+}
+
+Tensor keys_view(const Tensor& keys) {
+  if (keys.stride(2) == 1 || keys.stride(1) == 1) return keys;
+  return keys.contiguous();
+}
+
+Tensor as_i64(const Tensor& t) {
+  Tensor f = t.reshape({-1});
+  if (f.scalar_type() != at::kLong) f = f.to(at::kLong);
+  return f.contiguous();
+}
+
+OptT as_i64(const OptT& t) {
+  if (!t.has_value()) return std::nullopt;
+  return as_i64(*t);
+}
+
+Tensor sorted_i32(const Tensor& s) {
+  Tensor f = s.reshape({-1});
+  if (f.scalar_type() != at::kInt) f = f.to(at::kInt);
+  return f.contiguous();
+}
+
+bool fast_path(at::ScalarType op, int64_t d_in, int64_t d_out) {
+  return (op == at::kBFloat16 || op == at::kHalf) && d_in % 8 == 0 && d_out % 8 == 0;
+}
+
+at::TensorOptions opts(const Tensor& like, at::ScalarType dt) {
+  return at::TensorOptions().dtype(dt).device(like.device());
+}
+
+// Scratch kept per (device, stream): calls on one stream run in stream order,
+// so they can share it.
+struct Scratch {
+  Tensor buf;
+  size_t clean = 0;  // length of the prefix known to be zero
+};
+std::mutex g_mu;
+std::map<std::pair<int, int64_t>, Scratch> g_sort_ws, g_wgrad_ws;
+
+Tensor sort_workspace(const Tensor& like, int64_t stream, size_t bytes) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  Scratch& s = g_sort_ws[{(int)like.get_device(), stream}];
+  if (!s.buf.defined() || (size_t)s.buf.numel() < bytes)
+    s.buf = at::empty({(int64_t)std::max<size_t>(bytes, 1)}, opts(like, at::kByte));
+  return s.buf;
+}
+
+// ---------------------------------------------------------------------------
+// selector preparation: stable counting sort (cvmm.py:24-27, :1796-1803)
+// returns (sorted int32, perm int64, perm // top_k int64, offsets int64[E],
+// route_pos int32 = inverse of perm)
+// ---------------------------------------------------------------------------
+std::vector<Tensor> sort_routes(const Tensor& raw, int64_t n_experts, int64_t top_k, int64_t stream) {
+  require_device(raw, "sel");
+  Tensor flat = raw.reshape({-1});
+  if (flat.scalar_type() != at::kInt && flat.scalar_type() != at::kLong) flat = flat.to(at::kInt);
+  flat = flat.contiguous();
+  const int64_t R = flat.numel();
+  Tensor i32 = at::empty({2 * R}, opts(flat, at::kInt));
+  Tensor i64 = at::empty({2 * R + n_experts}, opts(flat, at::kLong));
+  Tensor ssel = i32.narrow(0, 0, R), pos = i32.narrow(0, R, R);
+  Tensor perm = i64.narrow(0, 0, R), tok = i64.narrow(0, R, R), off = i64.narrow(0, 2 * R, n_experts);
+  const size_t ws_bytes = cvmm_sort_workspace_bytes(R, (int32_t)n_experts);
+  Tensor ws = sort_workspace(flat, stream, ws_bytes);
+  check(cvmm_sort_routes(ptr(flat), flat.scalar_type() == at::kLong ? 1 : 0, R, (int32_t)n_experts,
+                         std::max<int64_t>(top_k, 1), tptr<int32_t>(ssel), tptr<int64_t>(perm), tptr<int64_t>(tok),
+                         tptr<int64_t>(off), tptr<int32_t>(pos), nullptr, ptr(ws), (size_t)ws.numel(),
+                         (void*)stream),
+        "cvmm_sort_routes");
+  return {ssel, perm, tok, off, pos};
+}
+
+Tensor expert_offsets(const Tensor& sorted, int64_t n_experts, int64_t stream) {
+  require_device(sorted, "sorted_experts");
+  Tensor s = sorted_i32(sorted);
+  Tensor out = at::empty({n_experts}, opts(s, at::kLong));
+  check(cvmm_expert_offsets(tptr<int32_t>(s), s.numel(), (int32_t)n_experts, tptr<int64_t>(out), (void*)stream),
+        "cvmm_expert_offsets");
+  return out;
+}
+
+// keys [E, d_in, d_out] -> op-dtype copies kt [E, d_out, d_in] (forward) and
+// kn [E, d_in, d_out] (grad-input), one pass.
+std::tuple<OptT, OptT> cast_keys(const Tensor& keys, int64_t op_id, bool want_t, bool want_n, int64_t stream) {
+  require_device(keys, "keys");
+  const auto op = dtype_of(op_id);
+  const int64_t E = keys.size(0), d_in = keys.size(1), d_out = keys.size(2);
+  OptT kt, kn;
+  if (want_t) kt = at::empty({E, d_out, d_in}, opts(keys, op));
+  if (want_n) kn = at::empty({E, d_in, d_out}, opts(keys, op));
+  check(cvmm_cast_keys(ptr(keys), dtype_id(keys.scalar_type()), (int32_t)E, d_in, d_out, keys.stride(0),
+                       keys.stride(1), keys.stride(2), (int32_t)op_id, ptr(kt), ptr(kn), (void*)stream),
+        "cvmm_cast_keys");
+  return {kt, kn};
+}
+
+// ---------------------------------------------------------------------------
+// forward (cvmm.py:1524-1550): returns [out_rows, d_out] in the op dtype
+// ---------------------------------------------------------------------------
+Tensor forward(const Tensor& x, const Tensor& keys, const OptT& keys_t, const Tensor& sel, const Tensor& sel_index,
+               const OptT& out_index, const Tensor& offsets, const OptT& route_pos, const OptT& rw, int64_t op_id,
+               int64_t flags, int64_t stream) {
+  require_device(x, "x");
+  require_device(keys, "keys");
+  require_device(sel, "sel");
+  require_device(sel_index, "sel_index");
+  const auto op = dtype_of(op_id);
+  const int64_t E = keys.size(0), d_in = keys.size(1), d_out = keys.size(2);
+  TORCH_CHECK(x.size(-1) == d_in, "cvmm: x.shape[-1] must equal keys.shape[1]");  // cvmm.py:825
+  Tensor xf, kv;
+  if (keys_t.has_value()) {
+    // op-dtype activations and the [E, d_out, d_in] weight copy, seen as a
+    // [E, d_in, d_out] view with unit stride on d_in: the fast kernels' layout
+    xf = rows_of(x.scalar_type() == op ? x : x.to(op), d_in);
+    kv = keys_t->transpose(1, 2);
+  } else {
+    xf = rows_of(storage_for(x, op), d_in);
+    kv = keys_view(storage_for(keys, op));
+  }
+  Tensor s32 = sorted_i32(sel);
+  const int64_t R = s32.numel();
+  Tensor si = as_i64(sel_index);
+  OptT oi = as_i64(out_index);
+  if (si.numel() != R || (oi.has_value() && oi->numel() != R))
+    throw py::value_error("cvmm: sel_index/out_index must have one entry per route");
+  OptT rwf;
+  int64_t k = 1, out_rows = R;
+  if (rw.has_value()) {
+    require_device(*rw, "reduction_weight");
+    if (rw->numel() != R) throw py::value_error("cvmm: reduction_weight must have one entry per route");
+    k = rw->size(-1);
+    rwf = rw->reshape({-1}).contiguous();
+    out_rows = R / k;
+  }
+  const int32_t od = (int32_t)op_id;
+  Tensor out = at::empty({out_rows, d_out}, opts(x, op));
+  const size_t ws_bytes = cvmm_fwd_workspace_bytes(R, (int32_t)E, d_out, out_rows, od, 1, rw.has_value() ? 1 : 0,
+                                                   (int32_t)flags);
+  OptT ws;
+  if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(x, at::kByte));
+  check(cvmm_fwd(ptr(xf), dtype_id(xf.scalar_type()), xf.size(0), xf.stride(0), ptr(kv), dtype_id(kv.scalar_type()),
+                 (int32_t)E, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2), tptr<int32_t>(s32),
+                 tptr<int64_t>(si), tptr<int64_t>(oi), R, tptr<int64_t>(offsets), tptr<int32_t>(route_pos),
+                 ptr(rwf), rwf.has_value() ? dtype_id(rwf->scalar_type()) : 0, k, od, ptr(out), od, out_rows, d_out,
+                 (int32_t)flags, ptr(ws), ws_bytes, (void*)stream),
+        "cvmm_fwd");
+  return out;
+}
+
+// ---------------------------------------------------------------------------
+// backward (cvmm.py:1552-1755): (grad_x, grad_keys, grad_reduction_weight)
+// ---------------------------------------------------------------------------
+std::tuple<OptT, OptT, OptT> backward(const Tensor& grad_output, const Tensor& x, const Tensor& keys,
+                                      const OptT& keys_n, const Tensor& sel, const Tensor& sel_index,
+                                      const OptT& out_index, const Tensor& offsets, const OptT& route_pos,
+                                      const OptT& rw, int64_t top_k, int64_t op_id, bool need_grad_x,
+                                      bool need_grad_keys, bool need_grad_rw, int64_t flags, int64_t stream) {
+  const auto op = dtype_of(op_id);
+  const int64_t E = keys.size(0), d_in = keys.size(1), d_out = keys.size(2);
+  const int64_t k = rw.has_value() ? rw->size(-1) : top_k;
+  const bool fast = fast_path(op, d_in, d_out);
+  Tensor g = rows_of(fast && grad_output.scalar_type() != op ? grad_output.to(op) : storage_for(grad_output, op),
+                     d_out);
+  Tensor s32 = sorted_i32(sel);
+  const int64_t R = s32.numel();
+  Tensor si = as_i64(sel_index);
+  OptT oi = as_i64(out_index);
+  OptT rwf;
+  if (rw.has_value()) rwf = rw->reshape({-1}).contiguous();
+  const int32_t rwd = rwf.has_value() ? dtype_id(rwf->scalar_type()) : 0;
+  const int32_t od = (int32_t)op_id;
+  OptT grad_x, grad_w, grad_rw;
+
+  if (need_grad_keys) {
+    Tensor xs = rows_of(fast && x.scalar_type() != op ? x.to(op) : storage_for(x, op), d_in);
+    grad_w = at::empty(keys.sizes(), opts(keys, keys.scalar_type()));
+    const size_t ws_bytes = cvmm_bwd_w_workspace_bytes(R, (int32_t)E, d_in, d_out, od, 1);
+    const size_t ctr_bytes = cvmm_bwd_w_counter_bytes(R, (int32_t)E, d_in, d_out, od);
+    Tensor ws;
+    bool zeroed;
+    {
+      // the tile counters at the start of the workspace are left zero by the
+      // kernel; a kept workspace is zeroed once (when allocated)
+      std::lock_guard<std::mutex> lk(g_mu);
+      Scratch& s = g_wgrad_ws[{(int)x.get_device(), stream}];
+      if (!s.buf.defined() || (size_t)s.buf.numel() < ws_bytes) {
+        s.buf = at::zeros({(int64_t)std::max<size_t>(ws_bytes, 1)}, opts(x, at::kByte));
+        s.clean = (size_t)s.buf.numel();
+      }
+      zeroed = ctr_bytes <= s.clean;
+      s.clean = ctr_bytes;  // partial tiles follow the counter region
+      ws = s.buf;
+    }
+    const int32_t wflags = (int32_t)flags | (zeroed ? CVMM_FLAG_COUNTERS_ZEROED : 0);
+    check(cvmm_bwd_w(ptr(xs), dtype_id(xs.scalar_type()), xs.size(0), xs.stride(0), ptr(g),
+                     dtype_id(g.scalar_type()), g.size(0), g.stride(0), (int32_t)E, d_in, d_out, tptr<int32_t>(s32),
+                     tptr<int64_t>(si), tptr<int64_t>(oi), R, tptr<int64_t>(offsets), ptr(rwf), rwd, k, od,
+                     ptr(grad_w), dtype_id(grad_w->scalar_type()), grad_w->stride(0), grad_w->stride(1),
+                     grad_w->stride(2), wflags, ptr(ws), (size_t)ws.numel(), (void*)stream),
+          "cvmm_bwd_w");
+  }
+
+  if (need_grad_x || need_grad_rw) {
+    Tensor kv = keys_n.has_value() ? *keys_n : keys_view(storage_for(keys, op));
+    Tensor xr = rows_of(x, d_in);
+    OptT gx;
+    if (need_grad_x) gx = at::empty(xr.sizes(), opts(x, x.scalar_type()));
+    if (need_grad_rw) grad_rw = at::empty(rw->sizes(), opts(*rw, rw->scalar_type()));
+    const int64_t gx_rows = gx.has_value() ? gx->size(0) : xr.size(0);
+    const size_t ws_bytes = cvmm_bwd_x_workspace_bytes(R, (int32_t)E, d_in, gx_rows, 1, rw.has_value() ? 1 : 0,
+                                                       oi.has_value() ? 1 : 0, k, dtype_id(x.scalar_type()), od,
+                                                       need_grad_rw ? 1 : 0, (int32_t)flags);
+    OptT ws;
+    if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(x, at::kByte));
+    check(cvmm_bwd_x(ptr(g), dtype_id(g.scalar_type()), g.size(0), g.stride(0), ptr(kv), dtype_id(kv.scalar_type()),
+                     (int32_t)E, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2), tptr<int32_t>(s32),
+                     tptr<int64_t>(si), tptr<int64_t>(oi), R, tptr<int64_t>(offsets), tptr<int32_t>(route_pos),
+                     ptr(rwf), rwd, k, ptr(xr), dtype_id(xr.scalar_type()), xr.size(0), xr.stride(0), od, ptr(gx),
+                     dtype_id(x.scalar_type()), gx_rows, d_in, ptr(grad_rw),
+                     rw.has_value() ? dtype_id(rw->scalar_type()) : 0, (int32_t)flags, ptr(ws), ws_bytes,
+                     (void*)stream),
+          "cvmm_bwd_x");
+    if (gx.has_value()) grad_x = gx->view(x.sizes());
+  }
+  return {grad_x, grad_w, grad_rw};
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "Host glue of cvmm_codex_amd: one call per CVMM phase into libcvmm_hip.so";
+  m.def("sort_routes", &sort_routes, py::arg("raw"), py::arg("n_experts"), py::arg("top_k"), py::arg("stream"));
+  m.def("expert_offsets", &expert_offsets, py::arg("sorted"), py::arg("n_experts"), py::arg("stream"));
+  m.def("cast_keys", &cast_keys, py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"),
+        py::arg("stream"));
+  m.def("forward", &forward);
+  m.def("backward", &backward);
+  // operand rules, exposed for tests
+  m.def("storage_for", [](const Tensor& t, int64_t op_id) { return storage_for(t, dtype_of(op_id)); });
+  m.def("keys_view", &keys_view);
+}
