@@ -1,5 +1,5 @@
-// Routed GEMM fast-path instantiations for op type f16_t (cvmm_gemm_panel.h, cvmm_gemm_nt.h).
-#include "cvmm_gemm_panel.h"
+// Routed GEMM fast-path instantiations for op type f16_t (cvmm_gemm_ring.h, cvmm_gemm_panel.h, cvmm_gemm_nt.h).
+#include "cvmm_gemm_ring.h"
 
 namespace cvmm {
 hipError_t launch_routed_gemm_nt_f16(const GemmParams& p, hipStream_t stream) {

@@ -47,6 +47,29 @@ __device__ __forceinline__ void wg_barrier() {
 
 __device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }
 
+// 16-byte LDS read issued as inline asm.  The compiler does not see it as an
+// LDS access, so its wait-count pass inserts no vmcnt wait for in-flight DMA
+// into other LDS buffers (it cannot always tell those apart and then waits
+// for all of them); the caller orders it after its own DMA wait and barrier
+// and must call lds_wait_tied on the results before using them.
+typedef unsigned int lds_u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ lds_u32x4 lds_read128(const char* p) {
+  lds_u32x4 v;
+  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a));
+  return v;
+}
+
+// lgkmcnt(0) tied to the registers of 8 inline-asm LDS reads, so no use of
+// them can be scheduled before the wait.
+__device__ __forceinline__ void lds_wait_tied(lds_u32x4 (&x)[4], lds_u32x4 (&y)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]));
+}
+
+__device__ __forceinline__ uint4 as_uint4(lds_u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); }
+
 template <int KP, int BN>
 struct PanelCfg {
   static constexpr int BM = 128;
@@ -288,14 +311,5 @@ hipError_t launch_routed_gemm_panel_out(const GemmParams& p, hipStream_t stream)
   return launch_routed_gemm_panel_t<OpT, OutT, 128, 64>(p, stream);
 }
 
-// Fast-path dispatch for 16-bit k-contiguous operands.
-template <typename OpT>
-hipError_t launch_routed_gemm_fast_op(const GemmParams& p, hipStream_t stream) {
-  if (panel_eligible(p, DTypeOf<OpT>::value)) {
-    if (p.out_dtype == kF32) return launch_routed_gemm_panel_out<OpT, float>(p, stream);
-    return launch_routed_gemm_panel_out<OpT, OpT>(p, stream);
-  }
-  return launch_routed_gemm_nt_op<OpT>(p, stream);
-}
 
 }  // namespace cvmm

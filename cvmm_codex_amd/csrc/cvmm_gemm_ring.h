@@ -1,0 +1,261 @@
+// Routed GEMM with a deep DMA ring for a long inner dimension (K > 128,
+// 16-bit k-contiguous operands): the ff_up forward (K = d_in = 1024, N = 128),
+// the ff_down input gradient (K = 1024, N = 128) and the SwitchHead V forward
+// / O input gradient (K = 2048, N = 64).
+//
+// A tile-per-workgroup GEMM with two LDS stages keeps one 32 KB stage in
+// flight while it computes on the other; with a DMA latency of about a
+// microsecond and a stage's MFMA work of a tenth of that, the workgroup waits
+// most of the time.  Here the k loop streams BK = 32 slices (16-20 KB each)
+// through STAGES statically named LDS buffers, STAGES - 1 of them in flight:
+//  * wait for slice s with vmcnt((STAGES - 2) * D): only DMA is in flight in
+//    the loop, D instructions per slice and lane, retiring in order;
+//  * one barrier, then slice s + STAGES - 1 goes into the buffer slice s - 1
+//    used (every wave has finished reading it);
+//  * MFMA on slice s, operands swapped (C^T = W x A^T) so that a lane ends
+//    with 4 consecutive output columns of one row; two lane swaps make that 8
+//    columns, stored as one 16-byte write.
+// Slices past K are loaded from the zero page, so every iteration issues the
+// same DMA count and the waits are the same constant.
+//
+// LDS rows are 64 bytes (BK = 32 16-bit values, four 16-byte chunks).  The
+// MFMA fragment reads (lane l: row l % 16, chunk l / 16) are free of bank
+// conflicts when the chunk of row r is stored at chunk ^ ((r >> 1) & 3): an
+// inline-asm ds_read_b128 probe on gfx950 measured SQ_LDS_BANK_CONFLICT = 0
+// for that swizzle and 16.8 M conflict cycles (the same as no swizzle) for
+// chunk ^ (r & 3), chunk ^ ((r >> 2) & 3) and two other XOR mixes.
+#pragma once
+
+#include "cvmm_gemm_panel.h"
+
+namespace cvmm {
+
+template <int BM, int BN, int STAGES>
+struct RingCfg {
+  static constexpr int BK = 32;                        // 16-bit values per k slice
+  static constexpr int ROWB = 64;                      // bytes per LDS row
+  static constexpr int A_BYTES = BM * ROWB;
+  static constexpr int B_BYTES = BN * ROWB;
+  static constexpr int SLICE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int D = SLICE_BYTES / 4096;         // DMA instructions per wave per slice
+  static constexpr int DA = A_BYTES / 4096;            // ... of which for A
+  static constexpr int WN = BN / 64, WM = BM / 64;     // wave grid, 64 x 64 per wave
+  static_assert(WM * WN == 4, "4 waves of 64x64");
+  static_assert(SLICE_BYTES % 4096 == 0, "whole DMA instructions per wave");
+  static_assert(STAGES >= 3 && STAGES <= 5, "ring depth");
+  static_assert((STAGES - 2) * D < 64, "vmcnt range");
+};
+
+__device__ __forceinline__ int ring_swz(int row) { return (row >> 1) & 3; }
+
+template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, int Role>
+__global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(const GemmParams p) {
+  using Cfg = RingCfg<BM, BN, STAGES>;
+  __shared__ __attribute__((aligned(1024))) char ring[STAGES * Cfg::SLICE_BYTES];
+  __shared__ RouteMeta<BM> meta;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t n_ntiles = (p.N + BN - 1) / BN;
+  const int64_t id = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t tile = id / n_ntiles;
+  const int64_t ntile = id % n_ntiles;
+  const int64_t n0 = ntile * BN;
+
+  if (!gemm_schedule<BM>(p, tile, meta)) return;
+  const int32_t expert = meta.expert;
+
+  // ---- per-lane DMA sources: instruction j of wave w fills LDS bytes
+  // [(w * D + j) * 1024, +1024) of a slice = 16 rows of 64 bytes; A rows first
+  const char* zero = reinterpret_cast<const char*>(g_cvmm_zero_page);
+  const char* src[Cfg::D];
+  int kc[Cfg::D];  // element offset of this lane's chunk within a slice
+#pragma unroll
+  for (int j = 0; j < Cfg::D; ++j) {
+    const int q = (wave * Cfg::D + j) * 64 + lane;  // 16-byte chunk index within the slice
+    const int row = q >> 2;
+    const int c = (q & 3) ^ ring_swz(row);
+    kc[j] = c * 8;
+    if (row < BM) {
+      const int64_t ar = meta.arow[row];
+      src[j] = ar >= 0 ? reinterpret_cast<const char*>(p.a) + (ar * p.a_ld + c * 8) * 2 : nullptr;
+    } else {
+      const int64_t gn = n0 + (row - BM);
+      src[j] = gn < p.N ? reinterpret_cast<const char*>(p.b) + ((int64_t)expert * p.b_se + gn * p.b_sn + c * 8) * 2
+                        : nullptr;
+    }
+  }
+  auto issue = [&](int64_t s, char* buf) {
+    const int64_t k0 = s * Cfg::BK;
+#pragma unroll
+    for (int j = 0; j < Cfg::D; ++j) {
+      const char* sp = (src[j] != nullptr && k0 + kc[j] < p.K) ? src[j] + k0 * 2 : zero;
+      dma16(sp, buf + (wave * Cfg::D + j) * 1024);
+    }
+  };
+
+  // ---- fragments: lane reads row (l % 16) of each 16-row block, chunk l / 16
+  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+  const int fr = lane & 15, fq = lane >> 4;
+  int a_off[4], b_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ra = wm * 64 + i * 16 + fr;
+    const int rb = BM + wn * 64 + i * 16 + fr;
+    a_off[i] = ra * Cfg::ROWB + ((fq ^ ring_swz(ra)) << 4);
+    b_off[i] = rb * Cfg::ROWB + ((fq ^ ring_swz(rb)) << 4);
+  }
+  f32x4_t acc[4][4];  // acc[i][j]: n-block i, m-block j (C^T orientation)
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const char* buf) {
+    lds_u32x4 af[4], bf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bf[i] = lds_read128(buf + b_off[i]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) af[j] = lds_read128(buf + a_off[j]);
+    lds_wait_tied(bf, af);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) MfmaOp<OpT>::step(acc[i][j], as_uint4(bf[i]), as_uint4(af[j]));
+  };
+
+  // ---- k loop: slices 0 .. nk-1 computed; slices up to nk + STAGES - 2 are
+  // issued (those past K read zeros) so that every wait is the same count
+  const int64_t nk = (p.K + Cfg::BK - 1) / Cfg::BK;
+#pragma unroll
+  for (int s0 = 0; s0 < STAGES - 1; ++s0) {
+    issue(s0, ring + s0 * Cfg::SLICE_BYTES);
+    issue_fence();
+  }
+  // the fragment reads are inline asm (lds_read128), invisible to the
+  // compiler's wait-count pass, so one ring array indexed at run time costs no
+  // extra waits; the slice is ready once this wave's own DMA for it has landed
+  // (vm_wait) and every other wave's has too (barrier)
+  int cur = 0, refill = STAGES - 1;
+  for (int64_t s = 0; s < nk; ++s) {
+    vm_wait<(STAGES - 2) * Cfg::D>();
+    wg_barrier();
+    issue(s + STAGES - 1, ring + refill * Cfg::SLICE_BYTES);
+    issue_fence();
+    compute(ring + cur * Cfg::SLICE_BYTES);
+    cur = cur + 1 == STAGES ? 0 : cur + 1;
+    refill = refill + 1 == STAGES ? 0 : refill + 1;
+  }
+  // slices past K may still be landing in LDS: drain them before the
+  // workgroup can end and its LDS be handed to another
+  vm_wait<0>();
+
+  // ---- epilogue from registers: lane holds C[m = wm*64 + j*16 + fr]
+  // [n = n0 + wn*64 + i*16 + 4*fq + {0..3}]
+  const bool has_w = p.w != nullptr;
+  const int64_t nwave = n0 + wn * 64;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = wm * 64 + j * 16 + fr;
+    const int64_t orow = meta.orow[m];
+    const float wv = meta.w[m];
+    float v[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float c = round_to(acc[i][j][q], p.val_dtype);
+        if (has_w) {
+          c = c * wv;
+          if (p.prod_dtype >= 0) c = round_to(c, p.prod_dtype);
+        }
+        v[i][q] = c;
+      }
+    char* rowp = orow >= 0 ? reinterpret_cast<char*>(p.out) + orow * p.out_ld * (int64_t)sizeof(OutT) : nullptr;
+    if constexpr (sizeof(OutT) == 4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t n = nwave + i * 16 + 4 * fq;
+        if (rowp != nullptr && n < p.N)
+          *reinterpret_cast<float4*>(rowp + n * 4) = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+      }
+    } else {
+      // blocks 2p, 2p+1 -> columns 32p + 8*fq + [0, 8) per lane (two lane swaps)
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) {
+        uint32_t a[2], b[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          union { uint32_t u; OutT e[2]; } pa, pb;
+          pa.e[0] = (OutT)v[2 * pr][2 * h];
+          pa.e[1] = (OutT)v[2 * pr][2 * h + 1];
+          pb.e[0] = (OutT)v[2 * pr + 1][2 * h];
+          pb.e[1] = (OutT)v[2 * pr + 1][2 * h + 1];
+          a[h] = pa.u;
+          b[h] = pb.u;
+        }
+        const auto s0 = __builtin_amdgcn_permlane32_swap(a[0], b[0], false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(a[1], b[1], false, false);
+        const auto t0 = __builtin_amdgcn_permlane16_swap(s0[0], s0[1], false, false);
+        const auto t1 = __builtin_amdgcn_permlane16_swap(s1[0], s1[1], false, false);
+        const int64_t n = nwave + pr * 32 + 8 * fq;
+        if (rowp != nullptr && n < p.N)
+          *reinterpret_cast<uint4*>(rowp + n * 2) = make_uint4(t0[0], t1[0], t0[1], t1[1]);
+      }
+    }
+  }
+}
+
+// The ring kernel applies: plain stores (optionally scaled by a per-row
+// routing weight), no routing-weight gradient, output in the op type or fp32,
+// N a multiple of 8 with 16-byte aligned output rows.
+inline bool ring_eligible(const GemmParams& p, int32_t op) {
+  const size_t esz = p.out_dtype == kF32 ? 4 : 2;
+  return p.K > 128 && p.epi == kEpiStore && p.dg == nullptr && p.out != nullptr &&
+         (p.out_dtype == op || p.out_dtype == kF32) && p.N % 8 == 0 &&
+         (reinterpret_cast<uintptr_t>(p.out) % 16) == 0 && ((size_t)p.out_ld * esz) % 16 == 0;
+}
+
+template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC>
+hipError_t launch_routed_gemm_ring_t(const GemmParams& p, hipStream_t stream) {
+  const int64_t m_tiles = (p.n_routes + BM - 1) / BM + (p.n_experts < p.n_routes ? p.n_experts : p.n_routes);
+  const int64_t n_ntiles = (p.N + BN - 1) / BN;
+  const int64_t grid = m_tiles * n_ntiles;
+  if (grid <= 0) return hipSuccess;
+  if (grid > 0x7fffffffll) return hipErrorInvalidValue;
+  if (p.role == 0)
+    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, 0>), dim3((unsigned)grid),
+                       dim3(kGemmThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, 1>), dim3((unsigned)grid),
+                       dim3(kGemmThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+// 128 x 128 tiles: 3 slices of 16 KB + route metadata = 53 KB of LDS, three
+// workgroups per CU (768 resident tiles: the whole ff_up forward at once);
+// 256 x 64 tiles: 3 slices of 20 KB + 9 KB = 69 KB, two per CU.
+template <typename OpT, typename OutT>
+hipError_t launch_routed_gemm_ring_out(const GemmParams& p, hipStream_t stream) {
+  if (p.N <= 64) return launch_routed_gemm_ring_t<OpT, OutT, 256, 64, 3, 2>(p, stream);
+  return launch_routed_gemm_ring_t<OpT, OutT, 128, 128, 3, 3>(p, stream);
+}
+
+// Fast-path dispatch for 16-bit k-contiguous operands: small K -> panel
+// kernel, long K -> ring kernel, anything else (routing-weight gradient,
+// atomics, unaligned output) -> the tiled kernel.
+template <typename OpT>
+hipError_t launch_routed_gemm_fast_op(const GemmParams& p, hipStream_t stream) {
+  constexpr int32_t op = DTypeOf<OpT>::value;
+  if (panel_eligible(p, op)) {
+    if (p.out_dtype == kF32) return launch_routed_gemm_panel_out<OpT, float>(p, stream);
+    return launch_routed_gemm_panel_out<OpT, OpT>(p, stream);
+  }
+  if (ring_eligible(p, op)) {
+    if (p.out_dtype == kF32) return launch_routed_gemm_ring_out<OpT, float>(p, stream);
+    return launch_routed_gemm_ring_out<OpT, OpT>(p, stream);
+  }
+  return launch_routed_gemm_nt_op<OpT>(p, stream);
+}
+
+}  // namespace cvmm
