@@ -7,14 +7,16 @@
 // flight while it computes on the other; with a DMA latency of about a
 // microsecond and a stage's MFMA work of a tenth of that, the workgroup waits
 // most of the time.  Here the k loop streams BK = 32 slices (16-20 KB each)
-// through STAGES statically named LDS buffers, STAGES - 1 of them in flight:
-//  * wait for slice s with vmcnt((STAGES - 2) * D): only DMA is in flight in
+// through a ring of STAGES LDS buffers, STAGES - 1 of them in flight:
+//  * wait for the next slice with a constant vmcnt: only DMA is in flight in
 //    the loop, D instructions per slice and lane, retiring in order;
-//  * one barrier, then slice s + STAGES - 1 goes into the buffer slice s - 1
-//    used (every wave has finished reading it);
-//  * MFMA on slice s, operands swapped (C^T = W x A^T) so that a lane ends
-//    with 4 consecutive output columns of one row; two lane swaps make that 8
+//  * one barrier, then the buffer every wave has finished reading is refilled;
+//  * MFMA with operands swapped (C^T = W x A^T) so that a lane ends with 4
+//    consecutive output columns of one row; two lane swaps make that 8
 //    columns, stored as one 16-byte write.
+// With read-ahead (RA) the fragments of slice s + 1 are read into a second
+// register set while the MFMAs of slice s run; that needs ~200 VGPRs, so it is
+// used where two workgroups per CU are the limit anyway (256 x 64 tiles).
 // Slices past K are loaded from the zero page, so every iteration issues the
 // same DMA count and the waits are the same constant.
 //
@@ -48,7 +50,7 @@ struct RingCfg {
 
 __device__ __forceinline__ int ring_swz(int row) { return (row >> 1) & 3; }
 
-template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, int Role>
+template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int Role>
 __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(const GemmParams p) {
   using Cfg = RingCfg<BM, BN, STAGES>;
   __shared__ __attribute__((aligned(1024))) char ring[STAGES * Cfg::SLICE_BYTES];
@@ -111,40 +113,73 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](const char* buf) {
-    lds_u32x4 af[4], bf[4];
+  auto read_frags = [&](const char* buf, lds_u32x4 (&af)[4], lds_u32x4 (&bf)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) bf[i] = lds_read128(buf + b_off[i]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) af[j] = lds_read128(buf + a_off[j]);
-    lds_wait_tied(bf, af);
+  };
+  auto mfma = [&](lds_u32x4 (&af)[4], lds_u32x4 (&bf)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) MfmaOp<OpT>::step(acc[i][j], as_uint4(bf[i]), as_uint4(af[j]));
   };
 
-  // ---- k loop: slices 0 .. nk-1 computed; slices up to nk + STAGES - 2 are
-  // issued (those past K read zeros) so that every wait is the same count
   const int64_t nk = (p.K + Cfg::BK - 1) / Cfg::BK;
+  if constexpr (RA) {
+    // ---- k loop with fragment read-ahead: the fragments of slice s + 1 are
+    // read while the MFMAs of slice s run (two register sets), so a slice's
+    // buffer is free once its reads have been waited for: iteration s refills
+    // the buffer of slice s with slice s + STAGES.
 #pragma unroll
-  for (int s0 = 0; s0 < STAGES - 1; ++s0) {
-    issue(s0, ring + s0 * Cfg::SLICE_BYTES);
-    issue_fence();
-  }
-  // the fragment reads are inline asm (lds_read128), invisible to the
-  // compiler's wait-count pass, so one ring array indexed at run time costs no
-  // extra waits; the slice is ready once this wave's own DMA for it has landed
-  // (vm_wait) and every other wave's has too (barrier)
-  int cur = 0, refill = STAGES - 1;
-  for (int64_t s = 0; s < nk; ++s) {
-    vm_wait<(STAGES - 2) * Cfg::D>();
+    for (int s0 = 0; s0 < STAGES; ++s0) {
+      issue(s0, ring + s0 * Cfg::SLICE_BYTES);
+      issue_fence();
+    }
+    lds_u32x4 a0[4], b0[4], a1[4], b1[4];
+    vm_wait<(STAGES - 1) * Cfg::D>();
     wg_barrier();
-    issue(s + STAGES - 1, ring + refill * Cfg::SLICE_BYTES);
-    issue_fence();
-    compute(ring + cur * Cfg::SLICE_BYTES);
-    cur = cur + 1 == STAGES ? 0 : cur + 1;
-    refill = refill + 1 == STAGES ? 0 : refill + 1;
+    read_frags(ring, a0, b0);
+    lds_wait_tied(b0, a0);
+    int buf = 0;  // buffer of slice s
+    auto step = [&](int64_t s, lds_u32x4 (&ac)[4], lds_u32x4 (&bc)[4], lds_u32x4 (&an)[4], lds_u32x4 (&bn)[4]) {
+      const int nxt = buf + 1 == STAGES ? 0 : buf + 1;
+      vm_wait<(STAGES - 2) * Cfg::D>();  // slice s + 1 has landed (only DMA is in flight)
+      wg_barrier();
+      issue(s + STAGES, ring + buf * Cfg::SLICE_BYTES);
+      issue_fence();
+      read_frags(ring + nxt * Cfg::SLICE_BYTES, an, bn);
+      mfma(ac, bc);
+      lds_wait_tied(bn, an);
+      buf = nxt;
+    };
+    for (int64_t s = 0; s < nk; s += 2) {
+      step(s, a0, b0, a1, b1);
+      if (s + 1 >= nk) break;
+      step(s + 1, a1, b1, a0, b0);
+    }
+  } else {
+    // ---- k loop: wait for slice s, refill the buffer of slice s - 1 with
+    // slice s + STAGES - 1, then read and multiply slice s
+#pragma unroll
+    for (int s0 = 0; s0 < STAGES - 1; ++s0) {
+      issue(s0, ring + s0 * Cfg::SLICE_BYTES);
+      issue_fence();
+    }
+    int cur = 0, refill = STAGES - 1;
+    for (int64_t s = 0; s < nk; ++s) {
+      vm_wait<(STAGES - 2) * Cfg::D>();
+      wg_barrier();
+      issue(s + STAGES - 1, ring + refill * Cfg::SLICE_BYTES);
+      issue_fence();
+      lds_u32x4 af[4], bf[4];
+      read_frags(ring + cur * Cfg::SLICE_BYTES, af, bf);
+      lds_wait_tied(bf, af);
+      mfma(af, bf);
+      cur = cur + 1 == STAGES ? 0 : cur + 1;
+      refill = refill + 1 == STAGES ? 0 : refill + 1;
+    }
   }
   // slices past K may still be landing in LDS: drain them before the
   // workgroup can end and its LDS be handed to another
@@ -216,7 +251,7 @@ inline bool ring_eligible(const GemmParams& p, int32_t op) {
          (reinterpret_cast<uintptr_t>(p.out) % 16) == 0 && ((size_t)p.out_ld * esz) % 16 == 0;
 }
 
-template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC>
+template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA>
 hipError_t launch_routed_gemm_ring_t(const GemmParams& p, hipStream_t stream) {
   const int64_t m_tiles = (p.n_routes + BM - 1) / BM + (p.n_experts < p.n_routes ? p.n_experts : p.n_routes);
   const int64_t n_ntiles = (p.N + BN - 1) / BN;
@@ -224,10 +259,10 @@ hipError_t launch_routed_gemm_ring_t(const GemmParams& p, hipStream_t stream) {
   if (grid <= 0) return hipSuccess;
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
   if (p.role == 0)
-    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, 0>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 0>), dim3((unsigned)grid),
                        dim3(kGemmThreads), 0, stream, p);
   else
-    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, 1>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1>), dim3((unsigned)grid),
                        dim3(kGemmThreads), 0, stream, p);
   return hipGetLastError();
 }
@@ -237,8 +272,8 @@ hipError_t launch_routed_gemm_ring_t(const GemmParams& p, hipStream_t stream) {
 // 256 x 64 tiles: 3 slices of 20 KB + 9 KB = 69 KB, two per CU.
 template <typename OpT, typename OutT>
 hipError_t launch_routed_gemm_ring_out(const GemmParams& p, hipStream_t stream) {
-  if (p.N <= 64) return launch_routed_gemm_ring_t<OpT, OutT, 256, 64, 3, 2>(p, stream);
-  return launch_routed_gemm_ring_t<OpT, OutT, 128, 128, 3, 3>(p, stream);
+  if (p.N <= 64) return launch_routed_gemm_ring_t<OpT, OutT, 256, 64, 3, 2, true>(p, stream);
+  return launch_routed_gemm_ring_t<OpT, OutT, 128, 128, 3, 3, false>(p, stream);
 }
 
 // Fast-path dispatch for 16-bit k-contiguous operands: small K -> panel
