@@ -79,16 +79,16 @@ __global__ __launch_bounds__(kScanThreads) void sort_scan_kernel(
   }
 }
 
+// Stable scatter of one chunk: within every 256-route round, lanes with equal
+// buckets are ranked by a ballot per bucket bit and the waves take their
+// positions in order, so equal ids keep their input order.  `pos` holds this
+// chunk's next output position per bucket.
 template <typename IdxT>
-__global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
-    const IdxT* __restrict__ sel, int64_t n_routes, int32_t n_experts, int64_t chunk,
-    int64_t n_chunks, const int32_t* __restrict__ bases, int32_t n_bits, int64_t top_k,
-    int32_t* __restrict__ sorted_sel, int64_t* __restrict__ perm, int64_t* __restrict__ token_index,
-    int32_t* __restrict__ route_pos) {
-  extern __shared__ int32_t pos[];  // n_experts + 1 running output positions
+__device__ void scatter_chunk(const IdxT* __restrict__ sel, int64_t n_routes, int32_t n_experts, int64_t chunk,
+                              int32_t n_bits, int64_t top_k, int32_t* pos, int32_t* __restrict__ sorted_sel,
+                              int64_t* __restrict__ perm, int64_t* __restrict__ token_index,
+                              int32_t* __restrict__ route_pos) {
   const int64_t b = blockIdx.x;
-  for (int e = threadIdx.x; e <= n_experts; e += kSortThreads) pos[e] = bases[(int64_t)e * n_chunks + b];
-  __syncthreads();
   const int wave = threadIdx.x >> 6;
   const int lane = lane_id();
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -120,6 +120,19 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
       __syncthreads();
     }
   }
+}
+
+template <typename IdxT>
+__global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
+    const IdxT* __restrict__ sel, int64_t n_routes, int32_t n_experts, int64_t chunk,
+    int64_t n_chunks, const int32_t* __restrict__ bases, int32_t n_bits, int64_t top_k,
+    int32_t* __restrict__ sorted_sel, int64_t* __restrict__ perm, int64_t* __restrict__ token_index,
+    int32_t* __restrict__ route_pos) {
+  extern __shared__ int32_t pos[];  // n_experts + 1 running output positions
+  const int64_t b = blockIdx.x;
+  for (int e = threadIdx.x; e <= n_experts; e += kSortThreads) pos[e] = bases[(int64_t)e * n_chunks + b];
+  __syncthreads();
+  scatter_chunk(sel, n_routes, n_experts, chunk, n_bits, top_k, pos, sorted_sel, perm, token_index, route_pos);
 }
 
 // Upper-bound binary search per expert over an already sorted int32 array
