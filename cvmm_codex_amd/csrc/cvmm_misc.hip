@@ -91,29 +91,65 @@ __host__ __device__ inline bool vec_ok(const void* p, int32_t dt, int64_t ld) {
 // cvmm.py:1545).  row(r) = r, or, with a route-ordered buffer (row q holds
 // route rp[q]), row(r) = inv[r] checked against rp: a route no row holds adds
 // nothing.
-__global__ void combine_rows_kernel(const void* __restrict__ buf, int32_t buf_dtype, int64_t buf_ld,
-                                    const int32_t* __restrict__ inv, const int64_t* __restrict__ rp,
-                                    int64_t n_routes, const void* __restrict__ w, int32_t w_dtype,
-                                    int32_t w_round, int64_t k, int64_t n, int32_t mid_dtype,
-                                    void* __restrict__ out, int32_t out_dtype, int64_t out_ld, bool in_vec,
-                                    bool out_vec) {
+__global__ __launch_bounds__(256) void combine_rows_kernel(
+    const void* __restrict__ buf, int32_t buf_dtype, int64_t buf_ld, const int32_t* __restrict__ inv,
+    const int64_t* __restrict__ rp, int64_t n_routes, const void* __restrict__ w, int32_t w_dtype,
+    int32_t w_round, int64_t k, int64_t n, int32_t mid_dtype, void* __restrict__ out, int32_t out_dtype,
+    int64_t out_ld, bool in_vec, bool out_vec) {
+  // the token's routes are resolved once per workgroup (64 at a time) into
+  // LDS: row of the route in `buf` (-1: none) and its rounded weight
+  __shared__ int64_t s_row[64];
+  __shared__ float s_w[64];
   const int64_t t = blockIdx.x;
   const int64_t c = ((int64_t)blockIdx.y * blockDim.x + threadIdx.x) * 8;
-  if (c >= n) return;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int64_t j = 0; j < k; ++j) {
-    const int64_t r = t * k + j;
-    int64_t row = r;
-    if (inv != nullptr) {
-      row = inv[r];
-      if (row < 0 || row >= n_routes || rp[row] != r) continue;
+  for (int64_t j0 = 0; j0 < k; j0 += 64) {
+    const int64_t kj = k - j0 < 64 ? k - j0 : 64;
+    if (threadIdx.x < kj) {
+      const int64_t r = t * k + j0 + threadIdx.x;
+      int64_t row = r;
+      if (inv != nullptr) {
+        row = inv[r];
+        if (row < 0 || row >= n_routes || rp[row] != r) row = -1;
+      }
+      s_row[threadIdx.x] = row;
+      s_w[threadIdx.x] = w != nullptr ? round_to(load_as_f32(w, w_dtype, r), w_round) : 1.f;
     }
-    const float wv = w != nullptr ? round_to(load_as_f32(w, w_dtype, r), w_round) : 1.f;
-    float v[8];
-    load8_any(buf, buf_dtype, row * buf_ld + c, in_vec, n - c, v);
+    __syncthreads();
+    if (c < n) {
+      int64_t j = 0;
+      // four rows in flight, summed in route order
+      for (; j + 4 <= kj; j += 4) {
+        float v[4][8];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) acc[q] += wv * v[q];
+        for (int u = 0; u < 4; ++u) {
+          const int64_t row = s_row[j + u];
+          if (row >= 0) load8_any(buf, buf_dtype, row * buf_ld + c, in_vec, n - c, v[u]);
+          else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v[u][q] = 0.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float wv = s_w[j + u];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[q] += wv * v[u][q];
+        }
+      }
+      for (; j < kj; ++j) {
+        const int64_t row = s_row[j];
+        if (row < 0) continue;
+        float v[8];
+        load8_any(buf, buf_dtype, row * buf_ld + c, in_vec, n - c, v);
+        const float wv = s_w[j];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[q] += wv * v[q];
+      }
+    }
+    __syncthreads();
   }
+  if (c >= n) return;
   if (mid_dtype >= 0) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) acc[q] = round_to(acc[q], mid_dtype);
