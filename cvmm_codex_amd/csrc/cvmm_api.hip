@@ -39,18 +39,18 @@ hipError_t launch_routed_gemm(const GemmParams& p, int32_t op, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_wgrad_v2_bf16(const WgradParams& p, hipStream_t stream);
-hipError_t launch_wgrad_v2_f16(const WgradParams& p, hipStream_t stream);
+hipError_t launch_wgrad_v3_bf16(const WgradParams& p, hipStream_t stream);
+hipError_t launch_wgrad_v3_f16(const WgradParams& p, hipStream_t stream);
 
 // Fast path: 16-bit x and dY in the op dtype, 16-byte aligned rows, widths % 8.
-static bool wgrad_v2_eligible(const WgradParams& p, int32_t op) {
+static bool wgrad_fast_eligible(const WgradParams& p, int32_t op) {
   auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
   return (op == kBF16 || op == kF16) && p.x_dtype == op && p.g_dtype == op && p.M % 8 == 0 && p.N % 8 == 0 &&
          al(p.x) && al(p.g) && p.x_ld % 8 == 0 && p.g_ld % 8 == 0;
 }
 
 hipError_t launch_wgrad(const WgradParams& p, int32_t op, hipStream_t s) {
-  if (wgrad_v2_eligible(p, op)) return op == kBF16 ? launch_wgrad_v2_bf16(p, s) : launch_wgrad_v2_f16(p, s);
+  if (wgrad_fast_eligible(p, op)) return op == kBF16 ? launch_wgrad_v3_bf16(p, s) : launch_wgrad_v3_f16(p, s);
   if (op == kBF16) return launch_wgrad_bf16(p, s);
   if (op == kF16) return launch_wgrad_f16(p, s);
   if (op == kF32) return launch_wgrad_f32(p, s);

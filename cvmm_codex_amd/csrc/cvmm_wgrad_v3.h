@@ -1,0 +1,466 @@
+// Weight gradient fast path (16-bit operands, gfx950): dW[e] = X_e^T G_e.
+//
+// The reduction runs over the expert's routes, and both operands are gathered
+// route rows (an x row and a dY row per route).  A workgroup owns one
+// BM x BN tile of dW[e] (x columns m0.., dY columns n0..) and one chunk of the
+// expert's routes, and streams that chunk through LDS in slices of 32 routes:
+//  * Route table: the chunk's row indices (and rounded routing weights) are
+//    resolved once, coalesced, into an LDS table; the DMA lanes of each slice
+//    read their row from it.  Chunks longer than the table run in segments.
+//  * DMA ring: slices move by global_load_lds (16 bytes per lane, one 1 KB
+//    instruction = RPI rows) into a ring of STAGES buffers, STAGES - 1 in
+//    flight.  Only DMA is in flight in the loop, so the wait for slice s is the
+//    exact vmcnt of the slices issued after it.
+//  * Fragments without transposing writes: the slices keep the natural
+//    [route][column] layout, and ds_read_b64_tr_b16 hands each lane 4 routes
+//    of one column (lane L of a 16-lane group points at route L / 4, column
+//    4 * (L % 4)); two reads give the 8 routes of a 16x16x32 MFMA operand.
+//  * Operands swapped (dW^T tile = G^T X), so a lane ends holding 4
+//    consecutive dW columns of one row, stored as one 16-byte write straight
+//    from the accumulators.
+//  * Weighted routes (dY scaled by the routing weight, rounded to the op type
+//    as cvmm.py:590-599 does) are scaled while the dY fragments are in
+//    registers: each lane's 8 routes share one weight per route.
+//  * An expert with more routes than the split runs as several chunks; each
+//    writes its fp32 partial tile in fragment order, and the last to arrive
+//    (per-tile counter) sums them in chunk order -- deterministic -- and
+//    stores dW.
+// LDS rows are swizzled at 16-byte granularity so that a transposed read's
+// 16 lanes (4 routes x 32 bytes) hit distinct banks:
+//   256-byte rows: chunk ^ (2 * ((row & 3) | (((row >> 3) & 1) << 2)))
+//   128-byte rows: chunk ^ (2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1)))
+// and 512-byte rows use the 256-byte rule within each half.
+#pragma once
+
+#include "cvmm_gemm_panel.h"
+
+namespace cvmm {
+
+static __device__ uint4 g_cvmm_wg3_zero_page[64];
+
+typedef unsigned int lds_u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// Inline-asm LDS reads (invisible to the compiler's wait-count pass, see
+// lds_read128); results are used only after an lgkmcnt wait tied to them.
+template <int OFF>
+__device__ __forceinline__ lds_u32x2 lds_read_tr(uint32_t a) {
+  lds_u32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+  return v;
+}
+
+template <int OFF>
+__device__ __forceinline__ int32_t lds_read_i32(uint32_t a) {
+  int32_t v;
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+  return v;
+}
+
+template <int OFF>
+__device__ __forceinline__ lds_u32x4 lds_read128_at(uint32_t a) {
+  lds_u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+  return v;
+}
+
+template <int N>
+__device__ __forceinline__ void lgkm_wait_tied(int32_t (&r)[N]) {
+  if constexpr (N == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
+  } else if constexpr (N == 5) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]));
+  } else {
+    static_assert(N == 4 || N == 5, "DMA instructions per wave");
+  }
+}
+
+__device__ __forceinline__ void lgkm_wait_frags(lds_u32x2 (&g)[4][2], lds_u32x2 (&x)[4][2]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(g[0][0]), "+v"(g[0][1]), "+v"(g[1][0]), "+v"(g[1][1]), "+v"(g[2][0]), "+v"(g[2][1]),
+                 "+v"(g[3][0]), "+v"(g[3][1]), "+v"(x[0][0]), "+v"(x[0][1]), "+v"(x[1][0]), "+v"(x[1][1]),
+                 "+v"(x[2][0]), "+v"(x[2][1]), "+v"(x[3][0]), "+v"(x[3][1]));
+}
+
+__device__ __forceinline__ void lgkm_wait_w(lds_u32x4 (&w)[2]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(w[0]), "+v"(w[1]));
+}
+
+// Wait until at most `ahead` slices (D DMA instructions each) are in flight.
+template <int D, int K>
+__device__ __forceinline__ void vm_wait_slices(int ahead) {
+  if constexpr (K == 0) {
+    vm_wait<0>();
+  } else {
+    if (ahead >= K) vm_wait<K * D>();
+    else vm_wait_slices<D, K - 1>(ahead);
+  }
+}
+
+// 32 route rows of COLS 16-bit values.
+template <int COLS>
+struct RouteSlice {
+  static constexpr int ROWB = COLS * 2;
+  static constexpr int CPR = COLS / 8;        // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;        // rows per 1 KB DMA instruction
+  static constexpr int BYTES = 32 * ROWB;
+  static constexpr int INSTS = BYTES / 1024;
+  static_assert(CPR == 8 || CPR == 16 || CPR == 32, "64, 128 or 256 columns");
+  __device__ static __forceinline__ int swz(int row) {
+    if constexpr (CPR >= 16) return 2 * ((row & 3) | (((row >> 3) & 1) << 2));
+    else return 2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1));
+  }
+};
+
+template <int BM, int BN, int STAGES, bool WEIGHTED>
+struct Wg3Cfg {
+  using TA = RouteSlice<BM>;                   // x rows: dW rows m0 .. m0 + BM
+  using TB = RouteSlice<BN>;                   // dY rows: dW columns n0 .. n0 + BN
+  static constexpr int SLICE = TA::BYTES + TB::BYTES;
+  static constexpr int D = (TA::INSTS + TB::INSTS) / 4;  // DMA instructions per wave per slice
+  static_assert((TA::INSTS + TB::INSTS) % 4 == 0, "whole DMA instructions per wave");
+  static constexpr int WM = BM / 64, WN = BN / 64;       // wave grid, 64 x 64 per wave
+  static_assert(WM * WN == 4, "4 waves of 64x64");
+  static_assert((STAGES - 2) * D < 64, "vmcnt range");
+  // route table in what is left of 80 KB (two workgroups per CU)
+  static constexpr int ENTRY = WEIGHTED ? 12 : 8;
+  static constexpr int TBL = ((80 * 1024 - 512 - STAGES * SLICE) / ENTRY) / 32 * 32;
+  static_assert(TBL >= 256, "route table");
+};
+
+struct Wg3Sched {
+  int32_t expert, nch, last;
+  int64_t lo, hi, slot, base_slot;
+};
+
+// (expert, route chunk) of work slot `slot_id`: experts in order, each cut
+// into chunks of p.split routes (at least one chunk per expert).
+__device__ __forceinline__ bool wgrad_schedule(const WgradParams& p, int64_t slot_id, Wg3Sched& s) {
+  const int lane = threadIdx.x & 63;
+  if (threadIdx.x < 64) {
+    if (lane == 0) s.expert = -1;
+    int64_t carry = 0, carry_multi = 0;
+    for (int32_t base = 0; base < p.n_experts; base += 64) {
+      const int32_t e = base + lane;
+      int64_t start = 0, end = 0, nch = 0;
+      if (e < p.n_experts) {
+        end = p.offsets[e];
+        start = e > 0 ? p.offsets[e - 1] : 0;
+        end = end < 0 ? 0 : (end > p.n_routes ? p.n_routes : end);
+        start = start < 0 ? 0 : (start > p.n_routes ? p.n_routes : start);
+        if (end < start) end = start;
+        nch = (end - start + p.split - 1) / p.split;
+        if (nch < 1) nch = 1;
+      }
+      const int64_t multi = nch > 1 ? nch : 0;
+      const int64_t incl = wave_incl_scan(nch) + carry;
+      const int64_t incl_m = wave_incl_scan(multi) + carry_multi;
+      const int64_t excl = incl - nch;
+      if (e < p.n_experts && slot_id >= excl && slot_id < incl) {
+        const int64_t c = slot_id - excl;
+        s.expert = e;
+        s.nch = (int32_t)nch;
+        s.lo = start + c * p.split;
+        s.hi = (start + (c + 1) * p.split) < end ? start + (c + 1) * p.split : end;
+        s.base_slot = incl_m - multi;
+        s.slot = s.base_slot + c;
+      }
+      carry = __shfl(incl, 63, 64);
+      carry_multi = __shfl(incl_m, 63, 64);
+      if (slot_id < carry) break;
+    }
+  }
+  __syncthreads();
+  return s.expert >= 0;
+}
+
+template <typename OpT, int BM, int BN, int STAGES, bool WEIGHTED>
+__global__ __launch_bounds__(256, 2) void wgrad_v3_kernel(const WgradParams p) {
+  using Cfg = Wg3Cfg<BM, BN, STAGES, WEIGHTED>;
+  using TA = typename Cfg::TA;
+  using TB = typename Cfg::TB;
+  constexpr int D = Cfg::D;
+  constexpr int TBL = Cfg::TBL;
+  __shared__ __attribute__((aligned(1024))) char ring[STAGES * Cfg::SLICE];
+  __shared__ __attribute__((aligned(16))) int32_t t_x[TBL];
+  __shared__ __attribute__((aligned(16))) int32_t t_g[TBL];
+  __shared__ __attribute__((aligned(16))) float t_w[WEIGHTED ? TBL : 4];
+  __shared__ Wg3Sched sched;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t tiles_n = (p.N + BN - 1) / BN;
+  const int64_t tiles = ((p.M + BM - 1) / BM) * tiles_n;
+  const int64_t id = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t slot_id = id / tiles;
+  const int64_t tile = id % tiles;
+  const int64_t m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+
+  if (!wgrad_schedule(p, slot_id, sched)) return;
+  const int32_t expert = sched.expert;
+  const int64_t lo = sched.lo, hi = sched.hi;
+  const int32_t nch = sched.nch;
+
+  // ---- DMA geometry: instruction j of this wave fills slice bytes
+  // [(wave * D + j) * 1024, +1024): x rows (TA) first, then dY rows (TB)
+  const char* zero = reinterpret_cast<const char*>(g_cvmm_wg3_zero_page);
+  const char* xb = reinterpret_cast<const char*>(p.x) + m0 * 2;
+  const char* gb = reinterpret_cast<const char*>(p.g) + n0 * 2;
+  // Row bases and strides live in registers: nothing in the loop may load
+  // from memory, or the compiler's wait for it would also wait for the DMA.
+  uint32_t tab[D];         // LDS address of the table entry of this lane's row (slice 0)
+  const char* dbase[D];    // row 0 + this lane's 16-byte chunk, nullptr = past the edge
+  int64_t dld[D];          // row stride in bytes
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    const int gi = wave * D + j;
+    if (gi < TA::INSTS) {
+      const int row = gi * TA::RPI + lane / TA::CPR;
+      const int c = (lane % TA::CPR) ^ TA::swz(row);
+      tab[j] = lds_addr(t_x + row);
+      dbase[j] = m0 + c * 8 < p.M ? xb + c * 16 : nullptr;
+      dld[j] = p.x_ld * 2;
+    } else {
+      const int row = (gi - TA::INSTS) * TB::RPI + lane / TB::CPR;
+      const int c = (lane % TB::CPR) ^ TB::swz(row);
+      tab[j] = lds_addr(t_g + row);
+      dbase[j] = n0 + c * 8 < p.N ? gb + c * 16 : nullptr;
+      dld[j] = p.g_ld * 2;
+    }
+  }
+  auto issue = [&](int s, int slot) {
+    int32_t r[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) r[j] = lds_read_i32<0>(tab[j] + s * 128);
+    lgkm_wait_tied(r);
+    char* dst = ring + slot * Cfg::SLICE + wave * D * 1024;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const char* src = (r[j] >= 0 && dbase[j] != nullptr) ? dbase[j] + (int64_t)r[j] * dld[j] : zero;
+      dma16(src, dst + j * 1024);
+    }
+  };
+
+  // ---- fragment offsets: lane reads route row grp*8 + L/4 (+4), columns
+  // blk*16 + 4*(L%4); the swizzle sees row bits 0, 1, 3 only -> per-lane constant
+  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+  const int L = lane & 15, grp = lane >> 4;
+  const int trow = grp * 8 + (L >> 2);
+  const int lane_lo = ((L & 1) << 3) + (((L >> 1) & 1) << 4);
+  uint32_t xo[4], go[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    xo[i] = trow * TA::ROWB + lane_lo + (((wm * 8 + 2 * i) ^ TA::swz(trow)) << 4);
+    go[i] = TA::BYTES + trow * TB::ROWB + lane_lo + (((wn * 8 + 2 * i) ^ TB::swz(trow)) << 4);
+  }
+  const uint32_t ring_a = lds_addr(ring);
+  const uint32_t w_a = lds_addr(t_w) + grp * 32;
+
+  f32x4_t acc[4][4];  // acc[i][j]: dY column block i, x column block j (dW^T orientation)
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int s, int slot) {
+    const uint32_t base = ring_a + slot * Cfg::SLICE;
+    lds_u32x2 gf[4][2], xf[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      gf[i][0] = lds_read_tr<0>(base + go[i]);
+      gf[i][1] = lds_read_tr<4 * TB::ROWB>(base + go[i]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xf[j][0] = lds_read_tr<0>(base + xo[j]);
+      xf[j][1] = lds_read_tr<4 * TA::ROWB>(base + xo[j]);
+    }
+    uint4 g4[4];
+    if constexpr (WEIGHTED) {
+      lds_u32x4 w8[2];
+      w8[0] = lds_read128_at<0>(w_a + s * 128);
+      w8[1] = lds_read128_at<16>(w_a + s * 128);
+      lgkm_wait_w(w8);
+      lgkm_wait_frags(gf, xf);
+      float wv[8];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        // element copied to a scalar first: __builtin_bit_cast of a vector
+        // element expression reads element 0 with this compiler
+        const uint32_t lo = w8[0][v], hi = w8[1][v];
+        wv[v] = __uint_as_float(lo);
+        wv[4 + v] = __uint_as_float(hi);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        Chunk16 c;
+        c.u = make_uint4(gf[i][0].x, gf[i][0].y, gf[i][1].x, gf[i][1].y);
+        float v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = to_f32(reinterpret_cast<const OpT*>(&c)[q]) * wv[q];
+        g4[i] = pack_chunk<OpT>(v);
+      }
+    } else {
+      lgkm_wait_frags(gf, xf);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) g4[i] = make_uint4(gf[i][0].x, gf[i][0].y, gf[i][1].x, gf[i][1].y);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 x4 = make_uint4(xf[j][0].x, xf[j][0].y, xf[j][1].x, xf[j][1].y);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) MfmaOp<OpT>::step(acc[i][j], g4[i], x4);
+    }
+  };
+
+  // ---- segments of up to TBL routes: table, then the slice ring
+  for (int64_t seg = lo; seg < hi; seg += TBL) {
+    const int n_rt = (int)((hi - seg) < TBL ? (hi - seg) : TBL);
+    const int n_st = (n_rt + 31) / 32;
+    if (seg != lo) __syncthreads();  // every wave is done with the previous table
+    for (int r = tid; r < n_st * 32; r += 256) {
+      int32_t xr = -1, gr = -1;
+      float w = 0.f;
+      if (r < n_rt) {
+        const int64_t q = seg + r;
+        const int64_t xi = p.x_idx[q];
+        const int64_t graw = p.g_idx[q];
+        const int64_t gi = (graw >= 0 && graw < 0x7fffffffll) ? p.g_fdiv.div(graw) : -1;
+        if (xi >= 0 && xi < p.x_rows && gi >= 0 && gi < p.g_rows) {
+          xr = (int32_t)xi;
+          gr = (int32_t)gi;
+          if constexpr (WEIGHTED) {
+            const int64_t wi = p.w_idx[q];
+            w = (wi >= 0 && wi < p.n_routes) ? round_to(load_as_f32(p.w, p.w_dtype, wi), DTypeOf<OpT>::value) : 0.f;
+          }
+        }
+      }
+      t_x[r] = xr;
+      t_g[r] = gr;
+      if constexpr (WEIGHTED) t_w[r] = w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s0 = 0; s0 < STAGES - 1; ++s0) {
+      if (s0 < n_st) issue(s0, s0);
+      issue_fence();
+    }
+    int cur = 0;
+    for (int s = 0; s < n_st; ++s) {
+      const int ahead = (n_st - 1 - s) < (STAGES - 2) ? (n_st - 1 - s) : (STAGES - 2);
+      vm_wait_slices<D, STAGES - 2>(ahead);  // slice s has landed (this wave's part)
+      wg_barrier();                          // ... every wave's part; slot of s - 1 is free
+      if (s + STAGES - 1 < n_st) {
+        const int refill = cur == 0 ? STAGES - 1 : cur - 1;
+        issue(s + STAGES - 1, refill);
+        issue_fence();
+      }
+      compute(s, cur);
+      cur = cur + 1 == STAGES ? 0 : cur + 1;
+    }
+  }
+  vm_wait<0>();
+
+  // ---- epilogue: lane holds dW[m = m0 + wm*64 + j*16 + L][n = n0 + wn*64 + i*16 + 4*grp + {0..3}]
+  const bool dw_vec = p.dw_sn == 1 && p.dw_dtype == kF32 && p.dw_sm % 4 == 0 && p.dw_se % 4 == 0 &&
+                      (reinterpret_cast<uintptr_t>(p.dw) & 15) == 0;
+  auto store_dw = [&]() {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t m = m0 + wm * 64 + j * 16 + L;
+      if (m >= p.M) continue;
+      const int64_t off = (int64_t)expert * p.dw_se + m * p.dw_sm;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t n = n0 + wn * 64 + i * 16 + 4 * grp;
+        if (n >= p.N) continue;
+        if (dw_vec) {
+          *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.dw) + off + n) =
+              make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (n + v < p.N) store_from_f32(p.dw, p.dw_dtype, off + (n + v) * p.dw_sn, acc[i][j][v]);
+        }
+      }
+    }
+  };
+
+  if (nch == 1) {
+    store_dw();
+    return;
+  }
+
+  // ---- multi-chunk expert: fp32 partial tile in fragment order -> workspace;
+  // the last arriver sums the chunks in chunk order
+  const int64_t slot = sched.slot;
+  if (slot >= p.max_slots) return;  // cannot happen: workspace holds 2R/split + 1 slots
+  auto frag_ptr = [&](int64_t sl) {
+    return reinterpret_cast<float4*>(p.partial) + ((sl * tiles + tile) * 4 + wave) * 16 * 64 + lane;
+  };
+  {
+    float4* d = frag_ptr(slot);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d[(i * 4 + j) * 64] = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+  }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    int32_t* ctr = p.counters + (int64_t)expert * tiles + tile;
+    const int32_t prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    sched.last = (prev == nch - 1);
+    if (sched.last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!sched.last) return;
+  __threadfence();
+  const int64_t base_slot = sched.base_slot;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int32_t c = 0; c < nch; ++c) {
+    const float4* src = frag_ptr(base_slot + c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 v = src[(i * 4 + j) * 64];
+        acc[i][j][0] += v.x;
+        acc[i][j][1] += v.y;
+        acc[i][j][2] += v.z;
+        acc[i][j][3] += v.w;
+      }
+  }
+  store_dw();
+}
+
+template <typename OpT, int BM, int BN, int STAGES>
+hipError_t launch_wgrad_v3_t(const WgradParams& p, hipStream_t stream) {
+  const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  const int64_t grid = p.grid_chunks * tiles;
+  if (grid <= 0) return hipSuccess;
+  if (grid > 0x7fffffffll) return hipErrorInvalidValue;
+  if (p.w != nullptr)
+    hipLaunchKernelGGL((wgrad_v3_kernel<OpT, BM, BN, STAGES, true>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((wgrad_v3_kernel<OpT, BM, BN, STAGES, false>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <typename OpT>
+hipError_t launch_wgrad_v3_op(const WgradParams& p, hipStream_t stream) {
+  int bm, bn;
+  wgrad_tile(p.M, p.N, &bm, &bn);
+  if (bm == 256) return launch_wgrad_v3_t<OpT, 256, 64, 3>(p, stream);
+  if (bm == 64) return launch_wgrad_v3_t<OpT, 64, 256, 3>(p, stream);
+  return launch_wgrad_v3_t<OpT, 128, 128, 4>(p, stream);
+}
+
+}  // namespace cvmm
