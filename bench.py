@@ -267,6 +267,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["fwd", "bwd_w", "bwd_x", "cast_keys", "copy"], default=None,
                     help="launch only this phase --steps times, or the copy calibration (rocprofv3 runs)")
+    ap.add_argument("--tune", action="append", default=[], metavar="KNOB=VALUE",
+                    help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, gemm_order) before running")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -276,6 +278,17 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         sys.exit(1)
+
+    from cvmm_codex_amd import _native as N
+    knobs = {"panel_tiles_per_wg": N.TUNE_PANEL_TILES_PER_WG, "wgrad_order": N.TUNE_WGRAD_ORDER,
+             "gemm_order": N.TUNE_GEMM_ORDER}
+    for kv in args.tune:
+        name, _, value = kv.partition("=")
+        if name not in knobs:
+            ap.error(f"--tune: unknown knob {name!r} (known: {', '.join(sorted(knobs))})")
+        rc = N.lib().cvmm_tuning_set(knobs[name], int(value))
+        if rc != 0:
+            ap.error(f"--tune {kv}: {N.lib().cvmm_last_error().decode()}")
 
     dev = torch.device("cuda:0")
     if args.only == "copy":

@@ -19,6 +19,8 @@ F32, F16, BF16 = 0, 1, 2            # cvmm.py:36-44 dtype ids
 FLAG_ATOMIC_REDUCE = 1
 FLAG_COUNTERS_ZEROED = 2
 TUNE_PANEL_TILES_PER_WG = 1
+TUNE_WGRAD_ORDER = 2
+TUNE_GEMM_ORDER = 3
 
 # kernel classes of the timing hooks (include/cvmm_hip.h CVMM_KC_*)
 KC_SORT, KC_OFFSETS, KC_CAST_KEYS, KC_GEMM_FWD, KC_GEMM_BWDX, KC_WGRAD, KC_COMBINE, KC_FILL = (

@@ -96,6 +96,16 @@ struct TimedLaunch {
   hipEvent_t start, stop;
 };
 std::atomic<int32_t> g_panel_tpw{0};
+std::atomic<int32_t> g_wgrad_order{0};
+std::atomic<int32_t> g_gemm_order{0};
+
+// m-tile order of the routed GEMMs (see GemmParams::token_major): the knob's
+// choice, or -1 to let the kernel launcher decide
+int32_t gemm_token_major(int32_t n_experts) {
+  if (n_experts > kTokenMajorMaxExperts) return 0;
+  const int32_t o = g_gemm_order.load();
+  return o == 2 ? 1 : (o == 1 ? 0 : -1);
+}
 std::mutex g_timing_mu;
 uint32_t g_timing_mask = 0;
 std::vector<TimedLaunch> g_timed;
@@ -189,6 +199,16 @@ int cvmm_tuning_set(int32_t knob, int64_t value) {
   if (knob == CVMM_TUNE_PANEL_TILES_PER_WG) {
     if (value < 0 || value > 4096) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: tiles per workgroup out of range");
     g_panel_tpw.store((int32_t)value);
+    return CVMM_OK;
+  }
+  if (knob == CVMM_TUNE_GEMM_ORDER) {
+    if (value < 0 || value > 2) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: GEMM order must be 0, 1 or 2");
+    g_gemm_order.store((int32_t)value);
+    return CVMM_OK;
+  }
+  if (knob == CVMM_TUNE_WGRAD_ORDER) {
+    if (value < 0 || value > 2) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: weight-gradient order must be 0, 1 or 2");
+    g_wgrad_order.store((int32_t)value);
     return CVMM_OK;
   }
   return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: unknown knob %d", knob);
@@ -341,6 +361,7 @@ int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const
   p.prod_dtype = -1;
   p.w_idx = rp;
   p.panel_tpw = g_panel_tpw.load();
+  p.token_major = gemm_token_major(n_experts);
 
   if (!weighted) {
     p.epi = kEpiStore; p.out = out; p.out_dtype = out_dtype; p.out_ld = out_ld; p.out_rows = out_rows;
@@ -465,6 +486,7 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
   p.prod_dtype = -1;
   p.role = 1;
   p.panel_tpw = g_panel_tpw.load();
+  p.token_major = gemm_token_major(n_experts);
 
   void* route_buf = nullptr;
   const int32_t* inv = nullptr;
@@ -621,6 +643,10 @@ int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, con
   p.M = d_in; p.N = d_out;
   p.offsets = offs; p.n_experts = n_experts; p.n_routes = n_routes;
   p.dw = grad_keys; p.dw_dtype = grad_keys_dtype; p.dw_se = gk_se; p.dw_sm = gk_si; p.dw_sn = gk_sj;
+  // tile-major by default: measured faster on every benchmark shape (the
+  // activation column slice of one tile, shared by the top-k experts of each
+  // token, stays in one XCD's L2)
+  p.tile_major = g_wgrad_order.load() == 1 ? 0 : 1;
   return check_launch(timed(CVMM_KC_WGRAD, s, [&] { return launch_wgrad(p, op_dtype, s); }), "cvmm_bwd_w(gemm)");
 }
 

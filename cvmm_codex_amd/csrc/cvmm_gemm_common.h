@@ -9,6 +9,18 @@ namespace cvmm {
 
 constexpr int kGemmThreads = 256;
 
+// The launcher's tile order for the k-looped kernels (ring, tiled): token
+// major when every gathered A row feeds many routes (the SwitchHead products,
+// 64 routes per token) -- tile j of every expert covers the same token range,
+// so one XCD's workgroups share those rows in L2.  At top-8 fan-out the extra
+// weight traffic (every XCD reads every expert's weights) costs more than it
+// saves, and the small-K kernels, whose weights dominate, lose either way
+// (measured on the benchmark shapes).
+inline int32_t resolve_token_major(const GemmParams& p) {
+  if (p.token_major >= 0) return p.token_major;
+  return (p.n_experts <= kTokenMajorMaxExperts && p.a_rows > 0 && p.n_routes >= 32 * p.a_rows) ? 1 : 0;
+}
+
 template <int BM>
 struct RouteMeta {
   int64_t arow[BM];   // A row of tile row r, -1 if none
@@ -30,7 +42,65 @@ __device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& 
   const int lane = tid & 63;
   const int wave = tid >> 6;
   // ---- schedule: which expert / routes does m-tile `tile` cover? -----------
-  if (wave == 0) {
+  if (wave == 0 && p.token_major > 0) {
+    // Token-major order: all tiles with index j within their expert, in
+    // expert order, then index j + 1.  Routes of an expert are sorted by
+    // token, so tile j of every expert covers about the same token range and
+    // neighbouring workgroups (one XCD) gather the same activation rows.
+    // C(j) = sum_e min(nt_e, j) tiles come before index j; binary search.
+    constexpr int G = kTokenMajorMaxExperts / 64;
+    if (lane == 0) m.expert = -1;
+    int64_t st[G], en[G], nt[G], ntmax = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int32_t e = g * 64 + lane;
+      st[g] = en[g] = nt[g] = 0;
+      if (e < p.n_experts) {
+        int64_t end = p.offsets[e];
+        int64_t start = e > 0 ? p.offsets[e - 1] : 0;
+        end = end < 0 ? 0 : (end > p.n_routes ? p.n_routes : end);
+        start = start < 0 ? 0 : (start > p.n_routes ? p.n_routes : start);
+        if (end < start) end = start;
+        st[g] = start;
+        en[g] = end;
+        nt[g] = (end - start + BM - 1) / BM;
+      }
+      ntmax = nt[g] > ntmax ? nt[g] : ntmax;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      const int64_t v = __shfl_xor(ntmax, o, 64);
+      ntmax = v > ntmax ? v : ntmax;
+    }
+    auto before = [&](int64_t j) {
+      int64_t s = 0;
+#pragma unroll
+      for (int g = 0; g < G; ++g) s += nt[g] < j ? nt[g] : j;
+      return __shfl(wave_incl_scan(s), 63, 64);
+    };
+    if (tile < before(ntmax)) {
+      int64_t lo = 0, hi = ntmax;  // before(lo) <= tile < before(hi)
+      while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (before(mid) <= tile) lo = mid;
+        else hi = mid;
+      }
+      int64_t r = tile - before(lo);  // rank among the experts with more than lo tiles
+      const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const bool has = nt[g] > lo;
+        const uint64_t b = __ballot(has);
+        const int64_t cnt = __popcll(b);
+        if (r >= 0 && r < cnt && has && (int64_t)__popcll(b & lt_mask) == r) {
+          m.expert = g * 64 + lane;
+          const int64_t r0 = st[g] + lo * BM;
+          m.row0 = r0;
+          m.rows = (int32_t)((en[g] - r0) < BM ? (en[g] - r0) : BM);
+        }
+        r -= cnt;
+      }
+    }
+  } else if (wave == 0) {
     if (lane == 0) m.expert = -1;
     int64_t carry = 0;
     for (int32_t base = 0; base < p.n_experts; base += 64) {

@@ -383,7 +383,9 @@ hipError_t launch_routed_gemm_nloop_t(const GemmParams& p, int32_t ng, hipStream
 }
 
 template <typename OpT, int BM, int BN>
-hipError_t launch_routed_gemm_nt_t(const GemmParams& p, hipStream_t stream) {
+hipError_t launch_routed_gemm_nt_t(const GemmParams& p_in, hipStream_t stream) {
+  GemmParams p = p_in;
+  p.token_major = resolve_token_major(p);
   const int64_t n_ntiles = (p.N + BN - 1) / BN;
   const int64_t grid = p.grid_tiles * n_ntiles;
   if (grid <= 0) return hipSuccess;

@@ -252,7 +252,9 @@ inline bool ring_eligible(const GemmParams& p, int32_t op) {
 }
 
 template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA>
-hipError_t launch_routed_gemm_ring_t(const GemmParams& p, hipStream_t stream) {
+hipError_t launch_routed_gemm_ring_t(const GemmParams& p_in, hipStream_t stream) {
+  GemmParams p = p_in;
+  p.token_major = resolve_token_major(p);
   const int64_t m_tiles = (p.n_routes + BM - 1) / BM + (p.n_experts < p.n_routes ? p.n_experts : p.n_routes);
   const int64_t n_ntiles = (p.N + BN - 1) / BN;
   const int64_t grid = m_tiles * n_ntiles;

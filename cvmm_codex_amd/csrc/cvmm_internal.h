@@ -68,7 +68,12 @@ struct GemmParams {
   int32_t role;
   // n-tiles per workgroup of the small-K kernel (0: built-in choice)
   int32_t panel_tpw;
+  // m-tile order: 0 = expert-major (an expert's tiles are consecutive),
+  // 1 = token-major (tile j of every expert, then tile j + 1, ...), -1 = the
+  // launcher's choice; token major needs n_experts <= kTokenMajorMaxExperts
+  int32_t token_major;
 };
+constexpr int32_t kTokenMajorMaxExperts = 256;
 
 // op_dtype selects the MFMA type; returns hipErrorInvalidValue on unsupported combos.
 hipError_t launch_routed_gemm(const GemmParams& p, int32_t op_dtype, hipStream_t stream);
@@ -109,6 +114,7 @@ struct WgradParams {
   float* partial;          // [max_slots][M][N] fp32
   int64_t max_slots;
   int32_t* counters;       // [E][tiles_m*tiles_n], zero on entry
+  int32_t tile_major;      // workgroup order: 0 = chunk-major (a chunk's tiles adjacent), 1 = tile-major
 };
 
 hipError_t launch_wgrad(const WgradParams& p, int32_t op_dtype, hipStream_t stream);

@@ -196,8 +196,11 @@ __global__ __launch_bounds__(256, 2) void wgrad_v3_kernel(const WgradParams p) {
   const int64_t tiles_n = (p.N + BN - 1) / BN;
   const int64_t tiles = ((p.M + BM - 1) / BM) * tiles_n;
   const int64_t id = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t slot_id = id / tiles;
-  const int64_t tile = id % tiles;
+  // chunk-major: the tiles of one route chunk are adjacent (one XCD shares
+  // the chunk's rows); tile-major: one dW tile of every chunk is adjacent
+  // (one XCD shares the x / dY column slice of that tile across experts)
+  const int64_t slot_id = p.tile_major ? id % p.grid_chunks : id / tiles;
+  const int64_t tile = p.tile_major ? id / p.grid_chunks : id % tiles;
   const int64_t m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
 
   if (!wgrad_schedule(p, slot_id, sched)) return;

@@ -75,8 +75,17 @@ int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launche
 /* Tuning knobs (no counterpart in the reference; for tests and tuning
  * sweeps).  Process-wide; value 0 restores the built-in choice.
  *   CVMM_TUNE_PANEL_TILES_PER_WG: n-tiles per workgroup of the small-K
- *     routed GEMM (1..4096). */
+ *     routed GEMM (1..4096).
+ *   CVMM_TUNE_WGRAD_ORDER: workgroup order of the weight-gradient kernel,
+ *     1 = the tiles of one expert chunk on one XCD, 2 = one dW tile of every
+ *     expert on one XCD (the built-in choice).
+ *   CVMM_TUNE_GEMM_ORDER: m-tile order of the routed GEMMs (forward, grad
+ *     input), 1 = expert-major, 2 = token-major (tile j of every expert next
+ *     to each other; up to 256 experts).  Built in: token-major for the
+ *     long-K kernel when every gathered row feeds >= 32 routes. */
 #define CVMM_TUNE_PANEL_TILES_PER_WG 1
+#define CVMM_TUNE_WGRAD_ORDER 2
+#define CVMM_TUNE_GEMM_ORDER 3
 int cvmm_tuning_set(int32_t knob, int64_t value);
 
 /* ------------------------------------------------------------------------ */

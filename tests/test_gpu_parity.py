@@ -307,6 +307,48 @@ def test_weight_grad_is_deterministic():
         assert torch.equal(a[n], b[n]), n
 
 
+@pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True)])
+def test_weight_grad_order_does_not_change_bits(weighted, route_input):
+    """Both workgroup orders of the weight-gradient kernel compute every tile
+    and sum split chunks the same way: identical bits, hot expert included."""
+    from cvmm_codex_amd import _native as N
+    x, keys, sel, w, go = _rand_case(31, 4, 512, 128, 96, 8, 4, weighted, route_input, skew=0.7)
+    lib = N.lib()
+    try:
+        assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, 1) == 0
+        a = U.run_hip(x, keys, sel, w, go, route_input, True)
+        assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, 2) == 0
+        b = U.run_hip(x, keys, sel, w, go, route_input, True)
+    finally:
+        lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, 0)
+    assert torch.equal(a["keys_grad"], b["keys_grad"])
+    exp = U.run_oracle(x, keys, sel, w, go, route_input, True)
+    U.compare(b, exp, 2e-2)
+
+
+@pytest.mark.parametrize("weighted,route_input,skew", [(False, False, None), (True, True, 0.7), (True, False, 0.0)])
+def test_gemm_order_does_not_change_bits(weighted, route_input, skew):
+    """Expert-major and token-major m-tile orders of the routed GEMMs compute
+    every tile the same way: identical bits for every output."""
+    from cvmm_codex_amd import _native as N
+    x, keys, sel, w, go = _rand_case(33, 4, 512, 256, 192, 24, 6, weighted, route_input, skew=skew)
+    lib = N.lib()
+    try:
+        assert lib.cvmm_tuning_set(N.TUNE_GEMM_ORDER, 1) == 0
+        a = U.run_hip(x, keys, sel, w, go, route_input, True)
+        assert lib.cvmm_tuning_set(N.TUNE_GEMM_ORDER, 2) == 0
+        b = U.run_hip(x, keys, sel, w, go, route_input, True)
+    finally:
+        lib.cvmm_tuning_set(N.TUNE_GEMM_ORDER, 0)
+    for n in ("out", "x_grad", "keys_grad", "weights_grad"):
+        if a[n] is None:
+            assert b[n] is None
+        else:
+            assert torch.equal(a[n], b[n]), n
+    exp = U.run_oracle(x, keys, sel, w, go, route_input, True)
+    U.compare(b, exp, 2e-2)
+
+
 @pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True), (True, False)])
 def test_route_positions_from_sort_or_computed(weighted, route_input):
     """The route-ordered rows are gathered per token through the sort's
