@@ -4,20 +4,30 @@
 // (cvmm.py:24-27, cvmm.py:1796-1803) and the offsets binary search
 // (cvmm_expert_offsets_kernel, cvmm.py:315-335).
 //
-// Three launches over chunks of kSortChunk routes:
-//   1. histogram   counts[bucket][chunk]      (LDS atomics, bucket E = invalid id)
-//   2. scan        exclusive prefix over the bucket-major counts, and the
-//                  inclusive per-expert offsets the GEMM schedulers read
-//   3. scatter     each chunk walks its routes in index order; a route's rank
-//                  among equal keys of its wave comes from ballots over the key
-//                  bits, waves of a workgroup take turns, so the order is
-//                  stable (equal experts keep route order).
+// Two launches over chunks of routes:
+//   1. histogram   counts[chunk][bucket]      (LDS atomics, bucket E = invalid id)
+//   2. scatter     every workgroup first derives its own output positions from
+//                  the histogram rows: bucket totals over all chunks, their
+//                  exclusive scan (the bucket bases), plus this bucket's counts
+//                  in earlier chunks; workgroup 0 also writes the inclusive
+//                  per-expert offsets the GEMM schedulers read.  Then the chunk
+//                  walks its routes in index order; a route's rank among equal
+//                  keys of its wave comes from ballots over the key bits, waves
+//                  of a workgroup take turns, so the order is stable (equal
+//                  experts keep route order).
+// The chunk size keeps (E + 1) * n_chunks, the counts each workgroup reads,
+// at most 64K.
 #include "cvmm_common.h"
 #include "cvmm_internal.h"
 
 namespace cvmm {
 
 constexpr int kSortThreads = 256;
+constexpr int32_t kSortFastBuckets = 8192;  // buckets whose totals fit beside the positions in LDS
+// >= 4 rounds of 256 routes per workgroup: fewer chunks keep the count matrix
+// every scatter workgroup reads small (measured: ff_up 19.5 us with 256-route
+// chunks, 17.6 us with 1024)
+constexpr int64_t kSortMinChunk = 1024;
 
 template <typename IdxT>
 __device__ __forceinline__ int32_t bucket_of(IdxT raw, int32_t n_experts) {
@@ -39,44 +49,28 @@ __global__ __launch_bounds__(kSortThreads) void sort_hist_kernel(
     atomicAdd(&hist[bucket_of(sel[i], n_experts)], 1);
   }
   __syncthreads();
-  for (int e = threadIdx.x; e <= n_experts; e += kSortThreads) counts[(int64_t)e * n_chunks + b] = hist[e];
+  for (int e = threadIdx.x; e <= n_experts; e += kSortThreads) counts[b * (int64_t)(n_experts + 1) + e] = hist[e];
 }
 
-// Single workgroup: exclusive scan of `total` = (E+1)*n_chunks counts in place.
-// offsets[e] = #routes whose bucket <= e (the reference's inclusive cumsum).
-constexpr int kScanThreads = 1024;
-__global__ __launch_bounds__(kScanThreads) void sort_scan_kernel(
-    int32_t* __restrict__ counts, int64_t n_chunks, int32_t n_experts, int64_t* __restrict__ offsets,
-    int32_t* __restrict__ n_invalid, int64_t n_routes) {
-  __shared__ int64_t part[kScanThreads];
-  const int64_t total = (int64_t)(n_experts + 1) * n_chunks;
-  const int64_t per = (total + kScanThreads - 1) / kScanThreads;
-  const int64_t lo = min((int64_t)threadIdx.x * per, total);
-  const int64_t hi = min(lo + per, total);
-  int64_t s = 0;
-  for (int64_t j = lo; j < hi; ++j) s += counts[j];
-  part[threadIdx.x] = s;
+// Exclusive scan, in place, of the n values a[0, n) in LDS (whole workgroup).
+__device__ void block_exclusive_scan(int32_t* a, int32_t n) {
+  __shared__ int64_t wave_total[kSortThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t seg = (n + kSortThreads - 1) / kSortThreads;
+  const int32_t lo = min(tid * seg, n), hi = min(lo + seg, n);
+  int64_t sum = 0;
+  for (int32_t i = lo; i < hi; ++i) sum += a[i];
+  const int64_t incl = wave_incl_scan(sum);
+  if (lane == 63) wave_total[wave] = incl;
   __syncthreads();
-  // Hillis-Steele inclusive scan over the 1024 partial sums.
-  for (int d = 1; d < kScanThreads; d <<= 1) {
-    int64_t v = threadIdx.x >= d ? part[threadIdx.x - d] : 0;
-    __syncthreads();
-    part[threadIdx.x] += v;
-    __syncthreads();
+  int64_t run = incl - sum;
+  for (int w = 0; w < wave; ++w) run += wave_total[w];
+  for (int32_t i = lo; i < hi; ++i) {
+    const int32_t v = a[i];
+    a[i] = (int32_t)run;
+    run += v;
   }
-  int64_t run = part[threadIdx.x] - s;  // exclusive prefix of this segment
-  for (int64_t j = lo; j < hi; ++j) {
-    const int32_t c = counts[j];
-    // bucket boundary: j == (e+1)*n_chunks marks the end of expert e
-    if (j % n_chunks == 0 && j > 0) {
-      const int64_t e = j / n_chunks - 1;
-      if (e < n_experts) offsets[e] = run;
-      // the invalid bucket E starts after expert E-1: everything past it is invalid
-      if (e == n_experts - 1 && n_invalid != nullptr) *n_invalid = (int32_t)(n_routes - run);
-    }
-    counts[j] = (int32_t)run;
-    run += c;
-  }
+  __syncthreads();
 }
 
 // Stable scatter of one chunk: within every 256-route round, lanes with equal
@@ -125,12 +119,67 @@ __device__ void scatter_chunk(const IdxT* __restrict__ sel, int64_t n_routes, in
 template <typename IdxT>
 __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     const IdxT* __restrict__ sel, int64_t n_routes, int32_t n_experts, int64_t chunk,
-    int64_t n_chunks, const int32_t* __restrict__ bases, int32_t n_bits, int64_t top_k,
+    int64_t n_chunks, const int32_t* __restrict__ counts, int32_t n_bits, int64_t top_k,
     int32_t* __restrict__ sorted_sel, int64_t* __restrict__ perm, int64_t* __restrict__ token_index,
-    int32_t* __restrict__ route_pos) {
-  extern __shared__ int32_t pos[];  // n_experts + 1 running output positions
+    int32_t* __restrict__ route_pos, int64_t* __restrict__ offsets, int32_t* __restrict__ n_invalid) {
+  extern __shared__ int32_t sh[];  // pos[n_experts + 1] (+ tot[n_experts + 1] on the fast path)
+  int32_t* pos = sh;                 // running output positions of this chunk
   const int64_t b = blockIdx.x;
-  for (int e = threadIdx.x; e <= n_experts; e += kSortThreads) pos[e] = bases[(int64_t)e * n_chunks + b];
+  const int32_t nb = n_experts + 1;
+  if (nb <= kSortFastBuckets) {
+    // All threads stride over the whole count matrix (loads batched 16 deep);
+    // consecutive elements belong to distinct buckets, so the LDS adds of one
+    // wave instruction do not collide.
+    int32_t* tot = sh + nb;
+    for (int32_t e = threadIdx.x; e < nb; e += kSortThreads) pos[e] = tot[e] = 0;
+    __syncthreads();
+    const int32_t n = (int32_t)(n_chunks * nb);
+    constexpr int U = 16;
+    for (int32_t i0 = threadIdx.x; i0 < n; i0 += U * kSortThreads) {
+      int32_t v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int32_t i = i0 + u * kSortThreads;
+        v[u] = i < n ? counts[i] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int32_t i = i0 + u * kSortThreads;
+        if (i < n) {
+          const int32_t c = i / nb, e = i - c * nb;
+          atomicAdd(&tot[e], v[u]);
+          if (c < b) atomicAdd(&pos[e], v[u]);
+        }
+      }
+    }
+    __syncthreads();
+    if (b == 0 && threadIdx.x == 0 && n_invalid != nullptr) *n_invalid = tot[n_experts];
+    block_exclusive_scan(tot, nb);  // tot[e] = first output position of bucket e
+    if (b == 0) {
+      // inclusive offsets (the reference's cumsum)
+      for (int32_t e = threadIdx.x; e < n_experts; e += kSortThreads) offsets[e] = tot[e + 1];
+    }
+    for (int32_t e = threadIdx.x; e < nb; e += kSortThreads) pos[e] += tot[e];
+  } else {
+    // many buckets: per-bucket column sums, then the earlier chunks again
+    for (int32_t e = threadIdx.x; e < nb; e += kSortThreads) {
+      int32_t t = 0;
+      for (int64_t c = 0; c < n_chunks; ++c) t += counts[c * nb + e];
+      pos[e] = t;
+    }
+    __syncthreads();
+    if (b == 0 && threadIdx.x == 0 && n_invalid != nullptr) *n_invalid = pos[n_experts];
+    block_exclusive_scan(pos, nb);
+    if (b == 0) {
+      for (int32_t e = threadIdx.x; e < n_experts; e += kSortThreads) offsets[e] = pos[e + 1];
+    }
+    __syncthreads();  // the offsets above read pos before it is moved to this chunk
+    for (int32_t e = threadIdx.x; e < nb; e += kSortThreads) {
+      int32_t pre = 0;
+      for (int64_t c = 0; c < b; ++c) pre += counts[c * nb + e];
+      pos[e] += pre;
+    }
+  }
   __syncthreads();
   scatter_chunk(sel, n_routes, n_experts, chunk, n_bits, top_k, pos, sorted_sel, perm, token_index, route_pos);
 }
@@ -154,17 +203,15 @@ __global__ void expert_offsets_kernel(const int32_t* __restrict__ sorted_sel, in
 // host side
 // ---------------------------------------------------------------------------
 
-int64_t sort_chunk_size(int64_t n_routes) {
-  // ~256 workgroups at large R, at least 4 rounds of 256 routes per chunk.
-  int64_t c = (n_routes + 255) / 256;
-  c = (c + kSortThreads - 1) / kSortThreads * kSortThreads;
-  if (c < 1024) c = 1024;
-  if (c > 16384) c = 16384;
-  return c;
+int64_t sort_chunk_size(int64_t n_routes, int32_t n_experts) {
+  // >= kSortMinChunk routes; (E + 1) * n_chunks <= 64K
+  int64_t c = (n_routes * (int64_t)(n_experts + 1) + 65535) / 65536;
+  if (c < kSortMinChunk) c = kSortMinChunk;
+  return (c + kSortThreads - 1) / kSortThreads * kSortThreads;
 }
 
 size_t sort_workspace_bytes(int64_t n_routes, int32_t n_experts) {
-  const int64_t chunk = sort_chunk_size(n_routes);
+  const int64_t chunk = sort_chunk_size(n_routes, n_experts);
   const int64_t n_chunks = n_routes > 0 ? (n_routes + chunk - 1) / chunk : 1;
   size_t counts = (size_t)(n_experts + 1) * n_chunks * sizeof(int32_t);
   return align_up(counts, 256) + 256;  // + n_invalid counter
@@ -174,12 +221,11 @@ hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_rout
                               int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
                               int64_t* offsets, int32_t* route_pos, int32_t* n_invalid_out, void* ws,
                               hipStream_t stream) {
-  const int64_t chunk = sort_chunk_size(n_routes);
+  const int64_t chunk = sort_chunk_size(n_routes, n_experts);
   const int64_t n_chunks = (n_routes + chunk - 1) / chunk;
   int32_t* counts = (int32_t*)ws;
-  int32_t* n_invalid = n_invalid_out ? n_invalid_out
-                                     : (int32_t*)((char*)ws + align_up((size_t)(n_experts + 1) * n_chunks * 4, 256));
   const size_t lds = (size_t)(n_experts + 1) * sizeof(int32_t);
+  const size_t lds_scatter = (n_experts + 1 <= kSortFastBuckets ? 2 : 1) * lds;
   int n_bits = 0;
   while ((1ll << n_bits) <= (int64_t)n_experts) ++n_bits;  // buckets 0..E
   if (sel_is_int64) {
@@ -189,16 +235,14 @@ hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_rout
     hipLaunchKernelGGL(sort_hist_kernel<int32_t>, dim3(n_chunks), dim3(kSortThreads), lds, stream,
                        (const int32_t*)sel, n_routes, n_experts, chunk, n_chunks, counts);
   }
-  hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, counts, n_chunks, n_experts,
-                     offsets, n_invalid, n_routes);
   if (sel_is_int64) {
-    hipLaunchKernelGGL(sort_scatter_kernel<int64_t>, dim3(n_chunks), dim3(kSortThreads), lds, stream,
+    hipLaunchKernelGGL(sort_scatter_kernel<int64_t>, dim3(n_chunks), dim3(kSortThreads), lds_scatter, stream,
                        (const int64_t*)sel, n_routes, n_experts, chunk, n_chunks, counts, n_bits, top_k,
-                       sorted_sel, perm, token_index, route_pos);
+                       sorted_sel, perm, token_index, route_pos, offsets, n_invalid_out);
   } else {
-    hipLaunchKernelGGL(sort_scatter_kernel<int32_t>, dim3(n_chunks), dim3(kSortThreads), lds, stream,
+    hipLaunchKernelGGL(sort_scatter_kernel<int32_t>, dim3(n_chunks), dim3(kSortThreads), lds_scatter, stream,
                        (const int32_t*)sel, n_routes, n_experts, chunk, n_chunks, counts, n_bits, top_k,
-                       sorted_sel, perm, token_index, route_pos);
+                       sorted_sel, perm, token_index, route_pos, offsets, n_invalid_out);
   }
   return hipGetLastError();
 }
