@@ -1,41 +1,45 @@
-// Routed GEMM with a deep DMA ring for a long inner dimension (K > 128,
-// 16-bit k-contiguous operands): the ff_up forward (K = d_in = 1024, N = 128),
-// the ff_down input gradient (K = 1024, N = 128) and the SwitchHead V forward
-// / O input gradient (K = 2048, N = 64).
+// Routed GEMM with a DMA ring for a long inner dimension (K > 128, 16-bit
+// k-contiguous operands): the ff_up forward (K = d_in = 1024, N = 128), the
+// ff_down input gradient (K = 1024, N = 128) and the SwitchHead V forward /
+// O input gradient (K = 2048, N = 64).
 //
-// A tile-per-workgroup GEMM with two LDS stages keeps one 32 KB stage in
-// flight while it computes on the other; with a DMA latency of about a
-// microsecond and a stage's MFMA work of a tenth of that, the workgroup waits
-// most of the time.  Here the k loop streams BK = 32 slices (16-20 KB each)
-// through a ring of STAGES LDS buffers, STAGES - 1 of them in flight:
+// The k loop streams slices (BK = 64 or 32 values of k for every A row and B
+// row of the tile) through a ring of STAGES LDS buffers, STAGES - 1 of them
+// in flight:
 //  * wait for the next slice with a constant vmcnt: only DMA is in flight in
 //    the loop, D instructions per slice and lane, retiring in order;
 //  * one barrier, then the buffer every wave has finished reading is refilled;
 //  * MFMA with operands swapped (C^T = W x A^T) so that a lane ends with 4
 //    consecutive output columns of one row; two lane swaps make that 8
 //    columns, stored as one 16-byte write.
-// With read-ahead (RA) the fragments of slice s + 1 are read into a second
-// register set while the MFMAs of slice s run; that needs ~200 VGPRs, so it is
-// used where two workgroups per CU are the limit anyway (256 x 64 tiles).
+// Gathered A rows are read in 128-byte pieces with BK = 64 (whole L2 lines:
+// a probe of gathered 64-byte pieces from a 16 MiB activation measured 5.2
+// TB/s against 10.3 TB/s for 128-byte pieces).
+// With read-ahead (RA, BK = 32) the fragments of slice s + 1 are read into a
+// second register set while the MFMAs of slice s run; that needs ~200 VGPRs,
+// so it is used where two workgroups per CU are the limit anyway (256 x 64).
 // Slices past K are loaded from the zero page, so every iteration issues the
 // same DMA count and the waits are the same constant.
 //
-// LDS rows are 64 bytes (BK = 32 16-bit values, four 16-byte chunks).  The
-// MFMA fragment reads (lane l: row l % 16, chunk l / 16) are free of bank
-// conflicts when the chunk of row r is stored at chunk ^ ((r >> 1) & 3): an
-// inline-asm ds_read_b128 probe on gfx950 measured SQ_LDS_BANK_CONFLICT = 0
-// for that swizzle and 16.8 M conflict cycles (the same as no swizzle) for
-// chunk ^ (r & 3), chunk ^ ((r >> 2) & 3) and two other XOR mixes.
+// LDS rows are 64 or 128 bytes.  The MFMA fragment reads (lane l: row l % 16,
+// chunk l / 16) are free of bank conflicts with chunk ^ ((r >> 1) & 3) for
+// 64-byte rows and chunk ^ (r & 7) for 128-byte rows: an inline-asm
+// ds_read_b128 probe on gfx950 measured SQ_LDS_BANK_CONFLICT = 0 for both,
+// and 16.8 M conflict cycles for 64-byte rows with chunk ^ (r & 3),
+// chunk ^ ((r >> 2) & 3) or no swizzle.
 #pragma once
 
 #include "cvmm_gemm_panel.h"
 
 namespace cvmm {
 
-template <int BM, int BN, int STAGES>
+template <int BM, int BN, int STAGES, int BK_>
 struct RingCfg {
-  static constexpr int BK = 32;                        // 16-bit values per k slice
-  static constexpr int ROWB = 64;                      // bytes per LDS row
+  static constexpr int BK = BK_;                       // 16-bit values per k slice
+  static constexpr int ROWB = BK * 2;                  // bytes per LDS row
+  static constexpr int CPR = ROWB / 16;                // 16-byte chunks per row
+  static constexpr int KSS = BK / 32;                  // MFMA k steps per slice
+  static_assert(BK == 32 || BK == 64, "64- or 128-byte rows");
   static constexpr int A_BYTES = BM * ROWB;
   static constexpr int B_BYTES = BN * ROWB;
   static constexpr int SLICE_BYTES = A_BYTES + B_BYTES;
@@ -44,15 +48,21 @@ struct RingCfg {
   static constexpr int WN = BN / 64, WM = BM / 64;     // wave grid, 64 x 64 per wave
   static_assert(WM * WN == 4, "4 waves of 64x64");
   static_assert(SLICE_BYTES % 4096 == 0, "whole DMA instructions per wave");
-  static_assert(STAGES >= 3 && STAGES <= 5, "ring depth");
+  static_assert(STAGES >= 2 && STAGES <= 5, "ring depth");
   static_assert((STAGES - 2) * D < 64, "vmcnt range");
 };
 
-__device__ __forceinline__ int ring_swz(int row) { return (row >> 1) & 3; }
+// 64-byte rows: chunk ^ ((r >> 1) & 3); 128-byte rows: chunk ^ (r & 7).
+template <int CPR>
+__device__ __forceinline__ int ring_swz(int row) {
+  if constexpr (CPR == 4) return (row >> 1) & 3;
+  else return row & 7;
+}
 
-template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int Role>
+template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int Role, int BK>
 __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(const GemmParams p) {
-  using Cfg = RingCfg<BM, BN, STAGES>;
+  using Cfg = RingCfg<BM, BN, STAGES, BK>;
+  static_assert(!RA || Cfg::KSS == 1, "read-ahead keeps one k step per slice");
   __shared__ __attribute__((aligned(1024))) char ring[STAGES * Cfg::SLICE_BYTES];
   __shared__ RouteMeta<BM> meta;
 
@@ -76,8 +86,8 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
 #pragma unroll
   for (int j = 0; j < Cfg::D; ++j) {
     const int q = (wave * Cfg::D + j) * 64 + lane;  // 16-byte chunk index within the slice
-    const int row = q >> 2;
-    const int c = (q & 3) ^ ring_swz(row);
+    const int row = q / Cfg::CPR;
+    const int c = (q % Cfg::CPR) ^ ring_swz<Cfg::CPR>(row);
     kc[j] = c * 8;
     if (row < BM) {
       const int64_t ar = meta.arow[row];
@@ -100,24 +110,26 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   // ---- fragments: lane reads row (l % 16) of each 16-row block, chunk l / 16
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   const int fr = lane & 15, fq = lane >> 4;
-  int a_off[4], b_off[4];
+  int a_off[Cfg::KSS][4], b_off[Cfg::KSS][4];  // per k step of a slice
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ra = wm * 64 + i * 16 + fr;
-    const int rb = BM + wn * 64 + i * 16 + fr;
-    a_off[i] = ra * Cfg::ROWB + ((fq ^ ring_swz(ra)) << 4);
-    b_off[i] = rb * Cfg::ROWB + ((fq ^ ring_swz(rb)) << 4);
-  }
+  for (int kk = 0; kk < Cfg::KSS; ++kk)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ra = wm * 64 + i * 16 + fr;
+      const int rb = BM + wn * 64 + i * 16 + fr;
+      a_off[kk][i] = ra * Cfg::ROWB + (((kk * 4 + fq) ^ ring_swz<Cfg::CPR>(ra)) << 4);
+      b_off[kk][i] = rb * Cfg::ROWB + (((kk * 4 + fq) ^ ring_swz<Cfg::CPR>(rb)) << 4);
+    }
   f32x4_t acc[4][4];  // acc[i][j]: n-block i, m-block j (C^T orientation)
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  auto read_frags = [&](const char* buf, lds_u32x4 (&af)[4], lds_u32x4 (&bf)[4]) {
+  auto read_frags = [&](const char* buf, lds_u32x4 (&af)[4], lds_u32x4 (&bf)[4], int kk = 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) bf[i] = lds_read128(buf + b_off[i]);
+    for (int i = 0; i < 4; ++i) bf[i] = lds_read128(buf + b_off[kk][i]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) af[j] = lds_read128(buf + a_off[j]);
+    for (int j = 0; j < 4; ++j) af[j] = lds_read128(buf + a_off[kk][j]);
   };
   auto mfma = [&](lds_u32x4 (&af)[4], lds_u32x4 (&bf)[4]) {
 #pragma unroll
@@ -173,10 +185,13 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
       wg_barrier();
       issue(s + STAGES - 1, ring + refill * Cfg::SLICE_BYTES);
       issue_fence();
-      lds_u32x4 af[4], bf[4];
-      read_frags(ring + cur * Cfg::SLICE_BYTES, af, bf);
-      lds_wait_tied(bf, af);
-      mfma(af, bf);
+#pragma unroll
+      for (int kk = 0; kk < Cfg::KSS; ++kk) {
+        lds_u32x4 af[4], bf[4];
+        read_frags(ring + cur * Cfg::SLICE_BYTES, af, bf, kk);
+        lds_wait_tied(bf, af);
+        mfma(af, bf);
+      }
       cur = cur + 1 == STAGES ? 0 : cur + 1;
       refill = refill + 1 == STAGES ? 0 : refill + 1;
     }
@@ -188,24 +203,34 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   // ---- epilogue from registers: lane holds C[m = wm*64 + j*16 + fr]
   // [n = n0 + wn*64 + i*16 + 4*fq + {0..3}]
   const bool has_w = p.w != nullptr;
+  // plain: the value is the product rounded once to the output type, which
+  // the conversion at the store does by itself
+  const bool plain = !has_w && p.val_dtype == DTypeOf<OutT>::value;
   const int64_t nwave = n0 + wn * 64;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int m = wm * 64 + j * 16 + fr;
     const int64_t orow = meta.orow[m];
-    const float wv = meta.w[m];
     float v[4][4];
+    if (plain) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float c = round_to(acc[i][j][q], p.val_dtype);
-        if (has_w) {
-          c = c * wv;
-          if (p.prod_dtype >= 0) c = round_to(c, p.prod_dtype);
+        for (int q = 0; q < 4; ++q) v[i][q] = acc[i][j][q];
+    } else {
+      const float wv = meta.w[m];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float c = round_to(acc[i][j][q], p.val_dtype);
+          if (has_w) {
+            c = c * wv;
+            if (p.prod_dtype >= 0) c = round_to(c, p.prod_dtype);
+          }
+          v[i][q] = c;
         }
-        v[i][q] = c;
-      }
+    }
     char* rowp = orow >= 0 ? reinterpret_cast<char*>(p.out) + orow * p.out_ld * (int64_t)sizeof(OutT) : nullptr;
     if constexpr (sizeof(OutT) == 4) {
 #pragma unroll
@@ -251,7 +276,7 @@ inline bool ring_eligible(const GemmParams& p, int32_t op) {
          (reinterpret_cast<uintptr_t>(p.out) % 16) == 0 && ((size_t)p.out_ld * esz) % 16 == 0;
 }
 
-template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA>
+template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int BK>
 hipError_t launch_routed_gemm_ring_t(const GemmParams& p_in, hipStream_t stream) {
   GemmParams p = p_in;
   p.token_major = resolve_token_major(p);
@@ -261,21 +286,24 @@ hipError_t launch_routed_gemm_ring_t(const GemmParams& p_in, hipStream_t stream)
   if (grid <= 0) return hipSuccess;
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
   if (p.role == 0)
-    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 0>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 0, BK>), dim3((unsigned)grid),
                        dim3(kGemmThreads), 0, stream, p);
   else
-    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1, BK>), dim3((unsigned)grid),
                        dim3(kGemmThreads), 0, stream, p);
   return hipGetLastError();
 }
 
-// 128 x 128 tiles: 3 slices of 16 KB + route metadata = 53 KB of LDS, three
-// workgroups per CU (768 resident tiles: the whole ff_up forward at once);
-// 256 x 64 tiles: 3 slices of 20 KB + 9 KB = 69 KB, two per CU.
+// 128 x 128 tiles: two 32 KB slices of 64 k (128-byte rows: each gathered A
+// row is read in whole 128-byte lines) + route metadata = 69 KB of LDS, two
+// workgroups per CU.  Measured on the ff_up forward shape with the
+// benchmark's spread of expert loads: 35.9 us, against 45.7 us for three
+// 16 KB slices of 32 k at three workgroups per CU.
+// 256 x 64 tiles: 3 slices of 20 KB + 9 KB = 69 KB, two per CU, read-ahead.
 template <typename OpT, typename OutT>
 hipError_t launch_routed_gemm_ring_out(const GemmParams& p, hipStream_t stream) {
-  if (p.N <= 64) return launch_routed_gemm_ring_t<OpT, OutT, 256, 64, 3, 2, true>(p, stream);
-  return launch_routed_gemm_ring_t<OpT, OutT, 128, 128, 3, 3, false>(p, stream);
+  if (p.N <= 64) return launch_routed_gemm_ring_t<OpT, OutT, 256, 64, 3, 2, true, 32>(p, stream);
+  return launch_routed_gemm_ring_t<OpT, OutT, 128, 128, 2, 2, false, 64>(p, stream);
 }
 
 // Fast-path dispatch for 16-bit k-contiguous operands: small K -> panel
