@@ -70,22 +70,27 @@ __device__ __forceinline__ void lds_wait_tied(lds_u32x4 (&x)[4], lds_u32x4 (&y)[
 
 __device__ __forceinline__ uint4 as_uint4(lds_u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); }
 
-template <int KP, int BN>
+// WM waves along the m-tile (64 rows each), 4 / WM along the n-tile: 128-row
+// tiles (2 x 2 waves, three workgroups per CU) or 256-row tiles (4 x 1,
+// two per CU, half the weight reads per output row).
+template <int KP, int BN, int WM_>
 struct PanelCfg {
-  static constexpr int BM = 128;
+  static constexpr int WM = WM_, WN = 4 / WM_;
+  static constexpr int BM = 64 * WM;
   static constexpr int CPR = KP / 8;                  // 16-byte chunks per weight row
   static constexpr int TILE_BYTES = BN * KP * 2;      // one weight tile in LDS
   static constexpr int D = TILE_BYTES / (4 * 1024);   // DMA instructions per wave per tile
-  static constexpr int NI = BN / 32;                  // 16-column blocks per wave (wave: 64 x BN/2)
+  static constexpr int NI = BN / (16 * WN);           // 16-column blocks per wave (wave: 64 x BN/WN)
   static constexpr int KS = KP / 32;                  // MFMA k steps
-  static constexpr int OCC = 3;                       // workgroups per CU (LDS: 3 x 52.8 KB)
+  static constexpr int OCC = WM == 2 ? 3 : 2;         // workgroups per CU (LDS 52.8 / 57.5 KB)
   static_assert(CPR >= 8, "swizzle needs >= 8 chunks per row");
+  static_assert(WM == 2 || WM == 4, "128- or 256-row tiles");
 };
 
-template <typename OpT, typename OutT, int KP, int BN, int Role>
-__global__ __launch_bounds__(kGemmThreads, (PanelCfg<KP, BN>::OCC)) void routed_gemm_panel_kernel(const GemmParams p,
-                                                                                              int32_t tpw) {
-  using Cfg = PanelCfg<KP, BN>;
+template <typename OpT, typename OutT, int KP, int BN, int Role, int WM>
+__global__ __launch_bounds__(kGemmThreads, (PanelCfg<KP, BN, WM>::OCC)) void routed_gemm_panel_kernel(
+    const GemmParams p, int32_t tpw) {
+  using Cfg = PanelCfg<KP, BN, WM>;
   // store instructions per lane per tile: one per 16-byte piece
   constexpr int S = sizeof(OutT) == 4 ? 4 * Cfg::NI : 2 * Cfg::NI;
   static_assert(2 * S + Cfg::D < 64, "vmcnt range");
@@ -107,7 +112,7 @@ __global__ __launch_bounds__(kGemmThreads, (PanelCfg<KP, BN>::OCC)) void routed_
   if (!gemm_schedule<Cfg::BM>(p, tile, meta)) return;
   const int32_t expert = meta.expert;
 
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   const int fr = lane & 15, fq = lane >> 4;
   const char* zero = reinterpret_cast<const char*>(g_cvmm_zero_page);
 
@@ -161,7 +166,7 @@ __global__ __launch_bounds__(kGemmThreads, (PanelCfg<KP, BN>::OCC)) void routed_
       uint4 bf[Cfg::NI];
 #pragma unroll
       for (int i = 0; i < Cfg::NI; ++i) {
-        const int n = wn * (BN / 2) + i * 16 + fr;
+        const int n = wn * (BN / Cfg::WN) + i * 16 + fr;
         const int c = ks * 4 + fq;
         bf[i] = *reinterpret_cast<const uint4*>(buf + n * (Cfg::CPR * 16) + ((c ^ lds_swz(n)) << 4));
       }
@@ -171,7 +176,7 @@ __global__ __launch_bounds__(kGemmThreads, (PanelCfg<KP, BN>::OCC)) void routed_
         for (int j = 0; j < 4; ++j) MfmaOp<OpT>::step(acc[i][j], bf[i], af[j][ks]);
     }
     // lane holds C[m = wm*64 + j*16 + fr][n = nwave + i*16 + 4*fq + {0..3}]
-    const int64_t nwave = (nt0 + t) * BN + wn * (BN / 2);
+    const int64_t nwave = (nt0 + t) * BN + wn * (BN / Cfg::WN);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if constexpr (sizeof(OutT) == 4) {
@@ -273,45 +278,61 @@ inline bool panel_eligible(const GemmParams& p, int32_t op) {
 }
 
 // n-tiles per workgroup: enough workgroups for about 1.5 per slot
-// (3 per CU x 256 CUs), n-tiles split evenly over the groups of an m-tile.
-// Measured (n-tiles per workgroup 2/4/6/8/16): ff_up grad-input 70.9 / 52.6 /
-// 50.6 / 47.6 / 49.2 us, ff_down forward 70.7 / 52.1 / 51.4 / 46.7 / 48.7 us;
-// the SwitchHead shapes (4352 m-tiles) are best with all n-tiles in one group.
-inline int32_t panel_tiles_per_wg(int64_t m_tiles, int64_t n_ntiles) {
-  const int64_t slots = 3 * 256;
+// (occ per CU x 256 CUs), n-tiles split evenly over the groups of an m-tile.
+// Measured with 128-row tiles (n-tiles per workgroup 2/4/6/8/16): ff_up
+// grad-input 70.9 / 52.6 / 50.6 / 47.6 / 49.2 us, ff_down forward 70.7 / 52.1
+// / 51.4 / 46.7 / 48.7 us; the SwitchHead shapes (4352 m-tiles) are best with
+// all n-tiles in one group.
+inline int32_t panel_tiles_per_wg(int64_t m_tiles, int64_t n_ntiles, int occ) {
+  const int64_t slots = occ * 256;
   int64_t groups = (3 * slots / 2 + m_tiles - 1) / (m_tiles > 0 ? m_tiles : 1);
   if (groups < 1) groups = 1;
   if (groups > n_ntiles) groups = n_ntiles;
   return (int32_t)((n_ntiles + groups - 1) / groups);
 }
 
-template <typename OpT, typename OutT, int KP, int BN>
+template <typename OpT, typename OutT, int KP, int BN, int WM>
 hipError_t launch_routed_gemm_panel_t(const GemmParams& p, hipStream_t stream) {
-  // m-tile slots for 128-row tiles: every expert's last tile may be partial
-  const int64_t m_tiles = (p.n_routes + 127) / 128 + (p.n_experts < p.n_routes ? p.n_experts : p.n_routes);
+  using Cfg = PanelCfg<KP, BN, WM>;
+  // m-tile slots: every expert's last tile may be partial
+  const int64_t m_tiles = (p.n_routes + Cfg::BM - 1) / Cfg::BM + (p.n_experts < p.n_routes ? p.n_experts : p.n_routes);
   const int64_t n_ntiles = p.N / BN;
   const int32_t tpw = p.panel_tpw > 0 ? (int32_t)(p.panel_tpw < n_ntiles ? p.panel_tpw : n_ntiles)
-                                      : panel_tiles_per_wg(m_tiles, n_ntiles);
+                                      : panel_tiles_per_wg(m_tiles, n_ntiles, Cfg::OCC);
   const int64_t n_groups = (n_ntiles + tpw - 1) / tpw;
   const int64_t grid = m_tiles * n_groups;
   if (grid <= 0) return hipSuccess;
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
   if (p.role == 0)
-    hipLaunchKernelGGL((routed_gemm_panel_kernel<OpT, OutT, KP, BN, 0>), dim3((unsigned)grid), dim3(kGemmThreads),
-                       0, stream, p, tpw);
+    hipLaunchKernelGGL((routed_gemm_panel_kernel<OpT, OutT, KP, BN, 0, WM>), dim3((unsigned)grid),
+                       dim3(kGemmThreads), 0, stream, p, tpw);
   else
-    hipLaunchKernelGGL((routed_gemm_panel_kernel<OpT, OutT, KP, BN, 1>), dim3((unsigned)grid), dim3(kGemmThreads),
-                       0, stream, p, tpw);
+    hipLaunchKernelGGL((routed_gemm_panel_kernel<OpT, OutT, KP, BN, 1, WM>), dim3((unsigned)grid),
+                       dim3(kGemmThreads), 0, stream, p, tpw);
   return hipGetLastError();
+}
+
+// 256-row tiles when the average expert fills one (half the weight traffic
+// per output row; measured on the ff_up grad-input shape: 43.8 us against
+// 48.4 us for 128-row tiles), else 128-row tiles.
+template <typename OpT, typename OutT, int KP, int BN>
+hipError_t launch_routed_gemm_panel_m(const GemmParams& p, hipStream_t stream) {
+  // 256-row tiles keep 2 * (stores per tile) + DMA per tile within vmcnt
+  constexpr int kWideStores = (sizeof(OutT) == 4 ? 4 : 2) * (BN / 16);
+  if constexpr (2 * kWideStores + PanelCfg<KP, BN, 4>::D < 64) {
+    if (p.n_experts > 0 && p.n_routes >= 256 * (int64_t)p.n_experts)
+      return launch_routed_gemm_panel_t<OpT, OutT, KP, BN, 4>(p, stream);
+  }
+  return launch_routed_gemm_panel_t<OpT, OutT, KP, BN, 2>(p, stream);
 }
 
 template <typename OpT, typename OutT>
 hipError_t launch_routed_gemm_panel_out(const GemmParams& p, hipStream_t stream) {
   if (p.K <= 64) {
-    if (p.N % 128 == 0) return launch_routed_gemm_panel_t<OpT, OutT, 64, 128>(p, stream);
-    return launch_routed_gemm_panel_t<OpT, OutT, 64, 64>(p, stream);
+    if (p.N % 128 == 0) return launch_routed_gemm_panel_m<OpT, OutT, 64, 128>(p, stream);
+    return launch_routed_gemm_panel_m<OpT, OutT, 64, 64>(p, stream);
   }
-  return launch_routed_gemm_panel_t<OpT, OutT, 128, 64>(p, stream);
+  return launch_routed_gemm_panel_m<OpT, OutT, 128, 64>(p, stream);
 }
 
 
