@@ -51,9 +51,10 @@ class Runner:
         self.E = self.keys.shape[0]
 
     def prepare(self):
-        s = self.C.cvmm_prepare_sel2(self.p.sel, self.w, route_input=self.p.route_input)
-        s._resolve(self.E)
-        return s
+        # the public call pattern (benchmark_ffn_moe.py:95-98): the selection
+        # is sorted inside cvmm(), which knows the expert count, in the same
+        # launches as the step's weight cast
+        return self.C.cvmm_prepare_sel2(self.p.sel, self.w, route_input=self.p.route_input)
 
     def forward(self, s):
         with torch.autocast("cuda", dtype=torch.bfloat16, enabled=self.p.amp):
@@ -87,7 +88,8 @@ def time_steps(runner: Runner, steps: int, warmup: int):
 
 
 def time_phases(runner: Runner, iters: int):
-    """HIP events between the phases of a step (current stream)."""
+    """HIP events between the phases of a step (current stream).  "sel" is the
+    selector bookkeeping; the sort itself runs in "fwd" (inside cvmm())."""
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     acc = np.zeros(3)
     for _ in range(iters):

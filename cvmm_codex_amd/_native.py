@@ -43,6 +43,8 @@ _SIGS = {
     "cvmm_sort_workspace_bytes": (_SZ, [_I64, _I32]),
     "cvmm_sort_routes": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "cvmm_expert_offsets": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
+    "cvmm_sort_routes_cast_keys": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _SZ,
+                                                  _P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P]),
     "cvmm_cast_keys": (ctypes.c_int, [_P, _I32, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P]),
     "cvmm_fwd_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I32, _I32, _I32, _I32]),
     "cvmm_fwd": (ctypes.c_int, [

@@ -23,6 +23,7 @@ host sync).
 from __future__ import annotations
 
 import os
+import threading
 from typing import Dict, Optional, Tuple, Union
 
 import torch
@@ -98,6 +99,34 @@ def _sort_routes(raw_flat: torch.Tensor, n_experts: int, top_k: int):
     return ssel, perm, tok, offsets
 
 
+# Weight casts made together with a sort by cvmm(), for the CVMM.forward of
+# the same call: (keys, keys._version, op dtype, kt, kn).
+_cast_done = threading.local()
+
+
+def _sort_routes_cast(raw_flat: torch.Tensor, n_experts: int, top_k: int, cast):
+    """_sort_routes plus the step's weight cast in the same launches
+    (`cast` = (keys, op dtype, want kn)); the copies are left for CVMM.forward."""
+    keys, op, need_n = cast
+    (ssel, perm, tok, offsets, route_pos), kt, kn = N.host().sort_routes_cast(
+        raw_flat, n_experts, top_k, keys, N.dtype_id(op), True, need_n, N.stream_of(raw_flat.device))
+    perm._cvmm_route_pos = route_pos
+    _cast_done.entry = (keys, keys._version, op, kt, kn)
+    return ssel, perm, tok, offsets
+
+
+def _take_cast(keys: torch.Tensor, op: torch.dtype, need_n: bool):
+    """The weight copies cast with this call's sort, if they still match."""
+    entry = getattr(_cast_done, "entry", None)
+    _cast_done.entry = None
+    if entry is None:
+        return None
+    k, version, eop, kt, kn = entry
+    if k is not keys or version != keys._version or eop != op or (need_n and kn is None):
+        return None
+    return kt, kn
+
+
 def cvmm_expert_offsets(sorted_experts: torch.Tensor, n_experts: int) -> torch.Tensor:
     """Native offsets: out[e] = #{i : sorted[i] <= e} (cvmm.py:1108-1120)."""
     return N.host().expert_offsets(sorted_experts, n_experts, N.stream_of(sorted_experts.device))
@@ -140,10 +169,11 @@ class _Routing:
         self.by_e: Dict[int, Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]] = {}
         self.first_e: Optional[int] = None
 
-    def get(self, n_experts: int):
+    def get(self, n_experts: int, cast=None):
         hit = self.by_e.get(n_experts)
         if hit is None:
-            hit = _sort_routes(self.raw, n_experts, self.k)
+            hit = (_sort_routes_cast(self.raw, n_experts, self.k, cast) if cast is not None
+                   else _sort_routes(self.raw, n_experts, self.k))
             self.by_e[n_experts] = hit
             if self.first_e is None:
                 self.first_e = n_experts
@@ -206,11 +236,11 @@ class CVMMSel:
     def _pending(self) -> bool:
         return self._routing is not None and self._sel is None
 
-    def _resolve(self, n_experts: Optional[int] = None) -> None:
+    def _resolve(self, n_experts: Optional[int] = None, cast=None) -> None:
         if not self._pending():
             return
         r = self._routing
-        ssel, perm, tok, offsets = r.get(n_experts) if n_experts is not None else r.default()
+        ssel, perm, tok, offsets = r.get(n_experts, cast) if n_experts is not None else r.default()
         sel = ssel.view(self._raw_shape_tensor().shape)
         sel._cvmm_offsets = {e: v[3] for e, v in r.by_e.items()}
         sel._cvmm_i32 = ssel
@@ -375,7 +405,8 @@ class CVMM(torch.autograd.Function):
         keys_t = keys_n = None
         if _fast_path(out_type, keys.shape[1], keys.shape[2]):
             need_n = ctx.needs_input_grad[0] or ctx.needs_input_grad[6]
-            keys_t, keys_n = _cast_keys(keys, out_type, True, need_n)
+            pre = _take_cast(keys, out_type, need_n)
+            keys_t, keys_n = pre if pre is not None else _cast_keys(keys, out_type, True, need_n)
         res = _forward(x, sel_index, sel, keys, out_index, reduction_weight, out_type, keys_t)
         ctx.keys_n = keys_n
         ctx.op_type = out_type
@@ -412,7 +443,14 @@ def cvmm(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.Tensor)
     create_kernels()
     if not isinstance(sel, CVMMSel):
         sel = cvmm_prepare_sel(sel, keys.shape[0])
-    sel._resolve(keys.shape[0])
+    # a selection still to be sorted is sorted in the launches that also cast
+    # this step's weights (consumed by CVMM.forward below)
+    cast = None
+    op = get_dtype()
+    if sel._pending() and keys.is_cuda and _fast_path(op, keys.shape[1], keys.shape[2]):
+        rw = sel.reduction_weight
+        cast = (keys, op, torch.is_grad_enabled() and (x.requires_grad or (rw is not None and rw.requires_grad)))
+    sel._resolve(keys.shape[0], cast)
     if cvmm_log_shapes:
         sh = (x.shape, keys.shape)
         if sh not in known_shapes:

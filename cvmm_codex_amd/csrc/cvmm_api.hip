@@ -187,7 +187,7 @@ extern "C" {
 
 const char* cvmm_last_error(void) { return g_err.c_str(); }
 
-int cvmm_abi_version(void) { return 4; }
+int cvmm_abi_version(void) { return 5; }
 
 int cvmm_timing_enable(uint32_t class_mask) {
   std::lock_guard<std::mutex> lk(g_timing_mu);
@@ -287,6 +287,32 @@ int cvmm_cast_keys(const void* keys, int32_t keys_dtype, int32_t n_experts, int6
   return check_launch(timed(CVMM_KC_CAST_KEYS, (hipStream_t)stream, [&] { return launch_cast_keys(keys, keys_dtype, k_se, k_si, k_sj, n_experts, d_in, d_out, out_dtype,
                                        keys_t, keys_n, (hipStream_t)stream); }),
                       "cvmm_cast_keys");
+}
+
+int cvmm_sort_routes_cast_keys(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts,
+                               int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                               int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* workspace,
+                               size_t workspace_bytes, const void* keys, int32_t keys_dtype, int64_t d_in,
+                               int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj, int32_t out_dtype,
+                               void* keys_t, void* keys_n, void* stream) {
+  const bool fuse = n_routes > 0 && n_routes <= 0x7fffffffll && n_experts > 0 && n_experts <= 32767 && top_k > 0 &&
+                    sel && sorted_sel && perm && offsets && keys && (keys_t || keys_n) && d_in > 0 && d_out > 0 &&
+                    n_experts <= 65535 && (int64_t)n_experts * (d_in / 64) * (d_out / 64) < 0x7f000000ll &&
+                    cast_vec_ok(keys, keys_dtype, k_se, k_si, k_sj, d_in, d_out, out_dtype, keys_t, keys_n) &&
+                    workspace != nullptr && workspace_bytes >= sort_workspace_bytes(n_routes, n_experts);
+  if (!fuse) {
+    // separate calls, each with its own argument checks
+    int r = cvmm_sort_routes(sel, sel_is_int64, n_routes, n_experts, top_k, sorted_sel, perm, token_index, offsets,
+                             route_pos, n_invalid, workspace, workspace_bytes, stream);
+    if (r) return r;
+    return cvmm_cast_keys(keys, keys_dtype, n_experts, d_in, d_out, k_se, k_si, k_sj, out_dtype, keys_t, keys_n,
+                          stream);
+  }
+  hipStream_t s = (hipStream_t)stream;
+  const CastRequest cr{keys, k_se, k_si, n_experts, d_in, d_out, out_dtype, keys_t, keys_n};
+  return check_launch(timed(CVMM_KC_SORT, s, [&] { return launch_sort_routes(sel, sel_is_int64 != 0, n_routes, n_experts, top_k, sorted_sel, perm,
+                                         token_index, offsets, route_pos, n_invalid, workspace, s, &cr); }),
+                      "cvmm_sort_routes_cast_keys");
 }
 
 // ---------------------------------------------------------------------------

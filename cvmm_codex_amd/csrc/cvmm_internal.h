@@ -132,10 +132,28 @@ void wgrad_geometry(int64_t M, int64_t N, int64_t n_routes, int32_t n_experts, i
 // selector preparation
 // ---------------------------------------------------------------------------
 size_t sort_workspace_bytes(int64_t n_routes, int32_t n_experts);
+// A weight cast to run in the sort's scatter launch (vectorised cast only).
+struct CastRequest {
+  const void* keys;
+  int64_t se, si;
+  int32_t n_experts;
+  int64_t d_in, d_out;
+  int32_t out_dtype;
+  void* kt;
+  void* kn;
+};
+// The vectorised cast applies: fp32 keys with unit column stride, 16-byte
+// aligned rows, d_in and d_out multiples of 64, 16-bit output.
+inline bool cast_vec_ok(const void* keys, int32_t keys_dtype, int64_t se, int64_t si, int64_t sj, int64_t d_in,
+                        int64_t d_out, int32_t out_dtype, const void* kt, const void* kn) {
+  return keys_dtype == kF32 && sj == 1 && d_in % 64 == 0 && d_out % 64 == 0 && si % 4 == 0 && se % 4 == 0 &&
+         (reinterpret_cast<uintptr_t>(keys) & 15) == 0 && (reinterpret_cast<uintptr_t>(kt) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(kn) & 15) == 0 && (out_dtype == kBF16 || out_dtype == kF16);
+}
 hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_routes, int32_t n_experts,
                               int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
                               int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* ws,
-                              hipStream_t stream);
+                              hipStream_t stream, const CastRequest* cast = nullptr);
 hipError_t launch_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_experts,
                                  int64_t* offsets, hipStream_t stream);
 

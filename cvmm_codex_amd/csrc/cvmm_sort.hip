@@ -19,6 +19,7 @@
 // at most 64K.
 #include "cvmm_common.h"
 #include "cvmm_internal.h"
+#include "cvmm_keys.h"
 
 namespace cvmm {
 
@@ -81,8 +82,7 @@ template <typename IdxT>
 __device__ void scatter_chunk(const IdxT* __restrict__ sel, int64_t n_routes, int32_t n_experts, int64_t chunk,
                               int32_t n_bits, int64_t top_k, int32_t* pos, int32_t* __restrict__ sorted_sel,
                               int64_t* __restrict__ perm, int64_t* __restrict__ token_index,
-                              int32_t* __restrict__ route_pos) {
-  const int64_t b = blockIdx.x;
+                              int32_t* __restrict__ route_pos, int64_t b) {
   const int wave = threadIdx.x >> 6;
   const int lane = lane_id();
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -117,14 +117,32 @@ __device__ void scatter_chunk(const IdxT* __restrict__ sel, int64_t n_routes, in
 }
 
 template <typename IdxT>
-__global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
-    const IdxT* __restrict__ sel, int64_t n_routes, int32_t n_experts, int64_t chunk,
-    int64_t n_chunks, const int32_t* __restrict__ counts, int32_t n_bits, int64_t top_k,
-    int32_t* __restrict__ sorted_sel, int64_t* __restrict__ perm, int64_t* __restrict__ token_index,
-    int32_t* __restrict__ route_pos, int64_t* __restrict__ offsets, int32_t* __restrict__ n_invalid) {
-  extern __shared__ int32_t sh[];  // pos[n_experts + 1] (+ tot[n_experts + 1] on the fast path)
-  int32_t* pos = sh;                 // running output positions of this chunk
-  const int64_t b = blockIdx.x;
+struct ScatterArgs {
+  const IdxT* sel;
+  int64_t n_routes;
+  int32_t n_experts;
+  int64_t chunk, n_chunks;
+  const int32_t* counts;
+  int32_t n_bits;
+  int64_t top_k;
+  int32_t* sorted_sel;
+  int64_t* perm;
+  int64_t* token_index;
+  int32_t* route_pos;
+  int64_t* offsets;
+  int32_t* n_invalid;
+};
+
+// Chunk b: output positions from the histogram rows, then the stable scatter.
+// sh: n_experts + 1 positions (+ n_experts + 1 totals when <= kSortFastBuckets).
+template <typename IdxT>
+__device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b) {
+  const int64_t n_routes = a.n_routes, chunk = a.chunk, n_chunks = a.n_chunks, top_k = a.top_k;
+  const int32_t n_experts = a.n_experts, n_bits = a.n_bits;
+  const int32_t* __restrict__ counts = a.counts;
+  int64_t* __restrict__ offsets = a.offsets;
+  int32_t* __restrict__ n_invalid = a.n_invalid;
+  int32_t* pos = sh;  // running output positions of this chunk
   const int32_t nb = n_experts + 1;
   if (nb <= kSortFastBuckets) {
     // All threads stride over the whole count matrix (loads batched 16 deep);
@@ -181,7 +199,30 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     }
   }
   __syncthreads();
-  scatter_chunk(sel, n_routes, n_experts, chunk, n_bits, top_k, pos, sorted_sel, perm, token_index, route_pos);
+  scatter_chunk(a.sel, n_routes, n_experts, chunk, n_bits, top_k, pos, a.sorted_sel, a.perm, a.token_index,
+                a.route_pos, b);
+}
+
+template <typename IdxT>
+__global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(const ScatterArgs<IdxT> a) {
+  extern __shared__ int32_t sh[];
+  scatter_block(a, sh, blockIdx.x);
+}
+
+// The scatter and the per-step weight cast in one launch: workgroups
+// [0, n_chunks) scatter, the rest cast 64 x 64 weight tiles.  The scatter
+// (a few workgroups, latency-bound) runs in the shadow of the cast.
+template <typename IdxT, typename OutT>
+__global__ __launch_bounds__(kSortThreads) void sort_scatter_cast_kernel(const ScatterArgs<IdxT> a,
+                                                                         const CastArgs<OutT> c) {
+  extern __shared__ int32_t sh[];
+  if ((int64_t)blockIdx.x < a.n_chunks) {
+    scatter_block(a, sh, blockIdx.x);
+  } else {
+    const int64_t t = (int64_t)blockIdx.x - a.n_chunks;  // (expert, d_in tile, d_out tile)
+    const int64_t tj = c.d_out / 64, ti = c.d_in / 64;
+    cast_tile_vec(c, t / (ti * tj), (t / tj) % ti, t % tj);
+  }
 }
 
 // Upper-bound binary search per expert over an already sorted int32 array
@@ -217,10 +258,24 @@ size_t sort_workspace_bytes(int64_t n_routes, int32_t n_experts) {
   return align_up(counts, 256) + 256;  // + n_invalid counter
 }
 
+template <typename IdxT>
+void launch_scatter_cast(const ScatterArgs<IdxT>& a, const CastRequest& cr, size_t lds, hipStream_t stream) {
+  const int64_t grid = a.n_chunks + (int64_t)cr.n_experts * (cr.d_in / 64) * (cr.d_out / 64);
+  if (cr.out_dtype == kBF16) {
+    const CastArgs<bf16_t> c{(const float*)cr.keys, cr.se, cr.si, cr.d_in, cr.d_out, (bf16_t*)cr.kt, (bf16_t*)cr.kn};
+    hipLaunchKernelGGL((sort_scatter_cast_kernel<IdxT, bf16_t>), dim3((unsigned)grid), dim3(kSortThreads), lds, stream,
+                       a, c);
+  } else {
+    const CastArgs<f16_t> c{(const float*)cr.keys, cr.se, cr.si, cr.d_in, cr.d_out, (f16_t*)cr.kt, (f16_t*)cr.kn};
+    hipLaunchKernelGGL((sort_scatter_cast_kernel<IdxT, f16_t>), dim3((unsigned)grid), dim3(kSortThreads), lds, stream,
+                       a, c);
+  }
+}
+
 hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_routes, int32_t n_experts,
                               int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
                               int64_t* offsets, int32_t* route_pos, int32_t* n_invalid_out, void* ws,
-                              hipStream_t stream) {
+                              hipStream_t stream, const CastRequest* cast) {
   const int64_t chunk = sort_chunk_size(n_routes, n_experts);
   const int64_t n_chunks = (n_routes + chunk - 1) / chunk;
   int32_t* counts = (int32_t*)ws;
@@ -236,13 +291,19 @@ hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_rout
                        (const int32_t*)sel, n_routes, n_experts, chunk, n_chunks, counts);
   }
   if (sel_is_int64) {
-    hipLaunchKernelGGL(sort_scatter_kernel<int64_t>, dim3(n_chunks), dim3(kSortThreads), lds_scatter, stream,
-                       (const int64_t*)sel, n_routes, n_experts, chunk, n_chunks, counts, n_bits, top_k,
-                       sorted_sel, perm, token_index, route_pos, offsets, n_invalid_out);
+    const ScatterArgs<int64_t> a{(const int64_t*)sel, n_routes, n_experts, chunk, n_chunks, counts, n_bits, top_k,
+                                 sorted_sel, perm, token_index, route_pos, offsets, n_invalid_out};
+    if (cast == nullptr)
+      hipLaunchKernelGGL(sort_scatter_kernel<int64_t>, dim3(n_chunks), dim3(kSortThreads), lds_scatter, stream, a);
+    else
+      launch_scatter_cast(a, *cast, lds_scatter, stream);
   } else {
-    hipLaunchKernelGGL(sort_scatter_kernel<int32_t>, dim3(n_chunks), dim3(kSortThreads), lds_scatter, stream,
-                       (const int32_t*)sel, n_routes, n_experts, chunk, n_chunks, counts, n_bits, top_k,
-                       sorted_sel, perm, token_index, route_pos, offsets, n_invalid_out);
+    const ScatterArgs<int32_t> a{(const int32_t*)sel, n_routes, n_experts, chunk, n_chunks, counts, n_bits, top_k,
+                                 sorted_sel, perm, token_index, route_pos, offsets, n_invalid_out};
+    if (cast == nullptr)
+      hipLaunchKernelGGL(sort_scatter_kernel<int32_t>, dim3(n_chunks), dim3(kSortThreads), lds_scatter, stream, a);
+    else
+      launch_scatter_cast(a, *cast, lds_scatter, stream);
   }
   return hipGetLastError();
 }

@@ -148,6 +148,39 @@ std::vector<Tensor> sort_routes(const Tensor& raw, int64_t n_experts, int64_t to
   return {ssel, perm, tok, off, pos};
 }
 
+// The sort and the same step's weight cast in one call (the cast runs in the
+// scatter launch): (sorted, perm, perm // top_k, offsets, route_pos), kt, kn.
+std::tuple<std::vector<Tensor>, OptT, OptT> sort_routes_cast(const Tensor& raw, int64_t n_experts, int64_t top_k,
+                                                             const Tensor& keys, int64_t op_id, bool want_t,
+                                                             bool want_n, int64_t stream) {
+  require_device(raw, "sel");
+  require_device(keys, "keys");
+  Tensor flat = raw.reshape({-1});
+  if (flat.scalar_type() != at::kInt && flat.scalar_type() != at::kLong) flat = flat.to(at::kInt);
+  flat = flat.contiguous();
+  const int64_t R = flat.numel();
+  Tensor i32 = at::empty({2 * R}, opts(flat, at::kInt));
+  Tensor i64 = at::empty({2 * R + n_experts}, opts(flat, at::kLong));
+  Tensor ssel = i32.narrow(0, 0, R), pos = i32.narrow(0, R, R);
+  Tensor perm = i64.narrow(0, 0, R), tok = i64.narrow(0, R, R), off = i64.narrow(0, 2 * R, n_experts);
+  const auto op = dtype_of(op_id);
+  const int64_t E = keys.size(0), d_in = keys.size(1), d_out = keys.size(2);
+  if (E != n_experts) throw py::value_error("cvmm: keys.shape[0] differs from the expert count");
+  OptT kt, kn;
+  if (want_t) kt = at::empty({E, d_out, d_in}, opts(keys, op));
+  if (want_n) kn = at::empty({E, d_in, d_out}, opts(keys, op));
+  const size_t ws_bytes = cvmm_sort_workspace_bytes(R, (int32_t)n_experts);
+  Tensor ws = sort_workspace(flat, stream, ws_bytes);
+  check(cvmm_sort_routes_cast_keys(ptr(flat), flat.scalar_type() == at::kLong ? 1 : 0, R, (int32_t)n_experts,
+                                   std::max<int64_t>(top_k, 1), tptr<int32_t>(ssel), tptr<int64_t>(perm),
+                                   tptr<int64_t>(tok), tptr<int64_t>(off), tptr<int32_t>(pos), nullptr, ptr(ws),
+                                   (size_t)ws.numel(), ptr(keys), dtype_id(keys.scalar_type()), d_in, d_out,
+                                   keys.stride(0), keys.stride(1), keys.stride(2), (int32_t)op_id, ptr(kt), ptr(kn),
+                                   (void*)stream),
+        "cvmm_sort_routes_cast_keys");
+  return {{ssel, perm, tok, off, pos}, kt, kn};
+}
+
 Tensor expert_offsets(const Tensor& sorted, int64_t n_experts, int64_t stream) {
   require_device(sorted, "sorted_experts");
   Tensor s = sorted_i32(sorted);
@@ -309,6 +342,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "Host glue of cvmm_codex_amd: one call per CVMM phase into libcvmm_hip.so";
   m.def("sort_routes", &sort_routes, py::arg("raw"), py::arg("n_experts"), py::arg("top_k"), py::arg("stream"));
   m.def("expert_offsets", &expert_offsets, py::arg("sorted"), py::arg("n_experts"), py::arg("stream"));
+  m.def("sort_routes_cast", &sort_routes_cast, py::arg("raw"), py::arg("n_experts"), py::arg("top_k"),
+        py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"), py::arg("stream"));
   m.def("cast_keys", &cast_keys, py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"),
         py::arg("stream"));
   m.def("forward", &forward);

@@ -111,6 +111,20 @@ int cvmm_sort_routes(const void* sel, int32_t sel_is_int64, int64_t n_routes, in
                      int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* cvmm_sort_routes and cvmm_cast_keys in one call (no counterpart in the
+ * reference, whose sort and in-kernel weight cast are separate steps): the
+ * cast of the same step's weights runs in the launch that scatters the
+ * routes, so the latency-bound scatter hides behind it.  Arguments and
+ * outputs as in the two calls; the two keys/output arguments follow the
+ * cast's.  Falls back to the two separate launches where the vectorised cast
+ * does not apply. */
+int cvmm_sort_routes_cast_keys(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts,
+                               int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                               int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* workspace,
+                               size_t workspace_bytes, const void* keys, int32_t keys_dtype, int64_t d_in,
+                               int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj, int32_t out_dtype,
+                               void* keys_t, void* keys_n, void* stream);
+
 /* offsets[e] = #{i : sorted_sel[i] <= e}; replaces cvmm_expert_offsets
  * (cvmm.py:1108-1120, kernel cvmm.py:315-335). */
 int cvmm_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_experts, int64_t* offsets,

@@ -236,6 +236,49 @@ def test_sort_int64_ids_wrap_like_int32_cast():
     assert np.array_equal(s.sel_index.cpu().numpy(), m.sel_index)
 
 
+@pytest.mark.parametrize("R,E,k,d_in,d_out,fused", [
+    (65536, 64, 8, 1024, 128, True), (4000, 16, 4, 128, 192, True), (3000, 7, 3, 64, 64, True),
+    (777, 300, 1, 256, 64, True), (4000, 16, 4, 96, 128, False),
+])
+def test_sort_and_cast_in_one_call_match_the_separate_calls(R, E, k, d_in, d_out, fused):
+    """cvmm_sort_routes_cast_keys (scatter and weight cast in one launch where
+    the vectorised cast applies, else the two calls) gives the bits of
+    cvmm_sort_routes + cvmm_cast_keys; out-of-range ids included."""
+    from cvmm_codex_amd import _native as N
+    lib = N.lib()
+    g = torch.Generator().manual_seed(R + E)
+    raw = torch.randint(-1, E + 1, (R,), generator=g).cuda()
+    keys = torch.randn(E, d_in, d_out, generator=g).cuda()
+    st = N.stream_of(raw.device)
+    ws_b = lib.cvmm_sort_workspace_bytes(R, E)
+
+    def outputs():
+        return dict(ssel=torch.full((R,), -7, dtype=torch.int32, device="cuda"),
+                    perm=torch.full((R,), -7, dtype=torch.int64, device="cuda"),
+                    tok=torch.full((R,), -7, dtype=torch.int64, device="cuda"),
+                    off=torch.full((E,), -7, dtype=torch.int64, device="cuda"),
+                    pos=torch.full((R,), -7, dtype=torch.int32, device="cuda"),
+                    nin=torch.full((1,), -7, dtype=torch.int32, device="cuda"),
+                    kt=torch.zeros(E, d_out, d_in, dtype=torch.bfloat16, device="cuda"),
+                    kn=torch.zeros(E, d_in, d_out, dtype=torch.bfloat16, device="cuda"),
+                    ws=torch.empty(ws_b, dtype=torch.uint8, device="cuda"))
+
+    a, b = outputs(), outputs()
+    sort_args = lambda o: (N.ptr(raw), 1, R, E, k, N.ptr(o["ssel"]), N.ptr(o["perm"]), N.ptr(o["tok"]),
+                           N.ptr(o["off"]), N.ptr(o["pos"]), N.ptr(o["nin"]), N.ptr(o["ws"]), ws_b)
+    key_args = (N.ptr(keys), N.F32)
+    N.check(lib.cvmm_sort_routes(*sort_args(a), st), "sort")
+    N.check(lib.cvmm_cast_keys(*key_args, E, d_in, d_out, *keys.stride(), N.BF16, N.ptr(a["kt"]), N.ptr(a["kn"]), st),
+            "cast")
+    N.check(lib.cvmm_sort_routes_cast_keys(*sort_args(b), *key_args, d_in, d_out, *keys.stride(), N.BF16,
+                                           N.ptr(b["kt"]), N.ptr(b["kn"]), st), "sort+cast")
+    for n in ("ssel", "perm", "tok", "off", "pos", "nin", "kt", "kn"):
+        assert torch.equal(a[n], b[n]), n
+    assert torch.equal(b["kn"], keys.to(torch.bfloat16))
+    assert torch.equal(b["kt"], keys.transpose(1, 2).contiguous().to(torch.bfloat16))
+    assert fused == (d_in % 64 == 0 and d_out % 64 == 0)
+
+
 def test_sort_invalid_ids_go_last():
     """Ids outside [0, E) are counted, sorted stably after all valid routes and
     never read by the GEMMs."""
