@@ -29,10 +29,16 @@ from typing import Dict, Optional, Tuple, Union
 import torch
 
 from . import _native as N
+from . import compile_ops as _ops
+
+
+def _compiling() -> bool:
+    """Tracing under torch.compile: go through the custom ops (compile_ops)."""
+    return torch.compiler.is_compiling()
 
 __all__ = [
     "CVMMSel", "cvmm_prepare_sel", "cvmm_prepare_sel2", "cvmm", "CVMM", "get_dtype",
-    "dtype_to_type_id", "create_kernels", "cvmm_expert_offsets",
+    "dtype_to_type_id", "create_kernels", "cvmm_expert_offsets", "cvmm_triton_call",
 ]
 
 
@@ -54,6 +60,9 @@ cvmm_lowmem_chunk_size = int(os.environ.get("CVMM_LOWMEM_CHUNK_SIZE", "0"))
 cvmm_atomic_reduce = _env_on("CVMM_ATOMIC_REDUCE")
 # Print each new (x.shape, keys.shape) like the reference (cvmm.py:1778-1781).
 cvmm_log_shapes = _env_on("CVMM_LOG_SHAPES")
+# The forward primitive as a torch.library op, as the reference exposes
+# torch.ops.mylib.cvmm_triton (cvmm.py:1458-1459).
+cvmm_triton_call = torch.ops.cvmm_codex_amd.cvmm_triton
 
 
 def _require_device(t: torch.Tensor, what: str) -> None:
@@ -93,6 +102,9 @@ def _sort_routes(raw_flat: torch.Tensor, n_experts: int, top_k: int):
     inverse permutation (int32) is attached to perm as ``_cvmm_route_pos``: the
     forward/backward calls that receive this perm as their route index use it
     to gather each token's routes."""
+    if _compiling():
+        ssel, perm, tok, offsets, _ = _ops.sort_routes(raw_flat, n_experts, top_k)
+        return ssel, perm, tok, offsets
     ssel, perm, tok, offsets, route_pos = N.host().sort_routes(raw_flat, n_experts, top_k,
                                                                N.stream_of(raw_flat.device))
     perm._cvmm_route_pos = route_pos
@@ -129,6 +141,8 @@ def _take_cast(keys: torch.Tensor, op: torch.dtype, need_n: bool):
 
 def cvmm_expert_offsets(sorted_experts: torch.Tensor, n_experts: int) -> torch.Tensor:
     """Native offsets: out[e] = #{i : sorted[i] <= e} (cvmm.py:1108-1120)."""
+    if _compiling():
+        return _ops.expert_offsets(sorted_experts.reshape(-1).to(torch.int32), n_experts)
     return N.host().expert_offsets(sorted_experts, n_experts, N.stream_of(sorted_experts.device))
 
 
@@ -146,6 +160,8 @@ def _cvmm_expert_offsets(sorted_experts: torch.Tensor, n_experts: int) -> torch.
 
 def _offsets_for(sel: torch.Tensor, n_experts: int) -> torch.Tensor:
     """Per-expert offsets of a sorted selector, cached on the tensor object."""
+    if _compiling():
+        return cvmm_expert_offsets(sel, n_experts)
     cache: Optional[Dict[int, torch.Tensor]] = getattr(sel, "_cvmm_offsets", None)
     if cache is not None and n_experts in cache:
         return cache[n_experts]
@@ -242,8 +258,9 @@ class CVMMSel:
         r = self._routing
         ssel, perm, tok, offsets = r.get(n_experts, cast) if n_experts is not None else r.default()
         sel = ssel.view(self._raw_shape_tensor().shape)
-        sel._cvmm_offsets = {e: v[3] for e, v in r.by_e.items()}
-        sel._cvmm_i32 = ssel
+        if not _compiling():
+            sel._cvmm_offsets = {e: v[3] for e, v in r.by_e.items()}
+            sel._cvmm_i32 = ssel
         self._sel = sel
         if self._route_mode:
             self._sel_index, self._out_index = perm, None
@@ -343,6 +360,8 @@ def _keys_view(keys: torch.Tensor) -> torch.Tensor:
 
 def _route_pos(rp: Optional[torch.Tensor], n_routes: int) -> Optional[torch.Tensor]:
     """The sort's inverse permutation when `rp` is the perm it returned."""
+    if _compiling():
+        return None
     pos = getattr(rp, "_cvmm_route_pos", None) if rp is not None else None
     if pos is None or pos.numel() != n_routes or pos.dtype != torch.int32 or pos.device != rp.device:
         return None
@@ -362,6 +381,9 @@ def _cast_keys(keys: torch.Tensor, op: torch.dtype, want_t: bool, want_n: bool):
     """keys [E, d_in, d_out] -> op-dtype copies kt [E, d_out, d_in] (forward) and
     kn [E, d_in, d_out] (grad-input), one pass."""
     _require_device(keys, "keys")
+    if _compiling():
+        kt, kn = _ops.cast_keys(keys, op)
+        return kt, kn
     return N.host().cast_keys(keys, N.dtype_id(op), want_t, want_n, N.stream_of(keys.device))
 
 
@@ -370,9 +392,13 @@ def _forward(x, sel_index, sel, keys, out_index, rw, op_dtype, keys_t=None):
     _require_device(sel, "sel")
     n_experts = keys.shape[0]
     R = sel.numel()
-    out = N.host().forward(x, keys, keys_t, sel, sel_index, out_index, _offsets_for(sel, n_experts),
-                           _route_pos(out_index if out_index is not None else sel_index, R), rw,
-                           N.dtype_id(op_dtype), _flags(), N.stream_of(x.device))
+    if _compiling():
+        out = _ops.forward(x, keys, keys_t, sel, sel_index, out_index, _offsets_for(sel, n_experts), rw, op_dtype,
+                           _flags())
+    else:
+        out = N.host().forward(x, keys, keys_t, sel, sel_index, out_index, _offsets_for(sel, n_experts),
+                               _route_pos(out_index if out_index is not None else sel_index, R), rw,
+                               N.dtype_id(op_dtype), _flags(), N.stream_of(x.device))
     if rw is None:
         return out.view(*sel.shape, keys.shape[2])
     return out.view(*rw.shape[:-1], keys.shape[2])
@@ -383,6 +409,11 @@ def _backward(ctx, grad_output, x, keys, raw_sel, sel, sel_index, out_index, rw,
     """CVMM.backward's products (cvmm.py:1552-1755)."""
     top_k = raw_sel.shape[-1] if raw_sel.ndim > 0 else 1
     R = sel.numel()
+    if _compiling():
+        g = _ops.backward(grad_output, x, keys, keys_n, sel, sel_index, out_index, _offsets_for(sel, keys.shape[0]),
+                          rw, top_k, ctx.op_type, bool(need_grad_x), bool(need_grad_keys), bool(need_grad_rw),
+                          _flags())
+        return _ops.grads_or_none(g, [bool(need_grad_x), bool(need_grad_keys), bool(need_grad_rw)])
     return N.host().backward(grad_output, x, keys, keys_n, sel, sel_index, out_index,
                              _offsets_for(sel, keys.shape[0]),
                              _route_pos(out_index if out_index is not None else sel_index, R), rw, top_k,
@@ -405,7 +436,7 @@ class CVMM(torch.autograd.Function):
         keys_t = keys_n = None
         if _fast_path(out_type, keys.shape[1], keys.shape[2]):
             need_n = ctx.needs_input_grad[0] or ctx.needs_input_grad[6]
-            pre = _take_cast(keys, out_type, need_n)
+            pre = None if _compiling() else _take_cast(keys, out_type, need_n)
             keys_t, keys_n = pre if pre is not None else _cast_keys(keys, out_type, True, need_n)
         res = _forward(x, sel_index, sel, keys, out_index, reduction_weight, out_type, keys_t)
         ctx.keys_n = keys_n
@@ -440,14 +471,15 @@ def create_kernels() -> None:
 
 def cvmm(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.Tensor) -> torch.Tensor:
     """cvmm.py:1759-1783."""
-    create_kernels()
+    if not _compiling():  # the ops load the library when they run
+        create_kernels()
     if not isinstance(sel, CVMMSel):
         sel = cvmm_prepare_sel(sel, keys.shape[0])
     # a selection still to be sorted is sorted in the launches that also cast
     # this step's weights (consumed by CVMM.forward below)
     cast = None
     op = get_dtype()
-    if sel._pending() and keys.is_cuda and _fast_path(op, keys.shape[1], keys.shape[2]):
+    if sel._pending() and keys.is_cuda and _fast_path(op, keys.shape[1], keys.shape[2]) and not _compiling():
         rw = sel.reduction_weight
         cast = (keys, op, torch.is_grad_enabled() and (x.requires_grad or (rw is not None and rw.requires_grad)))
     sel._resolve(keys.shape[0], cast)

@@ -1,0 +1,87 @@
+"""torch.compile through the API (the reference registers its forward as a
+torch.library op with a fake implementation for this, cvmm.py:808-812,
+:1436-1456): compiled and eager steps run the same kernels and must agree bit
+for bit; the ops pass torch.library.opcheck."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import cvmm_codex_amd as C
+from cvmm_codex_amd import compile_ops as ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(seed, weighted, route_input, B=2, T=96, D=128, H=64, E=12, K=3):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*((B, T, K, D) if route_input else (B, T, D)), generator=g).to(torch.bfloat16).cuda()
+    keys = (torch.randn(E, D, H, generator=g) / D ** 0.5).cuda()
+    sel = torch.randint(0, E, (B, T, K), generator=g).cuda()
+    w = torch.rand(B, T, K, generator=g).cuda() if weighted else None
+    go = torch.randn(*((B, T, H) if weighted else (B, T, K, H)), generator=g).to(torch.bfloat16).cuda()
+    return x, keys, sel, w, go
+
+
+def _step(x, keys, sel, w, route_input):
+    s = C.cvmm_prepare_sel2(sel, w, route_input=route_input)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        return C.cvmm(x, s, keys)
+
+
+def _run(fn, x, keys, sel, w, go, route_input):
+    xs = x.clone().requires_grad_(True)
+    ks = keys.clone().requires_grad_(True)
+    ws = None if w is None else w.clone().requires_grad_(True)
+    y = fn(xs, ks, sel, ws, route_input)
+    y.backward(go.to(y.dtype))
+    torch.cuda.synchronize()
+    return y.detach(), xs.grad, ks.grad, None if ws is None else ws.grad
+
+
+@pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True), (True, False)])
+def test_compiled_step_matches_eager(weighted, route_input):
+    """One graph (fullgraph=True): selector, forward and backward all traced."""
+    torch._dynamo.reset()
+    case = _case(3, weighted, route_input)
+    eager = _run(_step, *case, route_input)
+    compiled = _run(torch.compile(_step, backend="aot_eager", fullgraph=True), *case, route_input)
+    for name, a, b in zip(("out", "x_grad", "keys_grad", "weights_grad"), eager, compiled):
+        if a is None:
+            assert b is None, name
+        else:
+            assert torch.equal(a, b), name
+
+
+def test_ops_pass_opcheck():
+    x, keys, sel, w, go = _case(4, True, False)
+    raw = sel.reshape(-1)
+    E = keys.shape[0]
+    utils = ("test_schema", "test_faketensor")
+    torch.library.opcheck(ops.sort_routes, (raw, E, 3), test_utils=utils)
+    ssel, perm, tok, off, _ = ops.sort_routes(raw, E, 3)
+    torch.library.opcheck(ops.expert_offsets, (ssel, E), test_utils=utils)
+    torch.library.opcheck(ops.cast_keys, (keys, torch.bfloat16), test_utils=utils)
+    xf = x.reshape(-1, x.shape[-1])
+    torch.library.opcheck(ops.forward, (xf, keys, None, ssel, tok, perm, off, w, torch.bfloat16, 0),
+                          test_utils=utils)
+    gy = go.reshape(-1, go.shape[-1])
+    torch.library.opcheck(ops.backward, (gy, xf, keys, None, ssel, tok, perm, off, w, 3, torch.bfloat16,
+                                         True, True, True, 0), test_utils=utils)
+    minus1 = torch.full((1,), -1, dtype=torch.int64, device="cuda")
+    torch.library.opcheck(ops.cvmm_triton, (xf, tok, ssel, keys, torch.bfloat16, perm, torch.bfloat16),
+                          test_utils=utils)
+    torch.library.opcheck(ops.cvmm_triton, (xf, tok, ssel, keys, torch.bfloat16, minus1, torch.bfloat16),
+                          test_utils=utils)
+
+
+def test_reference_op_schema_matches_the_api_forward():
+    """cvmm_triton (the reference op's schema) gives the per-route forward of cvmm()."""
+    x, keys, sel, _, _ = _case(5, False, False)
+    s = C.cvmm_prepare_sel2(sel)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = C.cvmm(x, s, keys)
+    z = C.cvmm_triton_call(x.reshape(-1, x.shape[-1]), s.sel_index, s.sel, keys.to(torch.bfloat16),
+                           torch.bfloat16, s.out_index, torch.bfloat16)
+    assert z.shape == y.shape
+    assert torch.equal(z, y)
