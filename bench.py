@@ -149,7 +149,7 @@ def _classes():
     from cvmm_codex_amd import _native as N
     return {"sort": N.KC_SORT, "offsets": N.KC_OFFSETS, "cast_keys": N.KC_CAST_KEYS,
             "gemm_fwd": N.KC_GEMM_FWD, "gemm_bwd_x": N.KC_GEMM_BWDX, "wgrad": N.KC_WGRAD,
-            "combine": N.KC_COMBINE, "fill": N.KC_FILL}
+            "combine": N.KC_COMBINE, "fill": N.KC_FILL, "reduce": N.KC_REDUCE}
 
 
 def kernel_times(runner: Runner, steps: int):
@@ -204,6 +204,12 @@ def kernel_work(proj: W.Projection, name: str):
     if name == "wgrad":
         g_rows = tokens if weighted else R
         return flops, x_rows * d_in * b + g_rows * d_out * b + E * d_in * d_out * 4
+    if name == "reduce":
+        # top-k sum without a route buffer (weighted forward of route rows, or
+        # the token gradient): gathered route rows (K wide), 8 bytes of route
+        # info per route, the weight copy, one output row (N wide) per token
+        K, n = (d_in, d_out) if proj.route_input else (d_out, d_in)
+        return flops, R * K * b + R * 8 + keys_b + tokens * n * b
     return None, None
 
 
@@ -270,7 +276,8 @@ def main():
     ap.add_argument("--only", choices=["fwd", "bwd_w", "bwd_x", "cast_keys", "copy"], default=None,
                     help="launch only this phase --steps times, or the copy calibration (rocprofv3 runs)")
     ap.add_argument("--tune", action="append", default=[], metavar="KNOB=VALUE",
-                    help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, gemm_order) before running")
+                    help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, gemm_order, "
+                         "reduce_min_topk) before running")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -283,7 +290,7 @@ def main():
 
     from cvmm_codex_amd import _native as N
     knobs = {"panel_tiles_per_wg": N.TUNE_PANEL_TILES_PER_WG, "wgrad_order": N.TUNE_WGRAD_ORDER,
-             "gemm_order": N.TUNE_GEMM_ORDER}
+             "gemm_order": N.TUNE_GEMM_ORDER, "reduce_min_topk": N.TUNE_REDUCE_MIN_TOPK}
     for kv in args.tune:
         name, _, value = kv.partition("=")
         if name not in knobs:

@@ -18,13 +18,15 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcvmm_hip
 F32, F16, BF16 = 0, 1, 2            # cvmm.py:36-44 dtype ids
 FLAG_ATOMIC_REDUCE = 1
 FLAG_COUNTERS_ZEROED = 2
+FLAG_ROUTES_STABLE = 4
 TUNE_PANEL_TILES_PER_WG = 1
 TUNE_WGRAD_ORDER = 2
 TUNE_GEMM_ORDER = 3
+TUNE_REDUCE_MIN_TOPK = 4
 
 # kernel classes of the timing hooks (include/cvmm_hip.h CVMM_KC_*)
-KC_SORT, KC_OFFSETS, KC_CAST_KEYS, KC_GEMM_FWD, KC_GEMM_BWDX, KC_WGRAD, KC_COMBINE, KC_FILL = (
-    1, 2, 4, 8, 16, 32, 64, 128)
+KC_SORT, KC_OFFSETS, KC_CAST_KEYS, KC_GEMM_FWD, KC_GEMM_BWDX, KC_WGRAD, KC_COMBINE, KC_FILL, KC_REDUCE = (
+    1, 2, 4, 8, 16, 32, 64, 128, 256)
 
 _DTYPE_ID = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -46,7 +48,7 @@ _SIGS = {
     "cvmm_sort_routes_cast_keys": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _SZ,
                                                   _P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P]),
     "cvmm_cast_keys": (ctypes.c_int, [_P, _I32, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P]),
-    "cvmm_fwd_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I32, _I32, _I32, _I32]),
+    "cvmm_fwd_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32]),
     "cvmm_fwd": (ctypes.c_int, [
         _P, _I32, _I64, _I64,                 # x, dtype, rows, ld
         _P, _I32, _I32, _I64, _I64,           # keys, dtype, E, d_in, d_out
@@ -55,7 +57,8 @@ _SIGS = {
         _P, _P, _P, _I32, _I64,               # offsets, route_pos, rw, rw dtype, reduce_k
         _I32, _P, _I32, _I64, _I64,           # op, out, out dtype, out rows, out ld
         _I32, _P, _SZ, _P]),                  # flags, ws, ws bytes, stream
-    "cvmm_bwd_x_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I32, _I32, _I32, _I64, _I32, _I32, _I32, _I32]),
+    "cvmm_bwd_x_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I64, _I32, _I32, _I32, _I64, _I32, _I32, _I32,
+                                         _I32]),
     "cvmm_bwd_x": (ctypes.c_int, [
         _P, _I32, _I64, _I64,                 # grad, dtype, rows, ld
         _P, _I32, _I32, _I64, _I64,           # keys, dtype, E, d_in, d_out

@@ -70,6 +70,83 @@ __device__ __forceinline__ void lds_wait_tied(lds_u32x4 (&x)[4], lds_u32x4 (&y)[
 
 __device__ __forceinline__ uint4 as_uint4(lds_u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); }
 
+// LDS address of a __shared__ object, for inline-asm LDS accesses.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// A 4-byte LDS load as inline asm, waited for at once (see lds_read128): for
+// scalar bookkeeping reads inside DMA loops.
+__device__ __forceinline__ int32_t lds_load_i32(const void* p) {
+  int32_t v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+  return v;
+}
+
+typedef unsigned int lds_u32x2 __attribute__((ext_vector_type(2)));
+
+// Inline-asm LDS reads (invisible to the compiler's wait-count pass, see
+// lds_read128); results are used only after an lgkmcnt wait tied to them.
+template <int OFF>
+__device__ __forceinline__ lds_u32x2 lds_read_tr(uint32_t a) {
+  lds_u32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+  return v;
+}
+
+__device__ __forceinline__ lds_u32x2 lds_read64(uint32_t a) {
+  lds_u32x2 v;
+  asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(a));
+  return v;
+}
+
+template <int OFF>
+__device__ __forceinline__ int32_t lds_read_i32(uint32_t a) {
+  int32_t v;
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+  return v;
+}
+
+template <int OFF>
+__device__ __forceinline__ lds_u32x4 lds_read128_at(uint32_t a) {
+  lds_u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+  return v;
+}
+
+template <int N>
+__device__ __forceinline__ void lgkm_wait_tied(int32_t (&r)[N]) {
+  if constexpr (N == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
+  } else if constexpr (N == 5) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]));
+  } else {
+    static_assert(N == 4 || N == 5, "DMA instructions per wave");
+  }
+}
+
+__device__ __forceinline__ void lgkm_wait_frags(lds_u32x2 (&g)[4][2], lds_u32x2 (&x)[4][2]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(g[0][0]), "+v"(g[0][1]), "+v"(g[1][0]), "+v"(g[1][1]), "+v"(g[2][0]), "+v"(g[2][1]),
+                 "+v"(g[3][0]), "+v"(g[3][1]), "+v"(x[0][0]), "+v"(x[0][1]), "+v"(x[1][0]), "+v"(x[1][1]),
+                 "+v"(x[2][0]), "+v"(x[2][1]), "+v"(x[3][0]), "+v"(x[3][1]));
+}
+
+__device__ __forceinline__ void lgkm_wait_w(lds_u32x4 (&w)[2]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(w[0]), "+v"(w[1]));
+}
+
+// Wait until at most `ahead` slices (D DMA instructions each) are in flight.
+template <int D, int K>
+__device__ __forceinline__ void vm_wait_slices(int ahead) {
+  if constexpr (K == 0) {
+    vm_wait<0>();
+  } else {
+    if (ahead >= K) vm_wait<K * D>();
+    else vm_wait_slices<D, K - 1>(ahead);
+  }
+}
+
 // WM waves along the m-tile (64 rows each), 4 / WM along the n-tile: 128-row
 // tiles (2 x 2 waves, three workgroups per CU) or 256-row tiles (4 x 1,
 // two per CU, half the weight reads per output row).

@@ -1,0 +1,8 @@
+// Reduce GEMM instantiations for op type f16_t (see cvmm_reduce.h).
+#include "cvmm_reduce.h"
+
+namespace cvmm {
+hipError_t launch_routed_reduce_f16(const ReduceParams& p, hipStream_t stream) {
+  return launch_routed_reduce_op<f16_t>(p, stream);
+}
+}  // namespace cvmm

@@ -38,68 +38,6 @@ namespace cvmm {
 
 static __device__ uint4 g_cvmm_wg3_zero_page[64];
 
-typedef unsigned int lds_u32x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
-}
-
-// Inline-asm LDS reads (invisible to the compiler's wait-count pass, see
-// lds_read128); results are used only after an lgkmcnt wait tied to them.
-template <int OFF>
-__device__ __forceinline__ lds_u32x2 lds_read_tr(uint32_t a) {
-  lds_u32x2 v;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
-  return v;
-}
-
-template <int OFF>
-__device__ __forceinline__ int32_t lds_read_i32(uint32_t a) {
-  int32_t v;
-  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
-  return v;
-}
-
-template <int OFF>
-__device__ __forceinline__ lds_u32x4 lds_read128_at(uint32_t a) {
-  lds_u32x4 v;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
-  return v;
-}
-
-template <int N>
-__device__ __forceinline__ void lgkm_wait_tied(int32_t (&r)[N]) {
-  if constexpr (N == 4) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
-  } else if constexpr (N == 5) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]));
-  } else {
-    static_assert(N == 4 || N == 5, "DMA instructions per wave");
-  }
-}
-
-__device__ __forceinline__ void lgkm_wait_frags(lds_u32x2 (&g)[4][2], lds_u32x2 (&x)[4][2]) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(g[0][0]), "+v"(g[0][1]), "+v"(g[1][0]), "+v"(g[1][1]), "+v"(g[2][0]), "+v"(g[2][1]),
-                 "+v"(g[3][0]), "+v"(g[3][1]), "+v"(x[0][0]), "+v"(x[0][1]), "+v"(x[1][0]), "+v"(x[1][1]),
-                 "+v"(x[2][0]), "+v"(x[2][1]), "+v"(x[3][0]), "+v"(x[3][1]));
-}
-
-__device__ __forceinline__ void lgkm_wait_w(lds_u32x4 (&w)[2]) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(w[0]), "+v"(w[1]));
-}
-
-// Wait until at most `ahead` slices (D DMA instructions each) are in flight.
-template <int D, int K>
-__device__ __forceinline__ void vm_wait_slices(int ahead) {
-  if constexpr (K == 0) {
-    vm_wait<0>();
-  } else {
-    if (ahead >= K) vm_wait<K * D>();
-    else vm_wait_slices<D, K - 1>(ahead);
-  }
-}
-
 // 32 route rows of COLS 16-bit values.
 template <int COLS>
 struct RouteSlice {

@@ -102,6 +102,18 @@ bool fast_path(at::ScalarType op, int64_t d_in, int64_t d_out) {
   return (op == at::kBFloat16 || op == at::kHalf) && d_in % 8 == 0 && d_out % 8 == 0;
 }
 
+// Operands that the reduce GEMM reads by 16-byte copies: rows of `a` (row
+// stride `ld`) and the weight view `kv` in the op dtype with unit stride
+// along the product's K dimension `k_dim` (1 = d_in, 2 = d_out).
+bool rows16(const Tensor& t, int64_t ld) {
+  return (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15) == 0 && (ld * (int64_t)t.element_size()) % 16 == 0;
+}
+bool reduce_operands_ok(const Tensor& a, const Tensor& kv, int k_dim, at::ScalarType op) {
+  const int n_dim = 3 - k_dim;
+  return kv.scalar_type() == op && kv.stride(k_dim) == 1 && rows16(kv, kv.stride(0)) && rows16(kv, kv.stride(n_dim)) &&
+         rows16(a, a.stride(0));
+}
+
 at::TensorOptions opts(const Tensor& like, at::ScalarType dt) {
   return at::TensorOptions().dtype(dt).device(like.device());
 }
@@ -245,8 +257,10 @@ Tensor forward(const Tensor& x, const Tensor& keys, const OptT& keys_t, const Te
   }
   const int32_t od = (int32_t)op_id;
   Tensor out = at::empty({out_rows, d_out}, opts(x, op));
-  const size_t ws_bytes = cvmm_fwd_workspace_bytes(R, (int32_t)E, d_out, out_rows, od, 1, rw.has_value() ? 1 : 0,
-                                                   (int32_t)flags);
+  // route_pos is passed only with the stable sort's own perm
+  if (route_pos.has_value() && reduce_operands_ok(xf, kv, 1, op)) flags |= CVMM_FLAG_ROUTES_STABLE;
+  const size_t ws_bytes = cvmm_fwd_workspace_bytes(R, (int32_t)E, d_in, d_out, out_rows, od, od, 1,
+                                                   rw.has_value() ? 1 : 0, (int32_t)flags);
   OptT ws;
   if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(x, at::kByte));
   check(cvmm_fwd(ptr(xf), dtype_id(xf.scalar_type()), xf.size(0), xf.stride(0), ptr(kv), dtype_id(kv.scalar_type()),
@@ -318,7 +332,9 @@ std::tuple<OptT, OptT, OptT> backward(const Tensor& grad_output, const Tensor& x
     if (need_grad_x) gx = at::empty(xr.sizes(), opts(x, x.scalar_type()));
     if (need_grad_rw) grad_rw = at::empty(rw->sizes(), opts(*rw, rw->scalar_type()));
     const int64_t gx_rows = gx.has_value() ? gx->size(0) : xr.size(0);
-    const size_t ws_bytes = cvmm_bwd_x_workspace_bytes(R, (int32_t)E, d_in, gx_rows, 1, rw.has_value() ? 1 : 0,
+    // route_pos is passed only with the stable sort's own perm
+    if (route_pos.has_value() && reduce_operands_ok(g, kv, 2, op)) flags |= CVMM_FLAG_ROUTES_STABLE;
+    const size_t ws_bytes = cvmm_bwd_x_workspace_bytes(R, (int32_t)E, d_in, d_out, gx_rows, 1, rw.has_value() ? 1 : 0,
                                                        oi.has_value() ? 1 : 0, k, dtype_id(x.scalar_type()), od,
                                                        need_grad_rw ? 1 : 0, (int32_t)flags);
     OptT ws;
