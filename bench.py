@@ -265,6 +265,49 @@ def load_traffic(kernel: str, workload: str):
     return None
 
 
+def router_times(iters: int = 50, T: int = 16384, E: int = 128, k: int = 8):
+    """The router of the FFN stack ([16384, 128]
+    bf16 logits, top-8, renormalised) two ways: the reference callers' torch
+    lines (softmax, topk, renormalise; benchmark_ffn_moe.py:92-95) followed by
+    this library's selector sort, and the fused cvmm_route_topk.  Forward, and
+    forward + backward to the logits; HIP events around `iters` calls each."""
+    import cvmm_codex_amd as C
+    g = torch.Generator().manual_seed(0)
+    logits = (torch.randn(T, E, generator=g) * 2).to(torch.bfloat16).cuda().requires_grad_(True)
+    gw = torch.randn(T, k, generator=g).cuda()
+
+    def torch_lines(backward):
+        probs = torch.softmax(logits.float(), dim=-1)
+        w, sel = probs.topk(k, dim=-1)
+        w = w / w.sum(dim=-1, keepdim=True).clamp_min(1e-20)
+        s = C.cvmm_prepare_sel2(sel)
+        s._resolve(E)
+        if backward:
+            w.backward(gw)
+
+    def fused(backward):
+        w, _, _ = C.cvmm_route_topk(logits, k, True)
+        if backward:
+            w.backward(gw)
+
+    def timed(fn, backward):
+        for _ in range(5):
+            fn(backward)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            fn(backward)
+        b.record()
+        b.synchronize()
+        return a.elapsed_time(b) * 1000.0 / iters
+
+    out = {"shape": {"tokens": T, "experts": E, "top_k": k, "logits": "bf16"}}
+    for name, fn in (("torch_lines", torch_lines), ("fused", fused)):
+        out[name] = {"fwd_us": round(timed(fn, False), 2), "fwd_bwd_us": round(timed(fn, True), 2)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -275,6 +318,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["fwd", "bwd_w", "bwd_x", "cast_keys", "copy"], default=None,
                     help="launch only this phase --steps times, or the copy calibration (rocprofv3 runs)")
+    ap.add_argument("--router", action="store_true",
+                    help="time the fused router against the torch router lines (one JSON line) and exit")
     ap.add_argument("--tune", action="append", default=[], metavar="KNOB=VALUE",
                     help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, gemm_order, "
                          "reduce_min_topk) before running")
@@ -300,6 +345,9 @@ def main():
             ap.error(f"--tune {kv}: {N.lib().cvmm_last_error().decode()}")
 
     dev = torch.device("cuda:0")
+    if args.router:
+        print(json.dumps({"router": router_times()}), flush=True)
+        return
     if args.only == "copy":
         copy_calibration(iters=args.steps)
         return

@@ -11,6 +11,7 @@ from .api import (  # noqa: F401
     cvmm_expert_offsets,
     cvmm_prepare_sel,
     cvmm_prepare_sel2,
+    cvmm_route_topk,
     cvmm_triton_call,
     dtype_to_type_id,
     get_dtype,

@@ -25,8 +25,8 @@ TUNE_GEMM_ORDER = 3
 TUNE_REDUCE_MIN_TOPK = 4
 
 # kernel classes of the timing hooks (include/cvmm_hip.h CVMM_KC_*)
-KC_SORT, KC_OFFSETS, KC_CAST_KEYS, KC_GEMM_FWD, KC_GEMM_BWDX, KC_WGRAD, KC_COMBINE, KC_FILL, KC_REDUCE = (
-    1, 2, 4, 8, 16, 32, 64, 128, 256)
+KC_SORT, KC_OFFSETS, KC_CAST_KEYS, KC_GEMM_FWD, KC_GEMM_BWDX, KC_WGRAD, KC_COMBINE, KC_FILL, KC_REDUCE, KC_ROUTE = (
+    1, 2, 4, 8, 16, 32, 64, 128, 256, 512)
 
 _DTYPE_ID = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -48,6 +48,10 @@ _SIGS = {
     "cvmm_sort_routes_cast_keys": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _SZ,
                                                   _P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P]),
     "cvmm_cast_keys": (ctypes.c_int, [_P, _I32, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P]),
+    "cvmm_route_topk_workspace_bytes": (_SZ, [_I64, _I32, _I64]),
+    "cvmm_route_topk": (ctypes.c_int, [_P, _I32, _I64, _I64, _I32, _I64, _I32, _P, _P,
+                                       _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "cvmm_route_topk_backward": (ctypes.c_int, [_P, _I32, _I64, _I64, _I32, _I64, _I32, _P, _P, _P, _I64, _P]),
     "cvmm_fwd_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32]),
     "cvmm_fwd": (ctypes.c_int, [
         _P, _I32, _I64, _I64,                 # x, dtype, rows, ld

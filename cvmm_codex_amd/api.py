@@ -6,7 +6,8 @@ Same public surface, argument meaning and error behaviour as the reference:
 Function ``CVMM`` (:1521-1755), ``get_dtype`` / ``dtype_to_type_id`` (:30-44),
 ``create_kernels`` and ``_cvmm_expert_offsets`` (:68-78), plus the module
 attributes the reference tests patch (``cvmm_expert_offsets_call``,
-``cvmm_lowmem_chunk_size``).
+``cvmm_lowmem_chunk_size``).  ``cvmm_route_topk`` (no counterpart in
+cvmm.py) fuses the router lines its callers write before ``cvmm``.
 
 All arithmetic runs in the HIP kernels of ``libcvmm_hip.so`` (C ABI in
 ``include/cvmm_hip.h``), launched on torch's current stream; nothing here
@@ -38,7 +39,7 @@ def _compiling() -> bool:
 
 __all__ = [
     "CVMMSel", "cvmm_prepare_sel", "cvmm_prepare_sel2", "cvmm", "CVMM", "get_dtype",
-    "dtype_to_type_id", "create_kernels", "cvmm_expert_offsets", "cvmm_triton_call",
+    "dtype_to_type_id", "create_kernels", "cvmm_expert_offsets", "cvmm_triton_call", "cvmm_route_topk",
 ]
 
 
@@ -341,6 +342,67 @@ def cvmm_prepare_sel2(sel: Union[torch.Tensor, CVMMSel], w: Optional[torch.Tenso
     _require_device(sel, "sel")
     n_per_batch = sel.shape[-1]
     return CVMMSel._deferred(sel, _Routing(sel.reshape(-1), n_per_batch), route_input, w)
+
+
+# ----------------------------------------------------------------------------
+# router
+# ----------------------------------------------------------------------------
+
+class _RouteTopK(torch.autograd.Function):
+    """Eager path of cvmm_route_topk: the native router forward, its native
+    backward for the weights' gradient (logits dtype)."""
+
+    @staticmethod
+    def forward(ctx, logits: torch.Tensor, top_k: int, renormalize: bool):
+        w, sel, ssel, perm, tok, offsets, route_pos = N.host().route_topk(logits, top_k, renormalize,
+                                                                         N.stream_of(logits.device))
+        ctx.save_for_backward(logits, sel)
+        ctx.top_k, ctx.renormalize = top_k, renormalize
+        ctx.mark_non_differentiable(sel, ssel, perm, tok, offsets, route_pos)
+        return w, sel, ssel, perm, tok, offsets, route_pos
+
+    @staticmethod
+    def backward(ctx, grad_w, *_):
+        logits, sel = ctx.saved_tensors
+        if grad_w is None:
+            return None, None, None
+        g = N.host().route_topk_backward(logits, sel, grad_w.contiguous(), ctx.top_k, ctx.renormalize,
+                                         N.stream_of(logits.device))
+        return g, None, None
+
+
+def cvmm_route_topk(logits: torch.Tensor, k: int, renormalize: bool = True):
+    """The router lines of the reference's MoE callers in one native call
+    (benchmark_ffn_moe.py:91-97, benchmark_framework_moe.py:129-135):
+
+        probs = torch.softmax(logits.float(), dim=-1)
+        weights, sel = probs.topk(k, dim=-1)
+        weights = weights / weights.sum(dim=-1, keepdim=True).clamp_min(1e-20)   # renormalize
+        sel_up = cvmm_prepare_sel2(sel)
+
+    Returns ``(weights, sel, sel_up)``: fp32 weights ``[..., k]`` (gradient
+    flows to ``logits``), int64 expert ids ``[..., k]`` in probability order
+    (ties to the lower id) and the token-input selector, already sorted
+    (``cvmm_prepare_sel2(sel_up, weights, route_input=True)`` gives the
+    down-projection selector).  At most 1024 experts and k <= 64.
+    """
+    _require_device(logits, "logits")
+    if logits.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        logits = logits.float()
+    E = logits.shape[-1]
+    if not (0 < k <= E):
+        raise ValueError(f"cvmm_route_topk: k={k} outside 1..{E}")
+    lead = logits.shape[:-1]
+    if _compiling():
+        w, sel, ssel, perm, tok, offsets, route_pos = _ops.route_topk(logits, k, renormalize)
+    else:
+        w, sel, ssel, perm, tok, offsets, route_pos = _RouteTopK.apply(logits, k, renormalize)
+        perm._cvmm_route_pos = route_pos
+    sel = sel.view(*lead, k)
+    routing = _Routing(sel.reshape(-1), k)
+    routing.by_e[E] = (ssel, perm, tok, offsets)
+    routing.first_e = E
+    return w.view(*lead, k), sel, CVMMSel._deferred(sel, routing, False, None)
 
 
 # ----------------------------------------------------------------------------

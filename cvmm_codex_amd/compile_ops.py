@@ -4,7 +4,8 @@ The reference registers its forward primitive as ``mylib::cvmm_triton`` with
 a fake (meta) implementation (cvmm.py:808-812, :1436-1456) so that compiled
 callers can trace through ``CVMM``.  Here every native phase the API calls
 is an op with a fake implementation: the selector sort, the expert offsets,
-the weight cast, the forward and the backward products, plus
+the weight cast, the forward and the backward products, the router (with its
+backward registered as the op's autograd formula), plus
 ``cvmm_codex_amd::cvmm_triton`` with the reference op's schema.  The API
 routes through these ops only while torch.compile traces
 (``torch.compiler.is_compiling()``); eager calls go to the host glue directly,
@@ -141,3 +142,55 @@ def cvmm_triton(x: torch.Tensor, sel_index: torch.Tensor, sel: torch.Tensor, key
 @cvmm_triton.register_fake
 def _(x, sel_index, sel, keys, out_dtype, out_index, op_dtype):
     return x.new_empty((*sel.shape, keys.shape[2]), dtype=out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# router (its callers' softmax -> top-k -> renormalise -> sort, see
+# api.cvmm_route_topk): weights fp32 [T, k], sel int64 [T, k], then the sort's
+# sorted int32, perm, perm // k, offsets and inverse permutation
+# ---------------------------------------------------------------------------
+@torch.library.custom_op(f"{NS}::route_topk", mutates_args=())
+def route_topk(logits: torch.Tensor, top_k: int, renormalize: bool) -> Tuple[torch.Tensor, torch.Tensor,
+                                                                            torch.Tensor, torch.Tensor,
+                                                                            torch.Tensor, torch.Tensor,
+                                                                            torch.Tensor]:
+    out = N.host().route_topk(logits, top_k, renormalize, N.stream_of(logits.device))
+    return tuple(t.clone() for t in out)
+
+
+@route_topk.register_fake
+def _(logits, top_k, renormalize):
+    T = logits.numel() // logits.shape[-1]
+    E = logits.shape[-1]
+    R = T * top_k
+    return (logits.new_empty((T, top_k), dtype=torch.float32), logits.new_empty((T, top_k), dtype=torch.int64),
+            logits.new_empty((R,), dtype=torch.int32), logits.new_empty((R,), dtype=torch.int64),
+            logits.new_empty((R,), dtype=torch.int64), logits.new_empty((E,), dtype=torch.int64),
+            logits.new_empty((R,), dtype=torch.int32))
+
+
+@torch.library.custom_op(f"{NS}::route_topk_backward", mutates_args=())
+def route_topk_backward(logits: torch.Tensor, sel: torch.Tensor, grad_weights: torch.Tensor, top_k: int,
+                        renormalize: bool) -> torch.Tensor:
+    return N.host().route_topk_backward(logits, sel, grad_weights, top_k, renormalize, N.stream_of(logits.device))
+
+
+@route_topk_backward.register_fake
+def _(logits, sel, grad_weights, top_k, renormalize):
+    return torch.empty_like(logits, memory_format=torch.contiguous_format)
+
+
+def _route_setup(ctx, inputs, output):
+    logits, top_k, renormalize = inputs
+    ctx.save_for_backward(logits, output[1])
+    ctx.top_k, ctx.renormalize = top_k, renormalize
+
+
+def _route_backward(ctx, grad_w, *_):
+    logits, sel = ctx.saved_tensors
+    if grad_w is None:
+        return None, None, None
+    return route_topk_backward(logits, sel, grad_w.contiguous(), ctx.top_k, ctx.renormalize), None, None
+
+
+route_topk.register_autograd(_route_backward, setup_context=_route_setup)

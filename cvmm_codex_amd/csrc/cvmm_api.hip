@@ -244,7 +244,7 @@ extern "C" {
 
 const char* cvmm_last_error(void) { return g_err.c_str(); }
 
-int cvmm_abi_version(void) { return 6; }
+int cvmm_abi_version(void) { return 7; }
 
 int cvmm_timing_enable(uint32_t class_mask) {
   std::lock_guard<std::mutex> lk(g_timing_mu);
@@ -333,6 +333,60 @@ int cvmm_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_e
   if (n_routes > 0 && sorted_sel == nullptr) return fail(CVMM_ERR_INVALID, "cvmm_expert_offsets: sorted_sel NULL");
   return check_launch(timed(CVMM_KC_OFFSETS, (hipStream_t)stream, [&] { return launch_expert_offsets(sorted_sel, n_routes, n_experts, offsets, (hipStream_t)stream); }),
                       "cvmm_expert_offsets");
+}
+
+// ---------------------------------------------------------------------------
+size_t cvmm_route_topk_workspace_bytes(int64_t n_tokens, int32_t n_experts, int64_t top_k) {
+  if (n_tokens < 0 || n_experts <= 0 || top_k <= 0) return 0;
+  return route_workspace_bytes(n_tokens, n_experts, top_k);
+}
+
+static int route_args_ok(const char* what, int32_t logits_dtype, int64_t n_tokens, int64_t logits_ld,
+                         int32_t n_experts, int64_t top_k) {
+  if (!valid_dtype(logits_dtype)) return fail(CVMM_ERR_INVALID, "%s: invalid logits dtype", what);
+  if (n_tokens < 0 || n_experts <= 0 || top_k <= 0 || top_k > n_experts || logits_ld < n_experts)
+    return fail(CVMM_ERR_INVALID, "%s: bad sizes (T=%lld, E=%d, k=%lld, ld=%lld)", what, (long long)n_tokens,
+                n_experts, (long long)top_k, (long long)logits_ld);
+  if (n_experts > kRouteMaxExperts || top_k > kRouteMaxK)
+    return fail(CVMM_ERR_UNSUPPORTED, "%s: at most %d experts and top-%lld", what, kRouteMaxExperts,
+                (long long)kRouteMaxK);
+  if (n_tokens > (int64_t)0x7fffffff / top_k) return fail(CVMM_ERR_UNSUPPORTED, "%s: too many routes", what);
+  return CVMM_OK;
+}
+
+int cvmm_route_topk(const void* logits, int32_t logits_dtype, int64_t n_tokens, int64_t logits_ld,
+                    int32_t n_experts, int64_t top_k, int32_t renormalize, float* weights, int64_t* sel,
+                    int32_t* sorted_sel, int64_t* perm, int64_t* token_index, int64_t* offsets,
+                    int32_t* route_pos, void* workspace, size_t workspace_bytes, void* stream) {
+  int r = route_args_ok("cvmm_route_topk", logits_dtype, n_tokens, logits_ld, n_experts, top_k);
+  if (r) return r;
+  const size_t need = route_workspace_bytes(n_tokens, n_experts, top_k);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(CVMM_ERR_WORKSPACE, "cvmm_route_topk: workspace too small (%zu < %zu)", workspace_bytes, need);
+  if (n_tokens == 0) return CVMM_OK;
+  if (!logits || !weights || !sel || !sorted_sel || !perm || !offsets)
+    return fail(CVMM_ERR_INVALID, "cvmm_route_topk: NULL pointer");
+  hipStream_t s = (hipStream_t)stream;
+  return check_launch(timed(CVMM_KC_ROUTE, s, [&] { return launch_route_topk(logits, logits_dtype, n_tokens, logits_ld, n_experts, top_k,
+                                                               renormalize, weights, sel, sorted_sel, perm,
+                                                               token_index, offsets, route_pos, workspace, s); }),
+                      "cvmm_route_topk");
+}
+
+int cvmm_route_topk_backward(const void* logits, int32_t logits_dtype, int64_t n_tokens, int64_t logits_ld,
+                             int32_t n_experts, int64_t top_k, int32_t renormalize, const int64_t* sel,
+                             const float* grad_weights, void* grad_logits, int64_t grad_ld, void* stream) {
+  int r = route_args_ok("cvmm_route_topk_backward", logits_dtype, n_tokens, logits_ld, n_experts, top_k);
+  if (r) return r;
+  if (grad_ld < n_experts) return fail(CVMM_ERR_INVALID, "cvmm_route_topk_backward: grad row stride too small");
+  if (n_tokens == 0) return CVMM_OK;
+  if (!logits || !sel || !grad_weights || !grad_logits)
+    return fail(CVMM_ERR_INVALID, "cvmm_route_topk_backward: NULL pointer");
+  hipStream_t s = (hipStream_t)stream;
+  return check_launch(timed(CVMM_KC_ROUTE, s, [&] { return launch_route_topk_backward(logits, logits_dtype, n_tokens, logits_ld, n_experts,
+                                                                        top_k, renormalize, sel, grad_weights,
+                                                                        grad_logits, grad_ld, s); }),
+                      "cvmm_route_topk_backward");
 }
 
 // ---------------------------------------------------------------------------

@@ -132,6 +132,7 @@ void wgrad_geometry(int64_t M, int64_t N, int64_t n_routes, int32_t n_experts, i
 // selector preparation
 // ---------------------------------------------------------------------------
 size_t sort_workspace_bytes(int64_t n_routes, int32_t n_experts);
+int64_t sort_chunk_size(int64_t n_routes, int32_t n_experts);
 // A weight cast to run in the sort's scatter launch (vectorised cast only).
 struct CastRequest {
   const void* keys;
@@ -225,6 +226,30 @@ bool reduce_shape_ok(int32_t op_dtype, int64_t K, int64_t N, int32_t n_experts, 
 // ... with k-contiguous weight rows and output rows on 16-byte boundaries.
 bool reduce_align_ok(const void* b, int64_t b_sk, int64_t b_se, int64_t b_sn, const void* out, int32_t out_dtype,
                      int64_t out_ld);
+
+// The stable scatter of cvmm_sort_routes over int64 ids whose per-chunk
+// histogram (counts[chunk][E + 1], chunks of `chunk` routes) is already built.
+hipError_t launch_sort_scatter(const int64_t* sel, int64_t n_routes, int32_t n_experts, int64_t chunk, int64_t top_k,
+                               const int32_t* counts, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                               int64_t* offsets, int32_t* route_pos, int32_t* n_invalid_out, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// router: softmax -> top-k -> renormalise -> stable sort by expert
+// ---------------------------------------------------------------------------
+constexpr int32_t kRouteMaxExperts = 1024;  // logits of a token held in registers (16 per lane)
+constexpr int64_t kRouteMaxK = 64;          // lane j holds the token's j-th choice
+// Tokens per router workgroup (= per sort chunk): whole tokens, at least the
+// sort's chunk size in routes.
+int64_t route_chunk_tokens(int64_t n_tokens, int32_t n_experts, int64_t top_k);
+size_t route_workspace_bytes(int64_t n_tokens, int32_t n_experts, int64_t top_k);
+hipError_t launch_route_topk(const void* logits, int32_t logits_dtype, int64_t n_tokens, int64_t logits_ld,
+                             int32_t n_experts, int64_t top_k, int32_t renormalize, float* weights, int64_t* sel,
+                             int32_t* sorted_sel, int64_t* perm, int64_t* token_index, int64_t* offsets,
+                             int32_t* route_pos, void* workspace, hipStream_t stream);
+hipError_t launch_route_topk_backward(const void* logits, int32_t logits_dtype, int64_t n_tokens, int64_t logits_ld,
+                                      int32_t n_experts, int64_t top_k, int32_t renormalize, const int64_t* sel,
+                                      const float* grad_weights, void* grad_logits, int64_t grad_ld,
+                                      hipStream_t stream);
 
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 // out[t][n] = rnd(rnd(sum_j rnd(w[t*k+j], w_round) * buf[t*k+j][n], mid_dtype), out_dtype)

@@ -308,6 +308,21 @@ hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_rout
   return hipGetLastError();
 }
 
+hipError_t launch_sort_scatter(const int64_t* sel, int64_t n_routes, int32_t n_experts, int64_t chunk, int64_t top_k,
+                               const int32_t* counts, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                               int64_t* offsets, int32_t* route_pos, int32_t* n_invalid_out, hipStream_t stream) {
+  if (n_routes <= 0) return hipSuccess;
+  const int64_t n_chunks = (n_routes + chunk - 1) / chunk;
+  const size_t lds = (size_t)(n_experts + 1) * sizeof(int32_t);
+  const size_t lds_scatter = (n_experts + 1 <= kSortFastBuckets ? 2 : 1) * lds;
+  int n_bits = 0;
+  while ((1ll << n_bits) <= (int64_t)n_experts) ++n_bits;  // buckets 0..E
+  const ScatterArgs<int64_t> a{sel, n_routes, n_experts, chunk, n_chunks, counts, n_bits, top_k,
+                               sorted_sel, perm, token_index, route_pos, offsets, n_invalid_out};
+  hipLaunchKernelGGL(sort_scatter_kernel<int64_t>, dim3(n_chunks), dim3(kSortThreads), lds_scatter, stream, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_experts,
                                  int64_t* offsets, hipStream_t stream) {
   const int threads = 256;

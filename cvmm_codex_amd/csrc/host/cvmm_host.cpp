@@ -193,6 +193,51 @@ std::tuple<std::vector<Tensor>, OptT, OptT> sort_routes_cast(const Tensor& raw, 
   return {{ssel, perm, tok, off, pos}, kt, kn};
 }
 
+// ---------------------------------------------------------------------------
+// router (no counterpart in cvmm.py; its callers' softmax -> top-k ->
+// renormalise -> cvmm_prepare_sel2): (weights fp32 [T, k], sel int64 [T, k],
+// sorted int32, perm, perm // k, offsets, route_pos)
+// ---------------------------------------------------------------------------
+std::vector<Tensor> route_topk(const Tensor& logits, int64_t top_k, bool renormalize, int64_t stream) {
+  require_device(logits, "logits");
+  Tensor l = logits.reshape({-1, logits.size(-1)});
+  if (l.stride(-1) != 1) l = l.contiguous();
+  const int64_t T = l.size(0), E = l.size(1);
+  const int64_t R = T * top_k;
+  Tensor w = at::empty({T, top_k}, opts(l, at::kFloat));
+  Tensor sel = at::empty({T, top_k}, opts(l, at::kLong));
+  Tensor i32 = at::empty({2 * R}, opts(l, at::kInt));
+  Tensor i64 = at::empty({2 * R + E}, opts(l, at::kLong));
+  Tensor ssel = i32.narrow(0, 0, R), pos = i32.narrow(0, R, R);
+  Tensor perm = i64.narrow(0, 0, R), tok = i64.narrow(0, R, R), off = i64.narrow(0, 2 * R, E);
+  const size_t ws_bytes = cvmm_route_topk_workspace_bytes(T, (int32_t)E, top_k);
+  Tensor ws = sort_workspace(l, stream, ws_bytes);
+  check(cvmm_route_topk(ptr(l), dtype_id(l.scalar_type()), T, l.stride(0), (int32_t)E, top_k, renormalize ? 1 : 0,
+                        tptr<float>(w), tptr<int64_t>(sel), tptr<int32_t>(ssel), tptr<int64_t>(perm),
+                        tptr<int64_t>(tok), tptr<int64_t>(off), tptr<int32_t>(pos), ptr(ws), (size_t)ws.numel(),
+                        (void*)stream),
+        "cvmm_route_topk");
+  return {w, sel, ssel, perm, tok, off, pos};
+}
+
+Tensor route_topk_backward(const Tensor& logits, const Tensor& sel, const Tensor& grad_weights, int64_t top_k,
+                           bool renormalize, int64_t stream) {
+  require_device(logits, "logits");
+  Tensor l = logits.reshape({-1, logits.size(-1)});
+  if (l.stride(-1) != 1) l = l.contiguous();
+  const int64_t T = l.size(0), E = l.size(1);
+  Tensor s = sel.reshape({-1}).contiguous();
+  Tensor g = grad_weights.reshape({-1}).to(at::kFloat).contiguous();
+  if (s.numel() != T * top_k || g.numel() != T * top_k)
+    throw py::value_error("cvmm_route_topk: sel / grad have the wrong size");
+  Tensor out = at::empty({T, E}, opts(l, l.scalar_type()));
+  check(cvmm_route_topk_backward(ptr(l), dtype_id(l.scalar_type()), T, l.stride(0), (int32_t)E, top_k,
+                                 renormalize ? 1 : 0, tptr<int64_t>(s), tptr<float>(g), ptr(out), out.stride(0),
+                                 (void*)stream),
+        "cvmm_route_topk_backward");
+  return out.view(logits.sizes());
+}
+
 Tensor expert_offsets(const Tensor& sorted, int64_t n_experts, int64_t stream) {
   require_device(sorted, "sorted_experts");
   Tensor s = sorted_i32(sorted);
@@ -358,6 +403,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "Host glue of cvmm_codex_amd: one call per CVMM phase into libcvmm_hip.so";
   m.def("sort_routes", &sort_routes, py::arg("raw"), py::arg("n_experts"), py::arg("top_k"), py::arg("stream"));
   m.def("expert_offsets", &expert_offsets, py::arg("sorted"), py::arg("n_experts"), py::arg("stream"));
+  m.def("route_topk", &route_topk, py::arg("logits"), py::arg("top_k"), py::arg("renormalize"), py::arg("stream"));
+  m.def("route_topk_backward", &route_topk_backward, py::arg("logits"), py::arg("sel"), py::arg("grad_weights"),
+        py::arg("top_k"), py::arg("renormalize"), py::arg("stream"));
   m.def("sort_routes_cast", &sort_routes_cast, py::arg("raw"), py::arg("n_experts"), py::arg("top_k"),
         py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"), py::arg("stream"));
   m.def("cast_keys", &cast_keys, py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"),

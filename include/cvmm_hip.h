@@ -61,6 +61,7 @@ extern "C" {
 #define CVMM_KC_COMBINE 64    /* top-k row combine / fp32 cast / gate-grad sum */
 #define CVMM_KC_FILL 128      /* zero fills */
 #define CVMM_KC_REDUCE 256    /* reduce GEMM of a top-k sum (its route gather: COMBINE) */
+#define CVMM_KC_ROUTE 512     /* router (softmax, top-k, histogram) + its scatter; router backward */
 
 /* Thread-local description of the last error. */
 const char* cvmm_last_error(void);
@@ -133,6 +134,32 @@ int cvmm_sort_routes_cast_keys(const void* sel, int32_t sel_is_int64, int64_t n_
                                size_t workspace_bytes, const void* keys, int32_t keys_dtype, int64_t d_in,
                                int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj, int32_t out_dtype,
                                void* keys_t, void* keys_n, void* stream);
+
+/* Router (no counterpart in cvmm.py; replaces its callers' router lines,
+ * benchmark_ffn_moe.py:91-97 and benchmark_framework_moe.py:129-135:
+ *   probs = softmax(logits.float()); weights, sel = probs.topk(top_k)
+ *   weights = weights / weights.sum(-1).clamp_min(1e-20)   (renormalize != 0)
+ *   cvmm_prepare_sel2(sel)                                  (cvmm.py:1786-1803)).
+ * logits: [n_tokens][n_experts] rows (row stride logits_ld), fp32 / bf16 /
+ * fp16.  Writes weights[n_tokens * top_k] (fp32) and sel[n_tokens * top_k]
+ * (int64) in probability order (descending, ties to the lower expert id, NaN
+ * lowest), then the outputs of cvmm_sort_routes for sel (token_index and
+ * route_pos may be NULL).  Two launches: the router (one wave per token,
+ * leaving the sort's per-chunk histogram) and the sort's stable scatter.
+ * Limits: n_experts <= 1024, top_k <= min(64, n_experts). */
+size_t cvmm_route_topk_workspace_bytes(int64_t n_tokens, int32_t n_experts, int64_t top_k);
+int cvmm_route_topk(const void* logits, int32_t logits_dtype, int64_t n_tokens, int64_t logits_ld,
+                    int32_t n_experts, int64_t top_k, int32_t renormalize, float* weights, int64_t* sel,
+                    int32_t* sorted_sel, int64_t* perm, int64_t* token_index, int64_t* offsets,
+                    int32_t* route_pos, void* workspace, size_t workspace_bytes, void* stream);
+/* Gradient of the router's weights with respect to the logits (the softmax,
+ * top-k and renormalisation backward of the lines above):
+ * grad_logits[t][e] = p_e (g_e - sum_i g_i p_i), g = d loss / d probs, in the
+ * logits dtype (row stride grad_ld).  sel and grad_weights as written and
+ * received for cvmm_route_topk's outputs. */
+int cvmm_route_topk_backward(const void* logits, int32_t logits_dtype, int64_t n_tokens, int64_t logits_ld,
+                             int32_t n_experts, int64_t top_k, int32_t renormalize, const int64_t* sel,
+                             const float* grad_weights, void* grad_logits, int64_t grad_ld, void* stream);
 
 /* offsets[e] = #{i : sorted_sel[i] <= e}; replaces cvmm_expert_offsets
  * (cvmm.py:1108-1120, kernel cvmm.py:315-335). */

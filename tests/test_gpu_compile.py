@@ -85,3 +85,49 @@ def test_reference_op_schema_matches_the_api_forward():
                            torch.bfloat16, s.out_index, torch.bfloat16)
     assert z.shape == y.shape
     assert torch.equal(z, y)
+
+
+def _router_ffn(x, gate, w_up, w_down, k=4):
+    """benchmark_ffn_moe.py:89-98 with the fused router."""
+    B, T, D = x.shape
+    H = w_up.shape[2]
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        logits = x @ gate
+        weights, _, sel_up = C.cvmm_route_topk(logits, k, True)
+        hidden = torch.nn.functional.gelu(C.cvmm(x, sel_up, w_up))
+        sel_down = C.cvmm_prepare_sel2(sel_up, weights, route_input=True)
+        return C.cvmm(hidden.view(B, T, k, H), sel_down, w_down)
+
+
+def test_compiled_router_stack_matches_eager():
+    """The FFN stack with the fused router, one graph: router op (with its
+    registered backward), both projections and the gate gradient."""
+    torch._dynamo.reset()
+    g = torch.Generator().manual_seed(8)
+    x0 = torch.randn(2, 64, 128, generator=g).to(torch.bfloat16).cuda()
+    gate0 = (torch.randn(128, 16, generator=g) / 12).cuda()
+    up0 = (torch.randn(16, 128, 64, generator=g) / 12).cuda()
+    down0 = (torch.randn(16, 64, 128, generator=g) / 8).cuda()
+    gy = torch.randn(2, 64, 128, generator=g).cuda()
+
+    def run(fn):
+        ts = [t.clone().requires_grad_(True) for t in (x0, gate0, up0, down0)]
+        y = fn(*ts)
+        y.backward(gy.to(y.dtype))
+        torch.cuda.synchronize()
+        return [y.detach()] + [t.grad for t in ts]
+
+    eager = run(_router_ffn)
+    compiled = run(torch.compile(_router_ffn, backend="aot_eager", fullgraph=True))
+    for name, a, b in zip(("out", "x", "gate", "up", "down"), eager, compiled):
+        assert torch.equal(a, b), name
+
+
+def test_router_ops_pass_opcheck():
+    g = torch.Generator().manual_seed(9)
+    logits = (torch.randn(40, 24, generator=g)).to(torch.bfloat16).cuda()
+    utils = ("test_schema", "test_faketensor")
+    torch.library.opcheck(ops.route_topk, (logits, 5, True), test_utils=utils)
+    w, sel, *_ = ops.route_topk(logits, 5, True)
+    gw = torch.randn(40, 5, generator=g).cuda()
+    torch.library.opcheck(ops.route_topk_backward, (logits, sel, gw, 5, True), test_utils=utils)

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.cvmm_abi_version() == 6
+    assert lib.cvmm_abi_version() == 7
 
 
 def test_workspace_queries(lib):
@@ -114,3 +114,18 @@ def test_tuning_knob_rejects_bad_values(lib):
     assert lib.cvmm_tuning_set(N.TUNE_GEMM_ORDER, 0) == 0
     assert lib.cvmm_tuning_set(N.TUNE_REDUCE_MIN_TOPK, -1) != 0
     assert lib.cvmm_tuning_set(N.TUNE_REDUCE_MIN_TOPK, 0) == 0
+
+
+def test_router_arguments_fail_before_launch(lib):
+    assert lib.cvmm_route_topk_workspace_bytes(16384, 128, 8) > 129 * 4
+    # k > E, E > 1024, k > 64, bad dtype, missing workspace
+    assert lib.cvmm_route_topk(None, 0, 16, 8, 8, 9, 1, None, None, None, None, None, None, None, None, 0, None) == 1
+    assert lib.cvmm_route_topk(None, 0, 16, 2048, 2048, 8, 1, None, None, None, None, None, None, None, None, 0,
+                               None) == 2
+    assert lib.cvmm_route_topk(None, 0, 16, 128, 128, 65, 1, None, None, None, None, None, None, None, None, 0,
+                               None) == 2
+    assert lib.cvmm_route_topk(None, 7, 16, 128, 128, 8, 1, None, None, None, None, None, None, None, None, 0,
+                               None) == 1
+    assert lib.cvmm_route_topk(None, 0, 16, 128, 128, 8, 1, None, None, None, None, None, None, None, None, 0,
+                               None) == 3
+    assert lib.cvmm_route_topk_backward(None, 0, 16, 128, 128, 8, 1, None, None, None, 64, None) == 1

@@ -315,3 +315,69 @@ def test_golden_catches_planted_mistakes(mutant):
 def test_golden_catches_offsets_off_by_one(monkeypatch):
     monkeypatch.setattr(O, "expert_offsets", _offsets_off_by_one)
     assert not _golden_passes(O)
+
+
+# ---------------------------------------------------------------------------
+# router oracle (oracle/router_oracle.py) against torch's own CPU routines
+# ---------------------------------------------------------------------------
+
+def _torch_router(logits: torch.Tensor, k: int, renormalize: bool):
+    """benchmark_ffn_moe.py:92-94 on the CPU in float64."""
+    probs = torch.softmax(logits.double(), dim=-1)
+    w, sel = probs.topk(k, dim=-1)
+    if renormalize:
+        w = w / w.sum(dim=-1, keepdim=True).clamp_min(1e-20)
+    return w, sel
+
+
+@pytest.mark.parametrize("T,E,k,renorm", [(64, 128, 8, True), (37, 100, 3, False), (16, 64, 64, True),
+                                          (9, 1000, 1, True), (33, 17, 17, False)])
+def test_router_oracle_matches_torch(T, E, k, renorm):
+    from oracle import router_oracle as RO
+    g = torch.Generator().manual_seed(T * 1000 + E + k)
+    logits = torch.randn(T, E, generator=g) * 3
+    w, sel, meta = RO.route_topk(logits.numpy(), k, renorm)
+    tw, tsel = _torch_router(logits, k, renorm)
+    np.testing.assert_array_equal(sel, tsel.numpy())
+    np.testing.assert_allclose(w, tw.numpy(), rtol=1e-12, atol=1e-15)
+    if renorm:
+        np.testing.assert_allclose(w.sum(-1), 1.0, rtol=1e-12)
+    ref = O.prepare_sel2(tsel.numpy())
+    np.testing.assert_array_equal(meta.sel, ref.sel)
+    np.testing.assert_array_equal(meta.sel_index, ref.sel_index)
+    np.testing.assert_array_equal(meta.out_index, ref.out_index)
+
+
+@pytest.mark.parametrize("E,k,renorm", [(128, 8, True), (128, 8, False), (40, 40, True), (300, 2, True)])
+def test_router_oracle_backward_matches_autograd(E, k, renorm):
+    from oracle import router_oracle as RO
+    g = torch.Generator().manual_seed(E * 7 + k)
+    T = 24
+    logits = (torch.randn(T, E, generator=g) * 2).double().requires_grad_(True)
+    w, sel = _torch_router(logits, k, renorm)
+    gw = torch.randn(T, k, generator=g).double()
+    w.backward(gw)
+    got = RO.route_topk_backward(logits.detach().numpy(), sel.numpy(), gw.numpy(), renorm)
+    np.testing.assert_allclose(got, logits.grad.numpy(), rtol=1e-10, atol=1e-13)
+
+
+def test_router_oracle_ties_go_to_the_lower_id():
+    from oracle import router_oracle as RO
+    logits = np.array([[0.0, 1.0, 1.0, 0.5, 1.0]])
+    w, sel, _ = RO.route_topk(logits, 3, False)
+    np.testing.assert_array_equal(sel, [[1, 2, 4]])
+    np.testing.assert_allclose(w[0], RO.softmax(logits)[0, [1, 2, 4]])
+
+
+def test_router_oracle_catches_a_planted_mistake(monkeypatch):
+    """A dropped renormalisation term in the backward fails the autograd check."""
+    from oracle import router_oracle as RO
+    g = torch.Generator().manual_seed(5)
+    logits = torch.randn(8, 32, generator=g).double().requires_grad_(True)
+    w, sel = _torch_router(logits, 4, True)
+    gw = torch.randn(8, 4, generator=g).double()
+    w.backward(gw)
+    good = RO.route_topk_backward(logits.detach().numpy(), sel.numpy(), gw.numpy(), True)
+    bad = RO.route_topk_backward(logits.detach().numpy(), sel.numpy(), gw.numpy(), False)
+    assert np.allclose(good, logits.grad.numpy(), rtol=1e-10, atol=1e-13)
+    assert not np.allclose(bad, logits.grad.numpy(), rtol=1e-6, atol=1e-9)
