@@ -308,6 +308,38 @@ def router_times(iters: int = 50, T: int = 16384, E: int = 128, k: int = 8):
     return out
 
 
+def ffn_times(steps: int = 10, warmup: int = 3):
+    """The FFN stack of BASELINE.json configs[4] (16384 tokens, 2048 -> 512 ->
+    2048, 128 experts, top-8, Zipf-skewed gate; benchmark_ffn_moe.py:89-98),
+    forward + backward, two ways: written as the reference's callers write it
+    (torch router lines, F.gelu around cvmm) and with the library's fused
+    router and up projection + GELU."""
+    s = W.c5_ffn_stack().to(torch.device("cuda"))
+    params = [t.clone().requires_grad_(True) for t in (s.x, s.gate, s.w_up, s.w_down)]
+    import cvmm_codex_amd as C
+
+    def step(fwd):
+        for t in params:
+            t.grad = None
+        out = fwd(s, C, *params)
+        out.backward(s.grad_out)
+
+    res = {"shape": {"tokens": 16384, "d_model": 2048, "hidden": 512, "experts": 128, "top_k": 8}}
+    for name, fwd in (("composed", W.ffn_forward), ("fused", W.ffn_forward_fused)):
+        for _ in range(warmup):
+            step(fwd)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            step(fwd)
+        b.record()
+        b.synchronize()
+        ms = a.elapsed_time(b) / steps
+        res[name] = {"ms_per_step": round(ms, 4), "tflops": round(s.flops / (ms * 1e-3) / 1e12, 2)}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -318,6 +350,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["fwd", "bwd_w", "bwd_x", "cast_keys", "copy"], default=None,
                     help="launch only this phase --steps times, or the copy calibration (rocprofv3 runs)")
+    ap.add_argument("--ffn", action="store_true",
+                    help="time the FFN stack (configs[4]) composed vs with the fused router and GELU (one JSON "
+                         "line) and exit")
     ap.add_argument("--router", action="store_true",
                     help="time the fused router against the torch router lines (one JSON line) and exit")
     ap.add_argument("--tune", action="append", default=[], metavar="KNOB=VALUE",
@@ -347,6 +382,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.router:
         print(json.dumps({"router": router_times()}), flush=True)
+        return
+    if args.ffn:
+        print(json.dumps({"ffn": ffn_times()}), flush=True)
         return
     if args.only == "copy":
         copy_calibration(iters=args.steps)

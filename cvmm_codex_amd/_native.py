@@ -61,6 +61,15 @@ _SIGS = {
         _P, _P, _P, _I32, _I64,               # offsets, route_pos, rw, rw dtype, reduce_k
         _I32, _P, _I32, _I64, _I64,           # op, out, out dtype, out rows, out ld
         _I32, _P, _SZ, _P]),                  # flags, ws, ws bytes, stream
+    "cvmm_fwd_gelu": (ctypes.c_int, [
+        _P, _I32, _I64, _I64,                 # x, dtype, rows, ld
+        _P, _I32, _I32, _I64, _I64,           # keys, dtype, E, d_in, d_out
+        _I64, _I64, _I64,                     # key strides
+        _P, _P, _P, _I64,                     # sorted_sel, sel_index, out_index, R
+        _P, _P,                               # offsets, route_pos
+        _I32, _P, _I32, _I64, _I64, _P,       # op, out, out dtype, out rows, out ld, pre_act
+        _I32, _P, _SZ, _P]),                  # flags, ws, ws bytes, stream
+    "cvmm_gelu_backward": (ctypes.c_int, [_P, _I32, _I64, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P]),
     "cvmm_bwd_x_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I64, _I32, _I32, _I32, _I64, _I32, _I32, _I32,
                                          _I32]),
     "cvmm_bwd_x": (ctypes.c_int, [

@@ -6,8 +6,9 @@ Same public surface, argument meaning and error behaviour as the reference:
 Function ``CVMM`` (:1521-1755), ``get_dtype`` / ``dtype_to_type_id`` (:30-44),
 ``create_kernels`` and ``_cvmm_expert_offsets`` (:68-78), plus the module
 attributes the reference tests patch (``cvmm_expert_offsets_call``,
-``cvmm_lowmem_chunk_size``).  ``cvmm_route_topk`` (no counterpart in
-cvmm.py) fuses the router lines its callers write before ``cvmm``.
+``cvmm_lowmem_chunk_size``).  ``cvmm_route_topk`` and ``cvmm_gelu`` (no
+counterpart in cvmm.py) fuse the router lines its callers write before
+``cvmm`` and the GELU they apply to the up projection.
 
 All arithmetic runs in the HIP kernels of ``libcvmm_hip.so`` (C ABI in
 ``include/cvmm_hip.h``), launched on torch's current stream; nothing here
@@ -40,6 +41,7 @@ def _compiling() -> bool:
 __all__ = [
     "CVMMSel", "cvmm_prepare_sel", "cvmm_prepare_sel2", "cvmm", "CVMM", "get_dtype",
     "dtype_to_type_id", "create_kernels", "cvmm_expert_offsets", "cvmm_triton_call", "cvmm_route_topk",
+    "cvmm_gelu",
 ]
 
 
@@ -518,6 +520,62 @@ class CVMM(torch.autograd.Function):
                                             keys_n=ctx.keys_n)
         ctx.keys_n = None
         return grad_x, None, None, None, grad_w, None, grad_rw
+
+
+class CVMMGelu(torch.autograd.Function):
+    """F.gelu(CVMM(...)) for unweighted selections: the forward GEMM writes
+    gelu(h) and keeps h (its own output) for the backward, which applies the
+    GELU derivative natively and then runs CVMM's backward."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, raw_sel: torch.Tensor, sel_index: torch.Tensor, sel: torch.Tensor,
+                keys: torch.Tensor, out_index: Optional[torch.Tensor] = None):
+        out_type = get_dtype()
+        keys_t = keys_n = None
+        if _fast_path(out_type, keys.shape[1], keys.shape[2]):
+            need_n = ctx.needs_input_grad[0]
+            pre = _take_cast(keys, out_type, need_n)
+            keys_t, keys_n = pre if pre is not None else _cast_keys(keys, out_type, True, need_n)
+        n_experts = keys.shape[0]
+        R = sel.numel()
+        y, h = N.host().forward_gelu(x, keys, keys_t, sel, sel_index, out_index, _offsets_for(sel, n_experts),
+                                     _route_pos(out_index if out_index is not None else sel_index, R),
+                                     N.dtype_id(out_type), _flags(), N.stream_of(x.device))
+        ctx.save_for_backward(x, keys, raw_sel, sel, sel_index, out_index, h)
+        ctx.keys_n = keys_n
+        ctx.op_type = out_type
+        return y.view(*sel.shape, keys.shape[2])
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        x, keys, raw_sel, sel, sel_index, out_index, h = ctx.saved_tensors
+        gh = N.host().gelu_backward(grad_output, h, N.stream_of(h.device))
+        grad_x, grad_w, _ = _backward(ctx, gh.view(grad_output.shape), x, keys, raw_sel, sel, sel_index,
+                                      out_index, None, ctx.needs_input_grad[0], ctx.needs_input_grad[4], False,
+                                      keys_n=ctx.keys_n)
+        ctx.keys_n = None
+        return grad_x, None, None, None, grad_w, None
+
+
+def cvmm_gelu(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.Tensor) -> torch.Tensor:
+    """``F.gelu(cvmm(x, sel, keys))`` -- the up projection of the reference's
+    MoE callers (benchmark_ffn_moe.py:96) -- with the GELU in the forward
+    GEMM's epilogue when that GEMM is the long-K kernel (d_in > 128, 16-bit
+    op): the pre-activation is written once, for the backward, instead of
+    being read back by a separate GELU pass.  Same results as the
+    composition; a weighted selection (or torch.compile tracing) runs the
+    composition itself."""
+    if not isinstance(sel, CVMMSel):
+        sel = cvmm_prepare_sel(sel, keys.shape[0])
+    if sel.reduction_weight is not None or _compiling():
+        return torch.nn.functional.gelu(cvmm(x, sel, keys))
+    create_kernels()
+    cast = None
+    op = get_dtype()
+    if sel._pending() and keys.is_cuda and _fast_path(op, keys.shape[1], keys.shape[2]):
+        cast = (keys, op, torch.is_grad_enabled() and x.requires_grad)
+    sel._resolve(keys.shape[0], cast)
+    return CVMMGelu.apply(x, sel._raw_shape_tensor(), sel.sel_index, sel.sel, keys, sel.out_index)
 
 
 known_shapes = set()

@@ -22,6 +22,7 @@ hipError_t launch_wgrad_f32(const WgradParams& p, hipStream_t stream);
 
 hipError_t launch_routed_gemm_nt_bf16(const GemmParams& p, hipStream_t stream);
 hipError_t launch_routed_gemm_nt_f16(const GemmParams& p, hipStream_t stream);
+bool routed_gemm_ring_applies(const GemmParams& p, int32_t op);
 
 // Fast path (DMA-staged, 16-bit k-contiguous operands) when eligible, else the
 // general kernel (any storage type / stride / width).
@@ -33,6 +34,7 @@ static bool nt_eligible(const GemmParams& p, int32_t op) {
 
 hipError_t launch_routed_gemm(const GemmParams& p, int32_t op, hipStream_t s) {
   if (nt_eligible(p, op)) return op == kBF16 ? launch_routed_gemm_nt_bf16(p, s) : launch_routed_gemm_nt_f16(p, s);
+  if (p.act != 0) return hipErrorInvalidValue;  // the activation epilogue exists in the ring kernel only
   if (op == kBF16) return launch_routed_gemm_bf16(p, s);
   if (op == kF16) return launch_routed_gemm_f16(p, s);
   if (op == kF32) return launch_routed_gemm_f32(p, s);
@@ -244,7 +246,7 @@ extern "C" {
 
 const char* cvmm_last_error(void) { return g_err.c_str(); }
 
-int cvmm_abi_version(void) { return 7; }
+int cvmm_abi_version(void) { return 8; }
 
 int cvmm_timing_enable(uint32_t class_mask) {
   std::lock_guard<std::mutex> lk(g_timing_mu);
@@ -451,13 +453,17 @@ size_t cvmm_fwd_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_i
   return c.used;
 }
 
-int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const void* keys, int32_t keys_dtype,
-             int32_t n_experts, int64_t d_in, int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj,
-             const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index, int64_t n_routes,
-             const int64_t* offsets, const int32_t* route_pos, const void* rw, int32_t rw_dtype, int64_t reduce_k,
-             int32_t op_dtype,
-             void* out, int32_t out_dtype, int64_t out_rows, int64_t out_ld, int32_t flags, void* workspace,
-             size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// cvmm_fwd; with pre_act != NULL (unweighted only) the stored values go
+// through the GELU: out = gelu(h), pre_act = h.
+static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const void* keys,
+                    int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out, int64_t k_se, int64_t k_si,
+                    int64_t k_sj, const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index,
+                    int64_t n_routes, const int64_t* offsets, const int32_t* route_pos, const void* rw,
+                    int32_t rw_dtype, int64_t reduce_k, int32_t op_dtype, void* out, int32_t out_dtype,
+                    int64_t out_rows, int64_t out_ld, void* pre_act, int32_t flags, void* workspace,
+                    size_t workspace_bytes, void* stream) {
   if (!valid_dtype(x_dtype) || !valid_dtype(keys_dtype) || !valid_dtype(op_dtype) || !valid_dtype(out_dtype) ||
       (rw && !valid_dtype(rw_dtype)))
     return fail(CVMM_ERR_INVALID, "cvmm_fwd: invalid dtype id");
@@ -518,6 +524,17 @@ int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const
 
   if (!weighted) {
     p.epi = kEpiStore; p.out = out; p.out_dtype = out_dtype; p.out_ld = out_ld; p.out_rows = out_rows;
+    if (pre_act != nullptr) {
+      p.act = 1; p.aux = pre_act;
+      if (!(nt_eligible(p, op_dtype) && routed_gemm_ring_applies(p, op_dtype))) {
+        // not the ring kernel: the products to pre_act, then a GELU pass
+        p.act = 0; p.aux = nullptr; p.out = pre_act;
+        int r = check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
+        if (r) return r;
+        return check_launch(timed_combine(s, [&] { return launch_gelu_rows(pre_act, out_dtype, out_ld, out_rows, d_out, out, out_dtype, out_ld, s); }),
+                            "cvmm_fwd_gelu(gelu)");
+      }
+    }
     return check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
   }
   if (red) {
@@ -558,6 +575,48 @@ int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const
   return check_launch(timed_combine(s, [&] { return launch_combine_rows(ybuf, out_dtype, d_out, inv, rp, rw, rw_dtype, out_dtype, out_rows, reduce_k, d_out,
                                           out_dtype, out, out_dtype, out_ld, s); }),
                       "cvmm_fwd(combine)");
+}
+
+
+extern "C" {
+
+int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const void* keys, int32_t keys_dtype,
+             int32_t n_experts, int64_t d_in, int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj,
+             const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index, int64_t n_routes,
+             const int64_t* offsets, const int32_t* route_pos, const void* rw, int32_t rw_dtype, int64_t reduce_k,
+             int32_t op_dtype,
+             void* out, int32_t out_dtype, int64_t out_rows, int64_t out_ld, int32_t flags, void* workspace,
+             size_t workspace_bytes, void* stream) {
+  return fwd_core(x, x_dtype, x_rows, x_ld, keys, keys_dtype, n_experts, d_in, d_out, k_se, k_si, k_sj, sorted_sel,
+                  sel_index, out_index, n_routes, offsets, route_pos, rw, rw_dtype, reduce_k, op_dtype, out,
+                  out_dtype, out_rows, out_ld, nullptr, flags, workspace, workspace_bytes, stream);
+}
+
+int cvmm_fwd_gelu(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const void* keys,
+                  int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out, int64_t k_se, int64_t k_si,
+                  int64_t k_sj, const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index,
+                  int64_t n_routes, const int64_t* offsets, const int32_t* route_pos, int32_t op_dtype, void* out,
+                  int32_t out_dtype, int64_t out_rows, int64_t out_ld, void* pre_act, int32_t flags,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  if (pre_act == nullptr && n_routes > 0) return fail(CVMM_ERR_INVALID, "cvmm_fwd_gelu: pre_act NULL");
+  return fwd_core(x, x_dtype, x_rows, x_ld, keys, keys_dtype, n_experts, d_in, d_out, k_se, k_si, k_sj, sorted_sel,
+                  sel_index, out_index, n_routes, offsets, route_pos, nullptr, 0, 1, op_dtype, out, out_dtype,
+                  out_rows, out_ld, pre_act, flags, workspace, workspace_bytes, stream);
+}
+
+int cvmm_gelu_backward(const void* grad, int32_t grad_dtype, int64_t grad_ld, const void* pre_act,
+                       int32_t pre_dtype, int64_t pre_ld, int64_t rows, int64_t cols, void* grad_pre,
+                       int32_t grad_pre_dtype, int64_t grad_pre_ld, void* stream) {
+  if (!valid_dtype(grad_dtype) || !valid_dtype(pre_dtype) || !valid_dtype(grad_pre_dtype))
+    return fail(CVMM_ERR_INVALID, "cvmm_gelu_backward: invalid dtype id");
+  if (rows < 0 || cols < 0 || grad_ld < cols || pre_ld < cols || grad_pre_ld < cols)
+    return fail(CVMM_ERR_INVALID, "cvmm_gelu_backward: bad sizes");
+  if (rows == 0 || cols == 0) return CVMM_OK;
+  if (!grad || !pre_act || !grad_pre) return fail(CVMM_ERR_INVALID, "cvmm_gelu_backward: NULL pointer");
+  hipStream_t s = (hipStream_t)stream;
+  return check_launch(timed_combine(s, [&] { return launch_gelu_backward(grad, grad_dtype, grad_ld, pre_act, pre_dtype, pre_ld, rows, cols,
+                                                            grad_pre, grad_pre_dtype, grad_pre_ld, s); }),
+                      "cvmm_gelu_backward");
 }
 
 // ---------------------------------------------------------------------------

@@ -43,6 +43,15 @@ __device__ __forceinline__ float round_to(float v, int32_t dt) {
   return v;
 }
 
+// GELU, erf form: 0.5 x (1 + erf(x / sqrt 2)) (torch's F.gelu default).
+__device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.f + erff(x * 0.70710678118654752f)); }
+// d gelu / dx = 0.5 (1 + erf(x / sqrt 2)) + x exp(-x^2 / 2) / sqrt(2 pi)
+__device__ __forceinline__ float gelu_erf_grad(float x) {
+  const float cdf = 0.5f * (1.f + erff(x * 0.70710678118654752f));
+  const float pdf = expf(-0.5f * x * x) * 0.39894228040143268f;
+  return cdf + x * pdf;
+}
+
 // Load element i of a tensor of runtime dtype `dt` as float.
 __device__ __forceinline__ float load_as_f32(const void* p, int32_t dt, int64_t i) {
   if (dt == kBF16) return (float)((const bf16_t*)p)[i];

@@ -5,4 +5,8 @@ namespace cvmm {
 hipError_t launch_routed_gemm_nt_bf16(const GemmParams& p, hipStream_t stream) {
   return launch_routed_gemm_fast_op<bf16_t>(p, stream);
 }
+
+// Whether the fast-path dispatch runs the ring kernel for these parameters
+// (the only kernel with the activation epilogue); same rules for f16.
+bool routed_gemm_ring_applies(const GemmParams& p, int32_t op) { return ring_eligible(p, op); }
 }  // namespace cvmm

@@ -349,7 +349,7 @@ __global__ __launch_bounds__(kGemmThreads, (PanelCfg<KP, BN, WM>::OCC)) void rou
 inline bool panel_eligible(const GemmParams& p, int32_t op) {
   const size_t osz = p.out_dtype == kF32 ? 16 : 8;
   const size_t esz = p.out_dtype == kF32 ? 4 : 2;
-  return p.K <= 128 && p.epi == kEpiStore && p.dg == nullptr && p.w == nullptr && p.out != nullptr &&
+  return p.K <= 128 && p.act == 0 && p.epi == kEpiStore && p.dg == nullptr && p.w == nullptr && p.out != nullptr &&
          p.val_dtype == p.out_dtype && (p.out_dtype == op || p.out_dtype == kF32) && p.N % 64 == 0 &&
          (reinterpret_cast<uintptr_t>(p.out) % osz) == 0 && ((size_t)p.out_ld * esz) % osz == 0;
 }

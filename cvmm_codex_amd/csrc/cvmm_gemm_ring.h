@@ -207,31 +207,9 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   // the conversion at the store does by itself
   const bool plain = !has_w && p.val_dtype == DTypeOf<OutT>::value;
   const int64_t nwave = n0 + wn * 64;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int m = wm * 64 + j * 16 + fr;
-    const int64_t orow = meta.orow[m];
-    float v[4][4];
-    if (plain) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[i][q] = acc[i][j][q];
-    } else {
-      const float wv = meta.w[m];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float c = round_to(acc[i][j][q], p.val_dtype);
-          if (has_w) {
-            c = c * wv;
-            if (p.prod_dtype >= 0) c = round_to(c, p.prod_dtype);
-          }
-          v[i][q] = c;
-        }
-    }
-    char* rowp = orow >= 0 ? reinterpret_cast<char*>(p.out) + orow * p.out_ld * (int64_t)sizeof(OutT) : nullptr;
+  // one row piece of 4 x 16 columns: lane values -> 16-byte (or 4 x 16-byte
+  // fp32) stores of row rowp
+  auto store_row = [&](char* rowp, const float (&v)[4][4]) {
     if constexpr (sizeof(OutT) == 4) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -263,6 +241,50 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
           *reinterpret_cast<uint4*>(rowp + n * 2) = make_uint4(t0[0], t1[0], t0[1], t1[1]);
       }
     }
+  };
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = wm * 64 + j * 16 + fr;
+    const int64_t orow = meta.orow[m];
+    float v[4][4];
+    if (plain) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[i][q] = acc[i][j][q];
+    } else {
+      const float wv = meta.w[m];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float c = round_to(acc[i][j][q], p.val_dtype);
+          if (has_w) {
+            c = c * wv;
+            if (p.prod_dtype >= 0) c = round_to(c, p.prod_dtype);
+          }
+          v[i][q] = c;
+        }
+    }
+    char* rowp = orow >= 0 ? reinterpret_cast<char*>(p.out) + orow * p.out_ld * (int64_t)sizeof(OutT) : nullptr;
+    if (p.act == 0) {
+      store_row(rowp, v);
+    } else {
+      // GELU: h = the product in the output type (kept for the backward),
+      // out = gelu(h) rounded to the output type
+      char* auxp = orow >= 0 ? reinterpret_cast<char*>(p.aux) + orow * p.out_ld * (int64_t)sizeof(OutT) : nullptr;
+      float y[4][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float h = (float)(OutT)v[i][q];
+          v[i][q] = h;
+          y[i][q] = gelu_erf(h);
+        }
+      store_row(auxp, v);
+      store_row(rowp, y);
+    }
   }
 }
 
@@ -272,6 +294,7 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
 inline bool ring_eligible(const GemmParams& p, int32_t op) {
   const size_t esz = p.out_dtype == kF32 ? 4 : 2;
   return p.K > 128 && p.epi == kEpiStore && p.dg == nullptr && p.out != nullptr &&
+         (p.act == 0 || (p.aux != nullptr && (reinterpret_cast<uintptr_t>(p.aux) % 16) == 0)) &&
          (p.out_dtype == op || p.out_dtype == kF32) && p.N % 8 == 0 &&
          (reinterpret_cast<uintptr_t>(p.out) % 16) == 0 && ((size_t)p.out_ld * esz) % 16 == 0;
 }
@@ -312,6 +335,7 @@ hipError_t launch_routed_gemm_ring_out(const GemmParams& p, hipStream_t stream) 
 template <typename OpT>
 hipError_t launch_routed_gemm_fast_op(const GemmParams& p, hipStream_t stream) {
   constexpr int32_t op = DTypeOf<OpT>::value;
+  if (p.act != 0 && !ring_eligible(p, op)) return hipErrorInvalidValue;  // only the ring kernel applies it
   if (panel_eligible(p, op)) {
     if (p.out_dtype == kF32) return launch_routed_gemm_panel_out<OpT, float>(p, stream);
     return launch_routed_gemm_panel_out<OpT, OpT>(p, stream);

@@ -72,6 +72,10 @@ struct GemmParams {
   // 1 = token-major (tile j of every expert, then tile j + 1, ...), -1 = the
   // launcher's choice; token major needs n_experts <= kTokenMajorMaxExperts
   int32_t token_major;
+  // activation of the forward's stored values (ring kernel only): 1 = GELU
+  // (erf form): out = gelu(h), and h (the product in the output type) to aux
+  int32_t act;
+  void* aux;
 };
 constexpr int32_t kTokenMajorMaxExperts = 256;
 
@@ -252,6 +256,13 @@ hipError_t launch_route_topk_backward(const void* logits, int32_t logits_dtype, 
                                       hipStream_t stream);
 
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
+// GELU (erf form) over rows: y = rnd(gelu(h)); its backward
+// dh = rnd(dy * gelu'(h)) (the formula of torch's gelu backward).
+hipError_t launch_gelu_rows(const void* h, int32_t h_dtype, int64_t h_ld, int64_t rows, int64_t cols, void* y,
+                            int32_t y_dtype, int64_t y_ld, hipStream_t stream);
+hipError_t launch_gelu_backward(const void* dy, int32_t dy_dtype, int64_t dy_ld, const void* h, int32_t h_dtype,
+                                int64_t h_ld, int64_t rows, int64_t cols, void* dh, int32_t dh_dtype, int64_t dh_ld,
+                                hipStream_t stream);
 // out[t][n] = rnd(rnd(sum_j rnd(w[t*k+j], w_round) * buf[t*k+j][n], mid_dtype), out_dtype)
 hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_ld, const int32_t* inv,
                                const int64_t* rp, const void* w, int32_t w_dtype, int32_t w_round, int64_t n_tokens,

@@ -327,3 +327,95 @@ hipError_t launch_sum_partials(const float* part, int64_t rows, int32_t ntiles, 
 }
 
 }  // namespace cvmm
+
+namespace cvmm {
+
+// The GELU passes walk a [rows][cols] block as a flat range of 8-element
+// pieces (cols % 8 == 0; row strides may differ from cols), 256 threads per
+// workgroup, so that narrow rows still make full workgroups.
+// (rows are split with 32-bit arithmetic; flat blocks need none)
+__device__ __forceinline__ void gelu_piece(int64_t i, int64_t cols8, bool flat, int64_t* r, int64_t* c) {
+  if (flat) {
+    *r = 0;
+    *c = i * 8;
+  } else {
+    const uint32_t q = (uint32_t)i / (uint32_t)cols8;
+    *r = q;
+    *c = ((int64_t)((uint32_t)i - q * (uint32_t)cols8)) * 8;
+  }
+}
+
+// y = rnd(gelu(h)) per element (F.gelu, erf form).
+__global__ __launch_bounds__(256) void gelu_rows_kernel(const void* __restrict__ h, int32_t h_dtype, int64_t h_ld,
+                                                        int64_t rows, int64_t cols, void* __restrict__ y,
+                                                        int32_t y_dtype, int64_t y_ld, bool in_vec, bool out_vec,
+                                                        bool flat) {
+  const int64_t cols8 = (cols + 7) / 8;
+  const int64_t n = rows * cols8;
+  const int64_t lim = flat ? rows * cols : cols;  // valid elements from the piece's row start
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t r, c;
+    gelu_piece(i, cols8, flat, &r, &c);
+    float v[8];
+    load8_any(h, h_dtype, r * h_ld + c, in_vec, lim - c, v);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = gelu_erf(v[q]);
+    store8_any(y, y_dtype, r * y_ld + c, out_vec, lim - c, v);
+  }
+}
+
+// dh = rnd(dy * gelu'(h)) per element (the gelu backward formula).
+__global__ __launch_bounds__(256) void gelu_backward_kernel(
+    const void* __restrict__ dy, int32_t dy_dtype, int64_t dy_ld, const void* __restrict__ h, int32_t h_dtype,
+    int64_t h_ld, int64_t rows, int64_t cols, void* __restrict__ dh, int32_t dh_dtype, int64_t dh_ld, bool dy_vec,
+    bool h_vec, bool out_vec, bool flat) {
+  const int64_t cols8 = (cols + 7) / 8;
+  const int64_t n = rows * cols8;
+  const int64_t lim = flat ? rows * cols : cols;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t r, c;
+    gelu_piece(i, cols8, flat, &r, &c);
+    float g[8], x[8];
+    load8_any(dy, dy_dtype, r * dy_ld + c, dy_vec, lim - c, g);
+    load8_any(h, h_dtype, r * h_ld + c, h_vec, lim - c, x);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) g[q] = g[q] * gelu_erf_grad(x[q]);
+    store8_any(dh, dh_dtype, r * dh_ld + c, out_vec, lim - c, g);
+  }
+}
+
+// A block whose rows are back to back (every row stride = cols, cols % 8 == 0)
+// is walked as one flat row.
+static bool gelu_flat(int64_t cols, int64_t a, int64_t b, int64_t c) {
+  return cols % 8 == 0 && a == cols && b == cols && c == cols;
+}
+
+static unsigned gelu_grid(int64_t rows, int64_t cols) {
+  const int64_t pieces = rows * ((cols + 7) / 8);
+  int64_t blocks = (pieces + 255) / 256;
+  if (blocks > 65536) blocks = 65536;  // grid-stride beyond
+  return (unsigned)(blocks < 1 ? 1 : blocks);
+}
+
+hipError_t launch_gelu_rows(const void* h, int32_t h_dtype, int64_t h_ld, int64_t rows, int64_t cols, void* y,
+                            int32_t y_dtype, int64_t y_ld, hipStream_t stream) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  if (rows * ((cols + 7) / 8) > 0xffffffffll) return hipErrorInvalidValue;  // 32-bit row split
+  hipLaunchKernelGGL(gelu_rows_kernel, dim3(gelu_grid(rows, cols)), dim3(256), 0, stream, h, h_dtype, h_ld, rows,
+                     cols, y, y_dtype, y_ld, vec_ok(h, h_dtype, h_ld), vec_ok(y, y_dtype, y_ld),
+                     gelu_flat(cols, h_ld, y_ld, cols));
+  return hipGetLastError();
+}
+
+hipError_t launch_gelu_backward(const void* dy, int32_t dy_dtype, int64_t dy_ld, const void* h, int32_t h_dtype,
+                                int64_t h_ld, int64_t rows, int64_t cols, void* dh, int32_t dh_dtype, int64_t dh_ld,
+                                hipStream_t stream) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  if (rows * ((cols + 7) / 8) > 0xffffffffll) return hipErrorInvalidValue;  // 32-bit row split
+  hipLaunchKernelGGL(gelu_backward_kernel, dim3(gelu_grid(rows, cols)), dim3(256), 0, stream, dy, dy_dtype, dy_ld, h,
+                     h_dtype, h_ld, rows, cols, dh, dh_dtype, dh_ld, vec_ok(dy, dy_dtype, dy_ld),
+                     vec_ok(h, h_dtype, h_ld), vec_ok(dh, dh_dtype, dh_ld), gelu_flat(cols, dy_ld, h_ld, dh_ld));
+  return hipGetLastError();
+}
+
+}  // namespace cvmm

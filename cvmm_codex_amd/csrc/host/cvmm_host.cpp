@@ -318,6 +318,65 @@ Tensor forward(const Tensor& x, const Tensor& keys, const OptT& keys_t, const Te
 }
 
 // ---------------------------------------------------------------------------
+// forward + GELU (no counterpart in cvmm.py: its callers' F.gelu(cvmm(...)),
+// benchmark_ffn_moe.py:96), unweighted selections: (gelu(h), h), [R, d_out]
+// in the op dtype
+// ---------------------------------------------------------------------------
+std::tuple<Tensor, Tensor> forward_gelu(const Tensor& x, const Tensor& keys, const OptT& keys_t, const Tensor& sel,
+                                        const Tensor& sel_index, const OptT& out_index, const Tensor& offsets,
+                                        const OptT& route_pos, int64_t op_id, int64_t flags, int64_t stream) {
+  require_device(x, "x");
+  require_device(keys, "keys");
+  require_device(sel, "sel");
+  require_device(sel_index, "sel_index");
+  const auto op = dtype_of(op_id);
+  const int64_t E = keys.size(0), d_in = keys.size(1), d_out = keys.size(2);
+  TORCH_CHECK(x.size(-1) == d_in, "cvmm: x.shape[-1] must equal keys.shape[1]");  // cvmm.py:825
+  Tensor xf, kv;
+  if (keys_t.has_value()) {
+    xf = rows_of(x.scalar_type() == op ? x : x.to(op), d_in);
+    kv = keys_t->transpose(1, 2);
+  } else {
+    xf = rows_of(storage_for(x, op), d_in);
+    kv = keys_view(storage_for(keys, op));
+  }
+  Tensor s32 = sorted_i32(sel);
+  const int64_t R = s32.numel();
+  Tensor si = as_i64(sel_index);
+  OptT oi = as_i64(out_index);
+  if (si.numel() != R || (oi.has_value() && oi->numel() != R))
+    throw py::value_error("cvmm: sel_index/out_index must have one entry per route");
+  const int32_t od = (int32_t)op_id;
+  Tensor out = at::empty({R, d_out}, opts(x, op));
+  Tensor pre = at::empty({R, d_out}, opts(x, op));
+  const size_t ws_bytes = cvmm_fwd_workspace_bytes(R, (int32_t)E, d_in, d_out, R, od, od, 1, 0, (int32_t)flags);
+  OptT ws;
+  if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(x, at::kByte));
+  check(cvmm_fwd_gelu(ptr(xf), dtype_id(xf.scalar_type()), xf.size(0), xf.stride(0), ptr(kv),
+                      dtype_id(kv.scalar_type()), (int32_t)E, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2),
+                      tptr<int32_t>(s32), tptr<int64_t>(si), tptr<int64_t>(oi), R, tptr<int64_t>(offsets),
+                      tptr<int32_t>(route_pos), od, ptr(out), od, R, d_out, ptr(pre), (int32_t)flags, ptr(ws),
+                      ws_bytes, (void*)stream),
+        "cvmm_fwd_gelu");
+  return {out, pre};
+}
+
+Tensor gelu_backward(const Tensor& grad, const Tensor& pre, int64_t stream) {
+  require_device(grad, "grad");
+  require_device(pre, "pre_act");
+  const int64_t cols = pre.size(-1);
+  Tensor g = rows_of(grad, cols);
+  Tensor h = rows_of(pre, cols);
+  if (g.size(0) != h.size(0)) throw py::value_error("cvmm_gelu: grad and pre-activation shapes differ");
+  Tensor out = at::empty({h.size(0), cols}, opts(h, h.scalar_type()));
+  check(cvmm_gelu_backward(ptr(g), dtype_id(g.scalar_type()), g.stride(0), ptr(h), dtype_id(h.scalar_type()),
+                           h.stride(0), h.size(0), cols, ptr(out), dtype_id(out.scalar_type()), out.stride(0),
+                           (void*)stream),
+        "cvmm_gelu_backward");
+  return out;
+}
+
+// ---------------------------------------------------------------------------
 // backward (cvmm.py:1552-1755): (grad_x, grad_keys, grad_reduction_weight)
 // ---------------------------------------------------------------------------
 std::tuple<OptT, OptT, OptT> backward(const Tensor& grad_output, const Tensor& x, const Tensor& keys,
@@ -411,6 +470,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("cast_keys", &cast_keys, py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"),
         py::arg("stream"));
   m.def("forward", &forward);
+  m.def("forward_gelu", &forward_gelu);
+  m.def("gelu_backward", &gelu_backward, py::arg("grad"), py::arg("pre_act"), py::arg("stream"));
   m.def("backward", &backward);
   // operand rules, exposed for tests
   m.def("storage_for", [](const Tensor& t, int64_t op_id) { return storage_for(t, dtype_of(op_id)); });

@@ -211,6 +211,28 @@ int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld,
              int64_t reduce_k, int32_t op_dtype, void* out, int32_t out_dtype, int64_t out_rows, int64_t out_ld,
              int32_t flags, void* workspace, size_t workspace_bytes, void* stream);
 
+/* cvmm_fwd followed by the GELU (erf form), for the up projection of the
+ * reference's MoE callers (no counterpart in cvmm.py: its callers write
+ * F.gelu(cvmm(...)), benchmark_ffn_moe.py:96).  Unweighted selections:
+ * pre_act = h = what cvmm_fwd writes to out, out = rnd_out(gelu(h)); pre_act
+ * has out's shape, dtype and row stride (kept for cvmm_gelu_backward).  When
+ * the long-K GEMM (d_in > 128, 16-bit op) runs, the GELU is in its epilogue
+ * and both outputs are written once; otherwise a GELU pass follows the GEMM.
+ * Workspace: cvmm_fwd_workspace_bytes of the unweighted call. */
+int cvmm_fwd_gelu(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld,
+                  const void* keys, int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out,
+                  int64_t k_se, int64_t k_si, int64_t k_sj,
+                  const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index, int64_t n_routes,
+                  const int64_t* offsets, const int32_t* route_pos, int32_t op_dtype, void* out, int32_t out_dtype,
+                  int64_t out_rows, int64_t out_ld, void* pre_act, int32_t flags, void* workspace,
+                  size_t workspace_bytes, void* stream);
+/* grad_pre = rnd(grad * gelu'(pre_act)) per element of a [rows][cols] block
+ * (the GELU backward; gelu'(x) = 0.5 (1 + erf(x / sqrt 2)) + x exp(-x^2/2) /
+ * sqrt(2 pi)). */
+int cvmm_gelu_backward(const void* grad, int32_t grad_dtype, int64_t grad_ld, const void* pre_act,
+                       int32_t pre_dtype, int64_t pre_ld, int64_t rows, int64_t cols, void* grad_pre,
+                       int32_t grad_pre_dtype, int64_t grad_pre_ld, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Backward, input side: grad_x and the reduction-weight gradient.          */
 /* Replaces cvmm_grouped_bwd_x_kernel (+ top-k .sum, cvmm.py:1204-1223),     */

@@ -26,6 +26,9 @@ Pinning (how each function is checked, see ``tests/test_oracle.py``):
     pure-Python triple loops on tiny inputs, top-1 == dense per-token GEMM,
     E == 1 == plain GEMM, and empty experts => zero weight gradient.
   * rounding emulation (bf16/f16): against torch's own dtype conversions.
+  * gelu / gelu_backward (the GELU the reference's callers apply to the up
+    projection, benchmark_ffn_moe.py:96): against torch's F.gelu and its
+    autograd in float64, and the derivative against central differences.
 No function here is "parity unpinned".
 """
 from __future__ import annotations
@@ -37,7 +40,7 @@ import numpy as np
 
 __all__ = [
     "Sel", "rnd", "prepare_sel", "prepare_sel2", "expert_offsets",
-    "forward", "backward", "bf16_bits_to_f32", "f32_to_bf16_bits",
+    "forward", "backward", "bf16_bits_to_f32", "f32_to_bf16_bits", "gelu", "gelu_backward",
 ]
 
 
@@ -277,3 +280,24 @@ def backward(x, meta: Sel, keys, grad_out, op: Optional[str] = None,
         dgate = (gk * x_plain[:, None, :]).sum(-1).reshape(-1)
     dgate = rnd(rnd(dgate, acc32, compute), w_dtype, compute)
     return dx.reshape(np.asarray(x).shape), dW, dgate.reshape(rw.shape)
+
+
+# ----------------------------------------------------------------------------
+# GELU of the up projection (benchmark_ffn_moe.py:96: F.gelu(cvmm(...)))
+# ----------------------------------------------------------------------------
+
+def gelu(h: np.ndarray, out: Optional[str] = None, compute=np.float64) -> np.ndarray:
+    """rnd_out(0.5 h (1 + erf(h / sqrt 2))): F.gelu (erf form) of the stored
+    up-projection values, computed in float and rounded to their dtype."""
+    from scipy.special import erf
+    x = np.asarray(h, dtype=compute)
+    return rnd(0.5 * x * (1.0 + erf(x / np.sqrt(2.0))), out, compute)
+
+
+def gelu_backward(grad: np.ndarray, h: np.ndarray, out: Optional[str] = None, compute=np.float64) -> np.ndarray:
+    """rnd_out(grad * gelu'(h)), gelu'(x) = 0.5 (1 + erf(x / sqrt 2)) +
+    x exp(-x^2 / 2) / sqrt(2 pi)."""
+    from scipy.special import erf
+    x = np.asarray(h, dtype=compute)
+    d = 0.5 * (1.0 + erf(x / np.sqrt(2.0))) + x * np.exp(-0.5 * x * x) / np.sqrt(2.0 * np.pi)
+    return rnd(np.asarray(grad, dtype=compute) * d, out, compute)

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.cvmm_abi_version() == 7
+    assert lib.cvmm_abi_version() == 8
 
 
 def test_workspace_queries(lib):

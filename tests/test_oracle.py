@@ -381,3 +381,23 @@ def test_router_oracle_catches_a_planted_mistake(monkeypatch):
     bad = RO.route_topk_backward(logits.detach().numpy(), sel.numpy(), gw.numpy(), False)
     assert np.allclose(good, logits.grad.numpy(), rtol=1e-10, atol=1e-13)
     assert not np.allclose(bad, logits.grad.numpy(), rtol=1e-6, atol=1e-9)
+
+
+def test_oracle_gelu_matches_torch():
+    g = torch.Generator().manual_seed(21)
+    h = (torch.randn(4096, generator=g) * 3).double().requires_grad_(True)
+    y = torch.nn.functional.gelu(h)
+    gy = torch.randn(4096, generator=g).double()
+    y.backward(gy)
+    np.testing.assert_allclose(O.gelu(h.detach().numpy()), y.detach().numpy(), rtol=1e-14, atol=1e-15)
+    np.testing.assert_allclose(O.gelu_backward(gy.numpy(), h.detach().numpy()), h.grad.numpy(), rtol=1e-12,
+                               atol=1e-14)
+    # the derivative against central differences
+    x = np.linspace(-6, 6, 97)
+    eps = 1e-6
+    num = (O.gelu(x + eps) - O.gelu(x - eps)) / (2 * eps)
+    np.testing.assert_allclose(O.gelu_backward(np.ones_like(x), x), num, rtol=1e-7, atol=1e-9)
+    # bf16 rounding of the stored values, as F.gelu on bf16 tensors
+    hb = torch.randn(2048, generator=g).to(torch.bfloat16)
+    np.testing.assert_array_equal(O.gelu(hb.float().numpy(), "bfloat16"),
+                                  torch.nn.functional.gelu(hb.double()).to(torch.bfloat16).double().numpy())

@@ -163,6 +163,19 @@ def ffn_forward(s: FFNStack, cvmm_mod, x, gate, w_up, w_down):
         return cvmm_mod.cvmm(hidden.view(B, T, s.k, H), sel_down, w_down)
 
 
+def ffn_forward_fused(s: FFNStack, cvmm_mod, x, gate, w_up, w_down):
+    """ffn_forward with the library's fused router (cvmm_route_topk) and
+    up projection + GELU (cvmm_gelu) in place of the torch lines."""
+    B, T, D = x.shape
+    E, _, H = w_up.shape
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        logits = x @ gate + s.bias
+        weights, _, sel_up = cvmm_mod.cvmm_route_topk(logits, s.k, True)
+        hidden = cvmm_mod.cvmm_gelu(x, sel_up, w_up)
+        sel_down = cvmm_mod.cvmm_prepare_sel2(sel_up, weights, route_input=True)
+        return cvmm_mod.cvmm(hidden.view(B, T, s.k, H), sel_down, w_down)
+
+
 PROJECTIONS = {
     "tiny_fp32": c1_tiny,
     "ff_up_1024": c2_ff_up,
