@@ -356,7 +356,7 @@ def main():
     ap.add_argument("--router", action="store_true",
                     help="time the fused router against the torch router lines (one JSON line) and exit")
     ap.add_argument("--tune", action="append", default=[], metavar="KNOB=VALUE",
-                    help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, gemm_order, "
+                    help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, wgrad_tile, gemm_order, "
                          "reduce_min_topk) before running")
     args = ap.parse_args()
 
@@ -370,7 +370,8 @@ def main():
 
     from cvmm_codex_amd import _native as N
     knobs = {"panel_tiles_per_wg": N.TUNE_PANEL_TILES_PER_WG, "wgrad_order": N.TUNE_WGRAD_ORDER,
-             "gemm_order": N.TUNE_GEMM_ORDER, "reduce_min_topk": N.TUNE_REDUCE_MIN_TOPK}
+             "gemm_order": N.TUNE_GEMM_ORDER, "reduce_min_topk": N.TUNE_REDUCE_MIN_TOPK,
+             "wgrad_tile": N.TUNE_WGRAD_TILE}
     for kv in args.tune:
         name, _, value = kv.partition("=")
         if name not in knobs:

@@ -23,6 +23,7 @@ TUNE_PANEL_TILES_PER_WG = 1
 TUNE_WGRAD_ORDER = 2
 TUNE_GEMM_ORDER = 3
 TUNE_REDUCE_MIN_TOPK = 4
+TUNE_WGRAD_TILE = 5
 
 # kernel classes of the timing hooks (include/cvmm_hip.h CVMM_KC_*)
 KC_SORT, KC_OFFSETS, KC_CAST_KEYS, KC_GEMM_FWD, KC_GEMM_BWDX, KC_WGRAD, KC_COMBINE, KC_FILL, KC_REDUCE, KC_ROUTE = (

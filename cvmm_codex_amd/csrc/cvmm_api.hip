@@ -80,10 +80,23 @@ void wgrad_geometry(int64_t M, int64_t N, int64_t n_routes, int32_t n_experts, i
   *tiles_mn = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
 }
 
-static int64_t wgrad_tile_elems(int64_t M, int64_t N) {
-  int bm, bn;
-  wgrad_tile(M, N, &bm, &bn);
-  return (int64_t)bm * bn;
+int32_t wgrad_auto_tile(int64_t M, int64_t N, int64_t grid_chunks) {
+  if (M < 256 || N < 256) return kWgTileBase;
+  const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  return grid_chunks * tiles >= 4 * 256 ? kWgTile256x256 : kWgTileBase;
+}
+
+// fp32 partial elements of one slot: the M x N rounding of the tile the
+// launch may take, at most (base or any coarser fast-path tile)
+int64_t wgrad_partial_elems(int64_t M, int64_t N) {
+  int64_t best = 0;
+  for (int32_t c = kWgTileBase; c <= kWgTile256x256; ++c) {
+    int bm, bn;
+    wgrad_fast_tile(M, N, c, &bm, &bn);
+    const int64_t e = ((M + bm - 1) / bm * bm) * ((N + bn - 1) / bn * bn);
+    best = e > best ? e : best;
+  }
+  return best;
 }
 
 }  // namespace cvmm
@@ -99,6 +112,7 @@ struct TimedLaunch {
 };
 std::atomic<int32_t> g_panel_tpw{0};
 std::atomic<int32_t> g_wgrad_order{0};
+std::atomic<int32_t> g_wgrad_tile{0};
 std::atomic<int32_t> g_gemm_order{0};
 std::atomic<int64_t> g_reduce_min_topk{0};
 
@@ -271,8 +285,13 @@ int cvmm_tuning_set(int32_t knob, int64_t value) {
     return CVMM_OK;
   }
   if (knob == CVMM_TUNE_WGRAD_ORDER) {
-    if (value < 0 || value > 2) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: weight-gradient order must be 0, 1 or 2");
+    if (value < 0 || value > 3) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: weight-gradient order must be 0 .. 3");
     g_wgrad_order.store((int32_t)value);
+    return CVMM_OK;
+  }
+  if (knob == CVMM_TUNE_WGRAD_TILE) {
+    if (value < 0 || value > 4) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: weight-gradient tile must be 0 .. 4");
+    g_wgrad_tile.store((int32_t)value);
     return CVMM_OK;
   }
   return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: unknown knob %d", knob);
@@ -818,7 +837,7 @@ size_t cvmm_bwd_w_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d
   Carver c(nullptr);
   c.take((size_t)n_experts * tiles * 4);  // counters first: see CVMM_FLAG_COUNTERS_ZEROED
   if (!has_offsets) c.take((size_t)n_experts * 8);
-  c.take((size_t)max_slots * tiles * wgrad_tile_elems(d_in, d_out) * 4);
+  c.take((size_t)max_slots * wgrad_partial_elems(d_in, d_out) * 4);
   return c.used;
 }
 
@@ -868,7 +887,7 @@ int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, con
     if (r) return r;
     offs = o;
   }
-  p.partial = (float*)c.take((size_t)p.max_slots * tiles * wgrad_tile_elems(d_in, d_out) * 4);
+  p.partial = (float*)c.take((size_t)p.max_slots * wgrad_partial_elems(d_in, d_out) * 4);
 
   const int64_t* rp = out_index ? out_index : sel_index;
   p.x = x; p.x_dtype = x_dtype; p.x_ld = x_ld; p.x_rows = x_rows;
@@ -885,7 +904,13 @@ int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, con
   // tile-major by default: measured faster on every benchmark shape (the
   // activation column slice of one tile, shared by the top-k experts of each
   // token, stays in one XCD's L2)
-  p.tile_major = g_wgrad_order.load() == 1 ? 0 : 1;
+  const int32_t order = g_wgrad_order.load();
+  p.order = order == 1 ? kWgOrderChunk : order == 3 ? kWgOrderChunkXcd : kWgOrderTile;
+  // dW tile: the knob, else 256 x 256 where both sides fill it and the grid
+  // still holds >= 4 workgroups per CU (C5's 2048 x 512: 1.6 -> 0.8 ms per
+  // launch; the gathered bytes per flop halve against 128 x 128)
+  const int32_t tile = g_wgrad_tile.load();
+  p.tile_choice = tile > 0 ? tile - 1 : wgrad_auto_tile(d_in, d_out, p.grid_chunks);
   return check_launch(timed(CVMM_KC_WGRAD, s, [&] { return launch_wgrad(p, op_dtype, s); }), "cvmm_bwd_w(gemm)");
 }
 

@@ -116,13 +116,9 @@ __device__ __forceinline__ lds_u32x4 lds_read128_at(uint32_t a) {
 
 template <int N>
 __device__ __forceinline__ void lgkm_wait_tied(int32_t (&r)[N]) {
-  if constexpr (N == 4) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
-  } else if constexpr (N == 5) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]));
-  } else {
-    static_assert(N == 4 || N == 5, "DMA instructions per wave");
-  }
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]));
+#pragma unroll
+  for (int i = 1; i < N; ++i) asm volatile("" : "+v"(r[i]));
 }
 
 __device__ __forceinline__ void lgkm_wait_frags(lds_u32x2 (&g)[4][2], lds_u32x2 (&x)[4][2]) {
@@ -130,6 +126,17 @@ __device__ __forceinline__ void lgkm_wait_frags(lds_u32x2 (&g)[4][2], lds_u32x2 
                : "+v"(g[0][0]), "+v"(g[0][1]), "+v"(g[1][0]), "+v"(g[1][1]), "+v"(g[2][0]), "+v"(g[2][1]),
                  "+v"(g[3][0]), "+v"(g[3][1]), "+v"(x[0][0]), "+v"(x[0][1]), "+v"(x[1][0]), "+v"(x[1][1]),
                  "+v"(x[2][0]), "+v"(x[2][1]), "+v"(x[3][0]), "+v"(x[3][1]));
+}
+
+// Any number of fragments: the wait, then empty statements that hand each
+// fragment on (volatile asm keeps its order, so every use follows the wait).
+template <int NG, int NX>
+__device__ __forceinline__ void lgkm_wait_frags_n(lds_u32x2 (&g)[NG][2], lds_u32x2 (&x)[NX][2]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(g[0][0]), "+v"(g[0][1]), "+v"(x[0][0]), "+v"(x[0][1]));
+#pragma unroll
+  for (int i = 1; i < NG; ++i) asm volatile("" : "+v"(g[i][0]), "+v"(g[i][1]));
+#pragma unroll
+  for (int i = 1; i < NX; ++i) asm volatile("" : "+v"(x[i][0]), "+v"(x[i][1]));
 }
 
 __device__ __forceinline__ void lgkm_wait_w(lds_u32x4 (&w)[2]) {

@@ -118,8 +118,21 @@ struct WgradParams {
   float* partial;          // [max_slots][M][N] fp32
   int64_t max_slots;
   int32_t* counters;       // [E][tiles_m*tiles_n], zero on entry
-  int32_t tile_major;      // workgroup order: 0 = chunk-major (a chunk's tiles adjacent), 1 = tile-major
+  int32_t order;           // workgroup order, one of kWgOrder*
+  int32_t tile_choice;     // 16-bit fast path tile: kWgTile*
 };
+
+// Weight-gradient workgroup orders.  The hardware places workgroup i on XCD
+// i % 8; each XCD has its own L2.
+//   chunk-major:  the tiles of one route chunk adjacent, contiguous ranges of
+//                 chunks per XCD (experts in order);
+//   tile-major:   one dW tile of every chunk adjacent (an XCD shares the
+//                 column slice of its tiles across experts);
+//   chunk-xcd:    chunk c on XCD c % 8 with all its tiles adjacent there: the
+//                 tiles running together on one XCD read the same routes'
+//                 rows, and every XCD gets every eighth chunk (hot and cold
+//                 experts spread evenly).
+constexpr int32_t kWgOrderChunk = 0, kWgOrderTile = 1, kWgOrderChunkXcd = 2;
 
 hipError_t launch_wgrad(const WgradParams& p, int32_t op_dtype, hipStream_t stream);
 
@@ -129,8 +142,25 @@ __host__ __device__ inline void wgrad_tile(int64_t M, int64_t N, int* bm, int* b
   else if (M <= 64 && N > 64) { *bm = 64; *bn = 256; }
   else { *bm = 128; *bn = 128; }
 }
+// The 16-bit fast path may take a coarser tile where the base tile is
+// 128 x 128: 256 x 128, 128 x 256 or 256 x 256 (fewer bytes gathered per
+// flop; 256 x 256 runs eight waves, one workgroup per CU).
+constexpr int32_t kWgTileBase = 0, kWgTile256x128 = 1, kWgTile128x256 = 2, kWgTile256x256 = 3;
+__host__ __device__ inline void wgrad_fast_tile(int64_t M, int64_t N, int32_t choice, int* bm, int* bn) {
+  wgrad_tile(M, N, bm, bn);
+  if (*bm != 128 || *bn != 128) return;
+  if (choice == kWgTile256x128) *bm = 256;
+  else if (choice == kWgTile128x256) *bn = 256;
+  else if (choice == kWgTile256x256) { *bm = 256; *bn = 256; }
+}
+// tiles_mn counts base tiles (the finest: one counter each, enough for any
+// coarser tile); partials are sized for the largest rounding of M x N.
 void wgrad_geometry(int64_t M, int64_t N, int64_t n_routes, int32_t n_experts, int32_t op_dtype,
                     int64_t* split, int64_t* grid_chunks, int64_t* max_slots, int64_t* tiles_mn);
+int64_t wgrad_partial_elems(int64_t M, int64_t N);
+// built-in tile choice (no knob): 256 x 256 where M, N >= 256 and the grid
+// holds >= 4 workgroups per CU, else the base tile
+int32_t wgrad_auto_tile(int64_t M, int64_t N, int64_t grid_chunks);
 
 // ---------------------------------------------------------------------------
 // selector preparation

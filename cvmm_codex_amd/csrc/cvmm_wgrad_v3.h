@@ -53,19 +53,27 @@ struct RouteSlice {
   }
 };
 
-template <int BM, int BN, int STAGES, bool WEIGHTED>
+// A BM x BN tile on a WM x WN grid of waves; each wave owns JM x IN blocks of
+// 16 x 16 (x columns x dY columns).  Up to 16 blocks per wave (64 accumulator
+// registers) run two workgroups per CU with 80 KB of LDS each; more blocks
+// run one workgroup per CU -- one wave per SIMD, whose 512 registers hold the
+// accumulators in AGPRs -- with all 160 KB.
+template <int BM, int BN, int WM, int WN, int STAGES, bool WEIGHTED>
 struct Wg3Cfg {
   using TA = RouteSlice<BM>;                   // x rows: dW rows m0 .. m0 + BM
   using TB = RouteSlice<BN>;                   // dY rows: dW columns n0 .. n0 + BN
+  static constexpr int NW = WM * WN, NT = NW * 64;
+  static_assert(NW == 4, "4 waves");
+  static constexpr int JM = BM / WM / 16, IN = BN / WN / 16;
+  static constexpr int OCC = JM * IN <= 16 ? 2 : 1;  // workgroups per CU
+  static_assert(JM * WM * 16 == BM && IN * WN * 16 == BN && JM >= 1 && IN >= 1, "wave grid");
   static constexpr int SLICE = TA::BYTES + TB::BYTES;
-  static constexpr int D = (TA::INSTS + TB::INSTS) / 4;  // DMA instructions per wave per slice
-  static_assert((TA::INSTS + TB::INSTS) % 4 == 0, "whole DMA instructions per wave");
-  static constexpr int WM = BM / 64, WN = BN / 64;       // wave grid, 64 x 64 per wave
-  static_assert(WM * WN == 4, "4 waves of 64x64");
+  static constexpr int D = (TA::INSTS + TB::INSTS) / NW;  // DMA instructions per wave per slice
+  static_assert((TA::INSTS + TB::INSTS) % NW == 0, "whole DMA instructions per wave");
   static_assert((STAGES - 2) * D < 64, "vmcnt range");
-  // route table in what is left of 80 KB (two workgroups per CU)
+  // route table in what is left of the workgroup's share of the 160 KB
   static constexpr int ENTRY = WEIGHTED ? 12 : 8;
-  static constexpr int TBL = ((80 * 1024 - 512 - STAGES * SLICE) / ENTRY) / 32 * 32;
+  static constexpr int TBL = (((160 / OCC) * 1024 - 512 - STAGES * SLICE) / ENTRY) / 32 * 32;
   static_assert(TBL >= 256, "route table");
 };
 
@@ -115,9 +123,17 @@ __device__ __forceinline__ bool wgrad_schedule(const WgradParams& p, int64_t slo
   return s.expert >= 0;
 }
 
-template <typename OpT, int BM, int BN, int STAGES, bool WEIGHTED>
-__global__ __launch_bounds__(256, 2) void wgrad_v3_kernel(const WgradParams p) {
-  using Cfg = Wg3Cfg<BM, BN, STAGES, WEIGHTED>;
+// dW contiguous fp32 rows, 16-byte aligned: a lane's 4 columns are one store.
+__host__ __device__ inline bool wgrad_dw_vec(const WgradParams& p) {
+  return p.dw_sn == 1 && p.dw_dtype == kF32 && p.dw_sm % 4 == 0 && p.dw_se % 4 == 0 &&
+         (reinterpret_cast<uintptr_t>(p.dw) & 15) == 0;
+}
+
+template <typename OpT, int BM, int BN, int WM, int WN, int STAGES, bool WEIGHTED>
+__global__ __launch_bounds__(256, (BM / WM / 16) * (BN / WN / 16) <= 16 ? 2 : 1) void wgrad_v3_kernel(
+    const WgradParams p) {
+  using Cfg = Wg3Cfg<BM, BN, WM, WN, STAGES, WEIGHTED>;
+  constexpr int JM = Cfg::JM, IN = Cfg::IN;
   using TA = typename Cfg::TA;
   using TB = typename Cfg::TB;
   constexpr int D = Cfg::D;
@@ -133,12 +149,16 @@ __global__ __launch_bounds__(256, 2) void wgrad_v3_kernel(const WgradParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t tiles_n = (p.N + BN - 1) / BN;
   const int64_t tiles = ((p.M + BM - 1) / BM) * tiles_n;
-  const int64_t id = xcd_remap(blockIdx.x, gridDim.x);
-  // chunk-major: the tiles of one route chunk are adjacent (one XCD shares
-  // the chunk's rows); tile-major: one dW tile of every chunk is adjacent
-  // (one XCD shares the x / dY column slice of that tile across experts)
-  const int64_t slot_id = p.tile_major ? id % p.grid_chunks : id / tiles;
-  const int64_t tile = p.tile_major ? id / p.grid_chunks : id % tiles;
+  int64_t slot_id, tile;
+  if (p.order == kWgOrderChunkXcd) {  // grid = round_up(grid_chunks, 8) * tiles
+    const int64_t xcd = blockIdx.x % 8, local = blockIdx.x / 8;
+    slot_id = (local / tiles) * 8 + xcd;
+    tile = local % tiles;
+  } else {
+    const int64_t id = xcd_remap(blockIdx.x, gridDim.x);
+    slot_id = p.order == kWgOrderTile ? id % p.grid_chunks : id / tiles;
+    tile = p.order == kWgOrderTile ? id / p.grid_chunks : id % tiles;
+  }
   const int64_t m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
 
   if (!wgrad_schedule(p, slot_id, sched)) return;
@@ -188,45 +208,45 @@ __global__ __launch_bounds__(256, 2) void wgrad_v3_kernel(const WgradParams p) {
 
   // ---- fragment offsets: lane reads route row grp*8 + L/4 (+4), columns
   // blk*16 + 4*(L%4); the swizzle sees row bits 0, 1, 3 only -> per-lane constant
-  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+  const int wm = wave / WN, wn = wave % WN;
   const int L = lane & 15, grp = lane >> 4;
   const int trow = grp * 8 + (L >> 2);
   const int lane_lo = ((L & 1) << 3) + (((L >> 1) & 1) << 4);
-  uint32_t xo[4], go[4];
+  uint32_t xo[JM], go[IN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    xo[i] = trow * TA::ROWB + lane_lo + (((wm * 8 + 2 * i) ^ TA::swz(trow)) << 4);
-    go[i] = TA::BYTES + trow * TB::ROWB + lane_lo + (((wn * 8 + 2 * i) ^ TB::swz(trow)) << 4);
-  }
+  for (int j = 0; j < JM; ++j) xo[j] = trow * TA::ROWB + lane_lo + (((wm * 2 * JM + 2 * j) ^ TA::swz(trow)) << 4);
+#pragma unroll
+  for (int i = 0; i < IN; ++i)
+    go[i] = TA::BYTES + trow * TB::ROWB + lane_lo + (((wn * 2 * IN + 2 * i) ^ TB::swz(trow)) << 4);
   const uint32_t ring_a = lds_addr(ring);
   const uint32_t w_a = lds_addr(t_w) + grp * 32;
 
-  f32x4_t acc[4][4];  // acc[i][j]: dY column block i, x column block j (dW^T orientation)
+  f32x4_t acc[IN][JM];  // acc[i][j]: dY column block i, x column block j (dW^T orientation)
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < IN; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < JM; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](int s, int slot) {
     const uint32_t base = ring_a + slot * Cfg::SLICE;
-    lds_u32x2 gf[4][2], xf[4][2];
+    lds_u32x2 gf[IN][2], xf[JM][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < IN; ++i) {
       gf[i][0] = lds_read_tr<0>(base + go[i]);
       gf[i][1] = lds_read_tr<4 * TB::ROWB>(base + go[i]);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < JM; ++j) {
       xf[j][0] = lds_read_tr<0>(base + xo[j]);
       xf[j][1] = lds_read_tr<4 * TA::ROWB>(base + xo[j]);
     }
-    uint4 g4[4];
+    uint4 g4[IN];
     if constexpr (WEIGHTED) {
       lds_u32x4 w8[2];
       w8[0] = lds_read128_at<0>(w_a + s * 128);
       w8[1] = lds_read128_at<16>(w_a + s * 128);
       lgkm_wait_w(w8);
-      lgkm_wait_frags(gf, xf);
+      lgkm_wait_frags_n(gf, xf);
       float wv[8];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -237,7 +257,7 @@ __global__ __launch_bounds__(256, 2) void wgrad_v3_kernel(const WgradParams p) {
         wv[4 + v] = __uint_as_float(hi);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < IN; ++i) {
         Chunk16 c;
         c.u = make_uint4(gf[i][0].x, gf[i][0].y, gf[i][1].x, gf[i][1].y);
         float v[8];
@@ -246,15 +266,15 @@ __global__ __launch_bounds__(256, 2) void wgrad_v3_kernel(const WgradParams p) {
         g4[i] = pack_chunk<OpT>(v);
       }
     } else {
-      lgkm_wait_frags(gf, xf);
+      lgkm_wait_frags_n(gf, xf);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) g4[i] = make_uint4(gf[i][0].x, gf[i][0].y, gf[i][1].x, gf[i][1].y);
+      for (int i = 0; i < IN; ++i) g4[i] = make_uint4(gf[i][0].x, gf[i][0].y, gf[i][1].x, gf[i][1].y);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < JM; ++j) {
       const uint4 x4 = make_uint4(xf[j][0].x, xf[j][0].y, xf[j][1].x, xf[j][1].y);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) MfmaOp<OpT>::step(acc[i][j], g4[i], x4);
+      for (int i = 0; i < IN; ++i) MfmaOp<OpT>::step(acc[i][j], g4[i], x4);
     }
   };
 
@@ -263,7 +283,7 @@ __global__ __launch_bounds__(256, 2) void wgrad_v3_kernel(const WgradParams p) {
     const int n_rt = (int)((hi - seg) < TBL ? (hi - seg) : TBL);
     const int n_st = (n_rt + 31) / 32;
     if (seg != lo) __syncthreads();  // every wave is done with the previous table
-    for (int r = tid; r < n_st * 32; r += 256) {
+    for (int r = tid; r < n_st * 32; r += Cfg::NT) {
       int32_t xr = -1, gr = -1;
       float w = 0.f;
       if (r < n_rt) {
@@ -306,33 +326,51 @@ __global__ __launch_bounds__(256, 2) void wgrad_v3_kernel(const WgradParams p) {
   }
   vm_wait<0>();
 
-  // ---- epilogue: lane holds dW[m = m0 + wm*64 + j*16 + L][n = n0 + wn*64 + i*16 + 4*grp + {0..3}]
-  const bool dw_vec = p.dw_sn == 1 && p.dw_dtype == kF32 && p.dw_sm % 4 == 0 && p.dw_se % 4 == 0 &&
-                      (reinterpret_cast<uintptr_t>(p.dw) & 15) == 0;
-  auto store_dw = [&]() {
+  // ---- epilogue: lane holds dW[m = m0 + wm*16*JM + j*16 + L][n = n0 + wn*16*IN + i*16 + 4*grp + {0..3}]
+  // one-workgroup-per-CU tiles are launched only for contiguous, aligned
+  // fp32 dW (wgrad_dw_vec): their accumulators never take the element path
+  constexpr bool VEC_ONLY = Cfg::OCC == 1;
+  const bool dw_vec = VEC_ONLY || wgrad_dw_vec(p);
+  // Stores are emitted per 16 x 16 block straight from where the block's sum
+  // lives (accumulators, or the chunk partials), with the layout test outside
+  // the block loops: no block waits in registers for another.
+  auto emit = [&](auto&& block) {
+    if (dw_vec) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t m = m0 + wm * 64 + j * 16 + L;
-      if (m >= p.M) continue;
-      const int64_t off = (int64_t)expert * p.dw_se + m * p.dw_sm;
+      for (int j = 0; j < JM; ++j) {
+        const int64_t m = m0 + wm * 16 * JM + j * 16 + L;
+        if (m >= p.M) continue;
+        float* row = reinterpret_cast<float*>(p.dw) + (int64_t)expert * p.dw_se + m * p.dw_sm;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t n = n0 + wn * 64 + i * 16 + 4 * grp;
-        if (n >= p.N) continue;
-        if (dw_vec) {
-          *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.dw) + off + n) =
-              make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
-        } else {
+        for (int i = 0; i < IN; ++i) {
+          const int64_t n = n0 + wn * 16 * IN + i * 16 + 4 * grp;
+          if (n < p.N) *reinterpret_cast<float4*>(row + n) = block(i, j);
+          __builtin_amdgcn_sched_barrier(0);  // block by block: no accumulator hoisted ahead
+        }
+      }
+    } else if constexpr (!VEC_ONLY) {
 #pragma unroll
-          for (int v = 0; v < 4; ++v)
-            if (n + v < p.N) store_from_f32(p.dw, p.dw_dtype, off + (n + v) * p.dw_sn, acc[i][j][v]);
+      for (int j = 0; j < JM; ++j) {
+        const int64_t m = m0 + wm * 16 * JM + j * 16 + L;
+        if (m >= p.M) continue;
+        const int64_t off = (int64_t)expert * p.dw_se + m * p.dw_sm;
+#pragma unroll
+        for (int i = 0; i < IN; ++i) {
+          const int64_t n = n0 + wn * 16 * IN + i * 16 + 4 * grp;
+          if (n >= p.N) continue;
+          const float4 v = block(i, j);
+          const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (n + q < p.N) store_from_f32(p.dw, p.dw_dtype, off + (n + q) * p.dw_sn, e[q]);
         }
       }
     }
   };
+  auto acc_block = [&](int i, int j) { return make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]); };
 
   if (nch == 1) {
-    store_dw();
+    emit(acc_block);
     return;
   }
 
@@ -341,14 +379,18 @@ __global__ __launch_bounds__(256, 2) void wgrad_v3_kernel(const WgradParams p) {
   const int64_t slot = sched.slot;
   if (slot >= p.max_slots) return;  // cannot happen: workspace holds 2R/split + 1 slots
   auto frag_ptr = [&](int64_t sl) {
-    return reinterpret_cast<float4*>(p.partial) + ((sl * tiles + tile) * 4 + wave) * 16 * 64 + lane;
+    return reinterpret_cast<float4*>(p.partial) + ((sl * tiles + tile) * Cfg::NW + wave) * (IN * JM) * 64 + lane;
   };
   {
     float4* d = frag_ptr(slot);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < IN; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) d[(i * 4 + j) * 64] = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      for (int j = 0; j < JM; ++j)
+      {
+        d[(i * JM + j) * 64] = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
   }
   __threadfence();
   __syncthreads();
@@ -361,47 +403,75 @@ __global__ __launch_bounds__(256, 2) void wgrad_v3_kernel(const WgradParams p) {
   __syncthreads();
   if (!sched.last) return;
   __threadfence();
-  const int64_t base_slot = sched.base_slot;
+  // each of the wave's blocks: 0 + chunk 0 + chunk 1 + ... in chunk order,
+  // GB blocks at a time (GB loads in flight per chunk); flat block index
+  // b = i * JM + j, as the partials are laid out
+  const float4* src = frag_ptr(sched.base_slot);
+  const int64_t stride = tiles * Cfg::NW * (IN * JM) * 64;  // float4 between chunks
+  constexpr int NB = IN * JM, GB = NB < 16 ? NB : 16;
+#pragma unroll 1
+  for (int g0 = 0; g0 < NB; g0 += GB) {
+    float4 t[GB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int b = 0; b < GB; ++b) t[b] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 1
+    for (int32_t c = 0; c < nch; ++c) {
+      const float4* q = src + c * stride + g0 * 64;
+      float4 v[GB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int32_t c = 0; c < nch; ++c) {
-    const float4* src = frag_ptr(base_slot + c);
+      for (int b = 0; b < GB; ++b) v[b] = q[b * 64];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float4 v = src[(i * 4 + j) * 64];
-        acc[i][j][0] += v.x;
-        acc[i][j][1] += v.y;
-        acc[i][j][2] += v.z;
-        acc[i][j][3] += v.w;
+      for (int b = 0; b < GB; ++b) {
+        t[b].x += v[b].x;
+        t[b].y += v[b].y;
+        t[b].z += v[b].z;
+        t[b].w += v[b].w;
       }
+    }
+#pragma unroll
+    for (int b = 0; b < GB; ++b) {
+      const int i = (g0 + b) / JM, j = (g0 + b) % JM;
+      const int64_t m = m0 + wm * 16 * JM + j * 16 + L, n = n0 + wn * 16 * IN + i * 16 + 4 * grp;
+      if (m >= p.M || n >= p.N) continue;
+      const int64_t off = (int64_t)expert * p.dw_se + m * p.dw_sm;
+      if (dw_vec) {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.dw) + off + n) = t[b];
+      } else if constexpr (!VEC_ONLY) {
+        const float e[4] = {t[b].x, t[b].y, t[b].z, t[b].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (n + q < p.N) store_from_f32(p.dw, p.dw_dtype, off + (n + q) * p.dw_sn, e[q]);
+      }
+    }
   }
-  store_dw();
 }
 
-template <typename OpT, int BM, int BN, int STAGES>
+template <typename OpT, int BM, int BN, int WM, int WN, int STAGES>
 hipError_t launch_wgrad_v3_t(const WgradParams& p, hipStream_t stream) {
   const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  const int64_t grid = p.grid_chunks * tiles;
+  const int64_t chunks = p.order == kWgOrderChunkXcd ? (p.grid_chunks + 7) / 8 * 8 : p.grid_chunks;
+  const int64_t grid = chunks * tiles;
   if (grid <= 0) return hipSuccess;
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
+  const dim3 block(WM * WN * 64);
   if (p.w != nullptr)
-    hipLaunchKernelGGL((wgrad_v3_kernel<OpT, BM, BN, STAGES, true>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((wgrad_v3_kernel<OpT, BM, BN, WM, WN, STAGES, true>), dim3((unsigned)grid), block, 0, stream, p);
   else
-    hipLaunchKernelGGL((wgrad_v3_kernel<OpT, BM, BN, STAGES, false>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((wgrad_v3_kernel<OpT, BM, BN, WM, WN, STAGES, false>), dim3((unsigned)grid), block, 0, stream,
+                       p);
   return hipGetLastError();
 }
 
 template <typename OpT>
 hipError_t launch_wgrad_v3_op(const WgradParams& p, hipStream_t stream) {
   int bm, bn;
-  wgrad_tile(p.M, p.N, &bm, &bn);
-  if (bm == 256) return launch_wgrad_v3_t<OpT, 256, 64, 3>(p, stream);
-  if (bm == 64) return launch_wgrad_v3_t<OpT, 64, 256, 3>(p, stream);
-  return launch_wgrad_v3_t<OpT, 128, 128, 4>(p, stream);
+  wgrad_fast_tile(p.M, p.N, wgrad_dw_vec(p) ? p.tile_choice : kWgTileBase, &bm, &bn);
+  if (bm == 256 && bn == 256) return launch_wgrad_v3_t<OpT, 256, 256, 2, 2, 4>(p, stream);
+  if (bm == 256 && bn == 128) return launch_wgrad_v3_t<OpT, 256, 128, 2, 2, 4>(p, stream);
+  if (bm == 128 && bn == 256) return launch_wgrad_v3_t<OpT, 128, 256, 2, 2, 4>(p, stream);
+  if (bm == 256) return launch_wgrad_v3_t<OpT, 256, 64, 4, 1, 3>(p, stream);
+  if (bm == 64) return launch_wgrad_v3_t<OpT, 64, 256, 1, 4, 3>(p, stream);
+  return launch_wgrad_v3_t<OpT, 128, 128, 2, 2, 4>(p, stream);
 }
 
 }  // namespace cvmm

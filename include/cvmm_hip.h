@@ -83,7 +83,12 @@ int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launche
  *     routed GEMM (1..4096).
  *   CVMM_TUNE_WGRAD_ORDER: workgroup order of the weight-gradient kernel,
  *     1 = the tiles of one expert chunk on one XCD, 2 = one dW tile of every
- *     expert on one XCD (the built-in choice).
+ *     expert on one XCD (the built-in choice), 3 = expert chunk c on XCD
+ *     c % 8 with all its tiles.
+ *   CVMM_TUNE_WGRAD_TILE: dW tile of the 16-bit weight-gradient kernel where
+ *     its base tile is 128 x 128 and dW is contiguous aligned fp32: 1 = 128 x
+ *     128, 2 = 256 x 128, 3 = 128 x 256, 4 = 256 x 256.  Built in: 256 x 256
+ *     when d_in, d_out >= 256 and the grid holds >= 4 workgroups per CU.
  *   CVMM_TUNE_GEMM_ORDER: m-tile order of the routed GEMMs (forward, grad
  *     input), 1 = expert-major, 2 = token-major (tile j of every expert next
  *     to each other; up to 256 experts).  Built in: token-major for the
@@ -96,6 +101,7 @@ int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launche
 #define CVMM_TUNE_WGRAD_ORDER 2
 #define CVMM_TUNE_GEMM_ORDER 3
 #define CVMM_TUNE_REDUCE_MIN_TOPK 4
+#define CVMM_TUNE_WGRAD_TILE 5
 int cvmm_tuning_set(int32_t knob, int64_t value);
 
 /* ------------------------------------------------------------------------ */

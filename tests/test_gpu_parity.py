@@ -350,23 +350,50 @@ def test_weight_grad_is_deterministic():
         assert torch.equal(a[n], b[n]), n
 
 
-@pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True)])
-def test_weight_grad_order_does_not_change_bits(weighted, route_input):
-    """Both workgroup orders of the weight-gradient kernel compute every tile
-    and sum split chunks the same way: identical bits, hot expert included."""
+@pytest.mark.parametrize("weighted,route_input,D,H", [(False, False, 128, 96), (True, True, 128, 96),
+                                                      (False, False, 512, 384), (True, True, 384, 512)])
+def test_weight_grad_order_and_tile_do_not_change_bits(weighted, route_input, D, H):
+    """Every workgroup order and dW tile of the weight-gradient kernel sums
+    each element over the same 32-route slices and the same split chunks in
+    the same order: identical bits, hot expert (split into chunks) included.
+    Widths cover partial coarse tiles (128 x 96 under a 256 x 256 tile) and
+    full ones."""
     from cvmm_codex_amd import _native as N
-    x, keys, sel, w, go = _rand_case(31, 4, 512, 128, 96, 8, 4, weighted, route_input, skew=0.7)
+    x, keys, sel, w, go = _rand_case(31, 4, 512, D, H, 8, 4, weighted, route_input, skew=0.7)
     lib = N.lib()
+    ref = None
     try:
-        assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, 1) == 0
-        a = U.run_hip(x, keys, sel, w, go, route_input, True)
-        assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, 2) == 0
-        b = U.run_hip(x, keys, sel, w, go, route_input, True)
+        for order in (1, 2, 3):
+            for tile in (1, 2, 3, 4):
+                assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, order) == 0
+                assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, tile) == 0
+                got = U.run_hip(x, keys, sel, w, go, route_input, True)
+                if ref is None:
+                    ref = got
+                else:
+                    assert torch.equal(ref["keys_grad"], got["keys_grad"]), (order, tile)
     finally:
         lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, 0)
-    assert torch.equal(a["keys_grad"], b["keys_grad"])
+        lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 0)
     exp = U.run_oracle(x, keys, sel, w, go, route_input, True)
-    U.compare(b, exp, 2e-2)
+    U.compare(ref, exp, 2e-2)
+
+
+def test_weight_grad_built_in_coarse_tile_matches_base_bits():
+    """1024 x 1024 dW over 64 experts and 65536 routes: the built-in choice is
+    the 256 x 256 tile (grid >= 4 workgroups per CU); its bits equal the
+    128 x 128 tile's, which the oracle tests pin."""
+    from cvmm_codex_amd import _native as N
+    x, keys, sel, w, go = _rand_case(41, 2, 4096, 1024, 1024, 64, 8, False, False, skew=0.3)
+    lib = N.lib()
+    try:
+        auto = U.run_hip(x, keys, sel, w, go, False, True)
+        assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 1) == 0
+        base = U.run_hip(x, keys, sel, w, go, False, True)
+    finally:
+        lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 0)
+    assert torch.equal(auto["keys_grad"], base["keys_grad"])
+    assert torch.isfinite(auto["keys_grad"]).all() and auto["keys_grad"].abs().max() > 0
 
 
 @pytest.mark.parametrize("weighted,route_input,skew", [(False, False, None), (True, True, 0.7), (True, False, 0.0)])

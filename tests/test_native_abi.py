@@ -107,9 +107,14 @@ def test_tuning_knob_rejects_bad_values(lib):
     assert lib.cvmm_tuning_set(N.TUNE_PANEL_TILES_PER_WG, 5000) != 0
     assert lib.cvmm_tuning_set(99, 1) != 0
     assert lib.cvmm_tuning_set(N.TUNE_PANEL_TILES_PER_WG, 0) == 0
-    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, 3) != 0
+    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, 4) != 0
     assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, -1) != 0
+    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, 3) == 0
     assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, 0) == 0
+    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 5) != 0
+    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, -1) != 0
+    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 4) == 0
+    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 0) == 0
     assert lib.cvmm_tuning_set(N.TUNE_GEMM_ORDER, 3) != 0
     assert lib.cvmm_tuning_set(N.TUNE_GEMM_ORDER, 0) == 0
     assert lib.cvmm_tuning_set(N.TUNE_REDUCE_MIN_TOPK, -1) != 0
