@@ -58,4 +58,69 @@ __device__ __forceinline__ void cast_tile_vec(const CastArgs<OutT>& a, int64_t e
   }
 }
 
+// One 64 x 128 block (expert e, d_in rows i0.., d_out columns j0..) where
+// d_out is a multiple of 128: each thread loads 8 consecutive d_out values
+// of 4 rows (two float4 each, all 8 loads in flight), stores them to kn as
+// one 16-byte piece per row, and through a padded fp32 LDS tile to kt as
+// 16-byte pieces of 8 consecutive d_in values.  LDS banks: the transposed
+// reads (lane l: d_in 8 * (l % 8) + k, d_out l / 8) hit 64 distinct banks
+// with the 129-float row pitch; the row writes conflict two ways.
+template <typename OutT>
+__device__ __forceinline__ void cast_tile_vec128(const CastArgs<OutT>& a, int64_t e, int64_t ti, int64_t tj) {
+  __shared__ float tile[64][129];
+  const int64_t i0 = ti * 64, j0 = tj * 128;
+  const int t = threadIdx.x;
+  const int c8 = (t & 15) * 8;
+  float4 v[4][2];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = q * 16 + (t >> 4);
+    const float* src = a.keys + e * a.se + (i0 + r) * a.si + j0 + c8;
+    v[q][0] = *reinterpret_cast<const float4*>(src);
+    v[q][1] = *reinterpret_cast<const float4*>(src + 4);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = q * 16 + (t >> 4);
+    const float f[8] = {v[q][0].x, v[q][0].y, v[q][0].z, v[q][0].w, v[q][1].x, v[q][1].y, v[q][1].z, v[q][1].w};
+    if (a.kn != nullptr) {
+      union { uint4 u; OutT h[8]; } pk;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) pk.h[k] = from_f32<OutT>(f[k]);
+      *reinterpret_cast<uint4*>(a.kn + (e * a.d_in + i0 + r) * a.d_out + j0 + c8) = pk.u;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) tile[r][c8 + k] = f[k];
+  }
+  if (a.kt == nullptr) return;
+  __syncthreads();
+  const int i8 = (t & 7) * 8;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int j = q * 32 + (t >> 3);
+    union { uint4 u; OutT h[8]; } pk;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) pk.h[k] = from_f32<OutT>(tile[i8 + k][j]);
+    *reinterpret_cast<uint4*>(a.kt + (e * a.d_out + j0 + j) * a.d_in + i0 + i8) = pk.u;
+  }
+}
+
+// Blocks of the vectorised cast: 64 x 128 where d_out % 128 == 0, else
+// 64 x 64; block t = (expert, d_in block, d_out block), d_out fastest.
+__host__ __device__ inline int64_t cast_block_cols(int64_t d_out) { return d_out % 128 == 0 ? 128 : 64; }
+__host__ __device__ inline int64_t cast_blocks(int64_t n_experts, int64_t d_in, int64_t d_out) {
+  return n_experts * (d_in / 64) * (d_out / cast_block_cols(d_out));
+}
+template <typename OutT>
+__device__ __forceinline__ void cast_block(const CastArgs<OutT>& a, int64_t t) {
+  const int64_t ti = a.d_in / 64;
+  if (a.d_out % 128 == 0) {
+    const int64_t tj = a.d_out / 128;
+    cast_tile_vec128(a, t / (ti * tj), (t / tj) % ti, t % tj);
+  } else {
+    const int64_t tj = a.d_out / 64;
+    cast_tile_vec(a, t / (ti * tj), (t / tj) % ti, t % tj);
+  }
+}
+
 }  // namespace cvmm

@@ -37,10 +37,10 @@ __global__ __launch_bounds__(256) void cast_keys_kernel(const void* __restrict__
   }
 }
 
-// Vectorised fast path (see cast_tile_vec): grid (d_out / 64, d_in / 64, E).
+// Vectorised fast path (see cast_block): one workgroup per block.
 template <typename OutT>
 __global__ __launch_bounds__(256) void cast_keys_vec_kernel(const CastArgs<OutT> a) {
-  cast_tile_vec(a, blockIdx.z, blockIdx.y, blockIdx.x);
+  cast_block(a, (int64_t)blockIdx.x);
 }
 
 hipError_t launch_cast_keys(const void* keys, int32_t keys_dtype, int64_t se, int64_t si, int64_t sj,
@@ -50,11 +50,14 @@ hipError_t launch_cast_keys(const void* keys, int32_t keys_dtype, int64_t se, in
   if (n_experts > 65535 || (d_in + 63) / 64 > 65535) return hipErrorInvalidValue;
   dim3 grid((unsigned)((d_out + 63) / 64), (unsigned)((d_in + 63) / 64), (unsigned)n_experts);
   if (cast_vec_ok(keys, keys_dtype, se, si, sj, d_in, d_out, out_dtype, kt, kn)) {
+    const int64_t blocks = cast_blocks(n_experts, d_in, d_out);
+    if (blocks > 0x7fffffffll) return hipErrorInvalidValue;
+    const dim3 vgrid((unsigned)blocks);
     if (out_dtype == kBF16)
-      hipLaunchKernelGGL(cast_keys_vec_kernel<bf16_t>, grid, dim3(256), 0, stream,
+      hipLaunchKernelGGL(cast_keys_vec_kernel<bf16_t>, vgrid, dim3(256), 0, stream,
                          CastArgs<bf16_t>{(const float*)keys, se, si, d_in, d_out, (bf16_t*)kt, (bf16_t*)kn});
     else
-      hipLaunchKernelGGL(cast_keys_vec_kernel<f16_t>, grid, dim3(256), 0, stream,
+      hipLaunchKernelGGL(cast_keys_vec_kernel<f16_t>, vgrid, dim3(256), 0, stream,
                          CastArgs<f16_t>{(const float*)keys, se, si, d_in, d_out, (f16_t*)kt, (f16_t*)kn});
     return hipGetLastError();
   }

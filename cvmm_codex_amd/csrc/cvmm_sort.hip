@@ -74,24 +74,36 @@ __device__ void block_exclusive_scan(int32_t* a, int32_t n) {
   __syncthreads();
 }
 
+// Ids of the first kSortPrefetch rounds of a chunk, loaded before the
+// count-matrix pass so that their latency overlaps it.
+constexpr int kSortPrefetch = 4;
+
 // Stable scatter of one chunk: within every 256-route round, lanes with equal
 // buckets are ranked by a ballot per bucket bit and the waves take their
 // positions in order, so equal ids keep their input order.  `pos` holds this
-// chunk's next output position per bucket.
+// chunk's next output position per bucket; `pre` the prefetched ids.
 template <typename IdxT>
 __device__ void scatter_chunk(const IdxT* __restrict__ sel, int64_t n_routes, int32_t n_experts, int64_t chunk,
                               int32_t n_bits, int64_t top_k, int32_t* pos, int32_t* __restrict__ sorted_sel,
                               int64_t* __restrict__ perm, int64_t* __restrict__ token_index,
-                              int32_t* __restrict__ route_pos, int64_t b) {
+                              int32_t* __restrict__ route_pos, int64_t b, const IdxT (&pre)[kSortPrefetch]) {
   const int wave = threadIdx.x >> 6;
   const int lane = lane_id();
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const int64_t lo = b * chunk;
   const int64_t hi = min(lo + chunk, n_routes);
-  for (int64_t base = lo; base < hi; base += kSortThreads) {
+  int round = 0;
+  for (int64_t base = lo; base < hi; base += kSortThreads, ++round) {
     const int64_t i = base + threadIdx.x;
     const bool valid = i < hi;
-    const IdxT key = valid ? sel[i] : (IdxT)0;
+    IdxT key = (IdxT)0;
+    if (round < kSortPrefetch) {
+#pragma unroll
+      for (int r = 0; r < kSortPrefetch; ++r)
+        if (r == round) key = pre[r];
+    } else if (valid) {
+      key = sel[i];
+    }
     const int32_t bucket = valid ? bucket_of(key, n_experts) : 0;
     uint64_t peers = __ballot(valid);
     for (int bit = 0; bit < n_bits; ++bit) {
@@ -114,6 +126,11 @@ __device__ void scatter_chunk(const IdxT* __restrict__ sel, int64_t n_routes, in
       __syncthreads();
     }
   }
+}
+
+size_t scatter_lds_bytes(int32_t n_experts) {
+  const int32_t nb = n_experts + 1;
+  return (size_t)(nb <= kSortFastBuckets ? 2 : 1) * nb * sizeof(int32_t);
 }
 
 template <typename IdxT>
@@ -144,15 +161,26 @@ __device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b
   int32_t* __restrict__ n_invalid = a.n_invalid;
   int32_t* pos = sh;  // running output positions of this chunk
   const int32_t nb = n_experts + 1;
+  // the first rounds' ids, loaded before the count-matrix pass so that their
+  // latency overlaps it
+  IdxT pre[kSortPrefetch];
+  {
+    const int64_t lo = b * chunk, hi = min(lo + chunk, n_routes);
+#pragma unroll
+    for (int r = 0; r < kSortPrefetch; ++r) {
+      const int64_t i = lo + r * kSortThreads + threadIdx.x;
+      pre[r] = i < hi ? a.sel[i] : (IdxT)0;
+    }
+  }
   if (nb <= kSortFastBuckets) {
-    // All threads stride over the whole count matrix (loads batched 16 deep);
+    // All threads stride over the whole count matrix (loads batched 32 deep);
     // consecutive elements belong to distinct buckets, so the LDS adds of one
     // wave instruction do not collide.
     int32_t* tot = sh + nb;
     for (int32_t e = threadIdx.x; e < nb; e += kSortThreads) pos[e] = tot[e] = 0;
     __syncthreads();
     const int32_t n = (int32_t)(n_chunks * nb);
-    constexpr int U = 16;
+    constexpr int U = 32;
     for (int32_t i0 = threadIdx.x; i0 < n; i0 += U * kSortThreads) {
       int32_t v[U];
 #pragma unroll
@@ -200,7 +228,7 @@ __device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b
   }
   __syncthreads();
   scatter_chunk(a.sel, n_routes, n_experts, chunk, n_bits, top_k, pos, a.sorted_sel, a.perm, a.token_index,
-                a.route_pos, b);
+                a.route_pos, b, pre);
 }
 
 template <typename IdxT>
@@ -219,9 +247,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_cast_kernel(const S
   if ((int64_t)blockIdx.x < a.n_chunks) {
     scatter_block(a, sh, blockIdx.x);
   } else {
-    const int64_t t = (int64_t)blockIdx.x - a.n_chunks;  // (expert, d_in tile, d_out tile)
-    const int64_t tj = c.d_out / 64, ti = c.d_in / 64;
-    cast_tile_vec(c, t / (ti * tj), (t / tj) % ti, t % tj);
+    cast_block(c, (int64_t)blockIdx.x - a.n_chunks);
   }
 }
 
@@ -260,7 +286,7 @@ size_t sort_workspace_bytes(int64_t n_routes, int32_t n_experts) {
 
 template <typename IdxT>
 void launch_scatter_cast(const ScatterArgs<IdxT>& a, const CastRequest& cr, size_t lds, hipStream_t stream) {
-  const int64_t grid = a.n_chunks + (int64_t)cr.n_experts * (cr.d_in / 64) * (cr.d_out / 64);
+  const int64_t grid = a.n_chunks + cast_blocks(cr.n_experts, cr.d_in, cr.d_out);
   if (cr.out_dtype == kBF16) {
     const CastArgs<bf16_t> c{(const float*)cr.keys, cr.se, cr.si, cr.d_in, cr.d_out, (bf16_t*)cr.kt, (bf16_t*)cr.kn};
     hipLaunchKernelGGL((sort_scatter_cast_kernel<IdxT, bf16_t>), dim3((unsigned)grid), dim3(kSortThreads), lds, stream,
@@ -280,7 +306,7 @@ hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_rout
   const int64_t n_chunks = (n_routes + chunk - 1) / chunk;
   int32_t* counts = (int32_t*)ws;
   const size_t lds = (size_t)(n_experts + 1) * sizeof(int32_t);
-  const size_t lds_scatter = (n_experts + 1 <= kSortFastBuckets ? 2 : 1) * lds;
+  const size_t lds_scatter = scatter_lds_bytes(n_experts);
   int n_bits = 0;
   while ((1ll << n_bits) <= (int64_t)n_experts) ++n_bits;  // buckets 0..E
   if (sel_is_int64) {
@@ -314,7 +340,7 @@ hipError_t launch_sort_scatter(const int64_t* sel, int64_t n_routes, int32_t n_e
   if (n_routes <= 0) return hipSuccess;
   const int64_t n_chunks = (n_routes + chunk - 1) / chunk;
   const size_t lds = (size_t)(n_experts + 1) * sizeof(int32_t);
-  const size_t lds_scatter = (n_experts + 1 <= kSortFastBuckets ? 2 : 1) * lds;
+  const size_t lds_scatter = scatter_lds_bytes(n_experts);
   int n_bits = 0;
   while ((1ll << n_bits) <= (int64_t)n_experts) ++n_bits;  // buckets 0..E
   const ScatterArgs<int64_t> a{sel, n_routes, n_experts, chunk, n_chunks, counts, n_bits, top_k,
