@@ -159,10 +159,12 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(
 
 // The same sum with one wave per token, for 16-bit row buffers with aligned
 // rows, n % 8 == 0 and k <= 64: lane j resolves route t*k + j, and every lane
-// then holds 16 bytes of each of the token's rows in flight (8 rows x two
-// 512-column passes at a time) before summing them in route order -- no LDS,
-// no barriers, four tokens per workgroup.
-template <typename BufT>
+// then holds 16 bytes of each of NP 512-column pieces of 16 / NP rows in
+// flight before summing them in route order -- no LDS, no barriers, four
+// tokens per workgroup.  NP = 4 reads whole 4 KB rows of 2048 columns per
+// batch (one DRAM page run per row instead of two 1 KB halves at different
+// times).
+template <typename BufT, int NP>
 __global__ __launch_bounds__(256) void combine_rows_wave_kernel(
     const BufT* __restrict__ buf, int64_t buf_ld, const int32_t* __restrict__ inv, const int64_t* __restrict__ rp,
     int64_t n_routes, const void* __restrict__ w, int32_t w_dtype, int32_t w_round, int64_t k, int64_t n,
@@ -182,16 +184,20 @@ __global__ __launch_bounds__(256) void combine_rows_wave_kernel(
     my_row = row;
     my_w = w != nullptr ? round_to(load_as_f32(w, w_dtype, r), w_round) : 1.f;
   }
-  constexpr int RB = 8;  // rows per batch
+  constexpr int RB = 16 / NP;  // rows per batch
   // the column loop is uniform over the wave (the row shuffles need every
   // lane active); columns past n only mask the loads and stores
-  for (int64_t cb = 0; cb < n; cb += 1024) {
-    const int64_t c0 = cb + lane * 8, c1 = c0 + 512;
-    const bool in0 = c0 < n, in1 = c1 < n;
-    float acc0[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float acc1[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int64_t cb = 0; cb < n; cb += 512 * NP) {
+    bool in[NP];
+    float acc[NP][8];
+#pragma unroll
+    for (int pc = 0; pc < NP; ++pc) {
+      in[pc] = cb + pc * 512 + lane * 8 < n;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[pc][q] = 0.f;
+    }
     for (int64_t j0 = 0; j0 < k; j0 += RB) {
-      uint4 v0[RB], v1[RB];
+      uint4 v[RB][NP];
       float wv[RB];
 #pragma unroll
       for (int u = 0; u < RB; ++u) {
@@ -199,32 +205,32 @@ __global__ __launch_bounds__(256) void combine_rows_wave_kernel(
         const int64_t row = __shfl(my_row, src, 64);
         wv[u] = __shfl(my_w, src, 64);
         const bool ok = j0 + u < k && row >= 0;
-        const BufT* rowp = buf + (ok ? row : 0) * buf_ld;
-        v0[u] = ok && in0 ? *reinterpret_cast<const uint4*>(rowp + c0) : make_uint4(0, 0, 0, 0);
-        v1[u] = ok && in1 ? *reinterpret_cast<const uint4*>(rowp + c1) : make_uint4(0, 0, 0, 0);
+        const BufT* rowp = buf + (ok ? row : 0) * buf_ld + cb + lane * 8;
+#pragma unroll
+        for (int pc = 0; pc < NP; ++pc)
+          v[u][pc] = ok && in[pc] ? *reinterpret_cast<const uint4*>(rowp + pc * 512) : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
       for (int u = 0; u < RB; ++u) {
         if (j0 + u >= k) break;
-        Chunk16 a, b;
-        a.u = v0[u];
-        b.u = v1[u];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          acc0[q] += wv[u] * to_f32(reinterpret_cast<const BufT*>(&a)[q]);
-          acc1[q] += wv[u] * to_f32(reinterpret_cast<const BufT*>(&b)[q]);
+        for (int pc = 0; pc < NP; ++pc) {
+          Chunk16 a;
+          a.u = v[u][pc];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[pc][q] += wv[u] * to_f32(reinterpret_cast<const BufT*>(&a)[q]);
         }
       }
     }
-    if (mid_dtype >= 0) {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        acc0[q] = round_to(acc0[q], mid_dtype);
-        acc1[q] = round_to(acc1[q], mid_dtype);
+    for (int pc = 0; pc < NP; ++pc) {
+      if (mid_dtype >= 0) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[pc][q] = round_to(acc[pc][q], mid_dtype);
       }
+      const int64_t c = cb + pc * 512 + lane * 8;
+      if (in[pc]) store8_any(out, out_dtype, t * out_ld + c, true, n - c, acc[pc]);
     }
-    if (in0) store8_any(out, out_dtype, t * out_ld + c0, true, n - c0, acc0);
-    if (in1) store8_any(out, out_dtype, t * out_ld + c1, true, n - c1, acc1);
   }
 }
 
@@ -264,14 +270,20 @@ hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_l
                        vec_ok(buf, buf_dtype, buf_ld) && vec_ok(out, out_dtype, out_ld);
   if (wave_ok) {
     const dim3 grid((unsigned)((n_tokens + 3) / 4));
-    if (buf_dtype == kBF16)
-      hipLaunchKernelGGL(combine_rows_wave_kernel<bf16_t>, grid, dim3(256), 0, stream, (const bf16_t*)buf, buf_ld,
-                         inv, rp, n_tokens * k, w, w_dtype, w_round, k, n, mid_dtype, out, out_dtype, out_ld,
-                         n_tokens);
-    else
-      hipLaunchKernelGGL(combine_rows_wave_kernel<f16_t>, grid, dim3(256), 0, stream, (const f16_t*)buf, buf_ld,
-                         inv, rp, n_tokens * k, w, w_dtype, w_round, k, n, mid_dtype, out, out_dtype, out_ld,
-                         n_tokens);
+    // whole 2048-column rows per batch where rows are that wide; 1024 columns
+    // (two pieces) otherwise
+    const bool wide = n >= 2048;
+#define CVMM_COMBINE(T, NP)                                                                                      \
+  hipLaunchKernelGGL((combine_rows_wave_kernel<T, NP>), grid, dim3(256), 0, stream, (const T*)buf, buf_ld, inv, \
+                     rp, n_tokens * k, w, w_dtype, w_round, k, n, mid_dtype, out, out_dtype, out_ld, n_tokens)
+    if (buf_dtype == kBF16) {
+      if (wide) CVMM_COMBINE(bf16_t, 4);
+      else CVMM_COMBINE(bf16_t, 2);
+    } else {
+      if (wide) CVMM_COMBINE(f16_t, 4);
+      else CVMM_COMBINE(f16_t, 2);
+    }
+#undef CVMM_COMBINE
     return hipGetLastError();
   }
   dim3 grid, block;
