@@ -20,6 +20,11 @@
 // so it is used where two workgroups per CU are the limit anyway (256 x 64).
 // Slices past K are loaded from the zero page, so every iteration issues the
 // same DMA count and the waits are the same constant.
+// The weighted input gradient also yields the routing-weight gradient
+// (dgate_r = sum_n rnd(acc) * x_r[n], cvmm.py:1101): the DG variant sums each
+// tile row over its n tile in a fixed order (a lane's 16 columns, the row's 4
+// lanes, the waves through LDS) and stores one partial per n tile; a later
+// pass adds the n tiles in order.
 //
 // LDS rows are 64 or 128 bytes.  The MFMA fragment reads (lane l: row l % 16,
 // chunk l / 16) are free of bank conflicts with chunk ^ ((r >> 1) & 3) for
@@ -59,7 +64,7 @@ __device__ __forceinline__ int ring_swz(int row) {
   else return row & 7;
 }
 
-template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int Role, int BK>
+template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int Role, int BK, bool DG = false>
 __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(const GemmParams p) {
   using Cfg = RingCfg<BM, BN, STAGES, BK>;
   static_assert(!RA || Cfg::KSS == 1, "read-ahead keeps one k step per slice");
@@ -286,14 +291,96 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
       store_row(rowp, y);
     }
   }
+
+  if constexpr (DG) {
+    // routing-weight gradient partial of this n tile for each tile row:
+    // sum_n rnd(acc, dg_val) * x[dgrow][n].  Fixed order: each lane its 16
+    // columns (blocks i, then the 4 columns), the 4 lanes of a row (xor 16,
+    // then xor 32), then the waves of the tile row in wn order through LDS.
+    // x pieces of 4 columns as one 8-byte (16-bit x) or 16-byte (fp32 x) load
+    const bool x16 = p.dg_x_dtype != kF32;
+    const bool xvec = (reinterpret_cast<uintptr_t>(p.dg_x) & (x16 ? 7 : 15)) == 0 && p.dg_x_ld % 4 == 0;
+    float part[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = wm * 64 + j * 16 + fr;
+      const int64_t xr = meta.dgrow[m];
+      float xv[4][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t n = nwave + i * 16 + 4 * fq;
+        const int64_t o = xr * p.dg_x_ld + n;
+        if (xr < 0) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) xv[i][q] = 0.f;
+        } else if (xvec && n + 3 < p.N) {
+          if (x16) {
+            union { uint2 u; bf16_t b[4]; f16_t h[4]; } c;
+            c.u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.dg_x) + o);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) xv[i][q] = p.dg_x_dtype == kBF16 ? (float)c.b[q] : (float)c.h[q];
+          } else {
+            const float4 f = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.dg_x) + o);
+            xv[i][0] = f.x;
+            xv[i][1] = f.y;
+            xv[i][2] = f.z;
+            xv[i][3] = f.w;
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) xv[i][q] = n + q < p.N ? load_as_f32(p.dg_x, p.dg_x_dtype, o + q) : 0.f;
+        }
+      }
+      float sum = 0.f;
+      if (xr >= 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (nwave + i * 16 + 4 * fq + q < p.N) sum += round_to(acc[i][j][q], p.dg_val_dtype) * xv[i][q];
+      }
+      sum += __shfl_xor(sum, 16, 64);
+      sum += __shfl_xor(sum, 32, 64);
+      part[j] = sum;
+    }
+    if constexpr (Cfg::WN == 1) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = wm * 64 + j * 16 + fr;
+        if (fq == 0 && meta.dgrow[m] >= 0 && meta.widx[m] >= 0) p.dg[meta.widx[m] * p.dg_ntiles + ntile] = part[j];
+      }
+    } else {
+      // every wave is past its last LDS read of the ring (the DMA drained
+      // above): the ring's first bytes take the per-wave partials
+      float* red = reinterpret_cast<float*>(ring);
+      wg_barrier();
+      if (fq == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[wn * BM + wm * 64 + j * 16 + fr] = part[j];
+      }
+      __syncthreads();
+      if (wn == 0 && fq == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = wm * 64 + j * 16 + fr;
+          float sum = red[m];
+#pragma unroll
+          for (int w = 1; w < Cfg::WN; ++w) sum += red[w * BM + m];
+          if (meta.dgrow[m] >= 0 && meta.widx[m] >= 0) p.dg[meta.widx[m] * p.dg_ntiles + ntile] = sum;
+        }
+      }
+    }
+  }
 }
 
 // The ring kernel applies: plain stores (optionally scaled by a per-row
-// routing weight), no routing-weight gradient, output in the op type or fp32,
-// N a multiple of 8 with 16-byte aligned output rows.
+// routing weight, optionally with the routing-weight gradient partials of
+// its n tile, of gemm_bn(N) columns), output in the op type or fp32, N a
+// multiple of 8 with 16-byte aligned output rows.
 inline bool ring_eligible(const GemmParams& p, int32_t op) {
   const size_t esz = p.out_dtype == kF32 ? 4 : 2;
-  return p.K > 128 && p.epi == kEpiStore && p.dg == nullptr && p.out != nullptr &&
+  return p.K > 128 && p.epi == kEpiStore && p.out != nullptr &&
+         (p.dg == nullptr || (p.act == 0 && p.dg_ntiles == (p.N + (p.N <= 64 ? 63 : 127)) / (p.N <= 64 ? 64 : 128))) &&
          (p.act == 0 || (p.aux != nullptr && (reinterpret_cast<uintptr_t>(p.aux) % 16) == 0)) &&
          (p.out_dtype == op || p.out_dtype == kF32) && p.N % 8 == 0 &&
          (reinterpret_cast<uintptr_t>(p.out) % 16) == 0 && ((size_t)p.out_ld * esz) % 16 == 0;
@@ -308,12 +395,16 @@ hipError_t launch_routed_gemm_ring_t(const GemmParams& p_in, hipStream_t stream)
   const int64_t grid = m_tiles * n_ntiles;
   if (grid <= 0) return hipSuccess;
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
-  if (p.role == 0)
+  // the routing-weight gradient only ever comes with the grad-input product
+  if (p.role == 0 && p.dg == nullptr)
     hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 0, BK>), dim3((unsigned)grid),
                        dim3(kGemmThreads), 0, stream, p);
-  else
+  else if (p.dg == nullptr)
     hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1, BK>), dim3((unsigned)grid),
                        dim3(kGemmThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1, BK, true>),
+                       dim3((unsigned)grid), dim3(kGemmThreads), 0, stream, p);
   return hipGetLastError();
 }
 
