@@ -591,7 +591,7 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
   p.o_idx = nullptr;
   r = check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
   if (r) return r;
-  return check_launch(timed_combine(s, [&] { return launch_combine_rows(ybuf, out_dtype, d_out, inv, rp, rw, rw_dtype, out_dtype, out_rows, reduce_k, d_out,
+  return check_launch(timed_combine(s, [&] { return launch_combine_rows(ybuf, out_dtype, d_out, inv, rp, offs + (n_experts - 1), rw, rw_dtype, out_dtype, out_rows, reduce_k, d_out,
                                           out_dtype, out, out_dtype, out_ld, s); }),
                       "cvmm_fwd(combine)");
 }
@@ -805,7 +805,7 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
                        "cvmm_bwd_x(cast)");
     } else {
       const int32_t bdt = weighted ? op_dtype : grad_x_dtype;
-      r = check_launch(timed_combine(s, [&] { return launch_combine_rows(route_buf, bdt, d_in, inv, rp, weighted ? rw : nullptr, rw_dtype, op_dtype,
+      r = check_launch(timed_combine(s, [&] { return launch_combine_rows(route_buf, bdt, d_in, inv, rp, offs + (n_experts - 1), weighted ? rw : nullptr, rw_dtype, op_dtype,
                                            grad_x_rows, top_k, d_in, weighted ? op_dtype : -1, grad_x, grad_x_dtype,
                                            grad_x_ld, s); }),
                        "cvmm_bwd_x(combine)");

@@ -293,9 +293,13 @@ hipError_t launch_gelu_rows(const void* h, int32_t h_dtype, int64_t h_ld, int64_
 hipError_t launch_gelu_backward(const void* dy, int32_t dy_dtype, int64_t dy_ld, const void* h, int32_t h_dtype,
                                 int64_t h_ld, int64_t rows, int64_t cols, void* dh, int32_t dh_dtype, int64_t dh_ld,
                                 hipStream_t stream);
-// out[t][n] = rnd(rnd(sum_j rnd(w[t*k+j], w_round) * buf[t*k+j][n], mid_dtype), out_dtype)
+// out[t][n] = rnd(rnd(sum_j rnd(w[t*k+j], w_round) * buf[row(t*k+j)][n], mid_dtype), out_dtype)
+// row(r) = inv[r] (checked against rp), or r when inv == NULL; rows at or past
+// *rows_end (device pointer, when not NULL: the routes with a valid expert
+// id, which the GEMMs wrote) count as absent.
 hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_ld, const int32_t* inv,
-                               const int64_t* rp, const void* w, int32_t w_dtype, int32_t w_round, int64_t n_tokens,
+                               const int64_t* rp, const int64_t* rows_end, const void* w, int32_t w_dtype,
+                               int32_t w_round, int64_t n_tokens,
                                int64_t k, int64_t n, int32_t mid_dtype, void* out, int32_t out_dtype, int64_t out_ld,
                                hipStream_t stream);
 hipError_t launch_invert_rows(const int64_t* rp, int64_t n_routes, int32_t* inv, hipStream_t stream);

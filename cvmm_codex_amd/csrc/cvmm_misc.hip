@@ -93,9 +93,9 @@ __host__ __device__ inline bool vec_ok(const void* p, int32_t dt, int64_t ld) {
 // nothing.
 __global__ __launch_bounds__(256) void combine_rows_kernel(
     const void* __restrict__ buf, int32_t buf_dtype, int64_t buf_ld, const int32_t* __restrict__ inv,
-    const int64_t* __restrict__ rp, int64_t n_routes, const void* __restrict__ w, int32_t w_dtype,
-    int32_t w_round, int64_t k, int64_t n, int32_t mid_dtype, void* __restrict__ out, int32_t out_dtype,
-    int64_t out_ld, bool in_vec, bool out_vec) {
+    const int64_t* __restrict__ rp, int64_t n_routes, const int64_t* __restrict__ rows_end, const void* __restrict__ w,
+    int32_t w_dtype, int32_t w_round, int64_t k, int64_t n, int32_t mid_dtype, void* __restrict__ out,
+    int32_t out_dtype, int64_t out_ld, bool in_vec, bool out_vec) {
   // the token's routes are resolved once per workgroup (64 at a time) into
   // LDS: row of the route in `buf` (-1: none) and its rounded weight
   __shared__ int64_t s_row[64];
@@ -110,7 +110,8 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(
       int64_t row = r;
       if (inv != nullptr) {
         row = inv[r];
-        if (row < 0 || row >= n_routes || rp[row] != r) row = -1;
+        const int64_t lim = rows_end != nullptr && *rows_end < n_routes ? *rows_end : n_routes;
+        if (row < 0 || row >= lim || rp[row] != r) row = -1;
       }
       s_row[threadIdx.x] = row;
       s_w[threadIdx.x] = w != nullptr ? round_to(load_as_f32(w, w_dtype, r), w_round) : 1.f;
@@ -167,8 +168,9 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(
 template <typename BufT, int NP>
 __global__ __launch_bounds__(256) void combine_rows_wave_kernel(
     const BufT* __restrict__ buf, int64_t buf_ld, const int32_t* __restrict__ inv, const int64_t* __restrict__ rp,
-    int64_t n_routes, const void* __restrict__ w, int32_t w_dtype, int32_t w_round, int64_t k, int64_t n,
-    int32_t mid_dtype, void* __restrict__ out, int32_t out_dtype, int64_t out_ld, int64_t n_tokens) {
+    int64_t n_routes, const int64_t* __restrict__ rows_end, const void* __restrict__ w, int32_t w_dtype,
+    int32_t w_round, int64_t k, int64_t n, int32_t mid_dtype, void* __restrict__ out, int32_t out_dtype,
+    int64_t out_ld, int64_t n_tokens) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= n_tokens) return;
@@ -179,7 +181,8 @@ __global__ __launch_bounds__(256) void combine_rows_wave_kernel(
     int64_t row = r;
     if (inv != nullptr) {
       row = inv[r];
-      if (row < 0 || row >= n_routes || rp[row] != r) row = -1;
+      const int64_t lim = rows_end != nullptr && *rows_end < n_routes ? *rows_end : n_routes;
+      if (row < 0 || row >= lim || rp[row] != r) row = -1;
     }
     my_row = row;
     my_w = w != nullptr ? round_to(load_as_f32(w, w_dtype, r), w_round) : 1.f;
@@ -260,7 +263,8 @@ static void rows_grid(int64_t rows, int64_t n, dim3* grid, dim3* block) {
 }
 
 hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_ld, const int32_t* inv,
-                               const int64_t* rp, const void* w, int32_t w_dtype, int32_t w_round, int64_t n_tokens,
+                               const int64_t* rp, const int64_t* rows_end, const void* w, int32_t w_dtype,
+                               int32_t w_round, int64_t n_tokens,
                                int64_t k, int64_t n, int32_t mid_dtype, void* out, int32_t out_dtype, int64_t out_ld,
                                hipStream_t stream) {
   if (n_tokens <= 0 || n <= 0) return hipSuccess;
@@ -275,7 +279,7 @@ hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_l
     const bool wide = n >= 2048;
 #define CVMM_COMBINE(T, NP)                                                                                      \
   hipLaunchKernelGGL((combine_rows_wave_kernel<T, NP>), grid, dim3(256), 0, stream, (const T*)buf, buf_ld, inv, \
-                     rp, n_tokens * k, w, w_dtype, w_round, k, n, mid_dtype, out, out_dtype, out_ld, n_tokens)
+                     rp, n_tokens * k, rows_end, w, w_dtype, w_round, k, n, mid_dtype, out, out_dtype, out_ld, n_tokens)
     if (buf_dtype == kBF16) {
       if (wide) CVMM_COMBINE(bf16_t, 4);
       else CVMM_COMBINE(bf16_t, 2);
@@ -288,8 +292,8 @@ hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_l
   }
   dim3 grid, block;
   rows_grid(n_tokens, n, &grid, &block);
-  hipLaunchKernelGGL(combine_rows_kernel, grid, block, 0, stream, buf, buf_dtype, buf_ld, inv, rp, n_tokens * k, w,
-                     w_dtype, w_round, k, n, mid_dtype, out, out_dtype, out_ld, vec_ok(buf, buf_dtype, buf_ld),
+  hipLaunchKernelGGL(combine_rows_kernel, grid, block, 0, stream, buf, buf_dtype, buf_ld, inv, rp, n_tokens * k,
+                     rows_end, w, w_dtype, w_round, k, n, mid_dtype, out, out_dtype, out_ld, vec_ok(buf, buf_dtype, buf_ld),
                      vec_ok(out, out_dtype, out_ld));
   return hipGetLastError();
 }

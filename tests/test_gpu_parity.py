@@ -279,6 +279,43 @@ def test_sort_and_cast_in_one_call_match_the_separate_calls(R, E, k, d_in, d_out
     assert fused == (d_in % 64 == 0 and d_out % 64 == 0)
 
 
+@pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True), (True, False)])
+def test_invalid_ids_contribute_nothing(weighted, route_input):
+    """Routes whose expert id is outside [0, E) sort last and no GEMM writes
+    their rows; the top-k sums (the token gradient of a token-input
+    selection, the weighted forward) leave them out instead of reading
+    unwritten rows.  Checked against the oracle with those routes sent to
+    expert 0 with a zero grad row (token input) or a zero routing weight
+    (weighted), which contribute exact zeros; outputs that belong to an
+    invalid route itself (its forward row, its route-input gradient row, its
+    weight gradient) have no defined value and are left out."""
+    x, keys, sel, w, go = _rand_case(51, 2, 256, 128, 192, 8, 4, weighted, route_input)
+    g = torch.Generator().manual_seed(52)
+    bad = torch.rand(sel.shape, generator=g) < 0.1
+    sel_bad = sel.clone()
+    sel_bad[bad] = torch.where(torch.rand(sel.shape, generator=g) < 0.5, -1, 8 + 3)[bad]
+    got = U.run_hip(x, keys, sel_bad, w, go, route_input, True)
+    sel_ok = sel.clone()
+    sel_ok[bad] = 0
+    if weighted:
+        w_ok = w.clone()
+        w_ok[bad] = 0
+        exp = U.run_oracle(x, keys, sel_ok, w_ok, go, route_input, True)
+        keep = ~bad.reshape(-1).numpy()
+        if route_input:  # per-route input rows: only the valid routes' are defined
+            got["x_grad"] = got["x_grad"].reshape(-1, x.shape[-1])[torch.from_numpy(keep).cuda()]
+            exp["x_grad"] = exp["x_grad"].reshape(-1, x.shape[-1])[keep]
+        got["weights_grad"] = got["weights_grad"].reshape(-1)[torch.from_numpy(keep).cuda()]
+        exp["weights_grad"] = exp["weights_grad"].reshape(-1)[keep]
+        U.compare(got, exp, 2e-2)
+    else:
+        go_ok = go.clone()
+        go_ok[bad] = 0
+        exp = U.run_oracle(x, keys, sel_ok, None, go_ok, route_input, True)
+        got["out"] = exp["out"] = None
+        U.compare(got, exp, 2e-2, names=("x_grad", "keys_grad"))
+
+
 def test_sort_invalid_ids_go_last():
     """Ids outside [0, E) are counted, sorted stably after all valid routes and
     never read by the GEMMs."""
