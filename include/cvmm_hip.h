@@ -205,7 +205,10 @@ int cvmm_cast_keys(const void* keys, int32_t keys_dtype, int32_t n_experts, int6
  * [R, N] buffer, sums in expert order), else the
  * route-ordered buffer and a per-token sum in route order.  A flagged call
  * whose operands do not fit the reduce GEMM is the call without the flag,
- * with that call's workspace. */
+ * with that call's workspace.
+ * Routes whose expert id is outside [0, E) (no counterpart: the reference
+ * indexes keys with them) are left out: the top-k sums skip them, and their
+ * own rows of out (unweighted) or grad_x (route input) are not written. */
 size_t cvmm_fwd_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out, int64_t out_rows,
                                 int32_t out_dtype, int32_t op_dtype, int32_t has_offsets, int32_t weighted,
                                 int32_t flags);
