@@ -387,16 +387,20 @@ def test_weight_grad_is_deterministic():
         assert torch.equal(a[n], b[n]), n
 
 
-@pytest.mark.parametrize("weighted,route_input,D,H", [(False, False, 128, 96), (True, True, 128, 96),
-                                                      (False, False, 512, 384), (True, True, 384, 512)])
-def test_weight_grad_order_and_tile_do_not_change_bits(weighted, route_input, D, H):
+@pytest.mark.parametrize("weighted,route_input,D,H,amp", [
+    (False, False, 128, 96, torch.bfloat16), (True, True, 128, 96, torch.bfloat16),
+    (False, False, 512, 384, torch.bfloat16), (True, True, 384, 512, torch.bfloat16),
+    (True, False, 512, 256, torch.float16),
+])
+def test_weight_grad_order_and_tile_do_not_change_bits(weighted, route_input, D, H, amp):
     """Every workgroup order and dW tile of the weight-gradient kernel sums
     each element over the same 32-route slices and the same split chunks in
     the same order: identical bits, hot expert (split into chunks) included.
     Widths cover partial coarse tiles (128 x 96 under a 256 x 256 tile) and
-    full ones."""
+    full ones; one case runs the fp16 kernels."""
     from cvmm_codex_amd import _native as N
-    x, keys, sel, w, go = _rand_case(31, 4, 512, D, H, 8, 4, weighted, route_input, skew=0.7)
+    x, keys, sel, w, go = _rand_case(31, 4, 512, D, H, 8, 4, weighted, route_input, skew=0.7,
+                                     x_dt=amp)
     lib = N.lib()
     ref = None
     try:
@@ -404,7 +408,7 @@ def test_weight_grad_order_and_tile_do_not_change_bits(weighted, route_input, D,
             for tile in (1, 2, 3, 4):
                 assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, order) == 0
                 assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, tile) == 0
-                got = U.run_hip(x, keys, sel, w, go, route_input, True)
+                got = U.run_hip(x, keys, sel, w, go, route_input, True, amp_dtype=amp)
                 if ref is None:
                     ref = got
                 else:
@@ -412,7 +416,8 @@ def test_weight_grad_order_and_tile_do_not_change_bits(weighted, route_input, D,
     finally:
         lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, 0)
         lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 0)
-    exp = U.run_oracle(x, keys, sel, w, go, route_input, True)
+    exp = U.run_oracle(x, keys, sel, w, go, route_input, True,
+                       amp_dtype="float16" if amp == torch.float16 else "bfloat16")
     U.compare(ref, exp, 2e-2)
 
 
@@ -482,6 +487,16 @@ def test_fp16_autocast():
     x, keys, sel, w, go = _rand_case(13, 2, 64, 96, 80, 6, 2, x_dt=torch.float16)
     got = U.run_hip(x, keys, sel, w, go.to(torch.float16), False, True, amp_dtype=torch.float16)
     exp = U.run_oracle(x, keys, sel, w, go.to(torch.float16), False, True, amp_dtype="float16")
+    U.compare(got, exp, 2e-2)
+
+
+@pytest.mark.parametrize("route_input", [True, False])
+def test_fp16_weighted_long_k(route_input):
+    """fp16 autocast through the long-K kernels with the weighted epilogue and
+    the routing-weight gradient (d_out = 320 > 128 on the input gradient)."""
+    x, keys, sel, w, go = _rand_case(15, 2, 256, 256, 320, 8, 4, True, route_input, x_dt=torch.float16)
+    got = U.run_hip(x, keys, sel, w, go.to(torch.float16), route_input, True, amp_dtype=torch.float16)
+    exp = U.run_oracle(x, keys, sel, w, go.to(torch.float16), route_input, True, amp_dtype="float16")
     U.compare(got, exp, 2e-2)
 
 
