@@ -25,6 +25,13 @@
 //    writes its fp32 partial tile in fragment order, and the last to arrive
 //    (per-tile counter) sums them in chunk order -- deterministic -- and
 //    stores dW.
+//  * Tiles: 128 x 128 (and 256 x 64 / 64 x 256 on a narrow side) at two
+//    workgroups per CU, each wave 64 x 64; or, for wide dW, 256 x 256 (or
+//    256 x 128 / 128 x 256) at one workgroup per CU, each wave up to 128 x 128
+//    with its accumulators in AGPRs.  Every tile sums each dW element over
+//    the same slices in the same order, so the tile choice never changes bits.
+// Workgroup orders (WgradParams::order): tile-major by default; chunk-major
+// and chunk-per-XCD for tuning.
 // LDS rows are swizzled at 16-byte granularity so that a transposed read's
 // 16 lanes (4 routes x 32 bytes) hit distinct banks:
 //   256-byte rows: chunk ^ (2 * ((row & 3) | (((row >> 3) & 1) << 2)))
