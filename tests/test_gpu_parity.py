@@ -490,13 +490,16 @@ def test_fp16_autocast():
     U.compare(got, exp, 2e-2)
 
 
-@pytest.mark.parametrize("route_input", [True, False])
-def test_fp16_weighted_long_k(route_input):
-    """fp16 autocast through the long-K kernels with the weighted epilogue and
-    the routing-weight gradient (d_out = 320 > 128 on the input gradient)."""
-    x, keys, sel, w, go = _rand_case(15, 2, 256, 256, 320, 8, 4, True, route_input, x_dt=torch.float16)
-    got = U.run_hip(x, keys, sel, w, go.to(torch.float16), route_input, True, amp_dtype=torch.float16)
-    exp = U.run_oracle(x, keys, sel, w, go.to(torch.float16), route_input, True, amp_dtype="float16")
+@pytest.mark.parametrize("route_input,D,amp", [(True, 256, torch.float16), (False, 256, torch.float16),
+                                               (True, 200, torch.bfloat16), (True, 40, torch.bfloat16)])
+def test_weighted_long_k_routing_weight_grad(route_input, D, amp):
+    """The long-K kernels with the weighted epilogue and the routing-weight
+    gradient (d_out = 320 > 128 on the input gradient): fp16, a last n tile
+    of 72 columns (d_in = 200) and a single narrow tile (d_in = 40)."""
+    x, keys, sel, w, go = _rand_case(15, 2, 256, D, 320, 8, 4, True, route_input, x_dt=amp)
+    op = "float16" if amp == torch.float16 else "bfloat16"
+    got = U.run_hip(x, keys, sel, w, go.to(amp), route_input, True, amp_dtype=amp)
+    exp = U.run_oracle(x, keys, sel, w, go.to(amp), route_input, True, amp_dtype=op)
     U.compare(got, exp, 2e-2)
 
 
