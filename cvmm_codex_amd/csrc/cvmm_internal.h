@@ -167,6 +167,8 @@ int32_t wgrad_auto_tile(int64_t M, int64_t N, int64_t grid_chunks);
 // ---------------------------------------------------------------------------
 size_t sort_workspace_bytes(int64_t n_routes, int32_t n_experts);
 int64_t sort_chunk_size(int64_t n_routes, int32_t n_experts);
+// bytes of a chunks x (E + 1) int32 count matrix, rounded up to 256
+size_t sort_counts_bytes(int64_t n_chunks, int32_t n_experts);
 // A weight cast to run in the sort's scatter launch (vectorised cast only).
 struct CastRequest {
   const void* keys;
@@ -264,7 +266,7 @@ bool reduce_align_ok(const void* b, int64_t b_sk, int64_t b_se, int64_t b_sn, co
 // The stable scatter of cvmm_sort_routes over int64 ids whose per-chunk
 // histogram (counts[chunk][E + 1], chunks of `chunk` routes) is already built.
 hipError_t launch_sort_scatter(const int64_t* sel, int64_t n_routes, int32_t n_experts, int64_t chunk, int64_t top_k,
-                               const int32_t* counts, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                               int32_t* counts, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
                                int64_t* offsets, int32_t* route_pos, int32_t* n_invalid_out, hipStream_t stream);
 
 // ---------------------------------------------------------------------------

@@ -256,7 +256,8 @@ int64_t route_chunk_tokens(int64_t n_tokens, int32_t n_experts, int64_t top_k) {
 size_t route_workspace_bytes(int64_t n_tokens, int32_t n_experts, int64_t top_k) {
   const int64_t tpc = route_chunk_tokens(n_tokens, n_experts, top_k);
   const int64_t n_chunks = n_tokens > 0 ? (n_tokens + tpc - 1) / tpc : 1;
-  return align_up((size_t)(n_experts + 1) * n_chunks * sizeof(int32_t), 256) + 256;  // + n_invalid
+  // counts, bucket totals for the column scan, 256 bytes ending in n_invalid
+  return sort_counts_bytes(n_chunks, n_experts) + align_up((size_t)(n_experts + 1) * sizeof(int32_t), 256) + 256;
 }
 
 template <typename LT, int LPT, int MAXV>

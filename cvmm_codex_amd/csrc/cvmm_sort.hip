@@ -148,6 +148,9 @@ struct ScatterArgs {
   int32_t* route_pos;
   int64_t* offsets;
   int32_t* n_invalid;
+  // not NULL: `counts` already holds each chunk's count of every bucket in
+  // the earlier chunks and tot[e] the bucket totals (sort_colscan_kernel)
+  const int32_t* tot;
 };
 
 // Chunk b: output positions from the histogram rows, then the stable scatter.
@@ -172,7 +175,22 @@ __device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b
       pre[r] = i < hi ? a.sel[i] : (IdxT)0;
     }
   }
-  if (nb <= kSortFastBuckets) {
+  if (a.tot != nullptr) {
+    // the column scan did the count-matrix pass: this chunk's row and the
+    // bucket totals only
+    int32_t* tot = sh + nb;
+    for (int32_t e = threadIdx.x; e < nb; e += kSortThreads) {
+      tot[e] = a.tot[e];
+      pos[e] = counts[b * (int64_t)nb + e];
+    }
+    __syncthreads();
+    if (b == 0 && threadIdx.x == 0 && n_invalid != nullptr) *n_invalid = tot[n_experts];
+    block_exclusive_scan(tot, nb);  // tot[e] = first output position of bucket e
+    if (b == 0) {
+      for (int32_t e = threadIdx.x; e < n_experts; e += kSortThreads) offsets[e] = tot[e + 1];
+    }
+    for (int32_t e = threadIdx.x; e < nb; e += kSortThreads) pos[e] += tot[e];
+  } else if (nb <= kSortFastBuckets) {
     // All threads stride over the whole count matrix (loads batched 32 deep);
     // consecutive elements belong to distinct buckets, so the LDS adds of one
     // wave instruction do not collide.
@@ -277,11 +295,81 @@ int64_t sort_chunk_size(int64_t n_routes, int32_t n_experts) {
   return (c + kSortThreads - 1) / kSortThreads * kSortThreads;
 }
 
+// Count matrices at least this large (chunks x buckets, with >= 64 buckets)
+// are scanned once by sort_colscan_kernel instead of by every scatter
+// workgroup (each of which would otherwise read all of it: 65K entries at
+// 524288 routes over 256 experts).
+constexpr int64_t kSortColscanMin = 16384;
+constexpr int kColscanWaves = 16;  // chunk segments per bucket
+constexpr int kColscanBatch = 16;  // loads in flight per lane
+
+bool sort_use_colscan(int64_t n_chunks, int32_t n_experts) {
+  const int64_t nb = (int64_t)n_experts + 1;
+  return nb >= 64 && nb <= kSortFastBuckets && n_chunks * nb >= kSortColscanMin;
+}
+
+// In place: counts[c][e] becomes sum_{c' < c} counts[c'][e]; tot[e] = the sum
+// over all chunks.  Workgroup = 64 buckets (lanes) x 16 chunk segments
+// (waves); each lane reads its segment in batches of 16 independent loads,
+// the waves' segment sums are scanned through LDS, and a second pass writes
+// the running prefixes.
+__global__ __launch_bounds__(64 * kColscanWaves) void sort_colscan_kernel(int32_t* __restrict__ counts,
+                                                                          int64_t n_chunks, int32_t nb,
+                                                                          int32_t* __restrict__ tot) {
+  __shared__ int32_t part[kColscanWaves][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int32_t e = blockIdx.x * 64 + lane;
+  const int64_t q = (n_chunks + kColscanWaves - 1) / kColscanWaves;
+  const int64_t c0 = min((int64_t)w * q, n_chunks), c1 = min(c0 + q, n_chunks);
+  int32_t sum = 0;
+  if (e < nb) {
+    for (int64_t cb = c0; cb < c1; cb += kColscanBatch) {
+      int32_t v[kColscanBatch];
+#pragma unroll
+      for (int u = 0; u < kColscanBatch; ++u) v[u] = cb + u < c1 ? counts[(cb + u) * nb + e] : 0;
+#pragma unroll
+      for (int u = 0; u < kColscanBatch; ++u) sum += v[u];
+    }
+  }
+  part[w][lane] = sum;
+  __syncthreads();
+  int32_t run = 0;
+  for (int v = 0; v < w; ++v) run += part[v][lane];
+  if (e < nb) {
+    for (int64_t cb = c0; cb < c1; cb += kColscanBatch) {
+      int32_t v[kColscanBatch];
+#pragma unroll
+      for (int u = 0; u < kColscanBatch; ++u) v[u] = cb + u < c1 ? counts[(cb + u) * nb + e] : 0;
+#pragma unroll
+      for (int u = 0; u < kColscanBatch; ++u) {
+        if (cb + u < c1) counts[(cb + u) * nb + e] = run;
+        run += v[u];
+      }
+    }
+    if (w == kColscanWaves - 1) tot[e] = run;
+  }
+}
+
+// counts (align_up to 256) + bucket totals (align_up to 256), then 256 bytes
+// whose last 4 hold the router's invalid-id counter.
+size_t sort_counts_bytes(int64_t n_chunks, int32_t n_experts) {
+  return align_up((size_t)(n_experts + 1) * n_chunks * sizeof(int32_t), 256);
+}
 size_t sort_workspace_bytes(int64_t n_routes, int32_t n_experts) {
   const int64_t chunk = sort_chunk_size(n_routes, n_experts);
   const int64_t n_chunks = n_routes > 0 ? (n_routes + chunk - 1) / chunk : 1;
-  size_t counts = (size_t)(n_experts + 1) * n_chunks * sizeof(int32_t);
-  return align_up(counts, 256) + 256;  // + n_invalid counter
+  return sort_counts_bytes(n_chunks, n_experts) + align_up((size_t)(n_experts + 1) * sizeof(int32_t), 256) + 256;
+}
+
+// The column scan when the matrix is large enough; returns the totals to pass
+// to the scatter (NULL: the scatter scans the matrix itself).
+static const int32_t* launch_colscan(int32_t* counts, int64_t n_chunks, int32_t n_experts, hipStream_t stream) {
+  if (!sort_use_colscan(n_chunks, n_experts)) return nullptr;
+  const int32_t nb = n_experts + 1;
+  int32_t* tot = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(counts) + sort_counts_bytes(n_chunks, n_experts));
+  hipLaunchKernelGGL(sort_colscan_kernel, dim3((unsigned)((nb + 63) / 64)), dim3(64 * kColscanWaves), 0, stream, counts,
+                     n_chunks, nb, tot);
+  return tot;
 }
 
 template <typename IdxT>
@@ -316,16 +404,17 @@ hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_rout
     hipLaunchKernelGGL(sort_hist_kernel<int32_t>, dim3(n_chunks), dim3(kSortThreads), lds, stream,
                        (const int32_t*)sel, n_routes, n_experts, chunk, n_chunks, counts);
   }
+  const int32_t* tot = launch_colscan(counts, n_chunks, n_experts, stream);
   if (sel_is_int64) {
     const ScatterArgs<int64_t> a{(const int64_t*)sel, n_routes, n_experts, chunk, n_chunks, counts, n_bits, top_k,
-                                 sorted_sel, perm, token_index, route_pos, offsets, n_invalid_out};
+                                 sorted_sel, perm, token_index, route_pos, offsets, n_invalid_out, tot};
     if (cast == nullptr)
       hipLaunchKernelGGL(sort_scatter_kernel<int64_t>, dim3(n_chunks), dim3(kSortThreads), lds_scatter, stream, a);
     else
       launch_scatter_cast(a, *cast, lds_scatter, stream);
   } else {
     const ScatterArgs<int32_t> a{(const int32_t*)sel, n_routes, n_experts, chunk, n_chunks, counts, n_bits, top_k,
-                                 sorted_sel, perm, token_index, route_pos, offsets, n_invalid_out};
+                                 sorted_sel, perm, token_index, route_pos, offsets, n_invalid_out, tot};
     if (cast == nullptr)
       hipLaunchKernelGGL(sort_scatter_kernel<int32_t>, dim3(n_chunks), dim3(kSortThreads), lds_scatter, stream, a);
     else
@@ -335,7 +424,7 @@ hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_rout
 }
 
 hipError_t launch_sort_scatter(const int64_t* sel, int64_t n_routes, int32_t n_experts, int64_t chunk, int64_t top_k,
-                               const int32_t* counts, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                               int32_t* counts, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
                                int64_t* offsets, int32_t* route_pos, int32_t* n_invalid_out, hipStream_t stream) {
   if (n_routes <= 0) return hipSuccess;
   const int64_t n_chunks = (n_routes + chunk - 1) / chunk;
@@ -343,8 +432,9 @@ hipError_t launch_sort_scatter(const int64_t* sel, int64_t n_routes, int32_t n_e
   const size_t lds_scatter = scatter_lds_bytes(n_experts);
   int n_bits = 0;
   while ((1ll << n_bits) <= (int64_t)n_experts) ++n_bits;  // buckets 0..E
+  const int32_t* tot = launch_colscan(counts, n_chunks, n_experts, stream);
   const ScatterArgs<int64_t> a{sel, n_routes, n_experts, chunk, n_chunks, counts, n_bits, top_k,
-                               sorted_sel, perm, token_index, route_pos, offsets, n_invalid_out};
+                               sorted_sel, perm, token_index, route_pos, offsets, n_invalid_out, tot};
   hipLaunchKernelGGL(sort_scatter_kernel<int64_t>, dim3(n_chunks), dim3(kSortThreads), lds_scatter, stream, a);
   return hipGetLastError();
 }

@@ -316,16 +316,17 @@ def test_invalid_ids_contribute_nothing(weighted, route_input):
         U.compare(got, exp, 2e-2, names=("x_grad", "keys_grad"))
 
 
-def test_sort_invalid_ids_go_last():
+@pytest.mark.parametrize("R,E", [(4000, 16), (524288, 256), (262144, 1000)])
+def test_sort_invalid_ids_go_last(R, E):
     """Ids outside [0, E) are counted, sorted stably after all valid routes and
-    never read by the GEMMs."""
-    E = 16
+    never read by the GEMMs.  The larger cases (SwitchHead's 524288 routes
+    over 256 experts; 1000 experts) have count matrices large enough for the
+    one-pass column scan."""
     g = torch.Generator().manual_seed(5)
-    sel = torch.randint(-3, E + 4, (4000,), generator=g)
+    sel = torch.randint(-3, E + 4, (R,), generator=g)
     raw = sel.to(torch.int32).cuda()
     from cvmm_codex_amd import _native as N
     lib = N.lib()
-    R = raw.numel()
     ssel = torch.empty(R, dtype=torch.int32, device="cuda")
     perm = torch.empty(R, dtype=torch.int64, device="cuda")
     off = torch.empty(E, dtype=torch.int64, device="cuda")
