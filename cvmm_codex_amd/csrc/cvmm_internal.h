@@ -144,7 +144,7 @@ __host__ __device__ inline void wgrad_tile(int64_t M, int64_t N, int* bm, int* b
 }
 // The 16-bit fast path may take a coarser tile where the base tile is
 // 128 x 128: 256 x 128, 128 x 256 or 256 x 256 (fewer bytes gathered per
-// flop; 256 x 256 runs eight waves, one workgroup per CU).
+// flop; four waves of up to 128 x 128, one workgroup per CU).
 constexpr int32_t kWgTileBase = 0, kWgTile256x128 = 1, kWgTile128x256 = 2, kWgTile256x256 = 3;
 __host__ __device__ inline void wgrad_fast_tile(int64_t M, int64_t N, int32_t choice, int* bm, int* bn) {
   wgrad_tile(M, N, bm, bn);
@@ -265,6 +265,9 @@ bool reduce_align_ok(const void* b, int64_t b_sk, int64_t b_se, int64_t b_sn, co
 
 // The stable scatter of cvmm_sort_routes over int64 ids whose per-chunk
 // histogram (counts[chunk][E + 1], chunks of `chunk` routes) is already built.
+// A large histogram is turned in place into per-chunk bucket prefixes, with
+// the bucket totals at sort_counts_bytes(chunks, E) bytes past `counts`: the
+// workspace holds both.
 hipError_t launch_sort_scatter(const int64_t* sel, int64_t n_routes, int32_t n_experts, int64_t chunk, int64_t top_k,
                                int32_t* counts, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
                                int64_t* offsets, int32_t* route_pos, int32_t* n_invalid_out, hipStream_t stream);
@@ -296,9 +299,9 @@ hipError_t launch_gelu_backward(const void* dy, int32_t dy_dtype, int64_t dy_ld,
                                 int64_t h_ld, int64_t rows, int64_t cols, void* dh, int32_t dh_dtype, int64_t dh_ld,
                                 hipStream_t stream);
 // out[t][n] = rnd(rnd(sum_j rnd(w[t*k+j], w_round) * buf[row(t*k+j)][n], mid_dtype), out_dtype)
-// row(r) = inv[r] (checked against rp), or r when inv == NULL; rows at or past
-// *rows_end (device pointer, when not NULL: the routes with a valid expert
-// id, which the GEMMs wrote) count as absent.
+// row(r) = inv[r] (checked against rp; rows at or past *rows_end, a device
+// pointer to the number of routes with a valid expert id -- the rows the
+// GEMMs wrote -- count as absent), or r when inv == NULL.
 hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_ld, const int32_t* inv,
                                const int64_t* rp, const int64_t* rows_end, const void* w, int32_t w_dtype,
                                int32_t w_round, int64_t n_tokens,
