@@ -907,7 +907,7 @@ int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, con
   const int32_t order = g_wgrad_order.load();
   p.order = order == 1 ? kWgOrderChunk : order == 3 ? kWgOrderChunkXcd : kWgOrderTile;
   // dW tile: the knob, else 256 x 256 where both sides fill it and the grid
-  // still holds >= 4 workgroups per CU (C5's 2048 x 512: 1.6 -> 0.8 ms per
+  // still holds >= 4 workgroups per CU (the FFN stack's 2048 x 512: 1.6 -> 0.8 ms per
   // launch; the gathered bytes per flop halve against 128 x 128)
   const int32_t tile = g_wgrad_tile.load();
   p.tile_choice = tile > 0 ? tile - 1 : wgrad_auto_tile(d_in, d_out, p.grid_chunks);
