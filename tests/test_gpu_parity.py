@@ -239,6 +239,7 @@ def test_sort_int64_ids_wrap_like_int32_cast():
 @pytest.mark.parametrize("R,E,k,d_in,d_out,fused", [
     (65536, 64, 8, 1024, 128, True), (4000, 16, 4, 128, 192, True), (3000, 7, 3, 64, 64, True),
     (777, 300, 1, 256, 64, True), (4000, 16, 4, 96, 128, False), (5000, 5, 2, 192, 384, True),
+    (524288, 256, 64, 2048, 64, True),   # SwitchHead size: the column-scan scatter beside the cast
 ])
 def test_sort_and_cast_in_one_call_match_the_separate_calls(R, E, k, d_in, d_out, fused):
     """cvmm_sort_routes_cast_keys (scatter and weight cast in one launch where
