@@ -212,6 +212,27 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   // the conversion at the store does by itself
   const bool plain = !has_w && p.val_dtype == DTypeOf<OutT>::value;
   const int64_t nwave = n0 + wn * 64;
+  // DG with 16-bit x: every x piece this lane needs (4 rows x 4 blocks of 4
+  // columns, 8 bytes each) is requested before the output stores, so the
+  // gathers' latency overlaps them
+  uint2 xpre[4][4];
+  bool xpre_ok = false;
+  if constexpr (DG) {
+    xpre_ok = p.dg_x_dtype != kF32 && (reinterpret_cast<uintptr_t>(p.dg_x) & 7) == 0 && p.dg_x_ld % 4 == 0;
+    if (xpre_ok) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t xr = meta.dgrow[wm * 64 + j * 16 + fr];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t n = nwave + i * 16 + 4 * fq;
+          xpre[j][i] = xr >= 0 && n + 3 < p.N
+                           ? *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.dg_x) + xr * p.dg_x_ld + n)
+                           : make_uint2(0, 0);
+        }
+      }
+    }
+  }
   // one row piece of 4 x 16 columns: lane values -> 16-byte (or 4 x 16-byte
   // fp32) stores of row rowp
   auto store_row = [&](char* rowp, const float (&v)[4][4]) {
@@ -313,6 +334,11 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
         if (xr < 0) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) xv[i][q] = 0.f;
+        } else if (xpre_ok && n + 3 < p.N) {
+          union { uint2 u; bf16_t b[4]; f16_t h[4]; } c;
+          c.u = xpre[j][i];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) xv[i][q] = p.dg_x_dtype == kBF16 ? (float)c.b[q] : (float)c.h[q];
         } else if (xvec && n + 3 < p.N) {
           if (x16) {
             union { uint2 u; bf16_t b[4]; f16_t h[4]; } c;
