@@ -505,6 +505,30 @@ def test_weighted_long_k_routing_weight_grad(route_input, D, amp):
     U.compare(got, exp, 2e-2)
 
 
+@pytest.mark.parametrize("route_input", [True, False])
+def test_routing_weight_grad_with_misaligned_x_rows(route_input):
+    """x as a view one element into rows of 257: neither its address nor its
+    row stride is 8-byte aligned.  The forward and the weight gradient take
+    the general kernels; the grad-input GEMM (aligned grad operand, d_out =
+    320) keeps the long-K kernel, whose routing-weight gradient then reads x
+    element by element instead of in prefetched 8-byte pieces."""
+    x, keys, sel, w, go = _rand_case(16, 2, 128, 256, 320, 8, 4, True, route_input)
+    dev = torch.device("cuda")
+    base = torch.zeros(*x.shape[:-1], x.shape[-1] + 1, dtype=x.dtype, device=dev)
+    base[..., 1:] = x.to(dev)
+    xd = base[..., 1:].requires_grad_(True)
+    assert xd.data_ptr() % 8 != 0 and xd.stride(-2) == 257
+    kd = keys.to(dev).requires_grad_(True)
+    wd = w.to(dev).requires_grad_(True)
+    s = C.cvmm_prepare_sel2(sel.to(dev), wd, route_input=route_input)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = C.cvmm(xd, s, kd)
+    y.backward(go.to(dev).to(y.dtype))
+    torch.cuda.synchronize()
+    got = {"out": y.detach(), "x_grad": xd.grad, "keys_grad": kd.grad, "weights_grad": wd.grad}
+    U.compare(got, U.run_oracle(x, keys, sel, w, go, route_input, True), 2e-2)
+
+
 def test_fp32_x_under_autocast():
     """fp32 activations with bf16 autocast: cast to bf16 inside the kernels."""
     x, keys, sel, w, go = _rand_case(14, 2, 64, 96, 80, 6, 3, True, False, x_dt=torch.float32)
