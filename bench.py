@@ -8,9 +8,13 @@ grad keys, grad reduction weight), launched by the drop-in API exactly as a
 training step would.  ``value`` is whole-job TFLOP/s = 6*R*d_in*d_out / step
 time (inputs resident in HBM).  Every kernel is also timed on its own: the
 library brackets each launch with HIP events on the stream it runs on, and the
-kernel class with the most device time per step gives ``roofline``
-(algorithmic bytes or flops of one launch / its average launch time).  The CPU
-oracle is timed on a bounded sample of the same workload as ``cpu_baseline``.
+GEMM class with the most device time per step gives ``roofline`` (its
+algorithmic flops or bytes per launch / its average launch time, against the
+config's bound: MFMA for the wide projections, HBM for the narrow SwitchHead
+ones, with both fractions reported); ``step_roofline`` does the same for the
+whole step.  ``cpu_baseline`` times the reference's PyTorch CPU path (sort +
+per-expert gather/matmul) on the host cores.  ``--ffn`` measures the full MoE
+FFN stack the same way.
 """
 from __future__ import annotations
 
@@ -149,7 +153,7 @@ def _classes():
     from cvmm_codex_amd import _native as N
     return {"sort": N.KC_SORT, "offsets": N.KC_OFFSETS, "cast_keys": N.KC_CAST_KEYS,
             "gemm_fwd": N.KC_GEMM_FWD, "gemm_bwd_x": N.KC_GEMM_BWDX, "wgrad": N.KC_WGRAD,
-            "combine": N.KC_COMBINE, "fill": N.KC_FILL, "reduce": N.KC_REDUCE}
+            "combine": N.KC_COMBINE, "fill": N.KC_FILL}
 
 
 def kernel_times(runner: Runner, steps: int):
@@ -178,39 +182,77 @@ def kernel_times(runner: Runner, steps: int):
     return out
 
 
-def kernel_work(proj: W.Projection, name: str):
-    """Algorithmic flops and HBM bytes of ONE launch of a hot kernel class:
-    every operand byte read once and every result byte written once, at the
-    storage widths the fast path uses (16-bit operands under autocast, fp32
-    weight gradient)."""
+# Roofline bound of each config (the per-config table of the measurement plan:
+# wide experts are MFMA-bound, the narrow SwitchHead products HBM-bound on the
+# per-route byte model).
+BOUND = {"tiny_fp32": "mfma", "ff_up_1024": "mfma", "ff_down_1024_weighted": "mfma",
+         "switch_v_2048": "hbm", "switch_o_2048_weighted": "hbm", "ffn_stack": "mfma"}
+# kernel class -> phase of the byte model
+PHASE = {"gemm_fwd": "fwd", "gemm_bwd_x": "dx", "wgrad": "dw"}
+
+
+def phase_work(proj: W.Projection, phase: str):
+    """Algorithmic flops and bytes of one phase (fwd, dx or dw) of one
+    projection, on the per-route gather model: every route reads its own
+    input row and dY row (a bytes per element: 2 under autocast, 4 in fp32),
+    the fp32 weights are read once per phase, outputs are written once at
+    op granularity (token rows for top-k sums), 12 bytes of route metadata
+    per route.  fwd: R*Din*a + E*Din*Dout*4 + out + R*12, out = R*Dout*a or
+    T*Dout*a + R*4 (weighted); dx: R*Dout*a + E*Din*Dout*4 + dX + R*12, dX =
+    x_rows*Din*a or 2*R*Din*a + 2*R*4 (weighted: x re-read for the gate
+    gradient, which is written); dw: R*Din*a + R*Dout*a (+ R*4 weighted) +
+    E*Din*Dout*4 + R*12."""
     R = proj.routes
     E, d_in, d_out = proj.keys.shape
     top_k = proj.sel.shape[-1]
-    b = 2 if proj.amp else 4
+    a = 2 if proj.amp else 4
     tokens = R // top_k
     weighted = proj.weights is not None
     x_rows = R if proj.route_input else tokens
-    keys_b = E * d_in * d_out * b
+    w32 = E * d_in * d_out * 4
     flops = 2.0 * R * d_in * d_out
-    if name == "gemm_fwd":
-        # x rows + weight copy + y (output rows, or the route-ordered buffer the combine reads)
-        return flops, x_rows * d_in * b + keys_b + R * d_out * b
-    if name == "gemm_bwd_x":
-        g_rows = tokens if weighted else R
-        by = g_rows * d_out * b + keys_b + R * d_in * b
-        if weighted:  # routing-weight gradient: x rows re-read, one fp32 partial per route and n-tile
-            by += x_rows * d_in * b + R * max(1, d_in // 128) * 4
-        return flops, by
-    if name == "wgrad":
-        g_rows = tokens if weighted else R
-        return flops, x_rows * d_in * b + g_rows * d_out * b + E * d_in * d_out * 4
-    if name == "reduce":
-        # top-k sum without a route buffer (weighted forward of route rows, or
-        # the token gradient): gathered route rows (K wide), 8 bytes of route
-        # info per route, the weight copy, one output row (N wide) per token
-        K, n = (d_in, d_out) if proj.route_input else (d_out, d_in)
-        return flops, R * K * b + R * 8 + keys_b + tokens * n * b
-    return None, None
+    if phase == "fwd":
+        out = tokens * d_out * a + R * 4 if weighted else R * d_out * a
+        return flops, R * d_in * a + w32 + out + R * 12
+    if phase == "dx":
+        dx = 2 * R * d_in * a + 2 * R * 4 if weighted else x_rows * d_in * a
+        return flops, R * d_out * a + w32 + dx + R * 12
+    if phase == "dw":
+        return flops, R * d_in * a + R * d_out * a + (R * 4 if weighted else 0) + w32 + R * 12
+    raise ValueError(phase)
+
+
+def kernel_work(proj: W.Projection, name: str):
+    """Algorithmic flops and bytes of ONE launch of a GEMM kernel class: those
+    of its phase (phase_work); (None, None) for the other classes."""
+    if name not in PHASE:
+        return None, None
+    return phase_work(proj, PHASE[name])
+
+
+def step_work(proj: W.Projection):
+    """(flops, route bytes) of a whole step: the three phases."""
+    f, b = zip(*(phase_work(proj, ph) for ph in ("fwd", "dx", "dw")))
+    return sum(f), sum(b)
+
+
+def roofline_of(bound: str, dtype: str, flops: float, nbytes: float, sec: float, traffic=None):
+    """Both fractions of one launch (or step) taking `sec` seconds; `frac` is
+    the one of the config's bound."""
+    mfma = flops / sec / 1e12
+    hbm = nbytes / sec / 1e9
+    out = {"bound": bound}
+    if bound == "mfma":
+        out.update({"achieved": round(mfma, 3), "peak": PEAK[dtype], "unit": "TFLOP/s",
+                    "frac": round(mfma / PEAK[dtype], 5)})
+    else:
+        out.update({"achieved": round(hbm, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(hbm / HBM_PEAK_GBS, 5)})
+    out.update({"traffic": traffic, "mfma_frac": round(mfma / PEAK[dtype], 5),
+                "hbm_frac": round(hbm / HBM_PEAK_GBS, 5), "algorithmic_flops": flops,
+                "algorithmic_bytes": int(nbytes),
+                "traffic_over_algorithmic": None if traffic is None else round(traffic / nbytes, 3)})
+    return out
 
 
 def copy_calibration(nbytes: int = 256 << 20, iters: int = 5):
@@ -224,37 +266,45 @@ def copy_calibration(nbytes: int = 256 << 20, iters: int = 5):
     log(f"copied {nbytes} bytes {iters} times")
 
 
-def cpu_baseline(proj: W.Projection, budget_s: float = 12.0):
-    """The oracle on the host cores: forward+backward of the same workload in
-    float32 (the fp32 gather + per-expert matmul CPU path; rounding points
-    off), repeated until the time budget is spent (at least once)."""
-    from oracle import cvmm_oracle as O
+def _cpu_model() -> str:
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
     except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
-    op = None
-    xn = proj.x.float().numpy()
-    kn = proj.keys.float().numpy()
-    wn = None if proj.weights is None else proj.weights.float().numpy()
-    gn = proj.grad_out.float().numpy()
-    sel = proj.sel.numpy()
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        meta = O.prepare_sel2(sel, wn, route_input=proj.route_input)
-        O.forward(xn, meta, kn, op, op, compute=np.float32)
-        O.backward(xn, meta, kn, gn, op, compute=np.float32)
-        n += 1
+        pass
+    return "unknown"
+
+
+def cpu_baseline(proj: W.Projection, cap_s: float = 120.0):
+    """The reference's PyTorch CPU CVMM path (oracle/torch_cpu_path.py: stable
+    sort, per-expert gather + matmul, forward and backward) on the host cores
+    in float32: 1 warmup and 3 timed iterations of the full workload, median.
+    Threads: torch's count (the box's CPU share, OMP_NUM_THREADS)."""
+    from oracle import torch_cpu_path as P
+    x = proj.x.float()
+    keys = proj.keys.float()
+    w = None if proj.weights is None else proj.weights.float()
+    gy = proj.grad_out.float()
+    times = []
+    for i in range(4):
+        t0 = time.perf_counter()
+        P.step(x, proj.sel, keys, w, gy, proj.route_input)
         el = time.perf_counter() - t0
-        if el >= budget_s or n >= 50:
-            break
-    per = el / n
-    return {"value": round(proj.flops / per / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads),
-            "kind": "port",
-            "sample": f"full {proj.name} workload, {n} oracle sel+fwd+bwd iterations in {el:.1f}s "
-                      f"(numpy float32, rounding points off), {per * 1e3:.1f} ms/iter"}
+        if i > 0:
+            times.append(el)
+        if el > cap_s:
+            return {"value": None, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+                    "sample": f"skipped: one iteration took {el:.0f} s (> {cap_s:.0f} s)"}
+    med = sorted(times)[1]
+    return {"value": round(proj.flops / med / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port", "ms_per_iter": round(med * 1e3, 2), "os_cpu_count": os.cpu_count(),
+            "torch_threads": torch.get_num_threads(), "cpu_model": _cpu_model(),
+            "sample": f"full {proj.name} workload in float32, torch CPU path (sort + per-expert gather/matmul, "
+                      f"fwd + bwd), 1 warmup + 3 timed iterations, median of "
+                      f"{', '.join(f'{t * 1e3:.0f}' for t in times)} ms"}
 
 
 def load_traffic(kernel: str, workload: str):
@@ -308,12 +358,27 @@ def router_times(iters: int = 50, T: int = 16384, E: int = 128, k: int = 8):
     return out
 
 
-def ffn_times(steps: int = 10, warmup: int = 3):
+class _Shape:
+    """Shape stand-in of a Projection for phase_work (meta tensors)."""
+
+    def __init__(self, R, k, E, d_in, d_out, weighted, route_input):
+        m = torch.device("meta")
+        self.sel = torch.empty(R // k, k, device=m)
+        self.keys = torch.empty(E, d_in, d_out, device=m)
+        self.weights = torch.empty(R // k, k, device=m) if weighted else None
+        self.route_input, self.amp = route_input, True
+
+    @property
+    def routes(self):
+        return self.sel.numel()
+
+
+def ffn_line(steps: int = 10, warmup: int = 3, kernel_iters: int = 10):
     """The FFN stack of BASELINE.json configs[4] (16384 tokens, 2048 -> 512 ->
     2048, 128 experts, top-8, Zipf-skewed gate; benchmark_ffn_moe.py:89-98),
-    forward + backward, two ways: written as the reference's callers write it
-    (torch router lines, F.gelu around cvmm) and with the library's fused
-    router and up projection + GELU."""
+    forward + backward, as one bench line: the library's fused router and up
+    projection + GELU (``value``), beside the stack written as the
+    reference's callers write it (torch router lines, F.gelu around cvmm)."""
     s = W.c5_ffn_stack().to(torch.device("cuda"))
     params = [t.clone().requires_grad_(True) for t in (s.x, s.gate, s.w_up, s.w_down)]
     import cvmm_codex_amd as C
@@ -324,20 +389,58 @@ def ffn_times(steps: int = 10, warmup: int = 3):
         out = fwd(s, C, *params)
         out.backward(s.grad_out)
 
-    res = {"shape": {"tokens": 16384, "d_model": 2048, "hidden": 512, "experts": 128, "top_k": 8}}
+    def timed(fwd, n):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            step(fwd)
+        b.record()
+        b.synchronize()
+        return a.elapsed_time(b) / n
+
+    res = {}
     for name, fwd in (("composed", W.ffn_forward), ("fused", W.ffn_forward_fused)):
         for _ in range(warmup):
             step(fwd)
         torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(steps):
-            step(fwd)
-        b.record()
-        b.synchronize()
-        ms = a.elapsed_time(b) / steps
-        res[name] = {"ms_per_step": round(ms, 4), "tflops": round(s.flops / (ms * 1e-3) / 1e12, 2)}
-    return res
+        res[name] = timed(fwd, steps)
+    ms = res["fused"]
+
+    class _Runner:
+        def step(self):
+            step(W.ffn_forward_fused)
+
+    kt = kernel_times(_Runner(), kernel_iters)
+    T, D = s.x.shape[0] * s.x.shape[1], s.x.shape[2]
+    E, _, H = s.w_up.shape
+    R = T * s.k
+    up = _Shape(R, s.k, E, D, H, False, False)
+    down = _Shape(R, s.k, E, H, D, True, True)
+    dom = max((k for k in kt if k in PHASE), key=lambda k: kt[k]["ms_per_step"])
+    # both projections' launches of a class have the same flops (2 R D H)
+    flops = phase_work(up, PHASE[dom])[0]
+    nbytes = (phase_work(up, PHASE[dom])[1] + phase_work(down, PHASE[dom])[1]) / 2
+    roofline = roofline_of("mfma", "bf16", flops, nbytes, kt[dom]["avg_ms"] * 1e-3, load_traffic(dom, "ffn_stack"))
+    roofline.update({"kernel": dom, "avg_launch_ms": round(kt[dom]["avg_ms"], 5),
+                     "note": "per launch; the class runs once per projection, bytes averaged over the two"})
+    gate_flops = 6.0 * T * D * E
+    route_bytes = step_work(up)[1] + step_work(down)[1] + 3 * T * D * 2 + 3 * D * E * 4
+    step_roof = roofline_of("mfma", "bf16", s.flops, route_bytes, ms * 1e-3)
+    return {
+        "metric": METRIC, "value": round(s.flops / (ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded CPU generator, BASELINE.json recipe)",
+        "config": {"workload": "ffn_stack", "tokens": T, "d_model": D, "hidden": H, "n_experts": E,
+                   "top_k": s.k, "gate": "softmax top-8, Zipf(1.1) bias", "step": "router+up+gelu+down fwd+bwd",
+                   "gflop_per_step": round(s.flops / 1e9, 3), "gate_gflop": round(gate_flops / 1e9, 3)},
+        "composed_ms_per_step": round(res["composed"], 5),
+        "step_roofline": step_roof,
+        "kernel_ms_per_launch": {k: round(v["avg_ms"], 5) for k, v in kt.items()},
+        "kernel_launches_per_step": {k: v["launches_per_step"] for k, v in kt.items()},
+        "roofline": roofline,
+        "cpu_baseline": None,
+    }
 
 
 def main():
@@ -351,13 +454,13 @@ def main():
     ap.add_argument("--only", choices=["fwd", "bwd_w", "bwd_x", "cast_keys", "copy"], default=None,
                     help="launch only this phase --steps times, or the copy calibration (rocprofv3 runs)")
     ap.add_argument("--ffn", action="store_true",
-                    help="time the FFN stack (configs[4]) composed vs with the fused router and GELU (one JSON "
-                         "line) and exit")
+                    help="time the FFN stack (configs[4]) with the fused router and GELU, beside the composed "
+                         "stack (one JSON line) and exit")
     ap.add_argument("--router", action="store_true",
                     help="time the fused router against the torch router lines (one JSON line) and exit")
     ap.add_argument("--tune", action="append", default=[], metavar="KNOB=VALUE",
-                    help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, wgrad_tile, gemm_order, "
-                         "reduce_min_topk) before running")
+                    help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, wgrad_tile, gemm_order) "
+                         "before running")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -370,7 +473,7 @@ def main():
 
     from cvmm_codex_amd import _native as N
     knobs = {"panel_tiles_per_wg": N.TUNE_PANEL_TILES_PER_WG, "wgrad_order": N.TUNE_WGRAD_ORDER,
-             "gemm_order": N.TUNE_GEMM_ORDER, "reduce_min_topk": N.TUNE_REDUCE_MIN_TOPK,
+             "gemm_order": N.TUNE_GEMM_ORDER,
              "wgrad_tile": N.TUNE_WGRAD_TILE}
     for kv in args.tune:
         name, _, value = kv.partition("=")
@@ -384,8 +487,10 @@ def main():
     if args.router:
         print(json.dumps({"router": router_times()}), flush=True)
         return
+    import cvmm_codex_amd.api as C
+    C.cvmm_log_shapes = False   # stdout carries the one JSON line
     if args.ffn:
-        print(json.dumps({"ffn": ffn_times()}), flush=True)
+        print(json.dumps(ffn_line(args.steps, args.warmup, args.kernel_iters)), flush=True)
         return
     if args.only == "copy":
         copy_calibration(iters=args.steps)
@@ -414,21 +519,14 @@ def main():
     kt = kernel_times(runner, args.kernel_iters)
     log("kernel ms/launch " + json.dumps({k: round(v["avg_ms"], 5) for k, v in kt.items()}))
     dtype = "bf16" if proj.amp else "fp32"
-    peak = PEAK[dtype]
-    # dominant kernel: the hot kernel class with the most device time per step
-    dom = max((k for k in kt if kernel_work(proj, k)[0] is not None), key=lambda k: kt[k]["ms_per_step"])
+    bound = BOUND[proj.name]
+    # dominant kernel: the GEMM class with the most device time per step
+    dom = max((k for k in kt if k in PHASE), key=lambda k: kt[k]["ms_per_step"])
     flops, nbytes = kernel_work(proj, dom)
-    sec = kt[dom]["avg_ms"] * 1e-3
-    t_mfma, t_hbm = flops / (peak * 1e12), nbytes / (HBM_PEAK_GBS * 1e9)
-    if t_hbm >= t_mfma:
-        roofline = {"bound": "hbm", "achieved": round(nbytes / sec / 1e9, 2), "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 5)}
-    else:
-        roofline = {"bound": "mfma", "achieved": round(flops / sec / 1e12, 3), "peak": peak,
-                    "unit": "TFLOP/s", "frac": round(flops / sec / 1e12 / peak, 5)}
-    roofline.update({"traffic": load_traffic(dom, proj.name), "kernel": dom,
-                     "avg_launch_ms": round(kt[dom]["avg_ms"], 5), "algorithmic_bytes": int(nbytes),
-                     "algorithmic_flops": flops})
+    roofline = roofline_of(bound, dtype, flops, nbytes, kt[dom]["avg_ms"] * 1e-3, load_traffic(dom, proj.name))
+    roofline.update({"kernel": dom, "avg_launch_ms": round(kt[dom]["avg_ms"], 5)})
+    sflops, sbytes = step_work(proj)
+    step_roof = roofline_of(bound, dtype, sflops, sbytes, ms * 1e-3)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -445,7 +543,7 @@ def main():
                    "d_out": proj.keys.shape[2], "n_experts": proj.keys.shape[0],
                    "top_k": proj.sel.shape[-1], "weighted": proj.weights is not None,
                    "step": "sel+fwd+bwd", "gflop_per_step": round(proj.flops / 1e9, 3)},
-        "step_roofline_frac": round(value / PEAK[dtype], 5),
+        "step_roofline": step_roof,
         "breakdown_ms": {k: round(v, 5) for k, v in phases.items()},
         "kernel_ms_per_launch": {k: round(v["avg_ms"], 5) for k, v in kt.items()},
         "roofline": roofline,

@@ -18,16 +18,14 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcvmm_hip
 F32, F16, BF16 = 0, 1, 2            # cvmm.py:36-44 dtype ids
 FLAG_ATOMIC_REDUCE = 1
 FLAG_COUNTERS_ZEROED = 2
-FLAG_ROUTES_STABLE = 4
 TUNE_PANEL_TILES_PER_WG = 1
 TUNE_WGRAD_ORDER = 2
 TUNE_GEMM_ORDER = 3
-TUNE_REDUCE_MIN_TOPK = 4
 TUNE_WGRAD_TILE = 5
 
 # kernel classes of the timing hooks (include/cvmm_hip.h CVMM_KC_*)
-KC_SORT, KC_OFFSETS, KC_CAST_KEYS, KC_GEMM_FWD, KC_GEMM_BWDX, KC_WGRAD, KC_COMBINE, KC_FILL, KC_REDUCE, KC_ROUTE = (
-    1, 2, 4, 8, 16, 32, 64, 128, 256, 512)
+KC_SORT, KC_OFFSETS, KC_CAST_KEYS, KC_GEMM_FWD, KC_GEMM_BWDX, KC_WGRAD, KC_COMBINE, KC_FILL, KC_ROUTE = (
+    1, 2, 4, 8, 16, 32, 64, 128, 512)
 
 _DTYPE_ID = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 

@@ -15,10 +15,12 @@ All arithmetic runs in the HIP kernels of ``libcvmm_hip.so`` (C ABI in
 synchronises with the host.  There is no CPU or PyTorch fallback: CPU tensors
 and a missing library raise.
 
-Selector sorting is deferred: ``cvmm_prepare_sel2`` records the selection and
-the stable counting sort runs when ``cvmm`` first sees the selector, because the
-sort needs the expert count, which is ``keys.shape[0]`` and is not an argument
-of ``cvmm_prepare_sel2``.  Reading ``.sel`` / ``.sel_index`` / ``.out_index``
+Selector sorting is deferred: ``cvmm_prepare_sel2`` takes the int32 copy of
+the ids the reference takes (cvmm.py:1796), so later writes to the caller's
+``sel`` do not change the routing, and the stable counting sort of that copy
+runs when ``cvmm`` first sees the selector, because the sort needs the expert
+count, which is ``keys.shape[0]`` and is not an argument of
+``cvmm_prepare_sel2``.  Reading ``.sel`` / ``.sel_index`` / ``.out_index``
 earlier forces the sort (with the expert count taken from the largest id, one
 host sync).
 """
@@ -26,6 +28,7 @@ from __future__ import annotations
 
 import os
 import threading
+from dataclasses import dataclass
 from typing import Dict, Optional, Tuple, Union
 
 import torch
@@ -61,8 +64,9 @@ cvmm_lowmem_chunk_size = int(os.environ.get("CVMM_LOWMEM_CHUNK_SIZE", "0"))
 # Sum the top-k terms (weighted forward combine, token-input grad_x) with fp32
 # atomics into token rows instead of a route-ordered buffer + ordered row sum.
 cvmm_atomic_reduce = _env_on("CVMM_ATOMIC_REDUCE")
-# Print each new (x.shape, keys.shape) like the reference (cvmm.py:1778-1781).
-cvmm_log_shapes = _env_on("CVMM_LOG_SHAPES")
+# Print each new (x.shape, keys.shape) like the reference (cvmm.py:1778-1781);
+# on by default as there, CVMM_LOG_SHAPES=0 (or setting this to False) silences it.
+cvmm_log_shapes = _env_on("CVMM_LOG_SHAPES", "1")
 # The forward primitive as a torch.library op, as the reference exposes
 # torch.ops.mylib.cvmm_triton (cvmm.py:1458-1459).
 cvmm_triton_call = torch.ops.cvmm_codex_amd.cvmm_triton
@@ -205,45 +209,50 @@ class _Routing:
         return self.by_e[self.first_e]
 
 
+@dataclass(init=False)
 class CVMMSel:
-    """Selector metadata (cvmm.py:12-21): same constructor, fields and clone().
+    """Selector metadata (cvmm.py:12-21): the same dataclass fields, constructor
+    and clone(), so ``dataclasses.fields``/``replace``/``asdict`` work as on the
+    reference's selector.
 
-    Instances made by cvmm_prepare_sel2 resolve ``sel``/``sel_index``/``out_index``
-    lazily (see the module docstring); instances built directly are plain records.
+    Instances made by cvmm_prepare_sel2 hold a snapshot of the ids and sort it
+    lazily: ``sel``/``sel_index``/``out_index`` resolve on first read (see the
+    module docstring); instances built directly are plain records.
     """
+
+    raw_sel: torch.Tensor
+    sel: torch.Tensor
+    sel_index: torch.Tensor
+    out_index: Optional[torch.Tensor] = None
+    reduction_weight: Optional[torch.Tensor] = None
 
     def __init__(self, raw_sel: torch.Tensor, sel: torch.Tensor, sel_index: torch.Tensor,
                  out_index: Optional[torch.Tensor] = None, reduction_weight: Optional[torch.Tensor] = None):
+        # the fields' backing attributes (the fields are properties, below)
         self._raw_sel = raw_sel
-        self._raw_src: Optional[torch.Tensor] = None
+        self._raw_src = None
         self._sel = sel
         self._sel_index = sel_index
         self._out_index = out_index
         self.reduction_weight = reduction_weight
-        self._routing: Optional[_Routing] = None
+        self._routing = None
         self._route_mode = False
 
+    def clone(self) -> "CVMMSel":
+        if self._pending():
+            return CVMMSel._deferred(self._raw_shape_tensor(), self._routing, self._route_mode,
+                                     self.reduction_weight)
+        return CVMMSel(self.raw_sel, self.sel, self.sel_index, self.out_index, self.reduction_weight)
+
     @classmethod
-    def _deferred(cls, raw_src: torch.Tensor, routing: _Routing, route_mode: bool, w) -> "CVMMSel":
-        """`raw_src`: the selection as given (any integer dtype); the int32
-        copy the reference stores as raw_sel is made only if it is read."""
+    def _deferred(cls, raw_src: torch.Tensor, routing: "_Routing", route_mode: bool, w) -> "CVMMSel":
+        """`raw_src`: the ids as given (any integer dtype); the int32 tensor
+        the reference stores as raw_sel is made only if it is read."""
         s = cls(None, None, None, None, w)
         s._raw_src = raw_src
         s._routing = routing
         s._route_mode = route_mode
         return s
-
-    @property
-    def raw_sel(self):
-        if self._raw_sel is None and self._raw_src is not None:
-            src = self._raw_src
-            self._raw_sel = src if src.dtype == torch.int32 else src.reshape(-1).to(torch.int32).view(src.shape)
-        return self._raw_sel
-
-    @raw_sel.setter
-    def raw_sel(self, v):
-        self._raw_sel = v
-        self._raw_src = None
 
     def _raw_shape_tensor(self) -> torch.Tensor:
         """A tensor of raw_sel's shape without forcing the int32 copy (the
@@ -270,48 +279,46 @@ class CVMMSel:
         else:
             self._sel_index, self._out_index = tok, perm
 
-    @property
-    def sel(self):
-        self._resolve()
-        return self._sel
-
-    @sel.setter
-    def sel(self, v):
-        self._resolve()
-        self._sel = v
-
-    @property
-    def sel_index(self):
-        self._resolve()
-        return self._sel_index
-
-    @sel_index.setter
-    def sel_index(self, v):
-        self._resolve()
-        self._sel_index = v
-
-    @property
-    def out_index(self):
-        self._resolve()
-        return self._out_index
-
-    @out_index.setter
-    def out_index(self, v):
-        self._resolve()
-        self._out_index = v
-
-    def clone(self) -> "CVMMSel":
-        if self._pending():
-            return CVMMSel._deferred(self._raw_shape_tensor(), self._routing, self._route_mode,
-                                     self.reduction_weight)
-        return CVMMSel(self.raw_sel, self.sel, self.sel_index, self.out_index, self.reduction_weight)
-
     def __repr__(self) -> str:
         if self._pending():
             return (f"CVMMSel(raw_sel={tuple(self._raw_shape_tensor().shape)}, pending sort, "
                     f"route_input={self._route_mode})")
         return (f"CVMMSel(raw_sel={self.raw_sel!r}, sel={self._sel!r}, sel_index={self._sel_index!r}, "
                 f"out_index={self._out_index!r}, reduction_weight={self.reduction_weight!r})")
+
+
+# The dataclass fields above are served by properties: reading sel / sel_index
+# / out_index of a deferred selector runs its sort, raw_sel is made on demand.
+def _get_raw_sel(self):
+    if self._raw_sel is None and self._raw_src is not None:
+        src = self._raw_src
+        self._raw_sel = src if src.dtype == torch.int32 else src.reshape(-1).to(torch.int32).view(src.shape)
+    return self._raw_sel
+
+
+def _set_raw_sel(self, v):
+    self._raw_sel = v
+    self._raw_src = None
+
+
+def _resolved_field(name):
+    attr = "_" + name
+
+    def get(self):
+        self._resolve()
+        return getattr(self, attr)
+
+    def set_(self, v):
+        self._resolve()
+        setattr(self, attr, v)
+
+    return property(get, set_)
+
+
+CVMMSel.raw_sel = property(_get_raw_sel, _set_raw_sel)
+for _name in ("sel", "sel_index", "out_index"):
+    setattr(CVMMSel, _name, _resolved_field(_name))
+del _name
 
 
 def cvmm_prepare_sel(sel: torch.Tensor, n_experts: int) -> CVMMSel:
@@ -343,7 +350,13 @@ def cvmm_prepare_sel2(sel: Union[torch.Tensor, CVMMSel], w: Optional[torch.Tenso
 
     _require_device(sel, "sel")
     n_per_batch = sel.shape[-1]
-    return CVMMSel._deferred(sel, _Routing(sel.reshape(-1), n_per_batch), route_input, w)
+    # the reference's `fsel = sel.flatten().to(torch.int32)` (cvmm.py:1796):
+    # the routing is fixed here, whatever later happens to `sel`
+    fsel = sel.reshape(-1)
+    fsel = fsel.clone() if fsel.dtype == torch.int32 else fsel.to(torch.int32)
+    out = CVMMSel._deferred(fsel.view(sel.shape), _Routing(fsel, n_per_batch), route_input, w)
+    out._raw_sel = out._raw_src
+    return out
 
 
 # ----------------------------------------------------------------------------
@@ -462,7 +475,7 @@ def _forward(x, sel_index, sel, keys, out_index, rw, op_dtype, keys_t=None):
     else:
         out = N.host().forward(x, keys, keys_t, sel, sel_index, out_index, _offsets_for(sel, n_experts),
                                _route_pos(out_index if out_index is not None else sel_index, R), rw,
-                               N.dtype_id(op_dtype), _flags(), N.stream_of(x.device))
+                               N.dtype_id(op_dtype), -1, _flags(), N.stream_of(x.device))
     if rw is None:
         return out.view(*sel.shape, keys.shape[2])
     return out.view(*rw.shape[:-1], keys.shape[2])

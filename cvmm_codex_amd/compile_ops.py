@@ -83,7 +83,7 @@ def forward(x: torch.Tensor, keys: torch.Tensor, keys_t: Optional[torch.Tensor],
             sel_index: torch.Tensor, out_index: Optional[torch.Tensor], offsets: torch.Tensor,
             reduction_weight: Optional[torch.Tensor], op_dtype: torch.dtype, flags: int) -> torch.Tensor:
     return N.host().forward(x, keys, keys_t, sel, sel_index, out_index, offsets, None, reduction_weight,
-                            N.dtype_id(op_dtype), flags, N.stream_of(x.device))
+                            N.dtype_id(op_dtype), -1, flags, N.stream_of(x.device))
 
 
 @forward.register_fake
@@ -113,7 +113,8 @@ def backward(grad_output: torch.Tensor, x: torch.Tensor, keys: torch.Tensor, key
 @backward.register_fake
 def _(grad_output, x, keys, keys_n, sel, sel_index, out_index, offsets, reduction_weight, top_k, op_dtype,
       need_grad_x, need_grad_keys, need_grad_rw, flags):
-    gx = torch.empty_like(x) if need_grad_x else _empty(x)
+    # the real op's grad_x is always a fresh contiguous tensor of x's shape
+    gx = x.new_empty(x.shape) if need_grad_x else _empty(x)
     gw = torch.empty_like(keys, memory_format=torch.contiguous_format) if need_grad_keys else _empty(keys)
     grw = (torch.empty_like(reduction_weight, memory_format=torch.contiguous_format)
            if need_grad_rw and reduction_weight is not None else _empty(x))
@@ -131,12 +132,18 @@ def grads_or_none(g: Tuple[torch.Tensor, torch.Tensor, torch.Tensor], need: List
 @torch.library.custom_op(f"{NS}::cvmm_triton", mutates_args=())
 def cvmm_triton(x: torch.Tensor, sel_index: torch.Tensor, sel: torch.Tensor, keys: torch.Tensor,
                 out_dtype: torch.dtype, out_index: torch.Tensor, op_dtype: torch.dtype) -> torch.Tensor:
-    oi = None if (out_index.numel() == 1 and int(out_index.item()) == -1) else out_index
+    # one-element out_index holding -1 = "none" (cvmm.py:845-846); with more
+    # than one route a real out_index has more entries, so only a one-route
+    # selection needs its value read (a host sync, as in the reference)
+    R = sel.numel()
+    sentinel = out_index.numel() == 1 and (R != 1 or int(out_index.item()) == -1)
+    oi = None if sentinel else out_index
     s32 = sel.reshape(-1).to(torch.int32)
     off = N.host().expert_offsets(s32, keys.shape[0], N.stream_of(x.device))
-    out = N.host().forward(x, keys, None, s32, sel_index, oi, off, None, None, N.dtype_id(op_dtype), 0,
-                           N.stream_of(x.device))
-    return out.to(out_dtype).view(*sel.shape, keys.shape[2])
+    # products rounded once, straight to out_dtype (cvmm.py:832-833, :862-863)
+    out = N.host().forward(x, keys, None, s32, sel_index, oi, off, None, None, N.dtype_id(op_dtype),
+                           N.dtype_id(out_dtype), 0, N.stream_of(x.device))
+    return out.view(*sel.shape, keys.shape[2])
 
 
 @cvmm_triton.register_fake

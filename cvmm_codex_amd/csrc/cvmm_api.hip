@@ -114,7 +114,6 @@ std::atomic<int32_t> g_panel_tpw{0};
 std::atomic<int32_t> g_wgrad_order{0};
 std::atomic<int32_t> g_wgrad_tile{0};
 std::atomic<int32_t> g_gemm_order{0};
-std::atomic<int64_t> g_reduce_min_topk{0};
 
 // m-tile order of the routed GEMMs (see GemmParams::token_major): the knob's
 // choice, or -1 to let the kernel launcher decide
@@ -195,62 +194,6 @@ bool reduce_needed(int32_t weighted, int32_t token_input, int64_t top_k) {
 
 int64_t ntiles_of(int64_t n, int64_t bn) { return (n + bn - 1) / bn; }
 
-// The reduce GEMM takes the top-k sum in place of the routed GEMM + combine
-// when it is switched on (a top-k threshold set by the tuning knob; off by
-// default: it needs ~30x less workspace at high fan-out but is slower, see
-// cvmm_reduce.h), the caller vouches for the route order, no atomic reduce is
-// asked for, the fan-out reaches the threshold and the shapes fit the kernel.
-// Shapes only: the workspace query decides with it.
-bool use_reduce_gemm(int32_t flags, int32_t op_dtype, int64_t K, int64_t N, int32_t n_experts, int64_t n_routes,
-                     int64_t rows, int64_t top_k, int32_t out_dtype) {
-  const int64_t min_k = g_reduce_min_topk.load();
-  return min_k > 0 && (flags & CVMM_FLAG_ROUTES_STABLE) && !(flags & CVMM_FLAG_ATOMIC_REDUCE) && top_k >= min_k &&
-         reduce_shape_ok(op_dtype, K, N, n_experts, n_routes, rows, top_k, out_dtype);
-}
-
-// Workspace of the reduce GEMM: gathered A rows, route info, group bounds,
-// stage lists.
-struct ReduceWs {
-  void* a_sorted;
-  RouteInfo* info;
-  int32_t* lo;
-  ReduceStage* stages;
-  int32_t* n_stages;
-  int32_t group, groups, maxr;
-};
-ReduceWs carve_reduce(Carver& c, int64_t n_routes, int64_t K, int32_t n_experts, int64_t rows) {
-  ReduceWs w;
-  w.group = reduce_group_tokens(K);
-  w.groups = (int32_t)((rows + w.group - 1) / w.group);
-  w.maxr = reduce_stage_routes(K, n_routes, w.groups, n_experts);
-  w.a_sorted = c.take((size_t)n_routes * K * 2);
-  w.info = (RouteInfo*)c.take((size_t)(n_routes + kReducePad) * sizeof(RouteInfo));
-  w.lo = (int32_t*)c.take((size_t)(w.groups + 1) * n_experts * 4);
-  w.stages = (ReduceStage*)c.take((size_t)w.groups * kReduceMaxStages * sizeof(ReduceStage));
-  w.n_stages = (int32_t*)c.take((size_t)w.groups * 4);
-  return w;
-}
-
-// Gather + reduce GEMM: out[t] = rnd_mid(sum_r w_r * rnd_val(A_r B_e(r))).
-int run_reduce(const ReduceWs& w, const void* a, int32_t a_dtype, int64_t a_ld, int64_t a_rows, const int64_t* a_idx,
-               int64_t a_div, const int64_t* rp, int64_t top_k, const void* rw, int32_t rw_dtype, int32_t w_round,
-               const void* b, int64_t b_se, int64_t b_sn, int64_t K, int64_t N, const int64_t* offs,
-               int32_t n_experts, int64_t n_routes, int32_t op_dtype, int32_t val_dtype, int32_t mid_dtype,
-               void* out, int32_t out_dtype, int64_t out_ld, int64_t rows, const char* what, hipStream_t s) {
-  int r = check_launch(timed_combine(s, [&] { return launch_reduce_prepare(a, a_dtype, a_ld, a_rows, a_idx, a_div, K, op_dtype, rp, top_k, rw,
-                                                           rw_dtype, w_round, offs, n_experts, n_routes, rows, w.group, w.maxr,
-                                                           w.a_sorted, w.info, w.lo, w.stages, w.n_stages, s); }),
-                       what);
-  if (r) return r;
-  ReduceParams q{};
-  q.a = w.a_sorted; q.info = w.info; q.stages = w.stages; q.n_stages = w.n_stages; q.maxr = w.maxr;
-  q.b = b; q.b_se = b_se; q.b_sn = b_sn; q.K = K; q.N = N;
-  q.n_experts = n_experts; q.n_routes = n_routes; q.n_tokens = rows; q.n_groups = w.groups; q.group = w.group;
-  q.val_dtype = val_dtype; q.weighted = rw != nullptr ? 1 : 0; q.mid_dtype = mid_dtype;
-  q.out = out; q.out_dtype = out_dtype; q.out_ld = out_ld;
-  return check_launch(timed(CVMM_KC_REDUCE, s, [&] { return launch_routed_reduce(q, op_dtype, s); }), what);
-}
-
 // n-tile width of the routed GEMM for output width n (256x64 tiles when narrow).
 int64_t gemm_bn(int64_t n) { return n <= 64 ? 64 : 128; }
 
@@ -260,7 +203,7 @@ extern "C" {
 
 const char* cvmm_last_error(void) { return g_err.c_str(); }
 
-int cvmm_abi_version(void) { return 8; }
+int cvmm_abi_version(void) { return 9; }
 
 int cvmm_timing_enable(uint32_t class_mask) {
   std::lock_guard<std::mutex> lk(g_timing_mu);
@@ -277,11 +220,6 @@ int cvmm_tuning_set(int32_t knob, int64_t value) {
   if (knob == CVMM_TUNE_GEMM_ORDER) {
     if (value < 0 || value > 2) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: GEMM order must be 0, 1 or 2");
     g_gemm_order.store((int32_t)value);
-    return CVMM_OK;
-  }
-  if (knob == CVMM_TUNE_REDUCE_MIN_TOPK) {
-    if (value < 0 || value > (1ll << 40)) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: top-k threshold out of range");
-    g_reduce_min_topk.store(value);
     return CVMM_OK;
   }
   if (knob == CVMM_TUNE_WGRAD_ORDER) {
@@ -459,10 +397,7 @@ size_t cvmm_fwd_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_i
   Carver c(nullptr);
   if (!has_offsets) c.take((size_t)n_experts * 8);
   if (weighted) {
-    const int64_t k = out_rows > 0 ? n_routes / out_rows : 0;
-    if (use_reduce_gemm(flags, op_dtype, d_in, d_out, n_experts, n_routes, out_rows, k, out_dtype)) {
-      carve_reduce(c, n_routes, d_in, n_experts, out_rows);
-    } else if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
+    if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
       c.take((size_t)out_rows * d_out * 4);
     } else {
       c.take((size_t)n_routes * d_out * dtype_size(out_dtype));
@@ -494,13 +429,6 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
   if (weighted && (reduce_k <= 0 || n_routes % reduce_k != 0 || out_rows != n_routes / reduce_k))
     return fail(CVMM_ERR_INVALID, "cvmm_fwd: weighted output needs out_rows = R / reduce_k");
   if (!weighted && out_rows != n_routes) return fail(CVMM_ERR_INVALID, "cvmm_fwd: out_rows must equal R");
-  // the reduce GEMM when the flag, the shapes and the operands allow it;
-  // otherwise the call is the one without the flag (and its workspace)
-  const bool red = weighted &&
-                   use_reduce_gemm(flags, op_dtype, d_in, d_out, n_experts, n_routes, out_rows, reduce_k, out_dtype) &&
-                   keys_dtype == op_dtype && aligned16(x) && (x_ld * (int64_t)dtype_size(x_dtype)) % 16 == 0 &&
-                   aligned16(workspace) && reduce_align_ok(keys, k_si, k_se, k_sj, out, out_dtype, out_ld);
-  if (!red) flags &= ~CVMM_FLAG_ROUTES_STABLE;
   const size_t need = cvmm_fwd_workspace_bytes(n_routes, n_experts, d_in, d_out, out_rows, out_dtype, op_dtype,
                                                offsets != nullptr, weighted, flags);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
@@ -542,6 +470,13 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
   p.token_major = gemm_token_major(n_experts);
 
   if (!weighted) {
+    // rows of routes with an expert id outside [0, E) are zeroed after the GEMM
+    const int64_t* rows_end = offs + (n_experts - 1);
+    auto zero_unrouted = [&](void* buf) {
+      return check_launch(timed_fill(s, [&] { return launch_zero_unrouted_rows(buf, out_dtype, out_ld, d_out, out_rows, rp, 1,
+                                                                  rows_end, n_routes, s); }),
+                          "cvmm_fwd(zero unrouted)");
+    };
     p.epi = kEpiStore; p.out = out; p.out_dtype = out_dtype; p.out_ld = out_ld; p.out_rows = out_rows;
     if (pre_act != nullptr) {
       p.act = 1; p.aux = pre_act;
@@ -550,18 +485,15 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
         p.act = 0; p.aux = nullptr; p.out = pre_act;
         int r = check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
         if (r) return r;
+        if ((r = zero_unrouted(pre_act))) return r;
         return check_launch(timed_combine(s, [&] { return launch_gelu_rows(pre_act, out_dtype, out_ld, out_rows, d_out, out, out_dtype, out_ld, s); }),
                             "cvmm_fwd_gelu(gelu)");
       }
     }
-    return check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
-  }
-  if (red) {
-    // reduce GEMM: the combine's sums (rounding as below), no route buffer
-    const ReduceWs w = carve_reduce(c, n_routes, d_in, n_experts, out_rows);
-    return run_reduce(w, x, x_dtype, x_ld, x_rows, sel_index, 1, rp, reduce_k, rw, rw_dtype, out_dtype, keys, k_se,
-                      k_sj, d_in, d_out, offs, n_experts, n_routes, op_dtype, out_dtype, out_dtype, out, out_dtype,
-                      out_ld, out_rows, "cvmm_fwd(reduce)", s);
+    int r = check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
+    if (r) return r;
+    if (pre_act != nullptr && (r = zero_unrouted(pre_act))) return r;
+    return zero_unrouted(out);
   }
   if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
     // fused combine: y rounded to the output dtype, times rnd_out(w), fp32 atomics per token row
@@ -646,10 +578,7 @@ size_t cvmm_bwd_x_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d
   Carver c(nullptr);
   if (!has_offsets) c.take((size_t)n_experts * 8);
   if (reduce_needed(weighted, token_input, top_k)) {
-    if (!(weighted && need_grad_rw) &&
-        use_reduce_gemm(flags, op_dtype, d_out, d_in, n_experts, n_routes, grad_x_rows, top_k, grad_x_dtype)) {
-      carve_reduce(c, n_routes, d_out, n_experts, grad_x_rows);
-    } else if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
+    if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
       c.take((size_t)grad_x_rows * d_in * 4);
     } else {
       c.take((size_t)n_routes * d_in * dtype_size(weighted ? op_dtype : grad_x_dtype));
@@ -687,12 +616,6 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
       return fail(CVMM_ERR_INVALID, "cvmm_bwd_x: grad_x has %lld rows, expected %lld", (long long)grad_x_rows,
                   (long long)want);
   }
-  const bool red = grad_x && reduce && !(weighted && grad_rw) &&
-                   use_reduce_gemm(flags, op_dtype, d_out, d_in, n_experts, n_routes, grad_x_rows, top_k,
-                                   grad_x_dtype) &&
-                   keys_dtype == op_dtype && aligned16(grad) && (grad_ld * (int64_t)dtype_size(grad_dtype)) % 16 == 0 &&
-                   aligned16(workspace) && reduce_align_ok(keys, k_sj, k_se, k_si, grad_x, grad_x_dtype, grad_x_ld);
-  if (!red) flags &= ~CVMM_FLAG_ROUTES_STABLE;
   const size_t need = cvmm_bwd_x_workspace_bytes(n_routes, n_experts, d_in, d_out, grad_x_rows, offsets != nullptr,
                                                  weighted, token_input, top_k, grad_x_dtype, op_dtype,
                                                  grad_rw != nullptr, flags);
@@ -735,16 +658,6 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
   p.role = 1;
   p.panel_tpw = g_panel_tpw.load();
   p.token_major = gemm_token_major(n_experts);
-
-  if (red) {
-    // reduce GEMM: the combine's sums (rounding as below), no route buffer
-    const ReduceWs w = carve_reduce(c, n_routes, d_out, n_experts, grad_x_rows);
-    const int32_t vdt = weighted ? op_dtype : grad_x_dtype;
-    return run_reduce(w, grad, grad_dtype, grad_ld, grad_rows, rp, weighted ? top_k : 1, rp, top_k,
-                      weighted ? rw : nullptr, rw_dtype, op_dtype, keys, k_se, k_si, d_out, d_in, offs, n_experts,
-                      n_routes, op_dtype, vdt, weighted ? op_dtype : -1, grad_x, grad_x_dtype, grad_x_ld, grad_x_rows,
-                      "cvmm_bwd_x(reduce)", s);
-  }
 
   void* route_buf = nullptr;
   const int32_t* inv = nullptr;
@@ -798,6 +711,13 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
 
   int r = check_launch(timed(CVMM_KC_GEMM_BWDX, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_bwd_x(gemm)");
   if (r) return r;
+  if (grad_x && !reduce) {
+    // per-route rows of routes with an expert id outside [0, E): zero
+    r = check_launch(timed_fill(s, [&] { return launch_zero_unrouted_rows(grad_x, grad_x_dtype, grad_x_ld, d_in, grad_x_rows, rp, 1,
+                                                             offs + (n_experts - 1), n_routes, s); }),
+                     "cvmm_bwd_x(zero unrouted)");
+    if (r) return r;
+  }
   if (grad_x && reduce) {
     if (acc) {
       r = check_launch(timed_combine(s, [&] { return launch_cast_rows(acc, d_in, grad_x_rows, d_in, weighted ? op_dtype : -1, grad_x,

@@ -203,66 +203,6 @@ hipError_t launch_cast_keys(const void* keys, int32_t keys_dtype, int64_t se, in
 // ---------------------------------------------------------------------------
 // small kernels
 // ---------------------------------------------------------------------------
-// ---------------------------------------------------------------------------
-// reduce GEMM: a top-k sum of routed products without a route-ordered buffer
-// out[t] = rnd_mid(sum over the routes r of token t of w_r * rnd_val(A_r B_e(r)))
-// ---------------------------------------------------------------------------
-struct RouteInfo {
-  int32_t orow;  // output row (token) of the sorted route, -1 = none
-  float w;       // rounded routing weight (1 when unweighted)
-};
-// One stage of a token group: up to `maxr` routes of one expert, contiguous in
-// the sorted order from `r`; `er` = expert * 256 + route count.
-struct ReduceStage {
-  int32_t r, er;
-};
-struct ReduceParams {
-  const void* a;             // [R][K] rows in sorted order, op dtype (gathered)
-  const RouteInfo* info;     // [R + kReducePad]
-  const ReduceStage* stages; // [G][kReduceMaxStages]
-  const int32_t* n_stages;   // [G]
-  const void* b;             // weights, rows n with k contiguous: b + e*b_se + n*b_sn + k
-  int64_t b_se, b_sn;
-  int64_t K, N;
-  int32_t n_experts;
-  int64_t n_routes, n_tokens;
-  int32_t n_groups;
-  int32_t group;             // tokens per group (reduce_group_tokens(K))
-  int32_t maxr;              // routes per stage (reduce_stage_routes)
-  int32_t val_dtype;         // rounding of each route's product
-  int32_t weighted;
-  int32_t mid_dtype;         // rounding of the sum (-1: none) before the output cast
-  void* out;
-  int32_t out_dtype;
-  int64_t out_ld;
-};
-constexpr int64_t kReducePad = 128;       // RouteInfo entries past R (whole DMA instructions)
-constexpr int64_t kReduceCols = 64;       // output columns per workgroup
-constexpr int32_t kReduceMaxStages = 1024;  // stages of one token group (held in LDS)
-// Tokens per group: the fp32 sums of a group's 64-column slice stay in LDS.
-inline int32_t reduce_group_tokens(int64_t K) { return K <= 64 ? 256 : 128; }
-// Routes per stage, from the mean routes per (group, expert) m: 32 when
-// nearly every segment fits (m + 3 sqrt(m) <= 32), else the larger stage.
-int32_t reduce_stage_routes(int64_t K, int64_t n_routes, int64_t n_groups, int32_t n_experts);
-// Gather into sorted order + route info + group bounds + stage lists.
-hipError_t launch_reduce_prepare(const void* a, int32_t a_dtype, int64_t a_ld, int64_t a_rows, const int64_t* a_idx,
-                                 int64_t a_div, int64_t K, int32_t op_dtype, const int64_t* rp, int64_t top_k,
-                                 const void* w, int32_t w_dtype, int32_t w_round, const int64_t* offsets,
-                                 int32_t n_experts, int64_t n_routes, int64_t n_tokens, int32_t group, int32_t maxr,
-                                 void* a_sorted, RouteInfo* info, int32_t* lo, ReduceStage* stages,
-                                 int32_t* n_stages, hipStream_t stream);
-hipError_t launch_routed_reduce(const ReduceParams& p, int32_t op_dtype, hipStream_t stream);
-hipError_t launch_routed_reduce_bf16(const ReduceParams& p, hipStream_t stream);
-hipError_t launch_routed_reduce_f16(const ReduceParams& p, hipStream_t stream);
-// The reduce GEMM applies to: a 16-bit op, K in {64, 128}, N % 64 == 0, output
-// in the op dtype or fp32, and stage lists that fit kReduceMaxStages (at most
-// E + ceil(group * top_k / maxr) stages per group) ...
-bool reduce_shape_ok(int32_t op_dtype, int64_t K, int64_t N, int32_t n_experts, int64_t n_routes, int64_t n_tokens,
-                     int64_t top_k, int32_t out_dtype);
-// ... with k-contiguous weight rows and output rows on 16-byte boundaries.
-bool reduce_align_ok(const void* b, int64_t b_sk, int64_t b_se, int64_t b_sn, const void* out, int32_t out_dtype,
-                     int64_t out_ld);
-
 // The stable scatter of cvmm_sort_routes over int64 ids whose per-chunk
 // histogram (counts[chunk][E + 1], chunks of `chunk` routes) is already built.
 // A large histogram is turned in place into per-chunk bucket prefixes, with
@@ -308,6 +248,12 @@ hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_l
                                int64_t k, int64_t n, int32_t mid_dtype, void* out, int32_t out_dtype, int64_t out_ld,
                                hipStream_t stream);
 hipError_t launch_invert_rows(const int64_t* rp, int64_t n_routes, int32_t* inv, hipStream_t stream);
+// Zero out[row][0, width) for the sorted routes q in [*rows_end, n_routes)
+// (expert id outside [0, E): no GEMM tile stores them), row = o_idx[q] / o_div
+// or q when o_idx == NULL, rows outside [0, out_rows) skipped.
+hipError_t launch_zero_unrouted_rows(void* out, int32_t out_dtype, int64_t out_ld, int64_t width, int64_t out_rows,
+                                     const int64_t* o_idx, int64_t o_div, const int64_t* rows_end, int64_t n_routes,
+                                     hipStream_t stream);
 // out[t][n] = rnd(rnd(acc[t][n], mid_dtype), out_dtype)
 hipError_t launch_cast_rows(const float* acc, int64_t acc_ld, int64_t rows, int64_t n, int32_t mid_dtype,
                             void* out, int32_t out_dtype, int64_t out_ld, hipStream_t stream);

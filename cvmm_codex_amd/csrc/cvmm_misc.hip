@@ -33,6 +33,38 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Rows of routes whose expert id is outside [0, E): those sort past
+// *rows_end (the last inclusive offset) and no GEMM tile covers them.  Their
+// output rows (row = o_idx[q] / o_div, or q) are zeroed so that a direct
+// per-route store never leaves uninitialised memory.  One workgroup per
+// such route, grid-strided; nothing to do (the usual case) costs one read of
+// *rows_end per workgroup.
+__global__ __launch_bounds__(256) void zero_unrouted_rows_kernel(void* __restrict__ out, int32_t out_dtype,
+                                                                 int64_t out_ld, int64_t width, int64_t out_rows,
+                                                                 const int64_t* __restrict__ o_idx, int64_t o_div,
+                                                                 const int64_t* __restrict__ rows_end,
+                                                                 int64_t n_routes) {
+  int64_t q0 = *rows_end;
+  q0 = q0 < 0 ? 0 : q0;
+  const size_t esz = dtype_size(out_dtype);
+  for (int64_t q = q0 + blockIdx.x; q < n_routes; q += gridDim.x) {
+    const int64_t row = o_idx != nullptr ? o_idx[q] / o_div : q;
+    if (row < 0 || row >= out_rows) continue;
+    uint8_t* base = static_cast<uint8_t*>(out) + (size_t)(row * out_ld) * esz;
+    for (int64_t b = threadIdx.x; b < width * (int64_t)esz; b += blockDim.x) base[b] = 0;
+  }
+}
+
+hipError_t launch_zero_unrouted_rows(void* out, int32_t out_dtype, int64_t out_ld, int64_t width, int64_t out_rows,
+                                     const int64_t* o_idx, int64_t o_div, const int64_t* rows_end, int64_t n_routes,
+                                     hipStream_t stream) {
+  if (n_routes <= 0 || width <= 0) return hipSuccess;
+  const int64_t blocks = n_routes < 64 ? n_routes : 64;
+  hipLaunchKernelGGL(zero_unrouted_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, out, out_dtype, out_ld,
+                     width, out_rows, o_idx, o_div, rows_end, n_routes);
+  return hipGetLastError();
+}
+
 // 8 consecutive columns of any storage type as floats (vector when aligned).
 __device__ __forceinline__ void load8_any(const void* p, int32_t dt, int64_t off, bool vec, int64_t nvalid,
                                           float (&v)[8]) {

@@ -372,9 +372,20 @@ static const int32_t* launch_colscan(int32_t* counts, int64_t n_chunks, int32_t 
   return tot;
 }
 
+// Dynamic LDS above 64 KB (up to 128 KB: the scatter's positions at 32767
+// experts) is requested explicitly for the kernel that takes it.
+template <typename K>
+static hipError_t allow_lds(K kernel, size_t bytes) {
+  if (bytes <= 65536) return hipSuccess;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)bytes);
+}
+
 template <typename IdxT>
 void launch_scatter_cast(const ScatterArgs<IdxT>& a, const CastRequest& cr, size_t lds, hipStream_t stream) {
   const int64_t grid = a.n_chunks + cast_blocks(cr.n_experts, cr.d_in, cr.d_out);
+  allow_lds(sort_scatter_cast_kernel<IdxT, bf16_t>, lds);
+  allow_lds(sort_scatter_cast_kernel<IdxT, f16_t>, lds);
   if (cr.out_dtype == kBF16) {
     const CastArgs<bf16_t> c{(const float*)cr.keys, cr.se, cr.si, cr.d_in, cr.d_out, (bf16_t*)cr.kt, (bf16_t*)cr.kn};
     hipLaunchKernelGGL((sort_scatter_cast_kernel<IdxT, bf16_t>), dim3((unsigned)grid), dim3(kSortThreads), lds, stream,
@@ -395,6 +406,13 @@ hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_rout
   int32_t* counts = (int32_t*)ws;
   const size_t lds = (size_t)(n_experts + 1) * sizeof(int32_t);
   const size_t lds_scatter = scatter_lds_bytes(n_experts);
+  {
+    hipError_t e = sel_is_int64 ? allow_lds(sort_hist_kernel<int64_t>, lds) : allow_lds(sort_hist_kernel<int32_t>, lds);
+    if (e == hipSuccess)
+      e = sel_is_int64 ? allow_lds(sort_scatter_kernel<int64_t>, lds_scatter)
+                       : allow_lds(sort_scatter_kernel<int32_t>, lds_scatter);
+    if (e != hipSuccess) return e;
+  }
   int n_bits = 0;
   while ((1ll << n_bits) <= (int64_t)n_experts) ++n_bits;  // buckets 0..E
   if (sel_is_int64) {

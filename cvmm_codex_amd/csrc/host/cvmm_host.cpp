@@ -102,18 +102,6 @@ bool fast_path(at::ScalarType op, int64_t d_in, int64_t d_out) {
   return (op == at::kBFloat16 || op == at::kHalf) && d_in % 8 == 0 && d_out % 8 == 0;
 }
 
-// Operands that the reduce GEMM reads by 16-byte copies: rows of `a` (row
-// stride `ld`) and the weight view `kv` in the op dtype with unit stride
-// along the product's K dimension `k_dim` (1 = d_in, 2 = d_out).
-bool rows16(const Tensor& t, int64_t ld) {
-  return (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15) == 0 && (ld * (int64_t)t.element_size()) % 16 == 0;
-}
-bool reduce_operands_ok(const Tensor& a, const Tensor& kv, int k_dim, at::ScalarType op) {
-  const int n_dim = 3 - k_dim;
-  return kv.scalar_type() == op && kv.stride(k_dim) == 1 && rows16(kv, kv.stride(0)) && rows16(kv, kv.stride(n_dim)) &&
-         rows16(a, a.stride(0));
-}
-
 at::TensorOptions opts(const Tensor& like, at::ScalarType dt) {
   return at::TensorOptions().dtype(dt).device(like.device());
 }
@@ -267,7 +255,7 @@ std::tuple<OptT, OptT> cast_keys(const Tensor& keys, int64_t op_id, bool want_t,
 // ---------------------------------------------------------------------------
 Tensor forward(const Tensor& x, const Tensor& keys, const OptT& keys_t, const Tensor& sel, const Tensor& sel_index,
                const OptT& out_index, const Tensor& offsets, const OptT& route_pos, const OptT& rw, int64_t op_id,
-               int64_t flags, int64_t stream) {
+               int64_t out_id, int64_t flags, int64_t stream) {
   require_device(x, "x");
   require_device(keys, "keys");
   require_device(sel, "sel");
@@ -301,17 +289,18 @@ Tensor forward(const Tensor& x, const Tensor& keys, const OptT& keys_t, const Te
     out_rows = R / k;
   }
   const int32_t od = (int32_t)op_id;
-  Tensor out = at::empty({out_rows, d_out}, opts(x, op));
-  // route_pos is passed only with the stable sort's own perm
-  if (route_pos.has_value() && reduce_operands_ok(xf, kv, 1, op)) flags |= CVMM_FLAG_ROUTES_STABLE;
-  const size_t ws_bytes = cvmm_fwd_workspace_bytes(R, (int32_t)E, d_in, d_out, out_rows, od, od, 1,
+  // the output dtype: the op dtype (-1), or another one the products are
+  // rounded to directly (the reference op's out_dtype, cvmm.py:832-833)
+  const int32_t outd = out_id < 0 ? od : (int32_t)out_id;
+  Tensor out = at::empty({out_rows, d_out}, opts(x, dtype_of(outd)));
+  const size_t ws_bytes = cvmm_fwd_workspace_bytes(R, (int32_t)E, d_in, d_out, out_rows, outd, od, 1,
                                                    rw.has_value() ? 1 : 0, (int32_t)flags);
   OptT ws;
   if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(x, at::kByte));
   check(cvmm_fwd(ptr(xf), dtype_id(xf.scalar_type()), xf.size(0), xf.stride(0), ptr(kv), dtype_id(kv.scalar_type()),
                  (int32_t)E, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2), tptr<int32_t>(s32),
                  tptr<int64_t>(si), tptr<int64_t>(oi), R, tptr<int64_t>(offsets), tptr<int32_t>(route_pos),
-                 ptr(rwf), rwf.has_value() ? dtype_id(rwf->scalar_type()) : 0, k, od, ptr(out), od, out_rows, d_out,
+                 ptr(rwf), rwf.has_value() ? dtype_id(rwf->scalar_type()) : 0, k, od, ptr(out), outd, out_rows, d_out,
                  (int32_t)flags, ptr(ws), ws_bytes, (void*)stream),
         "cvmm_fwd");
   return out;
@@ -436,8 +425,6 @@ std::tuple<OptT, OptT, OptT> backward(const Tensor& grad_output, const Tensor& x
     if (need_grad_x) gx = at::empty(xr.sizes(), opts(x, x.scalar_type()));
     if (need_grad_rw) grad_rw = at::empty(rw->sizes(), opts(*rw, rw->scalar_type()));
     const int64_t gx_rows = gx.has_value() ? gx->size(0) : xr.size(0);
-    // route_pos is passed only with the stable sort's own perm
-    if (route_pos.has_value() && reduce_operands_ok(g, kv, 2, op)) flags |= CVMM_FLAG_ROUTES_STABLE;
     const size_t ws_bytes = cvmm_bwd_x_workspace_bytes(R, (int32_t)E, d_in, d_out, gx_rows, 1, rw.has_value() ? 1 : 0,
                                                        oi.has_value() ? 1 : 0, k, dtype_id(x.scalar_type()), od,
                                                        need_grad_rw ? 1 : 0, (int32_t)flags);

@@ -47,9 +47,6 @@ extern "C" {
                                      instead of a route-ordered buffer + ordered row sum */
 #define CVMM_FLAG_COUNTERS_ZEROED 2 /* cvmm_bwd_w: the counter region at the start of the
                                        workspace is already zero (see cvmm_bwd_w) */
-#define CVMM_FLAG_ROUTES_STABLE 4 /* cvmm_fwd / cvmm_bwd_x: within each expert the routes rp
-                                     increase (the order cvmm_sort_routes gives); allows the
-                                     reduce GEMM for top-k sums (see cvmm_fwd) */
 
 /* kernel classes for the timing hooks */
 #define CVMM_KC_SORT 1        /* histogram + scan + scatter of cvmm_sort_routes */
@@ -60,7 +57,6 @@ extern "C" {
 #define CVMM_KC_WGRAD 32      /* weight-gradient kernel of cvmm_bwd_w */
 #define CVMM_KC_COMBINE 64    /* top-k row combine / fp32 cast / gate-grad sum */
 #define CVMM_KC_FILL 128      /* zero fills */
-#define CVMM_KC_REDUCE 256    /* reduce GEMM of a top-k sum (its route gather: COMBINE) */
 #define CVMM_KC_ROUTE 512     /* router (softmax, top-k, histogram) + its scatter; router backward */
 
 /* Thread-local description of the last error. */
@@ -92,15 +88,10 @@ int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launche
  *   CVMM_TUNE_GEMM_ORDER: m-tile order of the routed GEMMs (forward, grad
  *     input), 1 = expert-major, 2 = token-major (tile j of every expert next
  *     to each other; up to 256 experts).  Built in: token-major for the
- *     long-K kernel when every gathered row feeds >= 32 routes.
- *   CVMM_TUNE_REDUCE_MIN_TOPK: smallest top-k for which a CVMM_FLAG_ROUTES_STABLE
- *     call takes the reduce GEMM (built in: never; it needs far less workspace
- *     at high fan-out -- ~70 MB instead of 2.1 GB for a 524288-route top-64
- *     sum of 2048-wide rows -- but is slower than the route buffer there). */
+ *     long-K kernel when every gathered row feeds >= 32 routes. */
 #define CVMM_TUNE_PANEL_TILES_PER_WG 1
 #define CVMM_TUNE_WGRAD_ORDER 2
 #define CVMM_TUNE_GEMM_ORDER 3
-#define CVMM_TUNE_REDUCE_MIN_TOPK 4
 #define CVMM_TUNE_WGRAD_TILE 5
 int cvmm_tuning_set(int32_t knob, int64_t value);
 
@@ -196,19 +187,12 @@ int cvmm_cast_keys(const void* keys, int32_t keys_dtype, int32_t n_experts, int6
  * route_pos (optional): the inverse of rp = out_index or sel_index, as
  * cvmm_sort_routes writes it; computed in the workspace when NULL.
  * Top-k sums (weighted here, token-input in cvmm_bwd_x) are taken in one of
- * three ways, each deterministic but the first: fp32 atomics
- * (CVMM_FLAG_ATOMIC_REDUCE), the reduce GEMM (CVMM_FLAG_ROUTES_STABLE, top-k
- * at or above the CVMM_TUNE_REDUCE_MIN_TOPK threshold when that knob is set,
- * 16-bit op, K = d_in of 64 or 128, N = d_out a multiple of 64, stage lists
- * within 1024 entries per token group, op-dtype keys with unit stride along K
- * and 16-byte aligned rows of the input, keys, output and workspace: no
- * [R, N] buffer, sums in expert order), else the
- * route-ordered buffer and a per-token sum in route order.  A flagged call
- * whose operands do not fit the reduce GEMM is the call without the flag,
- * with that call's workspace.
+ * two ways: fp32 atomics (CVMM_FLAG_ATOMIC_REDUCE, not deterministic in the
+ * last bits), else a route-ordered buffer and a per-token sum in route order
+ * (deterministic).
  * Routes whose expert id is outside [0, E) (no counterpart: the reference
  * indexes keys with them) are left out: the top-k sums skip them, and their
- * own rows of out (unweighted) or grad_x (route input) are not written. */
+ * own rows of out (unweighted) or grad_x (per-route gradient) are zero. */
 size_t cvmm_fwd_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out, int64_t out_rows,
                                 int32_t out_dtype, int32_t op_dtype, int32_t has_offsets, int32_t weighted,
                                 int32_t flags);

@@ -74,3 +74,30 @@ def test_storage_conversion_rules():
     assert C._keys_view(k2) is k2
     k3 = torch.zeros(5, 4, 3).permute(2, 1, 0)[:, ::2, ::2]
     assert C._keys_view(k3).is_contiguous()
+
+
+def test_cvmmsel_is_a_dataclass_like_the_reference():
+    """cvmm.py:12-21 declares CVMMSel a @dataclass: fields(), replace() and
+    asdict() work on it with the same field names and defaults."""
+    import dataclasses
+    s = _plain_sel()
+    assert dataclasses.is_dataclass(s)
+    assert [f.name for f in dataclasses.fields(C.CVMMSel)] == [
+        "raw_sel", "sel", "sel_index", "out_index", "reduction_weight"]
+    w = torch.rand(2, 2)
+    r = dataclasses.replace(s, reduction_weight=w)
+    assert isinstance(r, C.CVMMSel) and r.reduction_weight is w
+    assert r.raw_sel is s.raw_sel and r.sel is s.sel and r.out_index is s.out_index
+    d = dataclasses.asdict(s)
+    assert list(d) == ["raw_sel", "sel", "sel_index", "out_index", "reduction_weight"]
+    assert torch.equal(d["sel_index"], s.sel_index)
+    s.out_index = None                                  # plain field assignment
+    assert s.out_index is None
+
+
+def test_shape_log_is_on_by_default():
+    """The reference prints every new (x.shape, keys.shape) (cvmm.py:1778-1781)."""
+    import os
+    if "CVMM_LOG_SHAPES" in os.environ:
+        pytest.skip("CVMM_LOG_SHAPES set in the environment")
+    assert C.cvmm_log_shapes is True

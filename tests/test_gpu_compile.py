@@ -1,7 +1,9 @@
 """torch.compile through the API (the reference registers its forward as a
 torch.library op with a fake implementation for this, cvmm.py:808-812,
-:1436-1456): compiled and eager steps run the same kernels and must agree bit
-for bit; the ops pass torch.library.opcheck."""
+:1436-1456): compiled steps (aot_eager and inductor) match the CPU oracle at
+the north-star tolerance (2e-2 under bf16 autocast, 1e-4 in fp32), compiled
+and eager steps run the same kernels and agree bit for bit under aot_eager,
+and the ops pass torch.library.opcheck."""
 from __future__ import annotations
 
 import pytest
@@ -9,6 +11,7 @@ import torch
 
 import cvmm_codex_amd as C
 from cvmm_codex_amd import compile_ops as ops
+from tests import gpu_util as U
 
 pytestmark = pytest.mark.gpu
 
@@ -39,18 +42,75 @@ def _run(fn, x, keys, sel, w, go, route_input):
     return y.detach(), xs.grad, ks.grad, None if ws is None else ws.grad
 
 
+def _oracle(case, route_input, amp=True):
+    x, keys, sel, w, go = (None if t is None else t.cpu() for t in case)
+    return U.run_oracle(x, keys, sel, w, go, route_input, amp)
+
+
 @pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True), (True, False)])
-def test_compiled_step_matches_eager(weighted, route_input):
+def test_compiled_step_matches_eager_and_oracle(weighted, route_input):
     """One graph (fullgraph=True): selector, forward and backward all traced."""
     torch._dynamo.reset()
     case = _case(3, weighted, route_input)
     eager = _run(_step, *case, route_input)
     compiled = _run(torch.compile(_step, backend="aot_eager", fullgraph=True), *case, route_input)
-    for name, a, b in zip(("out", "x_grad", "keys_grad", "weights_grad"), eager, compiled):
+    names = ("out", "x_grad", "keys_grad", "weights_grad")
+    for name, a, b in zip(names, eager, compiled):
         if a is None:
             assert b is None, name
         else:
             assert torch.equal(a, b), name
+    U.compare(dict(zip(names, compiled)), _oracle(case, route_input), 2e-2)
+
+
+@pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True)])
+def test_inductor_step_matches_oracle(weighted, route_input):
+    """The same step compiled by inductor (the default backend): the custom
+    ops and their fakes hold up under its graph passes."""
+    torch._dynamo.reset()
+    case = _case(6, weighted, route_input)
+    compiled = _run(torch.compile(_step, fullgraph=True), *case, route_input)
+    names = ("out", "x_grad", "keys_grad", "weights_grad")
+    U.compare(dict(zip(names, compiled)), _oracle(case, route_input), 2e-2)
+
+
+def _step_fp32(x, keys, sel, w, route_input):
+    s = C.cvmm_prepare_sel2(sel, w, route_input=route_input)
+    return C.cvmm(x, s, keys)
+
+
+@pytest.mark.parametrize("backend", ["aot_eager", "inductor"])
+def test_compiled_fp32_step_matches_oracle(backend):
+    """fp32 mode (no autocast): 1e-4 against the oracle."""
+    torch._dynamo.reset()
+    x, keys, sel, w, go = _case(7, True, False)
+    x = x.float()
+    compiled = _run(torch.compile(_step_fp32, backend=backend, fullgraph=True), x, keys, sel, w, go, False)
+    names = ("out", "x_grad", "keys_grad", "weights_grad")
+    U.compare(dict(zip(names, compiled)), _oracle((x, keys, sel, w, go), False, amp=False), 1e-4)
+
+
+def test_compiled_step_with_transposed_x_matches_oracle():
+    """x as a permuted (dense, non-contiguous) view: the fake's grad_x layout
+    must be the real op's (a contiguous tensor of x's shape)."""
+    torch._dynamo.reset()
+    x, keys, sel, w, go = _case(8, False, False)
+    xt = x.transpose(0, 1).contiguous().transpose(0, 1)          # [B, T, D] with T-major storage
+    assert not xt.is_contiguous()
+
+    def run(fn):
+        xs = xt.clone(memory_format=torch.preserve_format).requires_grad_(True)
+        ks = keys.clone().requires_grad_(True)
+        y = fn(xs, ks, sel, None, False)
+        y.backward(go.to(y.dtype))
+        torch.cuda.synchronize()
+        return {"out": y.detach(), "x_grad": xs.grad, "keys_grad": ks.grad, "weights_grad": None}
+
+    exp = _oracle((x, keys, sel, None, go), False)
+    for backend in ("aot_eager", "inductor"):
+        torch._dynamo.reset()
+        got = run(torch.compile(_step, backend=backend, fullgraph=True))
+        U.compare(got, exp, 2e-2)
 
 
 def test_ops_pass_opcheck():
@@ -76,7 +136,8 @@ def test_ops_pass_opcheck():
 
 
 def test_reference_op_schema_matches_the_api_forward():
-    """cvmm_triton (the reference op's schema) gives the per-route forward of cvmm()."""
+    """cvmm_triton (the reference op's schema) gives the per-route forward of
+    cvmm(), and the oracle's."""
     x, keys, sel, _, _ = _case(5, False, False)
     s = C.cvmm_prepare_sel2(sel)
     with torch.autocast("cuda", dtype=torch.bfloat16):
@@ -85,6 +146,28 @@ def test_reference_op_schema_matches_the_api_forward():
                            torch.bfloat16, s.out_index, torch.bfloat16)
     assert z.shape == y.shape
     assert torch.equal(z, y)
+    exp = _oracle((x, keys, sel, None, torch.zeros(*sel.shape, keys.shape[2])), False)
+    assert U.norm_rel(U.to_np(z), exp["out"]) <= 2e-2
+
+
+def test_reference_op_rounds_once_to_out_dtype():
+    """out_dtype float32 with a bf16 op: products of bf16 operands, stored in
+    float32 directly (cvmm.py:832-833, :862-863), i.e. not rounded to bf16 on
+    the way; route-input form (out_index = the -1 sentinel)."""
+    from oracle import cvmm_oracle as O
+    x, keys, sel, _, _ = _case(9, False, True)
+    s = C.cvmm_prepare_sel2(sel, route_input=True)
+    minus1 = torch.full((1,), -1, dtype=torch.int64, device="cuda")
+    z = C.cvmm_triton_call(x.reshape(-1, x.shape[-1]), s.sel_index, s.sel, keys, torch.float32, minus1,
+                           torch.bfloat16)
+    assert z.dtype == torch.float32
+    meta = O.prepare_sel2(sel.cpu().numpy(), route_input=True)
+    xn, kn = U.to_np(x), U.to_np(keys)
+    once = O.forward(xn, meta, kn, "bfloat16", "float32")
+    twice = O.forward(xn, meta, kn, "bfloat16", "bfloat16")
+    zn = U.to_np(z)
+    assert U.norm_rel(zn, once) <= 1e-5
+    assert U.norm_rel(zn, twice) > 1e-4          # would be ~bf16 epsilon off with the extra rounding
 
 
 def _router_ffn(x, gate, w_up, w_down, k=4):

@@ -11,6 +11,15 @@ and a few experts (all their routes, posed as a one-route-per-row problem with
 the same rounding points), the hottest expert of the skewed C5 routing among
 them.  Tolerance: max|a - b| / max|b| <= 2e-2 (bf16 autocast), as for the
 other configs.
+
+Every token and every expert is covered as well: the torch restatement of
+the path (oracle/torch_cpu_path.py, pinned to the golden fixtures) runs in
+float32 on the GPU over the whole problem (no rounding points: at 2e-2 the
+bf16 roundings are far inside the bound), and every output row, every input
+gradient and every expert's weight gradient (each expert on its own scale)
+must agree with it.  This is what would catch a scheduling mistake in a tile
+or an expert that the samples miss (the token-major tile order and the
+coarse weight-gradient tiles only run at these sizes).
 """
 from __future__ import annotations
 
@@ -22,6 +31,7 @@ import torch.nn.functional as F
 import cvmm_codex_amd as C
 import workloads as W
 from oracle import cvmm_oracle as O
+from oracle import torch_cpu_path as P
 from tests.gpu_util import norm_rel
 
 pytestmark = pytest.mark.gpu
@@ -83,6 +93,43 @@ def _run_projection(p: W.Projection):
     y.backward(p.grad_out.to(dev).to(y.dtype))
     torch.cuda.synchronize()
     return y, x.grad, keys.grad, None if w is None else w.grad
+
+
+def _f32(t):
+    return None if t is None else t.detach().to(device="cuda", dtype=torch.float32).contiguous()
+
+
+def _full_check(tag, x, sel, keys, w, gy, route_input, got):
+    """All of (out, x_grad, keys_grad, weights_grad) against the torch path in
+    float32 on the GPU; keys_grad expert by expert."""
+    with torch.no_grad():
+        out, (dx, dw, dg) = P.step(_f32(x), sel.cuda(), _f32(keys), _f32(w), _f32(gy), route_input)
+    y, gx, gk, gw = got
+    errs = {"out": _check(f"{tag}.out", _np(y), _np(out)),
+            "x_grad": _check(f"{tag}.x_grad", _np(gx), _np(dx))}
+    if dg is not None:
+        errs["weights_grad"] = _check(f"{tag}.weights_grad", _np(gw), _np(dg))
+    counts = torch.bincount(sel.reshape(-1).cuda(), minlength=keys.shape[0])
+    worst = 0.0
+    for e in range(keys.shape[0]):
+        if counts[e] == 0:
+            assert torch.count_nonzero(gk[e]) == 0, f"{tag}.keys_grad[{e}] of an empty expert"
+            continue
+        a, b = gk[e].float(), dw[e]
+        err = float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+        assert err <= TOL, f"{tag}.keys_grad[{e}] ({int(counts[e])} routes): {err:.3e}"
+        worst = max(worst, err)
+    errs["keys_grad_worst_expert"] = worst
+    del out, dx, dw, dg
+    torch.cuda.empty_cache()
+    return errs
+
+
+@pytest.mark.parametrize("name", ["switch_v_2048", "switch_o_2048_weighted"])
+def test_c4_full_size_every_token_and_expert(name):
+    p = W.PROJECTIONS[name]()
+    got = _run_projection(p)
+    _full_check(name, p.x, p.sel, p.keys, p.weights, p.grad_out, p.route_input, got)
 
 
 @pytest.mark.parametrize("name", ["switch_v_2048", "switch_o_2048_weighted"])
@@ -168,3 +215,8 @@ def test_c5_ffn_stack_full_size_sampled():
         _check(f"w_up.grad[{e}]", gup[e], _expert_oracle(e, xn[t_idx], g_h[t_idx, j_idx], None, wu))
         _check(f"w_down.grad[{e}]", gdn[e],
                _expert_oracle(e, hn[t_idx, j_idx], gy[t_idx], wn[t_idx, j_idx], wd))
+
+    # every token and every expert of both projections
+    _full_check("up", x, sel.cpu(), w_up, None, h_pre.grad, False, (h_pre, x.grad, w_up.grad, None))
+    _full_check("down", hidden.view(B, Tn, k, H), sel.cpu(), w_down, weights, s.grad_out, True,
+                (y, hidden.grad, w_down.grad, weights.grad))

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.cvmm_abi_version() == 8
+    assert lib.cvmm_abi_version() == 9
 
 
 def test_workspace_queries(lib):
@@ -50,28 +50,9 @@ def test_workspace_queries(lib):
     assert lib.cvmm_fwd_workspace_bytes(65536, 64, 128, 1024, 8192, N.BF16, N.BF16, 1, 1, 0) >= 65536 * 1024 * 2
     assert (lib.cvmm_fwd_workspace_bytes(65536, 64, 128, 1024, 8192, N.BF16, N.BF16, 1, 1, N.FLAG_ATOMIC_REDUCE)
             >= 8192 * 1024 * 4)
-    # reduce GEMM (stable routes, top-64): gathered [R, d_in] rows + route info + group bounds, no [R, d_out] buffer
+    # token-input grad (top-64 sum): the route-ordered [R, d_in] buffer
     R, T, E = 524288, 8192, 256
-    buf = lib.cvmm_fwd_workspace_bytes(R, E, 64, 2048, T, N.BF16, N.BF16, 1, 1, 0)
-    # (off by default; the knob's threshold switches it on)
-    assert lib.cvmm_fwd_workspace_bytes(R, E, 64, 2048, T, N.BF16, N.BF16, 1, 1, N.FLAG_ROUTES_STABLE) == buf
-    assert lib.cvmm_tuning_set(N.TUNE_REDUCE_MIN_TOPK, 32) == 0
-    red = lib.cvmm_fwd_workspace_bytes(R, E, 64, 2048, T, N.BF16, N.BF16, 1, 1, N.FLAG_ROUTES_STABLE)
-    assert buf >= R * 2048 * 2
-    G = T // 256
-    assert R * 64 * 2 + R * 8 <= red <= R * 64 * 2 + (R + 128) * 8 + (G + 1) * E * 4 + G * (1024 * 8 + 4) + 5 * 256
-    # below the top-k threshold, with an fp32 op or an unsupported width the flag changes nothing
-    assert lib.cvmm_fwd_workspace_bytes(65536, 64, 128, 1024, 8192, N.BF16, N.BF16, 1, 1, N.FLAG_ROUTES_STABLE) == \
-        lib.cvmm_fwd_workspace_bytes(65536, 64, 128, 1024, 8192, N.BF16, N.BF16, 1, 1, 0)
-    assert lib.cvmm_fwd_workspace_bytes(R, E, 64, 2048, T, N.F32, N.F32, 1, 1, N.FLAG_ROUTES_STABLE) == \
-        lib.cvmm_fwd_workspace_bytes(R, E, 64, 2048, T, N.F32, N.F32, 1, 1, 0)
-    assert lib.cvmm_fwd_workspace_bytes(R, E, 96, 2048, T, N.BF16, N.BF16, 1, 1, N.FLAG_ROUTES_STABLE) == \
-        lib.cvmm_fwd_workspace_bytes(R, E, 96, 2048, T, N.BF16, N.BF16, 1, 1, 0)
-    # token-input grad (top-64 sum): the same saving
-    gbuf = lib.cvmm_bwd_x_workspace_bytes(R, E, 2048, 64, T, 1, 0, 1, 64, N.BF16, N.BF16, 0, 0)
-    gred = lib.cvmm_bwd_x_workspace_bytes(R, E, 2048, 64, T, 1, 0, 1, 64, N.BF16, N.BF16, 0, N.FLAG_ROUTES_STABLE)
-    assert gbuf >= R * 2048 * 2 and gred < R * 64 * 2 + R * 8 + G * (1024 * 8 + 4) + 65536
-    assert lib.cvmm_tuning_set(N.TUNE_REDUCE_MIN_TOPK, 0) == 0
+    assert lib.cvmm_bwd_x_workspace_bytes(R, E, 2048, 64, T, 1, 0, 1, 64, N.BF16, N.BF16, 0, 0) >= R * 2048 * 2
     # weight grad: counters + bounded partial slots
     assert lib.cvmm_bwd_w_workspace_bytes(65536, 64, 1024, 128, N.BF16, 1) > 64 * 8 * 4
 
@@ -117,8 +98,7 @@ def test_tuning_knob_rejects_bad_values(lib):
     assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 0) == 0
     assert lib.cvmm_tuning_set(N.TUNE_GEMM_ORDER, 3) != 0
     assert lib.cvmm_tuning_set(N.TUNE_GEMM_ORDER, 0) == 0
-    assert lib.cvmm_tuning_set(N.TUNE_REDUCE_MIN_TOPK, -1) != 0
-    assert lib.cvmm_tuning_set(N.TUNE_REDUCE_MIN_TOPK, 0) == 0
+    assert lib.cvmm_tuning_set(4, 32) != 0               # the retired reduce-GEMM threshold knob
 
 
 def test_router_arguments_fail_before_launch(lib):

@@ -401,3 +401,37 @@ def test_oracle_gelu_matches_torch():
     hb = torch.randn(2048, generator=g).to(torch.bfloat16)
     np.testing.assert_array_equal(O.gelu(hb.float().numpy(), "bfloat16"),
                                   torch.nn.functional.gelu(hb.double()).to(torch.bfloat16).double().numpy())
+
+
+# ---------------------------------------------------------------------------
+# the torch CPU path timed as bench.py's cpu_baseline (oracle/torch_cpu_path.py)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("fx", [f for f in FIXTURES if f.mode == "float32"], ids=lambda f: f.name)
+def test_torch_cpu_path_matches_golden(fx):
+    """The baseline's torch restatement gives the golden values (the reference
+    test's einsum definition, float64) on every golden case."""
+    from oracle import torch_cpu_path as P
+    t = lambda a: None if a is None else torch.from_numpy(np.asarray(a, dtype=np.float64))
+    out, (dx, dw, dg) = P.step(t(fx.x), torch.from_numpy(fx.sel), t(fx.keys), t(fx.weights), t(fx.grad_out),
+                               fx.case["route_input"])
+    exp = oracle_run.expected(fx)
+    for name, got in (("out", out), ("x_grad", dx), ("keys_grad", dw), ("weights_grad", dg)):
+        if exp[name] is None:
+            assert got is None, name
+            continue
+        e = np.asarray(exp[name], dtype=np.float64)
+        assert got.shape == e.shape, name
+        assert np.abs(got.numpy() - e).max() <= 1e-9 * max(np.abs(e).max(), 1.0), name
+
+
+def test_torch_cpu_path_catches_a_dropped_weight():
+    """A planted mistake in the baseline's restatement (the reduction weight
+    left out of grad_x) fails the golden comparison."""
+    from oracle import torch_cpu_path as P
+    fx = next(f for f in FIXTURES if f.mode == "float32" and f.weights is not None and f.case["route_input"])
+    t = lambda a: torch.from_numpy(np.asarray(a, dtype=np.float64))
+    r = P.Routes(torch.from_numpy(fx.sel), fx.keys.shape[0], True)
+    dx, _, _ = P.backward(t(fx.x), r, t(fx.keys), torch.ones_like(t(fx.weights)), t(fx.grad_out))
+    e = np.asarray(fx.exp_x_grad, dtype=np.float64)
+    assert np.abs(dx.numpy() - e).max() > 1e-3 * np.abs(e).max()
