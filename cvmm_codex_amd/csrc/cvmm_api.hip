@@ -286,6 +286,69 @@ int cvmm_sort_routes(const void* sel, int32_t sel_is_int64, int64_t n_routes, in
                       "cvmm_sort_routes");
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// cvmm_sort_routes_noalloc: the sort with its histogram scratch in a
+// file-scope device array instead of a caller workspace.  The sort's
+// workspace is bounded by construction (chunks * (E + 1) counts <= ~96K plus
+// E + 1 totals: at most 512 KiB for the 32767 experts the ABI accepts), so
+// 1 MiB holds every call.  Each GPU holds its own copy until the process
+// ends; its address is looked up once per device (hipGetSymbolAddress) and
+// only that address is ever passed to kernels.  Nothing in it needs to start
+// at zero: every call writes the histogram before reading it.  Calls that
+// overlap on one GPU (different streams) share the array and race.
+// ---------------------------------------------------------------------------
+constexpr size_t kSortScratchBytes = size_t(1) << 20;
+static __device__ __align__(256) uint8_t scratch[kSortScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The current device's copy of `scratch` (looked up on its first use there).
+int sort_scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(CVMM_ERR_LAUNCH, "cvmm_sort_routes_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(CVMM_ERR_UNSUPPORTED, "cvmm_sort_routes_noalloc: device %d beyond the %d supported", dev,
+                kMaxScratchDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(CVMM_ERR_LAUNCH, "cvmm_sort_routes_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return CVMM_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int cvmm_sort_routes_noalloc(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts,
+                             int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                             int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* stream) {
+  if (n_experts <= 0 || n_experts > 32767 || n_routes < 0 || n_routes > 0x7fffffffll || top_k <= 0 ||
+      offsets == nullptr)  // cvmm_sort_routes names the bad argument (before any HIP call)
+    return cvmm_sort_routes(sel, sel_is_int64, n_routes, n_experts, top_k, sorted_sel, perm, token_index, offsets,
+                            route_pos, n_invalid, nullptr, 0, stream);
+  const size_t need = sort_workspace_bytes(n_routes, n_experts);
+  if (need > kSortScratchBytes)
+    return fail(CVMM_ERR_WORKSPACE, "cvmm_sort_routes_noalloc: %lld routes over %d experts need %zu bytes of scratch, "
+                "the static scratch holds %zu", (long long)n_routes, n_experts, need, kSortScratchBytes);
+  void* ws = nullptr;
+  int r = sort_scratch_of_current_device(&ws);
+  if (r) return r;
+  return cvmm_sort_routes(sel, sel_is_int64, n_routes, n_experts, top_k, sorted_sel, perm, token_index, offsets,
+                          route_pos, n_invalid, ws, kSortScratchBytes, stream);
+}
+
 int cvmm_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_experts, int64_t* offsets,
                         void* stream) {
   if (n_experts <= 0 || offsets == nullptr) return fail(CVMM_ERR_INVALID, "cvmm_expert_offsets: bad arguments");

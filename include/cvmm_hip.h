@@ -118,6 +118,20 @@ int cvmm_sort_routes(const void* sel, int32_t sel_is_int64, int64_t n_routes, in
                      int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* cvmm_sort_routes without a workspace argument (no counterpart in the
+ * reference: for callers that cannot allocate device memory -- code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and outputs as cvmm_sort_routes minus the workspace; calls no
+ * hipMalloc/hipFree.  The scratch is a static device array of 1 MiB per GPU
+ * (held until the process ends), enough for every size cvmm_sort_routes
+ * accepts (<= 32767 experts need at most 512 KiB); a larger need would be
+ * refused with CVMM_ERR_WORKSPACE.  Call it with the stream's device
+ * current.  Calls that overlap on one GPU (different streams) share the
+ * scratch and race: serialise them. */
+int cvmm_sort_routes_noalloc(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts,
+                             int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                             int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* stream);
+
 /* cvmm_sort_routes and cvmm_cast_keys in one call (no counterpart in the
  * reference, whose sort and in-kernel weight cast are separate steps): the
  * cast of the same step's weights runs in the launch that scatters the

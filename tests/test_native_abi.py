@@ -44,6 +44,11 @@ def test_abi_version(lib):
 
 def test_workspace_queries(lib):
     assert lib.cvmm_sort_workspace_bytes(65536, 64) > 0
+    # the no-alloc sort's 1 MiB static scratch holds the sort's workspace at
+    # every accepted size (<= 32767 experts, < 2^31 routes)
+    worst = max(lib.cvmm_sort_workspace_bytes(R, E) for E in (1, 63, 64, 255, 1000, 8191, 8192, 16383, 32746, 32767)
+                for R in (1, 1024, 65535, 65537, 1 << 20, (1 << 31) - 1))
+    assert worst <= 1 << 20
     # no workspace needed for an unweighted forward with offsets given
     assert lib.cvmm_fwd_workspace_bytes(65536, 64, 1024, 128, 65536, N.BF16, N.BF16, 1, 0, 0) == 0
     # weighted combine: route-ordered buffer or fp32 token accumulator
@@ -61,6 +66,11 @@ def test_invalid_arguments_fail_before_launch(lib):
     rc = lib.cvmm_sort_routes(None, 0, 10, 0, 1, None, None, None, None, None, None, None, 0, None)
     assert rc == 1 and b"n_experts" in lib.cvmm_last_error()
     rc = lib.cvmm_sort_routes(None, 0, 10, 100000, 1, None, None, None, None, None, None, None, 0, None)
+    assert rc == 2
+    # the no-alloc sort names a bad argument before any HIP call, like the sort
+    rc = lib.cvmm_sort_routes_noalloc(None, 0, 10, 0, 1, None, None, None, None, None, None, None)
+    assert rc == 1 and b"n_experts" in lib.cvmm_last_error()
+    rc = lib.cvmm_sort_routes_noalloc(None, 0, 10, 100000, 1, None, None, None, None, None, None, None)
     assert rc == 2
     args = [None, 7, 1, 16, None, 0, 4, 16, 8, 128, 8, 1, None, None, None, 1, None, None, None, 0, 1,
             0, None, 0, 1, 8, 0, None, 0, None]
