@@ -443,6 +443,207 @@ def ffn_line(steps: int = 10, warmup: int = 3, kernel_iters: int = 10):
     }
 
 
+# ---------------------------------------------------------------------------
+# summaries of profile.sh runs (rocprofv3 CSVs -> the markdown under profiles/)
+# ---------------------------------------------------------------------------
+N_XCC, CU_NUM, SIMD_NUM = 8, 256, 1024
+COPY_BYTES = 256 << 20                      # the copy calibration's bytes read and written per launch
+
+
+def _demangle(names):
+    """Demangled kernel names; the bf16 type's mangling (DF16b) is given to
+    c++filt as a vendor type named bf16, which it does understand."""
+    import subprocess
+    names = list(names)
+    fixed = [n.replace("DF16b", "u4bf16") if n.startswith("_Z") else n for n in names]
+    try:
+        out = subprocess.run(["c++filt"], input="\n".join(fixed), capture_output=True, text=True,
+                             timeout=30).stdout.splitlines()
+        return out if len(out) == len(names) else names
+    except Exception:  # pragma: no cover
+        return names
+
+
+def _template_args(name: str):
+    """Top-level template arguments of a demangled kernel name."""
+    i = name.find("<")
+    if i < 0:
+        return []
+    depth, cur, out = 0, "", []
+    for ch in name[i + 1:]:
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            if depth == 0:
+                out.append(cur.strip())
+                break
+            depth -= 1
+        elif ch == "," and depth == 0:
+            out.append(cur.strip())
+            cur = ""
+            continue
+        cur += ch
+    return out
+
+
+def kernel_role(name: str):
+    """The kernel class of a demangled cvmm kernel name: its Role template
+    argument tells the forward GEMM (0) from the grad-input GEMM (1)."""
+    base = name.split("<")[0].split("(")[0].split()[-1] if name else ""
+    args = _template_args(name)
+    role_pos = {"cvmm::routed_gemm_ring_kernel": 7, "cvmm::routed_gemm_panel_kernel": 4,
+                "cvmm::routed_gemm_nt_kernel": 3, "cvmm::routed_gemm_nloop_kernel": 3}
+    if "wgrad" in base:
+        return "wgrad"
+    if base in role_pos and len(args) > role_pos[base]:
+        return "gemm_bwd_x" if args[role_pos[base]] == "1" else "gemm_fwd"
+    if base == "cvmm::routed_gemm_kernel":
+        return "gemm"
+    return None
+
+
+def _short(name: str, width: int = 90) -> str:
+    n = name.replace("__hip_bfloat16", "bf16").replace("_Float16", "f16").replace("cvmm::", "")
+    n = n.split("(")[0] if n.startswith("void ") or "(" in n else n
+    n = n.replace("void ", "")
+    return n if len(n) <= width else n[:width - 3] + "..."
+
+
+def _read_csv(path):
+    import csv
+    with open(path) as f:
+        return list(csv.DictReader(f))
+
+
+def _counters(pass_dir):
+    """{demangled kernel name: {counter: [per-dispatch values]}} of one pass."""
+    import glob
+    out = {}
+    files = glob.glob(os.path.join(pass_dir, "**", "*counter_collection.csv"), recursive=True)
+    rows = [r for f in files for r in _read_csv(f)]
+    names = dict(zip(sorted({r["Kernel_Name"] for r in rows}), _demangle(sorted({r["Kernel_Name"] for r in rows}))))
+    for r in rows:
+        d = out.setdefault(names[r["Kernel_Name"]], {})
+        d.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    return out
+
+
+def _copy_factors(copy_dir):
+    """Bytes per counter byte of FETCH_SIZE and WRITE_SIZE: what a plain
+    device copy of COPY_BYTES moves / what the counter reads for it."""
+    f = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        vals = []
+        for name, cs in _counters(os.path.join(copy_dir, c)).items():
+            vals += [v for v in cs.get(c, []) if v * 1024 > COPY_BYTES / 8]     # the big copy launches
+        if vals:
+            f[c] = COPY_BYTES / (sum(vals) / len(vals) * 1024)
+    return f
+
+
+def summarize(dirpath: str, copy_dir=None) -> str:
+    import glob
+    W_name = os.path.basename(os.path.normpath(dirpath))
+    lines = [f"# {W_name} -- rocprofv3 evidence", ""]
+    lines += ["Commands (repo root, one MI355X):", "", "```",
+              f"export TMPDIR=/tmp",
+              f"bash profile.sh {W_name} gpurun_out/prof   # bench line, kernel trace, three counter passes",
+              "bash profile.sh copy gpurun_out/prof         # FETCH_SIZE / WRITE_SIZE calibration",
+              f"python bench.py --summarize gpurun_out/prof/{W_name} --copy-dir gpurun_out/prof/copy", "```", ""]
+    bench = None
+    bj = os.path.join(dirpath, "bench.json")
+    if os.path.exists(bj):
+        txt = [ln for ln in open(bj).read().splitlines() if ln.strip().startswith("{")]
+        bench = json.loads(txt[-1]) if txt else None
+    if bench:
+        rf, sr = bench["roofline"], bench["step_roofline"]
+        lines += ["## bench.py line (HIP events)", "",
+                  f"- step: {bench['ms_per_step'] * 1e3:.1f} us = {bench['value']:.1f} TFLOP/s; step roofline "
+                  f"({sr['bound']}): frac {sr['frac']:.4f} (MFMA {sr['mfma_frac']:.4f}, HBM route bytes "
+                  f"{sr['hbm_frac']:.4f})",
+                  f"- dominant kernel `{rf['kernel']}`: {rf['avg_launch_ms'] * 1e3:.1f} us per launch, "
+                  f"{rf['achieved']} {rf['unit']} = frac {rf['frac']:.4f} of {rf['peak']} ({rf['bound']}); "
+                  f"MFMA frac {rf['mfma_frac']:.4f}, HBM frac {rf['hbm_frac']:.4f}",
+                  f"- kernel us per launch: " + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in
+                                                          bench["kernel_ms_per_launch"].items()), ""]
+    stats = glob.glob(os.path.join(dirpath, "trace", "**", "*kernel_stats.csv"), recursive=True)
+    avg_us = {}
+    if stats:
+        rows = _read_csv(stats[0])
+        names = _demangle([r["Name"] for r in rows])
+        lines += ["## Kernel trace (`rocprofv3 --kernel-trace --stats`, bench run of 20 steps)", "",
+                  "| kernel | class | calls | avg us | % |", "|---|---|---:|---:|---:|"]
+        for r, n in zip(rows, names):
+            avg_us[n] = float(r["AverageNs"]) / 1e3
+            if float(r["Percentage"]) < 0.5:
+                continue
+            lines.append(f"| `{_short(n)}` | {kernel_role(n) or ''} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} "
+                         f"| {float(r['Percentage']):.1f} |")
+        lines.append("")
+    cnt = {}
+    for pas in ("fetch", "write", "sq"):
+        for k, d in _counters(os.path.join(dirpath, pas)).items():
+            cnt.setdefault(k, {}).update(d)
+    fac = _copy_factors(copy_dir) if copy_dir else {}
+    proj = None
+    if W_name in W.PROJECTIONS:
+        proj = W.PROJECTIONS[W_name]()
+    if cnt:
+        lines += ["## Counters per dispatch of the GEMM kernels (averages over the counter runs' dispatches)", "",
+                  "FETCH/WRITE: `FETCH_SIZE` / `WRITE_SIZE` (KiB) x 1024 x the copy factor "
+                  f"(fetch {fac.get('FETCH_SIZE', float('nan')):.3f}, write {fac.get('WRITE_SIZE', float('nan')):.3f}: "
+                  "bytes a 256 MiB device copy moves / what the counter reads for it).  MFMA busy = "
+                  "`SQ_VALU_MFMA_BUSY_CYCLES` / (`GRBM_GUI_ACTIVE` / 8 XCDs x 1024 SIMDs).  MFMA GFLOP = "
+                  "`SQ_INSTS_VALU_MFMA_MOPS_*` x 512.  LDS conflict = `SQ_LDS_BANK_CONFLICT` cycles per "
+                  "`SQ_INSTS_LDS` instruction and as % of CU time (`SQ_LDS_BANK_CONFLICT` / (`GRBM_GUI_ACTIVE`/8 x 256)).  "
+                  "L2 hit = `TCC_HIT_sum` / (`TCC_HIT_sum` + `TCC_MISS_sum`).", "",
+                  "| kernel | class | trace us | FETCH MB | WRITE MB | alg. MB | traffic / alg. | L2 hit % | "
+                  "MFMA busy % | MFMA GFLOP (alg.) | LDS confl. cyc/inst | LDS confl. % |",
+                  "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+        for k, d in cnt.items():
+            role = kernel_role(k)
+            if role is None:
+                continue
+            mean = lambda c: (sum(d[c]) / len(d[c])) if c in d and d[c] else float("nan")
+            fetch = mean("FETCH_SIZE") * 1024 * fac.get("FETCH_SIZE", float("nan")) / 1e6
+            write = mean("WRITE_SIZE") * 1024 * fac.get("WRITE_SIZE", float("nan")) / 1e6
+            alg = phase_work(proj, PHASE[role])[1] / 1e6 if proj is not None and role in PHASE else float("nan")
+            hit = mean("TCC_HIT_sum") / (mean("TCC_HIT_sum") + mean("TCC_MISS_sum")) * 100
+            grbm = mean("GRBM_GUI_ACTIVE") / N_XCC
+            busy = mean("SQ_VALU_MFMA_BUSY_CYCLES") / (grbm * SIMD_NUM) * 100
+            mops = (mean("SQ_INSTS_VALU_MFMA_MOPS_BF16") if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in d else 0) + \
+                   (mean("SQ_INSTS_VALU_MFMA_MOPS_F32") if "SQ_INSTS_VALU_MFMA_MOPS_F32" in d else 0)
+            gflop = mops * 512 / 1e9
+            alg_gf = phase_work(proj, PHASE[role])[0] / 1e9 if proj is not None and role in PHASE else float("nan")
+            conf = mean("SQ_LDS_BANK_CONFLICT")
+            per_inst = conf / mean("SQ_INSTS_LDS") if mean("SQ_INSTS_LDS") else float("nan")
+            conf_pct = conf / (grbm * CU_NUM) * 100
+            us = avg_us.get(k, float("nan"))
+            lines.append(f"| `{_short(k, 70)}` | {role} | {us:.1f} | {fetch:.1f} | {write:.1f} | {alg:.1f} | "
+                         f"{(fetch + write) / alg:.2f} | {hit:.1f} | {busy:.1f} | {gflop:.2f} ({alg_gf:.2f}) | "
+                         f"{per_inst:.3f} | {conf_pct:.2f} |")
+        lines.append("")
+    return "\n".join(lines)
+
+
+def traffic_json(dirpath: str, copy_dir: str, kernel_class: str):
+    """FETCH_SIZE + WRITE_SIZE bytes per launch of the class's kernel (the
+    `traffic` field of bench.py's roofline), from a profile.sh run."""
+    cnt = {}
+    for pas in ("fetch", "write"):
+        for k, d in _counters(os.path.join(dirpath, pas)).items():
+            cnt.setdefault(k, {}).update(d)
+    fac = _copy_factors(copy_dir)
+    for k, d in cnt.items():
+        if kernel_role(k) == kernel_class and "FETCH_SIZE" in d and "WRITE_SIZE" in d:
+            f = sum(d["FETCH_SIZE"]) / len(d["FETCH_SIZE"]) * 1024 * fac["FETCH_SIZE"]
+            w = sum(d["WRITE_SIZE"]) / len(d["WRITE_SIZE"]) * 1024 * fac["WRITE_SIZE"]
+            return {"kernel": kernel_class, "kernel_name": k, "workload": os.path.basename(os.path.normpath(dirpath)),
+                    "bytes_per_launch": int(f + w), "fetch_bytes": int(f), "write_bytes": int(w),
+                    "copy_factor_fetch": fac["FETCH_SIZE"], "copy_factor_write": fac["WRITE_SIZE"]}
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -458,11 +659,23 @@ def main():
                          "stack (one JSON line) and exit")
     ap.add_argument("--router", action="store_true",
                     help="time the fused router against the torch router lines (one JSON line) and exit")
+    ap.add_argument("--summarize", metavar="DIR", default=None,
+                    help="print the markdown summary of a profile.sh output directory (no GPU needed) and exit")
+    ap.add_argument("--copy-dir", metavar="DIR", default=None,
+                    help="with --summarize: the profile.sh copy-calibration directory")
+    ap.add_argument("--traffic", metavar="CLASS", default=None,
+                    help="with --summarize: print the traffic JSON of this kernel class (gemm_fwd, gemm_bwd_x, wgrad)")
     ap.add_argument("--tune", action="append", default=[], metavar="KNOB=VALUE",
                     help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, wgrad_tile, gemm_order) "
                          "before running")
     args = ap.parse_args()
 
+    if args.summarize:
+        if args.traffic:
+            print(json.dumps(traffic_json(args.summarize, args.copy_dir, args.traffic), indent=1))
+        else:
+            print(summarize(args.summarize, args.copy_dir))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the path would shard over experts, which is not built here)", file=sys.stderr)
