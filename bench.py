@@ -129,18 +129,23 @@ def kernel_launchers(runner: Runner):
     keys = runner.keys.detach()
     fast = C._fast_path(op, keys.shape[1], keys.shape[2])
     kt, kn = C._cast_keys(keys, op, True, True) if fast else (None, None)
+    k = runner.p.weights.shape[-1] if runner.w is not None else runner.p.sel.shape[-1]
+    fwd_t, bwd_t, _, _ = C._plan_copies(keys, op, runner.p.routes, k, runner.w is not None,
+                                        not runner.p.route_input, True)
 
     def cast():
         C._cast_keys(keys, op, True, True)
 
     def fwd():
-        C._forward(runner.x.detach(), s.sel_index, s.sel, keys, s.out_index, args[6], op, kt)
+        C._forward(runner.x.detach(), s.sel_index, s.sel, keys, s.out_index, args[6], op,
+                   (kt if fwd_t else kn) if fast else None, fwd_t)
 
     def bwd_w():
         C._backward(Ctx, go, *args, False, True, False)
 
     def bwd_x():
-        C._backward(Ctx, go, *args, True, False, runner.w is not None, keys_n=kn)
+        C._backward(Ctx, go, *args, True, False, runner.w is not None,
+                    keys_x=(kt if bwd_t else kn) if fast else None, keys_x_is_t=bwd_t)
 
     out = {"fwd": fwd, "bwd_w": bwd_w, "bwd_x": bwd_x}
     if fast:
@@ -666,8 +671,8 @@ def main():
     ap.add_argument("--traffic", metavar="CLASS", default=None,
                     help="with --summarize: print the traffic JSON of this kernel class (gemm_fwd, gemm_bwd_x, wgrad)")
     ap.add_argument("--tune", action="append", default=[], metavar="KNOB=VALUE",
-                    help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, wgrad_tile, gemm_order) "
-                         "before running")
+                    help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, wgrad_tile, gemm_order, "
+                         "dense_topk) before running")
     args = ap.parse_args()
 
     if args.summarize:
@@ -687,7 +692,7 @@ def main():
     from cvmm_codex_amd import _native as N
     knobs = {"panel_tiles_per_wg": N.TUNE_PANEL_TILES_PER_WG, "wgrad_order": N.TUNE_WGRAD_ORDER,
              "gemm_order": N.TUNE_GEMM_ORDER,
-             "wgrad_tile": N.TUNE_WGRAD_TILE}
+             "wgrad_tile": N.TUNE_WGRAD_TILE, "dense_topk": N.TUNE_DENSE_TOPK}
     for kv in args.tune:
         name, _, value = kv.partition("=")
         if name not in knobs:

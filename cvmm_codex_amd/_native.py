@@ -22,6 +22,7 @@ TUNE_PANEL_TILES_PER_WG = 1
 TUNE_WGRAD_ORDER = 2
 TUNE_GEMM_ORDER = 3
 TUNE_WGRAD_TILE = 5
+TUNE_DENSE_TOPK = 6
 
 # kernel classes of the timing hooks (include/cvmm_hip.h CVMM_KC_*)
 KC_SORT, KC_OFFSETS, KC_CAST_KEYS, KC_GEMM_FWD, KC_GEMM_BWDX, KC_WGRAD, KC_COMBINE, KC_FILL, KC_ROUTE = (
@@ -39,6 +40,7 @@ _SIGS = {
     "cvmm_abi_version": (ctypes.c_int, []),
     "cvmm_timing_enable": (ctypes.c_int, [ctypes.c_uint32]),
     "cvmm_tuning_set": (ctypes.c_int, [_I32, _I64]),
+    "cvmm_topk_dense": (ctypes.c_int, [_I64, _I32, _I64, _I64, _I64, _I32]),
     "cvmm_timing_result": (ctypes.c_int, [ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
                                           ctypes.POINTER(ctypes.c_int64)]),
     "cvmm_sort_workspace_bytes": (_SZ, [_I64, _I32]),

@@ -125,25 +125,52 @@ _cast_done = threading.local()
 
 def _sort_routes_cast(raw_flat: torch.Tensor, n_experts: int, top_k: int, cast):
     """_sort_routes plus the step's weight cast in the same launches
-    (`cast` = (keys, op dtype, want kn)); the copies are left for CVMM.forward."""
-    keys, op, need_n = cast
+    (`cast` = (keys, op dtype, want kt, want kn)); the copies are left for
+    CVMM.forward."""
+    keys, op, want_t, want_n = cast
     (ssel, perm, tok, offsets, route_pos), kt, kn = N.host().sort_routes_cast(
-        raw_flat, n_experts, top_k, keys, N.dtype_id(op), True, need_n, N.stream_of(raw_flat.device))
+        raw_flat, n_experts, top_k, keys, N.dtype_id(op), want_t, want_n, N.stream_of(raw_flat.device))
     perm._cvmm_route_pos = route_pos
     _cast_done.entry = (keys, keys._version, op, kt, kn)
     return ssel, perm, tok, offsets
 
 
-def _take_cast(keys: torch.Tensor, op: torch.dtype, need_n: bool):
+def _take_cast(keys: torch.Tensor, op: torch.dtype, want_t: bool, want_n: bool):
     """The weight copies cast with this call's sort, if they still match."""
     entry = getattr(_cast_done, "entry", None)
     _cast_done.entry = None
     if entry is None:
         return None
     k, version, eop, kt, kn = entry
-    if k is not keys or version != keys._version or eop != op or (need_n and kn is None):
+    if k is not keys or version != keys._version or eop != op or (want_t and kt is None) or (want_n and kn is None):
         return None
     return kt, kn
+
+
+@torch._dynamo.assume_constant_result
+def _topk_dense(n_tokens: int, n_experts: int, K: int, N_: int, top_k: int, op_id: int) -> bool:
+    """Whether the library takes this top-k sum as one dense GEMM
+    (cvmm_topk_dense: shapes and a cost model; a constant for tracing)."""
+    return bool(N.lib().cvmm_topk_dense(n_tokens, n_experts, K, N_, top_k, op_id))
+
+
+def _plan_copies(keys: torch.Tensor, op: torch.dtype, n_routes: int, top_k: int, weighted: bool,
+                 token_input: bool, need_grad_input: bool):
+    """The op-dtype weight copies a call reads: (forward reads kt, grad-input
+    reads kt, want kt, want kn).  The routed GEMMs read their K dimension with
+    unit stride: kt [E, d_out, d_in] for the forward, kn [E, d_in, d_out] for
+    the grad-input.  A top-k sum taken as a dense GEMM (cvmm_topk_dense) reads
+    the weights as [E*K, N] rows instead: kn for the weighted forward, kt for
+    the token gradient."""
+    E, d_in, d_out = keys.shape
+    op_id = N.dtype_id(op)
+    T = n_routes // top_k if top_k > 0 else 0
+    fwd_dense = weighted and top_k >= 2 and _topk_dense(T, E, d_in, d_out, top_k, op_id)
+    bwd_dense = not weighted and token_input and top_k >= 2 and _topk_dense(T, E, d_out, d_in, top_k, op_id)
+    fwd_t, bwd_t = not fwd_dense, bwd_dense
+    want_t = fwd_t or (need_grad_input and bwd_t)
+    want_n = (not fwd_t) or (need_grad_input and not bwd_t)
+    return fwd_t, bwd_t, want_t, want_n
 
 
 def cvmm_expert_offsets(sorted_experts: torch.Tensor, n_experts: int) -> torch.Tensor:
@@ -464,16 +491,18 @@ def _cast_keys(keys: torch.Tensor, op: torch.dtype, want_t: bool, want_n: bool):
     return N.host().cast_keys(keys, N.dtype_id(op), want_t, want_n, N.stream_of(keys.device))
 
 
-def _forward(x, sel_index, sel, keys, out_index, rw, op_dtype, keys_t=None):
-    """cvmm_triton (cvmm.py:814-867) + the weighted combine (:1543-1545)."""
+def _forward(x, sel_index, sel, keys, out_index, rw, op_dtype, keys_op=None, keys_op_is_t=True):
+    """cvmm_triton (cvmm.py:814-867) + the weighted combine (:1543-1545).
+    `keys_op`: an op-dtype weight copy (kt when `keys_op_is_t`, else kn)."""
     _require_device(sel, "sel")
     n_experts = keys.shape[0]
     R = sel.numel()
     if _compiling():
-        out = _ops.forward(x, keys, keys_t, sel, sel_index, out_index, _offsets_for(sel, n_experts), rw, op_dtype,
-                           _flags())
+        out = _ops.forward(x, keys, keys_op, keys_op_is_t, sel, sel_index, out_index, _offsets_for(sel, n_experts),
+                           rw, op_dtype, _flags())
     else:
-        out = N.host().forward(x, keys, keys_t, sel, sel_index, out_index, _offsets_for(sel, n_experts),
+        out = N.host().forward(x, keys, keys_op, keys_op_is_t, sel, sel_index, out_index,
+                               _offsets_for(sel, n_experts),
                                _route_pos(out_index if out_index is not None else sel_index, R), rw,
                                N.dtype_id(op_dtype), -1, _flags(), N.stream_of(x.device))
     if rw is None:
@@ -482,20 +511,33 @@ def _forward(x, sel_index, sel, keys, out_index, rw, op_dtype, keys_t=None):
 
 
 def _backward(ctx, grad_output, x, keys, raw_sel, sel, sel_index, out_index, rw,
-              need_grad_x, need_grad_keys, need_grad_rw, keys_n=None):
-    """CVMM.backward's products (cvmm.py:1552-1755)."""
+              need_grad_x, need_grad_keys, need_grad_rw, keys_x=None, keys_x_is_t=False):
+    """CVMM.backward's products (cvmm.py:1552-1755).  `keys_x`: the
+    grad-input's op-dtype weight copy (kt when `keys_x_is_t`, else kn)."""
     top_k = raw_sel.shape[-1] if raw_sel.ndim > 0 else 1
     R = sel.numel()
     if _compiling():
-        g = _ops.backward(grad_output, x, keys, keys_n, sel, sel_index, out_index, _offsets_for(sel, keys.shape[0]),
-                          rw, top_k, ctx.op_type, bool(need_grad_x), bool(need_grad_keys), bool(need_grad_rw),
-                          _flags())
+        g = _ops.backward(grad_output, x, keys, keys_x, keys_x_is_t, sel, sel_index, out_index,
+                          _offsets_for(sel, keys.shape[0]), rw, top_k, ctx.op_type, bool(need_grad_x),
+                          bool(need_grad_keys), bool(need_grad_rw), _flags())
         return _ops.grads_or_none(g, [bool(need_grad_x), bool(need_grad_keys), bool(need_grad_rw)])
-    return N.host().backward(grad_output, x, keys, keys_n, sel, sel_index, out_index,
+    return N.host().backward(grad_output, x, keys, keys_x, keys_x_is_t, sel, sel_index, out_index,
                              _offsets_for(sel, keys.shape[0]),
                              _route_pos(out_index if out_index is not None else sel_index, R), rw, top_k,
                              N.dtype_id(ctx.op_type), bool(need_grad_x), bool(need_grad_keys), bool(need_grad_rw),
                              _flags(), N.stream_of(x.device))
+
+
+def _copies_for_call(ctx, keys, op, n_routes, top_k, weighted, token_input, need_grad_input):
+    """The forward's weight copy for CVMM(.Gelu).forward, the grad-input's
+    kept on ctx: cast with the sort when cvmm() did that, else here."""
+    fwd_t, bwd_t, want_t, want_n = _plan_copies(keys, op, n_routes, top_k, weighted, token_input,
+                                                need_grad_input)
+    pre = None if _compiling() else _take_cast(keys, op, want_t, want_n)
+    kt, kn = pre if pre is not None else _cast_keys(keys, op, want_t, want_n)
+    ctx.keys_x = (kt if bwd_t else kn) if need_grad_input else None
+    ctx.keys_x_is_t = bwd_t
+    return (kt if fwd_t else kn), fwd_t
 
 
 class CVMM(torch.autograd.Function):
@@ -510,13 +552,15 @@ class CVMM(torch.autograd.Function):
                 reduction_weight: Optional[torch.Tensor] = None):
         ctx.save_for_backward(x, keys, raw_sel, sel, sel_index, out_index, reduction_weight)
         out_type = get_dtype()
-        keys_t = keys_n = None
+        keys_op, fwd_t = None, True
+        ctx.keys_x, ctx.keys_x_is_t = None, False
         if _fast_path(out_type, keys.shape[1], keys.shape[2]):
-            need_n = ctx.needs_input_grad[0] or ctx.needs_input_grad[6]
-            pre = None if _compiling() else _take_cast(keys, out_type, need_n)
-            keys_t, keys_n = pre if pre is not None else _cast_keys(keys, out_type, True, need_n)
-        res = _forward(x, sel_index, sel, keys, out_index, reduction_weight, out_type, keys_t)
-        ctx.keys_n = keys_n
+            weighted = reduction_weight is not None
+            k = reduction_weight.shape[-1] if weighted else (raw_sel.shape[-1] if raw_sel.ndim > 0 else 1)
+            need = ctx.needs_input_grad[0] or ctx.needs_input_grad[6]
+            keys_op, fwd_t = _copies_for_call(ctx, keys, out_type, sel.numel(), k, weighted, out_index is not None,
+                                              need)
+        res = _forward(x, sel_index, sel, keys, out_index, reduction_weight, out_type, keys_op, fwd_t)
         ctx.op_type = out_type
         ctx.keys_type = keys.dtype
         ctx.dtype = out_type
@@ -530,8 +574,8 @@ class CVMM(torch.autograd.Function):
         need_grad_rw = ctx.needs_input_grad[6] and reduction_weight is not None
         grad_x, grad_w, grad_rw = _backward(ctx, grad_output, x, keys, raw_sel, sel, sel_index, out_index,
                                             reduction_weight, need_grad_x, need_grad_keys, need_grad_rw,
-                                            keys_n=ctx.keys_n)
-        ctx.keys_n = None
+                                            keys_x=ctx.keys_x, keys_x_is_t=ctx.keys_x_is_t)
+        ctx.keys_x = None
         return grad_x, None, None, None, grad_w, None, grad_rw
 
 
@@ -544,18 +588,18 @@ class CVMMGelu(torch.autograd.Function):
     def forward(ctx, x: torch.Tensor, raw_sel: torch.Tensor, sel_index: torch.Tensor, sel: torch.Tensor,
                 keys: torch.Tensor, out_index: Optional[torch.Tensor] = None):
         out_type = get_dtype()
-        keys_t = keys_n = None
+        keys_t = None
+        ctx.keys_x, ctx.keys_x_is_t = None, False
         if _fast_path(out_type, keys.shape[1], keys.shape[2]):
-            need_n = ctx.needs_input_grad[0]
-            pre = _take_cast(keys, out_type, need_n)
-            keys_t, keys_n = pre if pre is not None else _cast_keys(keys, out_type, True, need_n)
+            k = raw_sel.shape[-1] if raw_sel.ndim > 0 else 1
+            keys_t, _ = _copies_for_call(ctx, keys, out_type, sel.numel(), k, False, out_index is not None,
+                                         ctx.needs_input_grad[0])
         n_experts = keys.shape[0]
         R = sel.numel()
         y, h = N.host().forward_gelu(x, keys, keys_t, sel, sel_index, out_index, _offsets_for(sel, n_experts),
                                      _route_pos(out_index if out_index is not None else sel_index, R),
                                      N.dtype_id(out_type), _flags(), N.stream_of(x.device))
         ctx.save_for_backward(x, keys, raw_sel, sel, sel_index, out_index, h)
-        ctx.keys_n = keys_n
         ctx.op_type = out_type
         return y.view(*sel.shape, keys.shape[2])
 
@@ -565,8 +609,8 @@ class CVMMGelu(torch.autograd.Function):
         gh = N.host().gelu_backward(grad_output, h, N.stream_of(h.device))
         grad_x, grad_w, _ = _backward(ctx, gh.view(grad_output.shape), x, keys, raw_sel, sel, sel_index,
                                       out_index, None, ctx.needs_input_grad[0], ctx.needs_input_grad[4], False,
-                                      keys_n=ctx.keys_n)
-        ctx.keys_n = None
+                                      keys_x=ctx.keys_x, keys_x_is_t=ctx.keys_x_is_t)
+        ctx.keys_x = None
         return grad_x, None, None, None, grad_w, None
 
 
@@ -586,7 +630,10 @@ def cvmm_gelu(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.Te
     cast = None
     op = get_dtype()
     if sel._pending() and keys.is_cuda and _fast_path(op, keys.shape[1], keys.shape[2]):
-        cast = (keys, op, torch.is_grad_enabled() and x.requires_grad)
+        raw = sel._raw_shape_tensor()
+        _, _, want_t, want_n = _plan_copies(keys, op, raw.numel(), raw.shape[-1] if raw.ndim else 1, False,
+                                            not sel._route_mode, torch.is_grad_enabled() and x.requires_grad)
+        cast = (keys, op, want_t, want_n)
     sel._resolve(keys.shape[0], cast)
     return CVMMGelu.apply(x, sel._raw_shape_tensor(), sel.sel_index, sel.sel, keys, sel.out_index)
 
@@ -614,7 +661,11 @@ def cvmm(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.Tensor)
     op = get_dtype()
     if sel._pending() and keys.is_cuda and _fast_path(op, keys.shape[1], keys.shape[2]) and not _compiling():
         rw = sel.reduction_weight
-        cast = (keys, op, torch.is_grad_enabled() and (x.requires_grad or (rw is not None and rw.requires_grad)))
+        raw = sel._raw_shape_tensor()
+        k = rw.shape[-1] if rw is not None else (raw.shape[-1] if raw.ndim else 1)
+        need = torch.is_grad_enabled() and (x.requires_grad or (rw is not None and rw.requires_grad))
+        _, _, want_t, want_n = _plan_copies(keys, op, raw.numel(), k, rw is not None, not sel._route_mode, need)
+        cast = (keys, op, want_t, want_n)
     sel._resolve(keys.shape[0], cast)
     if cvmm_log_shapes:
         sh = (x.shape, keys.shape)

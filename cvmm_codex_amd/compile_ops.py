@@ -79,15 +79,15 @@ def _(keys, op_dtype):
 # forward (cvmm.py:1524-1550): [out_rows, d_out] in the op dtype
 # ---------------------------------------------------------------------------
 @torch.library.custom_op(f"{NS}::forward", mutates_args=())
-def forward(x: torch.Tensor, keys: torch.Tensor, keys_t: Optional[torch.Tensor], sel: torch.Tensor,
-            sel_index: torch.Tensor, out_index: Optional[torch.Tensor], offsets: torch.Tensor,
+def forward(x: torch.Tensor, keys: torch.Tensor, keys_op: Optional[torch.Tensor], keys_op_is_t: bool,
+            sel: torch.Tensor, sel_index: torch.Tensor, out_index: Optional[torch.Tensor], offsets: torch.Tensor,
             reduction_weight: Optional[torch.Tensor], op_dtype: torch.dtype, flags: int) -> torch.Tensor:
-    return N.host().forward(x, keys, keys_t, sel, sel_index, out_index, offsets, None, reduction_weight,
-                            N.dtype_id(op_dtype), -1, flags, N.stream_of(x.device))
+    return N.host().forward(x, keys, keys_op, keys_op_is_t, sel, sel_index, out_index, offsets, None,
+                            reduction_weight, N.dtype_id(op_dtype), -1, flags, N.stream_of(x.device))
 
 
 @forward.register_fake
-def _(x, keys, keys_t, sel, sel_index, out_index, offsets, reduction_weight, op_dtype, flags):
+def _(x, keys, keys_op, keys_op_is_t, sel, sel_index, out_index, offsets, reduction_weight, op_dtype, flags):
     R = sel.numel()
     rows = R if reduction_weight is None else R // reduction_weight.shape[-1]
     return x.new_empty((rows, keys.shape[2]), dtype=op_dtype)
@@ -98,12 +98,14 @@ def _(x, keys, keys_t, sel, sel_index, out_index, offsets, reduction_weight, op_
 # an empty tensor for a gradient that is not wanted
 # ---------------------------------------------------------------------------
 @torch.library.custom_op(f"{NS}::backward", mutates_args=())
-def backward(grad_output: torch.Tensor, x: torch.Tensor, keys: torch.Tensor, keys_n: Optional[torch.Tensor],
-             sel: torch.Tensor, sel_index: torch.Tensor, out_index: Optional[torch.Tensor], offsets: torch.Tensor,
+def backward(grad_output: torch.Tensor, x: torch.Tensor, keys: torch.Tensor, keys_x: Optional[torch.Tensor],
+             keys_x_is_t: bool, sel: torch.Tensor, sel_index: torch.Tensor, out_index: Optional[torch.Tensor],
+             offsets: torch.Tensor,
              reduction_weight: Optional[torch.Tensor], top_k: int, op_dtype: torch.dtype, need_grad_x: bool,
              need_grad_keys: bool, need_grad_rw: bool, flags: int) -> Tuple[torch.Tensor, torch.Tensor,
                                                                              torch.Tensor]:
-    gx, gw, grw = N.host().backward(grad_output, x, keys, keys_n, sel, sel_index, out_index, offsets, None,
+    gx, gw, grw = N.host().backward(grad_output, x, keys, keys_x, keys_x_is_t, sel, sel_index, out_index, offsets,
+                                    None,
                                     reduction_weight, top_k, N.dtype_id(op_dtype), need_grad_x, need_grad_keys,
                                     need_grad_rw, flags, N.stream_of(x.device))
     return (gx if gx is not None else _empty(x), gw if gw is not None else _empty(keys),
@@ -111,7 +113,7 @@ def backward(grad_output: torch.Tensor, x: torch.Tensor, keys: torch.Tensor, key
 
 
 @backward.register_fake
-def _(grad_output, x, keys, keys_n, sel, sel_index, out_index, offsets, reduction_weight, top_k, op_dtype,
+def _(grad_output, x, keys, keys_x, keys_x_is_t, sel, sel_index, out_index, offsets, reduction_weight, top_k, op_dtype,
       need_grad_x, need_grad_keys, need_grad_rw, flags):
     # the real op's grad_x is always a fresh contiguous tensor of x's shape
     gx = x.new_empty(x.shape) if need_grad_x else _empty(x)
@@ -141,7 +143,7 @@ def cvmm_triton(x: torch.Tensor, sel_index: torch.Tensor, sel: torch.Tensor, key
     s32 = sel.reshape(-1).to(torch.int32)
     off = N.host().expert_offsets(s32, keys.shape[0], N.stream_of(x.device))
     # products rounded once, straight to out_dtype (cvmm.py:832-833, :862-863)
-    out = N.host().forward(x, keys, None, s32, sel_index, oi, off, None, None, N.dtype_id(op_dtype),
+    out = N.host().forward(x, keys, None, True, s32, sel_index, oi, off, None, None, N.dtype_id(op_dtype),
                            N.dtype_id(out_dtype), 0, N.stream_of(x.device))
     return out.view(*sel.shape, keys.shape[2])
 

@@ -114,6 +114,7 @@ std::atomic<int32_t> g_panel_tpw{0};
 std::atomic<int32_t> g_wgrad_order{0};
 std::atomic<int32_t> g_wgrad_tile{0};
 std::atomic<int32_t> g_gemm_order{0};
+std::atomic<int32_t> g_dense_topk{0};
 
 // m-tile order of the routed GEMMs (see GemmParams::token_major): the knob's
 // choice, or -1 to let the kernel launcher decide
@@ -194,6 +195,93 @@ bool reduce_needed(int32_t weighted, int32_t token_input, int64_t top_k) {
 
 int64_t ntiles_of(int64_t n, int64_t bn) { return (n + bn - 1) / bn; }
 
+// Dense top-k sum (cvmm_dense.hip) for a sum over top_k routes per token of
+// [K] x [K, N] products: the shapes it handles ...
+bool dense_topk_shape_ok(int32_t op_dtype, int64_t n_tokens, int32_t n_experts, int64_t K, int64_t N,
+                         int64_t top_k) {
+  const int64_t lim = 0x7fffffffll;
+  return (op_dtype == kBF16 || op_dtype == kF16) && K % 8 == 0 && top_k >= 2 && top_k <= 64 &&
+         n_experts <= kDenseMaxExperts && n_tokens > 0 && n_tokens <= lim && N <= lim &&
+         (int64_t)n_experts * K <= lim && n_tokens * top_k <= lim;
+}
+// ... and when it is the faster way (rates measured on MI355X: the library
+// GEMM at ~1.2 PFLOP/s over E/top_k times the useful flops plus the slotted
+// rows written and read at ~6 TB/s, against the routed GEMM at ~0.5 PFLOP/s
+// plus the [R, N] route buffer written and read at ~5 TB/s); the
+// CVMM_TUNE_DENSE_TOPK knob overrides it (1 never, 2 whenever the shapes fit).
+bool use_dense_topk(int32_t op_dtype, int64_t n_tokens, int32_t n_experts, int64_t K, int64_t N, int64_t top_k) {
+  if (!dense_topk_shape_ok(op_dtype, n_tokens, n_experts, K, N, top_k)) return false;
+  const int32_t knob = g_dense_topk.load();
+  if (knob == 1) return false;
+  if (knob == 2) return true;
+  const double T = (double)n_tokens, R = T * (double)top_k;
+  const double t_dense = 2.0 * T * n_experts * K * N / 1.2e15 + 2.0 * T * n_experts * K * 2 / 6e12;
+  const double t_route = R * N * 2 * 2 / 5e12 + 2.0 * R * K * N / 0.5e15;
+  return t_dense < t_route;
+}
+
+// Workspace of a dense top-k sum: the slotted rows, a weight copy in the
+// [E*K][N] layout (used when the caller's keys are not already that copy)
+// and the inverse route permutation (when not given).
+struct DenseWs {
+  void* a;
+  void* b;
+  int32_t* inv;
+};
+DenseWs carve_dense(Carver& c, int64_t n_tokens, int32_t n_experts, int64_t K, int64_t N, int64_t n_routes,
+                    int32_t op_dtype) {
+  DenseWs w;
+  w.a = c.take((size_t)n_tokens * n_experts * K * dtype_size(op_dtype));
+  w.b = c.take((size_t)n_experts * K * N * dtype_size(op_dtype));
+  w.inv = (int32_t*)c.take((size_t)n_routes * 4);
+  return w;
+}
+
+// The dense top-k sum: out[t] = sum_j s_tj src[row(t, j)] @ B_e.  `keys` (the
+// logical [E, d_in, d_out] view with its strides) is used as B when it is
+// already the op-dtype [E*K][N] row layout (kn_layout: K = d_in; otherwise K
+// = d_out), else cast into the workspace.
+int run_dense_topk(const DenseWs& w, const void* src, int32_t src_dtype, int64_t src_ld, bool src_per_route,
+                   const int32_t* sorted_sel, const int32_t* route_pos, const int64_t* rp, const int64_t* offs,
+                   int64_t n_routes, int64_t n_tokens, int64_t top_k, int32_t n_experts, const void* keys,
+                   int32_t keys_dtype, int64_t d_in, int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj,
+                   bool kn_layout, const void* rw, int32_t rw_dtype, int32_t w_round, int32_t op_dtype, void* out,
+                   int32_t out_dtype, int64_t out_ld, uint32_t gemm_class, const char* what, hipStream_t s) {
+  const int64_t K = kn_layout ? d_in : d_out, N = kn_layout ? d_out : d_in;
+  const void* B = keys;
+  const bool direct = keys_dtype == op_dtype && k_se == d_in * d_out &&
+                      (kn_layout ? (k_sj == 1 && k_si == d_out) : (k_si == 1 && k_sj == d_in));
+  if (!direct) {
+    // kn_layout: the [E][d_in][d_out] copy; else the [E][d_out][d_in] copy
+    int r = check_launch(timed(CVMM_KC_CAST_KEYS, s, [&] {
+      return launch_cast_keys(keys, keys_dtype, k_se, k_si, k_sj, n_experts, d_in, d_out, op_dtype,
+                              kn_layout ? nullptr : w.b, kn_layout ? w.b : nullptr, s);
+    }), what);
+    if (r) return r;
+    B = w.b;
+  }
+  const int32_t* inv = route_pos;
+  if (!inv) {
+    int r = check_launch(timed_combine(s, [&] { return launch_invert_rows(rp, n_routes, w.inv, s); }), what);
+    if (r) return r;
+    inv = w.inv;
+  }
+  int r = check_launch(timed_combine(s, [&] {
+    return launch_slot_rows(src, src_dtype, src_ld, src_per_route, sorted_sel, inv, rp, offs + (n_experts - 1),
+                            n_tokens, top_k, n_experts, K, rw, rw_dtype, w_round, op_dtype, w.a, s);
+  }), what);
+  if (r) return r;
+  int status = 0;
+  const hipError_t e = timed(gemm_class, s, [&] {
+    return dense_rows_gemm(w.a, B, n_tokens, (int64_t)n_experts * K, N, op_dtype, out, out_dtype, out_ld, s, &status);
+  });
+  if (e != hipSuccess) {
+    if (status != 0) return fail(CVMM_ERR_LAUNCH, "%s: rocblas_gemm_ex failed (status %d)", what, status);
+    return check_launch(e, what);
+  }
+  return CVMM_OK;
+}
+
 // n-tile width of the routed GEMM for output width n (256x64 tiles when narrow).
 int64_t gemm_bn(int64_t n) { return n <= 64 ? 64 : 128; }
 
@@ -203,7 +291,7 @@ extern "C" {
 
 const char* cvmm_last_error(void) { return g_err.c_str(); }
 
-int cvmm_abi_version(void) { return 9; }
+int cvmm_abi_version(void) { return 10; }
 
 int cvmm_timing_enable(uint32_t class_mask) {
   std::lock_guard<std::mutex> lk(g_timing_mu);
@@ -222,6 +310,11 @@ int cvmm_tuning_set(int32_t knob, int64_t value) {
     g_gemm_order.store((int32_t)value);
     return CVMM_OK;
   }
+  if (knob == CVMM_TUNE_DENSE_TOPK) {
+    if (value < 0 || value > 2) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: dense top-k choice must be 0, 1 or 2");
+    g_dense_topk.store((int32_t)value);
+    return CVMM_OK;
+  }
   if (knob == CVMM_TUNE_WGRAD_ORDER) {
     if (value < 0 || value > 3) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: weight-gradient order must be 0 .. 3");
     g_wgrad_order.store((int32_t)value);
@@ -233,6 +326,10 @@ int cvmm_tuning_set(int32_t knob, int64_t value) {
     return CVMM_OK;
   }
   return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: unknown knob %d", knob);
+}
+
+int cvmm_topk_dense(int64_t n_tokens, int32_t n_experts, int64_t K, int64_t N, int64_t top_k, int32_t op_dtype) {
+  return use_dense_topk(op_dtype, n_tokens, n_experts, K, N, top_k) ? 1 : 0;
 }
 
 int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launches) {
@@ -460,7 +557,10 @@ size_t cvmm_fwd_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_i
   Carver c(nullptr);
   if (!has_offsets) c.take((size_t)n_experts * 8);
   if (weighted) {
-    if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
+    const int64_t k = out_rows > 0 ? n_routes / out_rows : 0;
+    if (!(flags & CVMM_FLAG_ATOMIC_REDUCE) && use_dense_topk(op_dtype, out_rows, n_experts, d_in, d_out, k)) {
+      carve_dense(c, out_rows, n_experts, d_in, d_out, n_routes, op_dtype);
+    } else if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
       c.take((size_t)out_rows * d_out * 4);
     } else {
       c.take((size_t)n_routes * d_out * dtype_size(out_dtype));
@@ -558,6 +658,14 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
     if (pre_act != nullptr && (r = zero_unrouted(pre_act))) return r;
     return zero_unrouted(out);
   }
+  if (!(flags & CVMM_FLAG_ATOMIC_REDUCE) && use_dense_topk(op_dtype, out_rows, n_experts, d_in, d_out, reduce_k)) {
+    // high fan-out: expert-slotted x rows (scaled by rnd_out(w)) and one GEMM
+    // against the [E*d_in][d_out] weight rows, no route buffer
+    const DenseWs w = carve_dense(c, out_rows, n_experts, d_in, d_out, n_routes, op_dtype);
+    return run_dense_topk(w, x, x_dtype, x_ld, out_index == nullptr, sorted_sel, route_pos, rp, offs, n_routes,
+                          out_rows, reduce_k, n_experts, keys, keys_dtype, d_in, d_out, k_se, k_si, k_sj, true, rw,
+                          rw_dtype, out_dtype, op_dtype, out, out_dtype, out_ld, CVMM_KC_GEMM_FWD, "cvmm_fwd(dense)", s);
+  }
   if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
     // fused combine: y rounded to the output dtype, times rnd_out(w), fp32 atomics per token row
     float* acc = (float*)c.take((size_t)out_rows * d_out * 4);
@@ -641,7 +749,10 @@ size_t cvmm_bwd_x_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d
   Carver c(nullptr);
   if (!has_offsets) c.take((size_t)n_experts * 8);
   if (reduce_needed(weighted, token_input, top_k)) {
-    if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
+    if (!weighted && !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
+        use_dense_topk(op_dtype, grad_x_rows, n_experts, d_out, d_in, top_k)) {
+      carve_dense(c, grad_x_rows, n_experts, d_out, d_in, n_routes, op_dtype);
+    } else if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
       c.take((size_t)grad_x_rows * d_in * 4);
     } else {
       c.take((size_t)n_routes * d_in * dtype_size(weighted ? op_dtype : grad_x_dtype));
@@ -701,6 +812,16 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
     offs = o;
   }
   const int64_t* rp = token_input ? out_index : sel_index;
+
+  if (grad_x && reduce && !weighted && !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
+      use_dense_topk(op_dtype, grad_x_rows, n_experts, d_out, d_in, top_k)) {
+    // high fan-out: expert-slotted dY rows and one GEMM against the
+    // [E*d_out][d_in] weight rows, no route buffer
+    const DenseWs w = carve_dense(c, grad_x_rows, n_experts, d_out, d_in, n_routes, op_dtype);
+    return run_dense_topk(w, grad, grad_dtype, grad_ld, true, sorted_sel, route_pos, rp, offs, n_routes, grad_x_rows,
+                          top_k, n_experts, keys, keys_dtype, d_in, d_out, k_se, k_si, k_sj, false, nullptr, 0, 0,
+                          op_dtype, grad_x, grad_x_dtype, grad_x_ld, CVMM_KC_GEMM_BWDX, "cvmm_bwd_x(dense)", s);
+  }
 
   // grad @ keys[e]^T: K = d_out, N = d_in, B[k][n] = keys[e][n][k]
   GemmParams p{};

@@ -253,9 +253,13 @@ std::tuple<OptT, OptT> cast_keys(const Tensor& keys, int64_t op_id, bool want_t,
 // ---------------------------------------------------------------------------
 // forward (cvmm.py:1524-1550): returns [out_rows, d_out] in the op dtype
 // ---------------------------------------------------------------------------
-Tensor forward(const Tensor& x, const Tensor& keys, const OptT& keys_t, const Tensor& sel, const Tensor& sel_index,
-               const OptT& out_index, const Tensor& offsets, const OptT& route_pos, const OptT& rw, int64_t op_id,
-               int64_t out_id, int64_t flags, int64_t stream) {
+// The op-dtype weight copy a call reads, as the logical [E, d_in, d_out]
+// view: `copy` is the [E, d_out, d_in] copy when `is_t`, else [E, d_in, d_out].
+Tensor copy_view(const Tensor& copy, bool is_t) { return is_t ? copy.transpose(1, 2) : copy; }
+
+Tensor forward(const Tensor& x, const Tensor& keys, const OptT& keys_op, bool keys_op_is_t, const Tensor& sel,
+               const Tensor& sel_index, const OptT& out_index, const Tensor& offsets, const OptT& route_pos,
+               const OptT& rw, int64_t op_id, int64_t out_id, int64_t flags, int64_t stream) {
   require_device(x, "x");
   require_device(keys, "keys");
   require_device(sel, "sel");
@@ -264,11 +268,12 @@ Tensor forward(const Tensor& x, const Tensor& keys, const OptT& keys_t, const Te
   const int64_t E = keys.size(0), d_in = keys.size(1), d_out = keys.size(2);
   TORCH_CHECK(x.size(-1) == d_in, "cvmm: x.shape[-1] must equal keys.shape[1]");  // cvmm.py:825
   Tensor xf, kv;
-  if (keys_t.has_value()) {
-    // op-dtype activations and the [E, d_out, d_in] weight copy, seen as a
-    // [E, d_in, d_out] view with unit stride on d_in: the fast kernels' layout
+  if (keys_op.has_value()) {
+    // op-dtype activations and an op-dtype weight copy: the [E, d_out, d_in]
+    // copy (unit stride on d_in, the routed kernels' layout) or the
+    // [E, d_in, d_out] one (the dense top-k GEMM's rows)
     xf = rows_of(x.scalar_type() == op ? x : x.to(op), d_in);
-    kv = keys_t->transpose(1, 2);
+    kv = copy_view(*keys_op, keys_op_is_t);
   } else {
     xf = rows_of(storage_for(x, op), d_in);
     kv = keys_view(storage_for(keys, op));
@@ -369,7 +374,7 @@ Tensor gelu_backward(const Tensor& grad, const Tensor& pre, int64_t stream) {
 // backward (cvmm.py:1552-1755): (grad_x, grad_keys, grad_reduction_weight)
 // ---------------------------------------------------------------------------
 std::tuple<OptT, OptT, OptT> backward(const Tensor& grad_output, const Tensor& x, const Tensor& keys,
-                                      const OptT& keys_n, const Tensor& sel, const Tensor& sel_index,
+                                      const OptT& keys_x, bool keys_x_is_t, const Tensor& sel, const Tensor& sel_index,
                                       const OptT& out_index, const Tensor& offsets, const OptT& route_pos,
                                       const OptT& rw, int64_t top_k, int64_t op_id, bool need_grad_x,
                                       bool need_grad_keys, bool need_grad_rw, int64_t flags, int64_t stream) {
@@ -419,7 +424,9 @@ std::tuple<OptT, OptT, OptT> backward(const Tensor& grad_output, const Tensor& x
   }
 
   if (need_grad_x || need_grad_rw) {
-    Tensor kv = keys_n.has_value() ? *keys_n : keys_view(storage_for(keys, op));
+    // the grad-input's weight copy: [E, d_in, d_out] for the routed GEMM, the
+    // transposed one for a dense top-k sum, else the keys as stored
+    Tensor kv = keys_x.has_value() ? copy_view(*keys_x, keys_x_is_t) : keys_view(storage_for(keys, op));
     Tensor xr = rows_of(x, d_in);
     OptT gx;
     if (need_grad_x) gx = at::empty(xr.sizes(), opts(x, x.scalar_type()));

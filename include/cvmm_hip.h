@@ -88,12 +88,37 @@ int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launche
  *   CVMM_TUNE_GEMM_ORDER: m-tile order of the routed GEMMs (forward, grad
  *     input), 1 = expert-major, 2 = token-major (tile j of every expert next
  *     to each other; up to 256 experts).  Built in: token-major for the
- *     long-K kernel when every gathered row feeds >= 32 routes. */
+ *     long-K kernel when every gathered row feeds >= 32 routes.
+ *   CVMM_TUNE_DENSE_TOPK: how top-k sums are taken (the weighted forward
+ *     combine, the token gradient of a token-input selection): 1 = always
+ *     the routed GEMM + route-ordered buffer, 2 = the dense GEMM over
+ *     expert-slotted rows wherever its shapes fit (see cvmm_topk_dense).
+ *     Built in: the cost model of cvmm_topk_dense. */
 #define CVMM_TUNE_PANEL_TILES_PER_WG 1
 #define CVMM_TUNE_WGRAD_ORDER 2
 #define CVMM_TUNE_GEMM_ORDER 3
 #define CVMM_TUNE_WGRAD_TILE 5
+#define CVMM_TUNE_DENSE_TOPK 6
 int cvmm_tuning_set(int32_t knob, int64_t value);
+
+/* Whether a top-k sum -- out[t] = sum over the top_k routes (t, j) of
+ * [K]-row x [K, N] expert products, for n_tokens tokens over n_experts
+ * experts -- is taken as one dense GEMM (no counterpart in the reference,
+ * which writes every route's product and sums them afterwards,
+ * cvmm.py:1204-1223, :1541-1545).  The dense form places each token's K-wide
+ * operand rows in expert slots, A[t][e*K + k], and multiplies A [T, E*K] by
+ * the weights as [E*K, N] rows (a library GEMM, fp32 accumulation, one
+ * rounding, deterministic): E / top_k times the useful flops, but no [R, N]
+ * route-ordered buffer (2.1 GB at SwitchHead size).  It is taken when the
+ * shapes fit (16-bit op, K % 8 == 0, 2 <= top_k <= 64, <= 4096 experts) and,
+ * unless CVMM_TUNE_DENSE_TOPK says otherwise, a cost model of the two ways
+ * (measured rates) favours it: at high fan-out (top_k / E >= ~1/4).
+ *   cvmm_fwd, weighted:          K = d_in,  N = d_out; the weights are read
+ *     fastest as the op-dtype [E][d_in][d_out] copy (unit stride on d_out);
+ *   cvmm_bwd_x, unweighted token input, top_k > 1: K = d_out, N = d_in; the
+ *     weights as the op-dtype [E][d_out][d_in] copy (unit stride on d_in).
+ * Other keys are cast into the workspace.  Returns 1 or 0. */
+int cvmm_topk_dense(int64_t n_tokens, int32_t n_experts, int64_t K, int64_t N, int64_t top_k, int32_t op_dtype);
 
 /* ------------------------------------------------------------------------ */
 /* Selector preparation                                                      */
@@ -201,9 +226,12 @@ int cvmm_cast_keys(const void* keys, int32_t keys_dtype, int32_t n_experts, int6
  * route_pos (optional): the inverse of rp = out_index or sel_index, as
  * cvmm_sort_routes writes it; computed in the workspace when NULL.
  * Top-k sums (weighted here, token-input in cvmm_bwd_x) are taken in one of
- * two ways: fp32 atomics (CVMM_FLAG_ATOMIC_REDUCE, not deterministic in the
- * last bits), else a route-ordered buffer and a per-token sum in route order
- * (deterministic).
+ * three ways: fp32 atomics (CVMM_FLAG_ATOMIC_REDUCE, not deterministic in the
+ * last bits); the dense GEMM over expert-slotted rows where cvmm_topk_dense
+ * says so (the per-token sum in the GEMM's fp32 accumulators, one rounding);
+ * else a route-ordered buffer and a per-token sum in route order (each
+ * route's product rounded first, as the reference does).  The last two are
+ * deterministic.
  * Routes whose expert id is outside [0, E) (no counterpart: the reference
  * indexes keys with them) are left out: the top-k sums skip them, and their
  * own rows of out (unweighted) or grad_x (per-route gradient) are zero. */

@@ -123,10 +123,10 @@ def test_ops_pass_opcheck():
     torch.library.opcheck(ops.expert_offsets, (ssel, E), test_utils=utils)
     torch.library.opcheck(ops.cast_keys, (keys, torch.bfloat16), test_utils=utils)
     xf = x.reshape(-1, x.shape[-1])
-    torch.library.opcheck(ops.forward, (xf, keys, None, ssel, tok, perm, off, w, torch.bfloat16, 0),
+    torch.library.opcheck(ops.forward, (xf, keys, None, True, ssel, tok, perm, off, w, torch.bfloat16, 0),
                           test_utils=utils)
     gy = go.reshape(-1, go.shape[-1])
-    torch.library.opcheck(ops.backward, (gy, xf, keys, None, ssel, tok, perm, off, w, 3, torch.bfloat16,
+    torch.library.opcheck(ops.backward, (gy, xf, keys, None, False, ssel, tok, perm, off, w, 3, torch.bfloat16,
                                          True, True, True, 0), test_utils=utils)
     minus1 = torch.full((1,), -1, dtype=torch.int64, device="cuda")
     torch.library.opcheck(ops.cvmm_triton, (xf, tok, ssel, keys, torch.bfloat16, perm, torch.bfloat16),

@@ -1,0 +1,177 @@
+"""The dense form of the top-k sums (expert-slotted rows + one library GEMM,
+cvmm_dense.hip): the weighted forward combine (cvmm.py:1541-1545) and the
+token gradient of a token-input selection (cvmm.py:1204-1223).
+
+The built-in cost model takes it only at high fan-out (the full-size
+SwitchHead tests run it); here the tuning knob forces it on small shapes so
+that every layout is checked against the oracle at the north-star tolerance:
+token and route input, weighted and not, fp16, fp32 activations under
+autocast, tokens that pick one expert twice, out-of-range ids, selectors the
+sort did not make (no inverse permutation), keys that are not the GEMM's row
+layout (cast into the workspace).  The sum over a token's routes runs in the
+GEMM's fp32 accumulators (one rounding, where the routed path rounds each
+route's product first), which the tolerance covers.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import cvmm_codex_amd.api as C
+from cvmm_codex_amd import _native as N
+from tests import gpu_util as U
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture
+def dense():
+    lib = N.lib()
+    assert lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 2) == 0
+    yield lib
+    lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 0)
+
+
+def _case(seed, B, T, D, H, E, K, weighted, route_input, x_dt=torch.bfloat16, dup=False):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*((B, T, K, D) if route_input else (B, T, D)), generator=g).to(x_dt)
+    keys = torch.randn(E, D, H, generator=g) / D ** 0.5
+    if dup:   # independent draws: some tokens pick an expert twice
+        sel = torch.randint(0, E, (B, T, K), generator=g)
+    else:
+        sel = torch.rand(B, T, E, generator=g).topk(K, dim=-1).indices
+    w = torch.rand(B, T, K, generator=g) if weighted else None
+    go = torch.randn(*((B, T, H) if weighted else (B, T, K, H)), generator=g).to(torch.bfloat16)
+    return x, keys, sel, w, go
+
+
+@pytest.mark.parametrize("weighted,route_input,D,H,E,K", [
+    (False, False, 64, 128, 16, 4),      # token gradient (unweighted token input)
+    (False, False, 128, 64, 32, 8),
+    (False, False, 64, 64, 64, 64),      # SwitchHead-like fan-out: 64 routes per token
+    (True, True, 64, 128, 32, 16),       # weighted forward, route input (SwitchHead O / FFN down)
+    (True, True, 128, 256, 16, 4),
+    (True, False, 96, 64, 12, 3),        # weighted forward, token input
+])
+def test_dense_topk_matches_oracle(dense, weighted, route_input, D, H, E, K):
+    x, keys, sel, w, go = _case(D + H + E + K, 2, 200, D, H, E, K, weighted, route_input)
+    got = U.run_hip(x, keys, sel, w, go, route_input, True)
+    U.compare(got, U.run_oracle(x, keys, sel, w, go, route_input, True), 2e-2)
+
+
+@pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True)])
+def test_dense_and_routed_agree(weighted, route_input):
+    """Both forms of the same sums, against each other (one rounding step
+    apart) and against the oracle."""
+    lib = N.lib()
+    x, keys, sel, w, go = _case(5, 2, 256, 64, 128, 32, 8, weighted, route_input)
+    out = {}
+    try:
+        for mode in (1, 2):
+            assert lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, mode) == 0
+            out[mode] = U.run_hip(x, keys, sel, w, go, route_input, True)
+    finally:
+        lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 0)
+    exp = U.run_oracle(x, keys, sel, w, go, route_input, True)
+    for mode in (1, 2):
+        U.compare(out[mode], exp, 2e-2)
+    name = "out" if weighted else "x_grad"
+    assert U.norm_rel(U.to_np(out[2][name]), U.to_np(out[1][name])) <= 1e-2
+
+
+def test_dense_topk_is_deterministic(dense):
+    x, keys, sel, w, go = _case(6, 2, 300, 64, 64, 16, 8, False, False)
+    a = U.run_hip(x, keys, sel, w, go, False, True)
+    b = U.run_hip(x, keys, sel, w, go, False, True)
+    assert torch.equal(a["x_grad"], b["x_grad"]) and torch.equal(a["out"], b["out"])
+
+
+def test_dense_topk_fp16(dense):
+    for weighted, route_input in ((False, False), (True, True)):
+        x, keys, sel, w, go = _case(7, 2, 128, 64, 96, 16, 4, weighted, route_input, x_dt=torch.float16)
+        got = U.run_hip(x, keys, sel, w, go, route_input, True, amp_dtype=torch.float16)
+        U.compare(got, U.run_oracle(x, keys, sel, w, go, route_input, True, amp_dtype="float16"), 2e-2)
+
+
+def test_dense_topk_fp32_activations_under_autocast(dense):
+    """x stored in fp32: the slotted rows round it to the op dtype."""
+    for weighted, route_input in ((False, False), (True, True)):
+        x, keys, sel, w, go = _case(8, 1, 160, 64, 64, 16, 4, weighted, route_input, x_dt=torch.float32)
+        got = U.run_hip(x, keys, sel, w, go, route_input, True)
+        U.compare(got, U.run_oracle(x, keys, sel, w, go, route_input, True), 2e-2)
+
+
+def test_dense_topk_duplicate_experts(dense):
+    """Tokens that pick one expert twice: both routes land in the same slot
+    (their rows are added before the GEMM)."""
+    for weighted, route_input in ((False, False), (True, True), (True, False)):
+        x, keys, sel, w, go = _case(9, 2, 128, 64, 64, 4, 6, weighted, route_input, dup=True)
+        assert any(len(set(r)) < 6 for r in sel.reshape(-1, 6).tolist())
+        got = U.run_hip(x, keys, sel, w, go, route_input, True)
+        U.compare(got, U.run_oracle(x, keys, sel, w, go, route_input, True), 2e-2)
+
+
+def test_dense_topk_invalid_ids_contribute_nothing(dense):
+    E = 8
+    for weighted, route_input in ((False, False), (True, True)):
+        x, keys, sel, w, go = _case(10, 2, 128, 64, 64, E, 4, weighted, route_input)
+        g = torch.Generator().manual_seed(11)
+        bad = torch.rand(sel.shape, generator=g) < 0.1
+        sel_bad = sel.clone()
+        sel_bad[bad] = torch.where(torch.rand(sel.shape, generator=g) < 0.5, -1, E + 2)[bad]
+        got = U.run_hip(x, keys, sel_bad, w, go, route_input, True)
+        sel_ok = sel.clone()
+        sel_ok[bad] = 0
+        if weighted:   # a zero routing weight: the route adds exact zeros
+            w_ok = w.clone()
+            w_ok[bad] = 0
+            exp = U.run_oracle(x, keys, sel_ok, w_ok, go, route_input, True)
+            assert U.norm_rel(U.to_np(got["out"]), exp["out"]) <= 2e-2
+        else:          # a zero gradient row: the route adds exact zeros
+            go_ok = go.clone()
+            go_ok[bad] = 0
+            exp = U.run_oracle(x, keys, sel_ok, None, go_ok, route_input, True)
+            assert U.norm_rel(U.to_np(got["x_grad"]), exp["x_grad"]) <= 2e-2
+
+
+def test_dense_topk_with_a_foreign_selector(dense):
+    """A CVMMSel built from torch.sort (no inverse permutation attached): the
+    call inverts the route index itself."""
+    x, keys, sel, _, go = _case(12, 2, 200, 64, 128, 16, 4, False, False)
+    sd = sel.cuda()
+    fsel = sd.flatten().to(torch.int32)
+    ssel, perm = fsel.sort(stable=True)
+    s = C.CVMMSel(fsel.view_as(sd), ssel.view_as(sd), perm // 4, perm)
+    xd = x.cuda().requires_grad_(True)
+    kd = keys.cuda().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = C.cvmm(xd, s, kd)
+    y.backward(go.cuda().to(y.dtype))
+    got = {"out": y.detach(), "x_grad": xd.grad, "keys_grad": kd.grad, "weights_grad": None}
+    U.compare(got, U.run_oracle(x, keys, sel, None, go, False, True), 2e-2)
+
+
+def test_dense_topk_keys_cast_into_the_workspace(dense):
+    """Keys that are not the GEMM's op-dtype row layout (the fp32 keys
+    themselves) are cast into the workspace by the call."""
+    x, keys, sel, _, go = _case(13, 2, 160, 64, 64, 16, 4, False, False)
+    s = C.cvmm_prepare_sel2(sel.cuda())
+    C.create_kernels()
+    s._resolve(16)
+    xd, kd, gd = x.cuda(), keys.cuda(), go.cuda()
+
+    class Ctx:
+        op_type = torch.bfloat16
+
+    gx, _, _ = C._backward(Ctx, gd, xd, kd, s.raw_sel, s.sel, s.sel_index, s.out_index, None, True, False, False,
+                           keys_x=None)
+    exp = U.run_oracle(x, keys, sel, None, go, False, True)
+    assert U.norm_rel(U.to_np(gx), exp["x_grad"]) <= 2e-2
+    # and the weighted forward with the fp32 keys
+    x2, keys2, sel2, w2, go2 = _case(14, 2, 160, 64, 64, 16, 4, True, True)
+    s2 = C.cvmm_prepare_sel2(sel2.cuda(), w2.cuda(), route_input=True)
+    s2._resolve(16)
+    y = C._forward(x2.cuda(), s2.sel_index, s2.sel, keys2.cuda(), s2.out_index, w2.cuda(), torch.bfloat16)
+    exp2 = U.run_oracle(x2, keys2, sel2, w2, go2, True, True)
+    assert U.norm_rel(U.to_np(y), exp2["out"]) <= 2e-2

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.cvmm_abi_version() == 9
+    assert lib.cvmm_abi_version() == 10
 
 
 def test_workspace_queries(lib):
@@ -55,9 +55,13 @@ def test_workspace_queries(lib):
     assert lib.cvmm_fwd_workspace_bytes(65536, 64, 128, 1024, 8192, N.BF16, N.BF16, 1, 1, 0) >= 65536 * 1024 * 2
     assert (lib.cvmm_fwd_workspace_bytes(65536, 64, 128, 1024, 8192, N.BF16, N.BF16, 1, 1, N.FLAG_ATOMIC_REDUCE)
             >= 8192 * 1024 * 4)
-    # token-input grad (top-64 sum): the route-ordered [R, d_in] buffer
+    # token-input grad (top-64 sum) with the routed path: the route-ordered [R, d_in] buffer
     R, T, E = 524288, 8192, 256
-    assert lib.cvmm_bwd_x_workspace_bytes(R, E, 2048, 64, T, 1, 0, 1, 64, N.BF16, N.BF16, 0, 0) >= R * 2048 * 2
+    assert lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 1) == 0
+    try:
+        assert lib.cvmm_bwd_x_workspace_bytes(R, E, 2048, 64, T, 1, 0, 1, 64, N.BF16, N.BF16, 0, 0) >= R * 2048 * 2
+    finally:
+        lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 0)
     # weight grad: counters + bounded partial slots
     assert lib.cvmm_bwd_w_workspace_bytes(65536, 64, 1024, 128, N.BF16, 1) > 64 * 8 * 4
 
@@ -124,3 +128,34 @@ def test_router_arguments_fail_before_launch(lib):
     assert lib.cvmm_route_topk(None, 0, 16, 128, 128, 8, 1, None, None, None, None, None, None, None, None, 0,
                                None) == 3
     assert lib.cvmm_route_topk_backward(None, 0, 16, 128, 128, 8, 1, None, None, None, 64, None) == 1
+
+
+def test_dense_topk_choice(lib):
+    """The top-k sum's dense form is chosen at SwitchHead fan-out (64 of 256
+    experts, K = 64, N = 2048), not at top-8 of 64 (ff_up / ff_down) or of 128
+    (the FFN stack); only for 16-bit ops, 2 <= top_k <= 64 and K % 8 == 0;
+    the knob forces either way."""
+    BF, F32 = N.BF16, N.F32
+    assert lib.cvmm_topk_dense(8192, 256, 64, 2048, 64, BF) == 1        # switch_v grad-input, switch_o forward
+    assert lib.cvmm_topk_dense(8192, 64, 128, 1024, 8, BF) == 0          # ff_up grad-input, ff_down forward
+    assert lib.cvmm_topk_dense(16384, 128, 512, 2048, 8, BF) == 0        # the FFN stack's down projection
+    assert lib.cvmm_topk_dense(8192, 256, 64, 2048, 64, F32) == 0        # fp32 op: routed path
+    assert lib.cvmm_topk_dense(8192, 256, 60, 2048, 64, BF) == 0         # K % 8 != 0
+    assert lib.cvmm_topk_dense(8192, 256, 64, 2048, 65, BF) == 0         # top_k > 64
+    assert lib.cvmm_topk_dense(8192, 5000, 64, 2048, 64, BF) == 0        # too many experts for the slot table
+    try:
+        assert lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 2) == 0
+        assert lib.cvmm_topk_dense(8192, 64, 128, 1024, 8, BF) == 1
+        assert lib.cvmm_topk_dense(100, 7, 16, 24, 2, N.F16) == 1
+        assert lib.cvmm_topk_dense(100, 7, 16, 24, 1, N.F16) == 0        # top-1 has no sum
+        assert lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 1) == 0
+        assert lib.cvmm_topk_dense(8192, 256, 64, 2048, 64, BF) == 0
+        assert lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 3) != 0
+    finally:
+        lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 0)
+    # workspace: the dense form needs the slotted rows (T x E*K), not the [R, N] route buffer
+    R, T, E = 524288, 8192, 256
+    ws = lib.cvmm_bwd_x_workspace_bytes(R, E, 2048, 64, T, 1, 0, 1, 64, BF, BF, 0, 0)
+    assert T * E * 64 * 2 <= ws < R * 2048 * 2 // 4
+    ws = lib.cvmm_fwd_workspace_bytes(R, E, 64, 2048, T, BF, BF, 1, 1, 0)
+    assert T * E * 64 * 2 <= ws < R * 2048 * 2 // 4
