@@ -46,6 +46,7 @@ _SIGS = {
     "cvmm_sort_workspace_bytes": (_SZ, [_I64, _I32]),
     "cvmm_sort_routes": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "cvmm_sort_routes_noalloc": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P]),
+    "cvmm_copy_ids": (ctypes.c_int, [_P, _I32, _I64, _P, _P]),
     "cvmm_expert_offsets": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
     "cvmm_sort_routes_cast_keys": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _SZ,
                                                   _P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P]),

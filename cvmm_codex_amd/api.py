@@ -379,8 +379,11 @@ def cvmm_prepare_sel2(sel: Union[torch.Tensor, CVMMSel], w: Optional[torch.Tenso
     n_per_batch = sel.shape[-1]
     # the reference's `fsel = sel.flatten().to(torch.int32)` (cvmm.py:1796):
     # the routing is fixed here, whatever later happens to `sel`
-    fsel = sel.reshape(-1)
-    fsel = fsel.clone() if fsel.dtype == torch.int32 else fsel.to(torch.int32)
+    if _compiling():
+        fsel = sel.reshape(-1)
+        fsel = fsel.clone() if fsel.dtype == torch.int32 else fsel.to(torch.int32)
+    else:
+        fsel = N.host().copy_ids(sel, N.stream_of(sel.device)).reshape(-1)
     out = CVMMSel._deferred(fsel.view(sel.shape), _Routing(fsel, n_per_batch), route_input, w)
     out._raw_sel = out._raw_src
     return out

@@ -446,6 +446,14 @@ int cvmm_sort_routes_noalloc(const void* sel, int32_t sel_is_int64, int64_t n_ro
                           route_pos, n_invalid, ws, kSortScratchBytes, stream);
 }
 
+int cvmm_copy_ids(const void* sel, int32_t sel_is_int64, int64_t n, int32_t* out, void* stream) {
+  if (n < 0) return fail(CVMM_ERR_INVALID, "cvmm_copy_ids: n < 0");
+  if (n > 0 && (!sel || !out)) return fail(CVMM_ERR_INVALID, "cvmm_copy_ids: NULL pointer");
+  return check_launch(timed(CVMM_KC_SORT, (hipStream_t)stream, [&] {
+    return launch_copy_ids(sel, sel_is_int64 != 0, n, out, (hipStream_t)stream);
+  }), "cvmm_copy_ids");
+}
+
 int cvmm_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_experts, int64_t* offsets,
                         void* stream) {
   if (n_experts <= 0 || offsets == nullptr) return fail(CVMM_ERR_INVALID, "cvmm_expert_offsets: bad arguments");
@@ -633,13 +641,9 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
   p.token_major = gemm_token_major(n_experts);
 
   if (!weighted) {
-    // rows of routes with an expert id outside [0, E) are zeroed after the GEMM
-    const int64_t* rows_end = offs + (n_experts - 1);
-    auto zero_unrouted = [&](void* buf) {
-      return check_launch(timed_fill(s, [&] { return launch_zero_unrouted_rows(buf, out_dtype, out_ld, d_out, out_rows, rp, 1,
-                                                                  rows_end, n_routes, s); }),
-                          "cvmm_fwd(zero unrouted)");
-    };
+    // rows of routes with an expert id outside [0, E): zeroed by the GEMM's
+    // workgroups past its last m-tile
+    p.zero_unrouted = 1;
     p.epi = kEpiStore; p.out = out; p.out_dtype = out_dtype; p.out_ld = out_ld; p.out_rows = out_rows;
     if (pre_act != nullptr) {
       p.act = 1; p.aux = pre_act;
@@ -648,15 +652,11 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
         p.act = 0; p.aux = nullptr; p.out = pre_act;
         int r = check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
         if (r) return r;
-        if ((r = zero_unrouted(pre_act))) return r;
         return check_launch(timed_combine(s, [&] { return launch_gelu_rows(pre_act, out_dtype, out_ld, out_rows, d_out, out, out_dtype, out_ld, s); }),
                             "cvmm_fwd_gelu(gelu)");
       }
     }
-    int r = check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
-    if (r) return r;
-    if (pre_act != nullptr && (r = zero_unrouted(pre_act))) return r;
-    return zero_unrouted(out);
+    return check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
   }
   if (!(flags & CVMM_FLAG_ATOMIC_REDUCE) && use_dense_topk(op_dtype, out_rows, n_experts, d_in, d_out, reduce_k)) {
     // high fan-out: expert-slotted x rows (scaled by rnd_out(w)) and one GEMM
@@ -849,6 +849,7 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
   if (grad_x) {
     if (!reduce) {
       p.epi = kEpiStore; p.out = grad_x; p.out_dtype = grad_x_dtype; p.out_ld = grad_x_ld; p.out_rows = grad_x_rows;
+      p.zero_unrouted = 1;  // per-route rows of out-of-range expert ids: zero
       if (weighted) {  // route-major weighted: rnd_op(rnd_op(g) * rnd_op(w))
         p.val_dtype = op_dtype; p.w = rw; p.w_dtype = rw_dtype; p.w_round = op_dtype; p.prod_dtype = op_dtype;
       } else {
@@ -895,13 +896,6 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
 
   int r = check_launch(timed(CVMM_KC_GEMM_BWDX, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_bwd_x(gemm)");
   if (r) return r;
-  if (grad_x && !reduce) {
-    // per-route rows of routes with an expert id outside [0, E): zero
-    r = check_launch(timed_fill(s, [&] { return launch_zero_unrouted_rows(grad_x, grad_x_dtype, grad_x_ld, d_in, grad_x_rows, rp, 1,
-                                                             offs + (n_experts - 1), n_routes, s); }),
-                     "cvmm_bwd_x(zero unrouted)");
-    if (r) return r;
-  }
   if (grad_x && reduce) {
     if (acc) {
       r = check_launch(timed_combine(s, [&] { return launch_cast_rows(acc, d_in, grad_x_rows, d_in, weighted ? op_dtype : -1, grad_x,

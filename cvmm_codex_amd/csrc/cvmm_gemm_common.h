@@ -77,7 +77,9 @@ __device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& 
       for (int g = 0; g < G; ++g) s += nt[g] < j ? nt[g] : j;
       return __shfl(wave_incl_scan(s), 63, 64);
     };
-    if (tile < before(ntmax)) {
+    const int64_t n_tiles = before(ntmax);
+    if (lane == 0 && tile >= n_tiles) m.row0 = n_tiles;  // past the last tile: the tile count
+    if (tile < n_tiles) {
       int64_t lo = 0, hi = ntmax;  // before(lo) <= tile < before(hi)
       while (hi - lo > 1) {
         const int64_t mid = (lo + hi) >> 1;
@@ -125,6 +127,7 @@ __device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& 
       carry = __shfl(incl, 63, 64);
       if (tile < carry) break;
     }
+    if (lane == 0 && m.expert < 0) m.row0 = carry;  // past the last tile: the tile count
   }
   __syncthreads();
   if (m.expert < 0) return false;
@@ -160,6 +163,32 @@ __device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& 
   __syncthreads();
 
   return true;
+}
+
+// Called by a workgroup past the last m-tile (gemm_schedule returned false,
+// leaving the tile count in m.row0): when the call asks for it, zero the
+// columns [c0, c1) of the output rows (and GELU pre-activation rows) of the
+// routes no tile covers -- expert id outside [0, E), sorted at or past
+// offsets[E - 1].  Surplus m-tile j of the n_surplus launched takes every
+// n_surplus-th such route; a launch of ceil(R / BM) + min(E, R) m-tiles has at
+// least one surplus m-tile whenever such routes exist.
+template <int BM>
+__device__ void zero_unrouted_cols(const GemmParams& p, const RouteMeta<BM>& m, int64_t tile, int64_t m_tiles,
+                                   int64_t c0, int64_t c1) {
+  if (!p.zero_unrouted || p.out == nullptr) return;
+  const int64_t j = tile - m.row0, n_surplus = m_tiles - m.row0;
+  if (j < 0 || n_surplus <= 0) return;
+  int64_t q0 = p.offsets[p.n_experts - 1];
+  q0 = q0 < 0 ? 0 : q0;
+  if (c1 > p.N) c1 = p.N;
+  for (int64_t q = q0 + j; q < p.n_routes; q += n_surplus) {
+    const int64_t oi = p.o_idx != nullptr ? p.o_idx[q] / p.o_div : q;
+    if (oi < 0 || oi >= p.out_rows) continue;
+    for (int64_t c = c0 + threadIdx.x; c < c1; c += kGemmThreads) {
+      store_from_f32(p.out, p.out_dtype, oi * p.out_ld + c, 0.f);
+      if (p.act != 0 && p.aux != nullptr) store_from_f32(p.aux, p.out_dtype, oi * p.out_ld + c, 0.f);
+    }
+  }
 }
 
 // Epilogue over the fp32 tile of rows [0, rows) and columns

@@ -73,7 +73,10 @@ __global__ __launch_bounds__(kGemmThreads, 2) void routed_gemm_nt_kernel(const G
   const int64_t ntile = id % n_ntiles;
   const int64_t n0 = ntile * BN;
 
-  if (!gemm_schedule<BM>(p, tile, meta)) return;
+  if (!gemm_schedule<BM>(p, tile, meta)) {
+    zero_unrouted_cols<BM>(p, meta, tile, gridDim.x / n_ntiles, n0, n0 + BN);
+    return;
+  }
   const int32_t expert = meta.expert;
 
   // ---- per-lane DMA sources (fixed across k stages) --------------------------
@@ -214,7 +217,10 @@ __global__ __launch_bounds__(kGemmThreads, 2) void routed_gemm_nloop_kernel(cons
   const int64_t nt_begin = (id % n_groups) * ng;
   const int64_t nt_end = nt_begin + ng < n_ntiles ? nt_begin + ng : n_ntiles;
 
-  if (!gemm_schedule<BM>(p, tile, meta)) return;
+  if (!gemm_schedule<BM>(p, tile, meta)) {
+    zero_unrouted_cols<BM>(p, meta, tile, gridDim.x / n_groups, nt_begin * BN, nt_end * BN);
+    return;
+  }
   const int32_t expert = meta.expert;
 
   const char* zero = reinterpret_cast<const char*>(g_cvmm_zero_page);

@@ -193,7 +193,10 @@ __global__ __launch_bounds__(kGemmThreads, (PanelCfg<KP, BN, WM>::OCC)) void rou
   const int64_t nt0 = (id % n_groups) * tpw;
   const int T = (int)((n_ntiles - nt0) < tpw ? (n_ntiles - nt0) : tpw);
 
-  if (!gemm_schedule<Cfg::BM>(p, tile, meta)) return;
+  if (!gemm_schedule<Cfg::BM>(p, tile, meta)) {
+    zero_unrouted_cols<Cfg::BM>(p, meta, tile, gridDim.x / n_groups, nt0 * BN, (nt0 + T) * BN);
+    return;
+  }
   const int32_t expert = meta.expert;
 
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;

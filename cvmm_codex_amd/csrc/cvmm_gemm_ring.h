@@ -80,7 +80,10 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   const int64_t ntile = id % n_ntiles;
   const int64_t n0 = ntile * BN;
 
-  if (!gemm_schedule<BM>(p, tile, meta)) return;
+  if (!gemm_schedule<BM>(p, tile, meta)) {
+    zero_unrouted_cols<BM>(p, meta, tile, gridDim.x / n_ntiles, n0, n0 + BN);
+    return;
+  }
   const int32_t expert = meta.expert;
 
   // ---- per-lane DMA sources: instruction j of wave w fills LDS bytes

@@ -76,6 +76,10 @@ struct GemmParams {
   // (erf form): out = gelu(h), and h (the product in the output type) to aux
   int32_t act;
   void* aux;
+  // zero the output rows (and aux rows) of the routes no tile covers: those
+  // whose expert id is outside [0, E), sorted past offsets[E - 1]; done by the
+  // workgroups past the last m-tile (direct per-route stores only)
+  int32_t zero_unrouted;
 };
 constexpr int32_t kTokenMajorMaxExperts = 256;
 
@@ -231,6 +235,8 @@ hipError_t launch_route_topk_backward(const void* logits, int32_t logits_dtype, 
                                       hipStream_t stream);
 
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
+// out[i] = (int32) sel[i] (int64 ids: their low 32 bits)
+hipError_t launch_copy_ids(const void* sel, bool sel_is_int64, int64_t n, int32_t* out, hipStream_t stream);
 // ---------------------------------------------------------------------------
 // dense top-k sums (cvmm_dense.hip): expert-slotted rows + one library GEMM
 // ---------------------------------------------------------------------------
@@ -266,12 +272,6 @@ hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_l
                                int64_t k, int64_t n, int32_t mid_dtype, void* out, int32_t out_dtype, int64_t out_ld,
                                hipStream_t stream);
 hipError_t launch_invert_rows(const int64_t* rp, int64_t n_routes, int32_t* inv, hipStream_t stream);
-// Zero out[row][0, width) for the sorted routes q in [*rows_end, n_routes)
-// (expert id outside [0, E): no GEMM tile stores them), row = o_idx[q] / o_div
-// or q when o_idx == NULL, rows outside [0, out_rows) skipped.
-hipError_t launch_zero_unrouted_rows(void* out, int32_t out_dtype, int64_t out_ld, int64_t width, int64_t out_rows,
-                                     const int64_t* o_idx, int64_t o_div, const int64_t* rows_end, int64_t n_routes,
-                                     hipStream_t stream);
 // out[t][n] = rnd(rnd(acc[t][n], mid_dtype), out_dtype)
 hipError_t launch_cast_rows(const float* acc, int64_t acc_ld, int64_t rows, int64_t n, int32_t mid_dtype,
                             void* out, int32_t out_dtype, int64_t out_ld, hipStream_t stream);

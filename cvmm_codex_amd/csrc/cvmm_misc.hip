@@ -33,35 +33,40 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Rows of routes whose expert id is outside [0, E): those sort past
-// *rows_end (the last inclusive offset) and no GEMM tile covers them.  Their
-// output rows (row = o_idx[q] / o_div, or q) are zeroed so that a direct
-// per-route store never leaves uninitialised memory.  One workgroup per
-// such route, grid-strided; nothing to do (the usual case) costs one read of
-// *rows_end per workgroup.
-__global__ __launch_bounds__(256) void zero_unrouted_rows_kernel(void* __restrict__ out, int32_t out_dtype,
-                                                                 int64_t out_ld, int64_t width, int64_t out_rows,
-                                                                 const int64_t* __restrict__ o_idx, int64_t o_div,
-                                                                 const int64_t* __restrict__ rows_end,
-                                                                 int64_t n_routes) {
-  int64_t q0 = *rows_end;
-  q0 = q0 < 0 ? 0 : q0;
-  const size_t esz = dtype_size(out_dtype);
-  for (int64_t q = q0 + blockIdx.x; q < n_routes; q += gridDim.x) {
-    const int64_t row = o_idx != nullptr ? o_idx[q] / o_div : q;
-    if (row < 0 || row >= out_rows) continue;
-    uint8_t* base = static_cast<uint8_t*>(out) + (size_t)(row * out_ld) * esz;
-    for (int64_t b = threadIdx.x; b < width * (int64_t)esz; b += blockDim.x) base[b] = 0;
+// The int32 copy of a selection (int32 or int64 ids, int64 read as its low
+// 32 bits): 4 ids per thread, vector loads and stores when aligned.
+template <typename IdxT>
+__global__ __launch_bounds__(256) void copy_ids_kernel(const IdxT* __restrict__ sel, int64_t n,
+                                                       int32_t* __restrict__ out, int32_t vec) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t n4 = vec ? n / 4 : 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    int4 o;
+    if constexpr (sizeof(IdxT) == 8) {
+      const longlong2 a = reinterpret_cast<const longlong2*>(sel)[2 * i];
+      const longlong2 b = reinterpret_cast<const longlong2*>(sel)[2 * i + 1];
+      o = make_int4((int32_t)a.x, (int32_t)a.y, (int32_t)b.x, (int32_t)b.y);
+    } else {
+      o = reinterpret_cast<const int4*>(sel)[i];
+    }
+    reinterpret_cast<int4*>(out)[i] = o;
   }
+  for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    out[i] = (int32_t)sel[i];
 }
 
-hipError_t launch_zero_unrouted_rows(void* out, int32_t out_dtype, int64_t out_ld, int64_t width, int64_t out_rows,
-                                     const int64_t* o_idx, int64_t o_div, const int64_t* rows_end, int64_t n_routes,
-                                     hipStream_t stream) {
-  if (n_routes <= 0 || width <= 0) return hipSuccess;
-  const int64_t blocks = n_routes < 64 ? n_routes : 64;
-  hipLaunchKernelGGL(zero_unrouted_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, out, out_dtype, out_ld,
-                     width, out_rows, o_idx, o_div, rows_end, n_routes);
+hipError_t launch_copy_ids(const void* sel, bool sel_is_int64, int64_t n, int32_t* out, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const size_t align = sel_is_int64 ? 16 : 16;
+  const int32_t vec = (reinterpret_cast<uintptr_t>(sel) % align) == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+  int64_t blocks = (n / 4 + 255) / 256 + 1;
+  if (blocks > 1024) blocks = 1024;
+  if (sel_is_int64)
+    hipLaunchKernelGGL(copy_ids_kernel<int64_t>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const int64_t*>(sel), n, out, vec);
+  else
+    hipLaunchKernelGGL(copy_ids_kernel<int32_t>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const int32_t*>(sel), n, out, vec);
   return hipGetLastError();
 }
 

@@ -226,6 +226,20 @@ Tensor route_topk_backward(const Tensor& logits, const Tensor& sel, const Tensor
   return out.view(logits.sizes());
 }
 
+// The int32 copy of the ids cvmm_prepare_sel2 takes (cvmm.py:1796), in the
+// ids' shape.
+Tensor copy_ids(const Tensor& sel, int64_t stream) {
+  require_device(sel, "sel");
+  Tensor flat = sel.reshape({-1});
+  if (flat.scalar_type() != at::kInt && flat.scalar_type() != at::kLong) flat = flat.to(at::kLong);
+  flat = flat.contiguous();
+  Tensor out = at::empty(sel.sizes(), opts(flat, at::kInt));
+  check(cvmm_copy_ids(ptr(flat), flat.scalar_type() == at::kLong ? 1 : 0, flat.numel(), tptr<int32_t>(out),
+                      (void*)stream),
+        "cvmm_copy_ids");
+  return out;
+}
+
 Tensor expert_offsets(const Tensor& sorted, int64_t n_experts, int64_t stream) {
   require_device(sorted, "sorted_experts");
   Tensor s = sorted_i32(sorted);
@@ -456,6 +470,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "Host glue of cvmm_codex_amd: one call per CVMM phase into libcvmm_hip.so";
   m.def("sort_routes", &sort_routes, py::arg("raw"), py::arg("n_experts"), py::arg("top_k"), py::arg("stream"));
   m.def("expert_offsets", &expert_offsets, py::arg("sorted"), py::arg("n_experts"), py::arg("stream"));
+  m.def("copy_ids", &copy_ids, py::arg("sel"), py::arg("stream"));
   m.def("route_topk", &route_topk, py::arg("logits"), py::arg("top_k"), py::arg("renormalize"), py::arg("stream"));
   m.def("route_topk_backward", &route_topk_backward, py::arg("logits"), py::arg("sel"), py::arg("grad_weights"),
         py::arg("top_k"), py::arg("renormalize"), py::arg("stream"));

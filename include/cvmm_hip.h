@@ -197,6 +197,11 @@ int cvmm_route_topk_backward(const void* logits, int32_t logits_dtype, int64_t n
                              int32_t n_experts, int64_t top_k, int32_t renormalize, const int64_t* sel,
                              const float* grad_weights, void* grad_logits, int64_t grad_ld, void* stream);
 
+/* out[i] = the int32 value of id i (int64 ids: their low 32 bits), n ids:
+ * the `fsel = sel.flatten().to(torch.int32)` copy cvmm_prepare_sel2 takes
+ * (cvmm.py:1796), which fixes the routing when the selector is prepared. */
+int cvmm_copy_ids(const void* sel, int32_t sel_is_int64, int64_t n, int32_t* out, void* stream);
+
 /* offsets[e] = #{i : sorted_sel[i] <= e}; replaces cvmm_expert_offsets
  * (cvmm.py:1108-1120, kernel cvmm.py:315-335). */
 int cvmm_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_experts, int64_t* offsets,

@@ -92,19 +92,6 @@ def _with_bad_ids(sel, E, seed):
     return s, bad
 
 
-def _poisoned_alloc(monkeypatch):
-    """Make torch's fresh allocations non-zero garbage (NaN bits), so a row
-    that nothing writes cannot pass for a zero row by luck."""
-    real_empty = torch.empty
-
-    def empty(*a, **k):
-        t = real_empty(*a, **k)
-        if t.is_cuda and t.is_floating_point():
-            t.fill_(float("nan"))
-        return t
-    return empty
-
-
 @pytest.mark.parametrize("route_input,amp,D,H", [(False, True, 256, 64), (True, True, 128, 64),
                                                  (False, False, 64, 48), (True, False, 40, 24),
                                                  (False, True, 96, 40)])
@@ -224,3 +211,19 @@ def test_sort_many_experts_through_the_api():
     go = torch.randn(1, 300, 2, H, generator=g).to(torch.bfloat16)
     got = U.run_hip(x, keys, sel, None, go, False, True)
     U.compare(got, U.run_oracle(x, keys, sel, None, go, False, True), 2e-2)
+
+
+@pytest.mark.parametrize("dtype,n,offset", [(torch.int64, 65536, 0), (torch.int64, 1001, 1), (torch.int32, 4099, 0),
+                                            (torch.int32, 77, 3), (torch.int64, 3, 0)])
+def test_copy_ids_is_the_int32_conversion(dtype, n, offset):
+    """cvmm_copy_ids (the ids copy cvmm_prepare_sel2 takes) equals torch's
+    int32 conversion, int64 ids >= 2^31 wrapping as there; aligned (vector)
+    and misaligned (element) views."""
+    from cvmm_codex_amd import _native as N
+    g = torch.Generator().manual_seed(n + offset)
+    base = torch.randint(-(2 ** 40), 2 ** 40, (n + offset,), generator=g, dtype=torch.int64).to(dtype).cuda()
+    sel = base[offset:]
+    out = torch.full((n,), -7, dtype=torch.int32, device="cuda")
+    N.check(N.lib().cvmm_copy_ids(N.ptr(sel), 1 if dtype == torch.int64 else 0, n, N.ptr(out),
+                                  N.stream_of(sel.device)), "cvmm_copy_ids")
+    assert torch.equal(out.cpu(), sel.cpu().to(torch.int32))
