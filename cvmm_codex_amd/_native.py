@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcvmm_hip
 F32, F16, BF16 = 0, 1, 2            # cvmm.py:36-44 dtype ids
 FLAG_ATOMIC_REDUCE = 1
 FLAG_COUNTERS_ZEROED = 2
+FLAG_WORKSPACE_ZEROED = 8
 TUNE_PANEL_TILES_PER_WG = 1
 TUNE_WGRAD_ORDER = 2
 TUNE_GEMM_ORDER = 3
@@ -41,6 +42,7 @@ _SIGS = {
     "cvmm_timing_enable": (ctypes.c_int, [ctypes.c_uint32]),
     "cvmm_tuning_set": (ctypes.c_int, [_I32, _I64]),
     "cvmm_topk_dense": (ctypes.c_int, [_I64, _I32, _I64, _I64, _I64, _I32]),
+    "cvmm_topk_dense_zero_bytes": (_SZ, [_I64, _I32, _I64, _I32]),
     "cvmm_timing_result": (ctypes.c_int, [ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
                                           ctypes.POINTER(ctypes.c_int64)]),
     "cvmm_sort_workspace_bytes": (_SZ, [_I64, _I32]),

@@ -220,9 +220,10 @@ bool use_dense_topk(int32_t op_dtype, int64_t n_tokens, int32_t n_experts, int64
   return t_dense < t_route;
 }
 
-// Workspace of a dense top-k sum: the slotted rows, a weight copy in the
-// [E*K][N] layout (used when the caller's keys are not already that copy)
-// and the inverse route permutation (when not given).
+// Workspace of a dense top-k sum: the slotted rows (first, so that a caller
+// can keep them zero between calls: CVMM_FLAG_WORKSPACE_ZEROED), a weight
+// copy in the [E*K][N] layout (used when the caller's keys are not already
+// that copy) and the inverse route permutation (when not given).
 struct DenseWs {
   void* a;
   void* b;
@@ -246,7 +247,8 @@ int run_dense_topk(const DenseWs& w, const void* src, int32_t src_dtype, int64_t
                    int64_t n_routes, int64_t n_tokens, int64_t top_k, int32_t n_experts, const void* keys,
                    int32_t keys_dtype, int64_t d_in, int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj,
                    bool kn_layout, const void* rw, int32_t rw_dtype, int32_t w_round, int32_t op_dtype, void* out,
-                   int32_t out_dtype, int64_t out_ld, uint32_t gemm_class, const char* what, hipStream_t s) {
+                   int32_t out_dtype, int64_t out_ld, bool a_zeroed, uint32_t gemm_class, const char* what,
+                   hipStream_t s) {
   const int64_t K = kn_layout ? d_in : d_out, N = kn_layout ? d_out : d_in;
   const void* B = keys;
   const bool direct = keys_dtype == op_dtype && k_se == d_in * d_out &&
@@ -266,10 +268,20 @@ int run_dense_topk(const DenseWs& w, const void* src, int32_t src_dtype, int64_t
     if (r) return r;
     inv = w.inv;
   }
-  int r = check_launch(timed_combine(s, [&] {
-    return launch_slot_rows(src, src_dtype, src_ld, src_per_route, sorted_sel, inv, rp, offs + (n_experts - 1),
-                            n_tokens, top_k, n_experts, K, rw, rw_dtype, w_round, op_dtype, w.a, s);
-  }), what);
+  // the slotted rows: into an A the caller keeps zero (and the call leaves
+  // zero again), else into a zero-filled A
+  const size_t a_bytes = (size_t)n_tokens * n_experts * K * dtype_size(op_dtype);
+  if (!a_zeroed) {
+    int r = check_launch(timed_fill(s, [&] { return launch_fill_zero(w.a, a_bytes, s); }), what);
+    if (r) return r;
+  }
+  auto slots = [&](bool clear) {
+    return check_launch(timed_combine(s, [&] {
+      return launch_slot_rows(src, src_dtype, src_ld, src_per_route, sorted_sel, inv, rp, offs + (n_experts - 1),
+                              n_tokens, top_k, n_experts, K, rw, rw_dtype, w_round, clear, op_dtype, w.a, s);
+    }), what);
+  };
+  int r = slots(false);
   if (r) return r;
   int status = 0;
   const hipError_t e = timed(gemm_class, s, [&] {
@@ -279,7 +291,7 @@ int run_dense_topk(const DenseWs& w, const void* src, int32_t src_dtype, int64_t
     if (status != 0) return fail(CVMM_ERR_LAUNCH, "%s: rocblas_gemm_ex failed (status %d)", what, status);
     return check_launch(e, what);
   }
-  return CVMM_OK;
+  return a_zeroed ? slots(true) : CVMM_OK;
 }
 
 // n-tile width of the routed GEMM for output width n (256x64 tiles when narrow).
@@ -330,6 +342,11 @@ int cvmm_tuning_set(int32_t knob, int64_t value) {
 
 int cvmm_topk_dense(int64_t n_tokens, int32_t n_experts, int64_t K, int64_t N, int64_t top_k, int32_t op_dtype) {
   return use_dense_topk(op_dtype, n_tokens, n_experts, K, N, top_k) ? 1 : 0;
+}
+
+size_t cvmm_topk_dense_zero_bytes(int64_t n_tokens, int32_t n_experts, int64_t K, int32_t op_dtype) {
+  if (n_tokens <= 0 || n_experts <= 0 || K <= 0) return 0;
+  return align_up((size_t)n_tokens * n_experts * K * dtype_size(op_dtype), 256);
 }
 
 int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launches) {
@@ -563,12 +580,13 @@ size_t cvmm_fwd_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_i
                                 int32_t out_dtype, int32_t op_dtype, int32_t has_offsets, int32_t weighted,
                                 int32_t flags) {
   Carver c(nullptr);
+  const int64_t k = weighted && out_rows > 0 ? n_routes / out_rows : 0;
+  const bool dense = weighted && !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
+                     use_dense_topk(op_dtype, out_rows, n_experts, d_in, d_out, k);
+  if (dense) carve_dense(c, out_rows, n_experts, d_in, d_out, n_routes, op_dtype);
   if (!has_offsets) c.take((size_t)n_experts * 8);
-  if (weighted) {
-    const int64_t k = out_rows > 0 ? n_routes / out_rows : 0;
-    if (!(flags & CVMM_FLAG_ATOMIC_REDUCE) && use_dense_topk(op_dtype, out_rows, n_experts, d_in, d_out, k)) {
-      carve_dense(c, out_rows, n_experts, d_in, d_out, n_routes, op_dtype);
-    } else if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
+  if (weighted && !dense) {
+    if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
       c.take((size_t)out_rows * d_out * 4);
     } else {
       c.take((size_t)n_routes * d_out * dtype_size(out_dtype));
@@ -612,6 +630,10 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
     return fail(CVMM_ERR_UNSUPPORTED, "cvmm_fwd: fp32 op needs fp32 x and keys");
   hipStream_t s = (hipStream_t)stream;
   Carver c(workspace);
+  const bool dense = weighted && !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
+                     use_dense_topk(op_dtype, out_rows, n_experts, d_in, d_out, reduce_k);
+  DenseWs dws{};
+  if (dense) dws = carve_dense(c, out_rows, n_experts, d_in, d_out, n_routes, op_dtype);
   const int64_t* offs = offsets;
   if (!offs) {
     int64_t* o = (int64_t*)c.take((size_t)n_experts * 8);
@@ -658,13 +680,13 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
     }
     return check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
   }
-  if (!(flags & CVMM_FLAG_ATOMIC_REDUCE) && use_dense_topk(op_dtype, out_rows, n_experts, d_in, d_out, reduce_k)) {
+  if (dense) {
     // high fan-out: expert-slotted x rows (scaled by rnd_out(w)) and one GEMM
     // against the [E*d_in][d_out] weight rows, no route buffer
-    const DenseWs w = carve_dense(c, out_rows, n_experts, d_in, d_out, n_routes, op_dtype);
-    return run_dense_topk(w, x, x_dtype, x_ld, out_index == nullptr, sorted_sel, route_pos, rp, offs, n_routes,
+    return run_dense_topk(dws, x, x_dtype, x_ld, out_index == nullptr, sorted_sel, route_pos, rp, offs, n_routes,
                           out_rows, reduce_k, n_experts, keys, keys_dtype, d_in, d_out, k_se, k_si, k_sj, true, rw,
-                          rw_dtype, out_dtype, op_dtype, out, out_dtype, out_ld, CVMM_KC_GEMM_FWD, "cvmm_fwd(dense)", s);
+                          rw_dtype, out_dtype, op_dtype, out, out_dtype, out_ld,
+                          (flags & CVMM_FLAG_WORKSPACE_ZEROED) != 0, CVMM_KC_GEMM_FWD, "cvmm_fwd(dense)", s);
   }
   if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
     // fused combine: y rounded to the output dtype, times rnd_out(w), fp32 atomics per token row
@@ -747,12 +769,13 @@ size_t cvmm_bwd_x_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d
                                   int64_t top_k, int32_t grad_x_dtype, int32_t op_dtype, int32_t need_grad_rw,
                                   int32_t flags) {
   Carver c(nullptr);
+  const bool dense = reduce_needed(weighted, token_input, top_k) && !weighted &&
+                     !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
+                     use_dense_topk(op_dtype, grad_x_rows, n_experts, d_out, d_in, top_k);
+  if (dense) carve_dense(c, grad_x_rows, n_experts, d_out, d_in, n_routes, op_dtype);
   if (!has_offsets) c.take((size_t)n_experts * 8);
-  if (reduce_needed(weighted, token_input, top_k)) {
-    if (!weighted && !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
-        use_dense_topk(op_dtype, grad_x_rows, n_experts, d_out, d_in, top_k)) {
-      carve_dense(c, grad_x_rows, n_experts, d_out, d_in, n_routes, op_dtype);
-    } else if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
+  if (reduce_needed(weighted, token_input, top_k) && !dense) {
+    if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
       c.take((size_t)grad_x_rows * d_in * 4);
     } else {
       c.take((size_t)n_routes * d_in * dtype_size(weighted ? op_dtype : grad_x_dtype));
@@ -804,6 +827,10 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
 
   hipStream_t s = (hipStream_t)stream;
   Carver c(workspace);
+  const bool dense = reduce && !weighted && !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
+                     use_dense_topk(op_dtype, grad_x_rows, n_experts, d_out, d_in, top_k);
+  DenseWs dws{};
+  if (dense) dws = carve_dense(c, grad_x_rows, n_experts, d_out, d_in, n_routes, op_dtype);
   const int64_t* offs = offsets;
   if (!offs) {
     int64_t* o = (int64_t*)c.take((size_t)n_experts * 8);
@@ -813,14 +840,13 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
   }
   const int64_t* rp = token_input ? out_index : sel_index;
 
-  if (grad_x && reduce && !weighted && !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
-      use_dense_topk(op_dtype, grad_x_rows, n_experts, d_out, d_in, top_k)) {
+  if (dense && grad_x) {
     // high fan-out: expert-slotted dY rows and one GEMM against the
     // [E*d_out][d_in] weight rows, no route buffer
-    const DenseWs w = carve_dense(c, grad_x_rows, n_experts, d_out, d_in, n_routes, op_dtype);
-    return run_dense_topk(w, grad, grad_dtype, grad_ld, true, sorted_sel, route_pos, rp, offs, n_routes, grad_x_rows,
-                          top_k, n_experts, keys, keys_dtype, d_in, d_out, k_se, k_si, k_sj, false, nullptr, 0, 0,
-                          op_dtype, grad_x, grad_x_dtype, grad_x_ld, CVMM_KC_GEMM_BWDX, "cvmm_bwd_x(dense)", s);
+    return run_dense_topk(dws, grad, grad_dtype, grad_ld, true, sorted_sel, route_pos, rp, offs, n_routes,
+                          grad_x_rows, top_k, n_experts, keys, keys_dtype, d_in, d_out, k_se, k_si, k_sj, false,
+                          nullptr, 0, 0, op_dtype, grad_x, grad_x_dtype, grad_x_ld,
+                          (flags & CVMM_FLAG_WORKSPACE_ZEROED) != 0, CVMM_KC_GEMM_BWDX, "cvmm_bwd_x(dense)", s);
   }
 
   // grad @ keys[e]^T: K = d_out, N = d_in, B[k][n] = keys[e][n][k]

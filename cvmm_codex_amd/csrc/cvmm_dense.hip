@@ -27,11 +27,14 @@ namespace cvmm {
 
 constexpr int kSlotWaves = 4;
 
-// One wave per token row of A.  Lane j < top_k finds the expert of route
-// (t, j) through the inverse permutation (its sorted position q = inv[r],
-// valid when q < *rows_end and rp[q] == r); a per-wave LDS table maps each
-// expert to its first route (bit 30 marks an expert the token picked twice),
-// then the wave writes the whole row, 8 elements (16 bytes) per lane and step.
+// One wave per token row of A; only the token's own slots are written (the
+// caller provides A zero elsewhere).  Lane j < top_k finds the expert of
+// route (t, j) through the inverse permutation (its sorted position q =
+// inv[r], valid when q < *rows_end and rp[q] == r); a per-wave LDS table maps
+// each expert to its first route (bit 30 marks an expert the token picked
+// twice: that slot gets the sum of both rows).  The wave then writes the
+// slots, K/8 16-byte pieces per route: the rows' values, or zeros when
+// `clear` (restoring an all-zero A after the GEMM).
 constexpr int32_t kSlotNone = 0xffff;
 template <typename OpT>
 __global__ __launch_bounds__(64 * kSlotWaves) void slot_rows_kernel(const void* __restrict__ src, int32_t src_dtype,
@@ -42,7 +45,7 @@ __global__ __launch_bounds__(64 * kSlotWaves) void slot_rows_kernel(const void* 
                                                                    const int64_t* __restrict__ rows_end,
                                                                    int64_t n_tokens, int32_t top_k, int32_t n_experts,
                                                                    int64_t K, const void* __restrict__ w,
-                                                                   int32_t w_dtype, int32_t w_round,
+                                                                   int32_t w_dtype, int32_t w_round, int32_t clear,
                                                                    OpT* __restrict__ A) {
   constexpr int32_t kOp = DTypeOf<OpT>::value;
   extern __shared__ int32_t lds[];  // per wave: n_experts slots, 64 ids, 64 scales
@@ -63,7 +66,7 @@ __global__ __launch_bounds__(64 * kSlotWaves) void slot_rows_kernel(const void* 
       const int32_t id = sorted_sel[q];
       if (id >= 0 && id < n_experts) e = id;
     }
-    if (w != nullptr) sc = round_to(load_as_f32(w, w_dtype, r), w_round);
+    if (w != nullptr && !clear) sc = round_to(load_as_f32(w, w_dtype, r), w_round);
   }
   for (int32_t i = lane; i < n_experts; i += 64) slot[i] = kSlotNone;
   ids[lane] = e;
@@ -75,17 +78,17 @@ __global__ __launch_bounds__(64 * kSlotWaves) void slot_rows_kernel(const void* 
   __syncthreads();
   if (!active) return;
 
-  const int64_t row_len = (int64_t)n_experts * K;
-  const int64_t chunks = row_len / 8;
-  OpT* out_row = A + t * row_len;
+  const int32_t cpr = (int32_t)(K / 8);  // 16-byte pieces per slot
+  OpT* out_row = A + t * (int64_t)n_experts * K;
   const bool vec_src = src_dtype == kOp && (src_ld % 8) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0;
-  for (int64_t c = lane; c < chunks; c += 64) {
-    const int64_t k0 = (c * 8) % K;
-    const int32_t ex = (int32_t)((c * 8) / K);
+  for (int32_t it = lane; it < top_k * cpr; it += 64) {
+    const int32_t j0 = it / cpr, c = it - j0 * cpr;
+    const int32_t ex = ids[j0];
+    if (ex < 0) continue;
     const int32_t sl = slot[ex];
-    const int32_t j0 = sl & 0xffff;
+    if ((sl & 0xffff) != j0) continue;  // a later route of a repeated expert: summed by the first
     Chunk16 ch;
-    if (j0 >= 64) {
+    if (clear) {
       ch.u = make_uint4(0, 0, 0, 0);
     } else {
       const bool dup = (sl >> 30) & 1;
@@ -96,7 +99,7 @@ __global__ __launch_bounds__(64 * kSlotWaves) void slot_rows_kernel(const void* 
         if (j != j0 && ids[j] != ex) continue;
         const int64_t row = src_per_route ? t * top_k + j : t;
         const float sj = scale[j];
-        const int64_t off = row * src_ld + k0;
+        const int64_t off = row * src_ld + (int64_t)c * 8;
         float v[8];
         if (vec_src) {
           Chunk16 in;
@@ -114,14 +117,15 @@ __global__ __launch_bounds__(64 * kSlotWaves) void slot_rows_kernel(const void* 
 #pragma unroll
       for (int i = 0; i < 8; ++i) reinterpret_cast<OpT*>(&ch)[i] = from_f32<OpT>(acc[i]);
     }
-    *reinterpret_cast<uint4*>(out_row + c * 8) = ch.u;
+    *reinterpret_cast<uint4*>(out_row + (int64_t)ex * K + (int64_t)c * 8) = ch.u;
   }
 }
 
 hipError_t launch_slot_rows(const void* src, int32_t src_dtype, int64_t src_ld, bool src_per_route,
                             const int32_t* sorted_sel, const int32_t* inv, const int64_t* rp, const int64_t* rows_end,
                             int64_t n_tokens, int64_t top_k, int32_t n_experts, int64_t K, const void* w,
-                            int32_t w_dtype, int32_t w_round, int32_t op_dtype, void* A, hipStream_t stream) {
+                            int32_t w_dtype, int32_t w_round, bool clear, int32_t op_dtype, void* A,
+                            hipStream_t stream) {
   const size_t lds = (size_t)kSlotWaves * (n_experts + 128) * sizeof(int32_t);
   const unsigned grid = (unsigned)((n_tokens + kSlotWaves - 1) / kSlotWaves);
   if (lds > 65536) {  // above 3968 experts: ask for the larger dynamic LDS
@@ -133,11 +137,11 @@ hipError_t launch_slot_rows(const void* src, int32_t src_dtype, int64_t src_ld, 
   if (op_dtype == kBF16)
     hipLaunchKernelGGL(slot_rows_kernel<bf16_t>, dim3(grid), dim3(64 * kSlotWaves), lds, stream, src, src_dtype, src_ld,
                        src_per_route ? 1 : 0, sorted_sel, inv, rp, rows_end, n_tokens, (int32_t)top_k, n_experts, K, w,
-                       w_dtype, w_round, (bf16_t*)A);
+                       w_dtype, w_round, clear ? 1 : 0, (bf16_t*)A);
   else
     hipLaunchKernelGGL(slot_rows_kernel<f16_t>, dim3(grid), dim3(64 * kSlotWaves), lds, stream, src, src_dtype, src_ld,
                        src_per_route ? 1 : 0, sorted_sel, inv, rp, rows_end, n_tokens, (int32_t)top_k, n_experts, K, w,
-                       w_dtype, w_round, (f16_t*)A);
+                       w_dtype, w_round, clear ? 1 : 0, (f16_t*)A);
   return hipGetLastError();
 }
 

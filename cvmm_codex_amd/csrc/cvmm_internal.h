@@ -240,15 +240,17 @@ hipError_t launch_copy_ids(const void* sel, bool sel_is_int64, int64_t n, int32_
 // ---------------------------------------------------------------------------
 // dense top-k sums (cvmm_dense.hip): expert-slotted rows + one library GEMM
 // ---------------------------------------------------------------------------
-// A[t][e*K + k] = sum over the routes j of token t with expert e of
-// rnd_op(s_tj * src[row][k]), zero elsewhere; row = t*top_k + j (src per
-// route) or t; s_tj = rnd(w[t*top_k + j], w_round), or 1 when w == NULL.  The
-// expert of route r is sorted_sel[inv[r]] when inv[r] < *rows_end and
-// rp[inv[r]] == r.  top_k <= 64, K % 8 == 0, 16-bit op.
+// The slots of A used by each token: A[t][e*K + k] = sum over the routes j
+// of token t with expert e of rnd_op(s_tj * src[row][k]), row = t*top_k + j
+// (src per route) or t, s_tj = rnd(w[t*top_k + j], w_round) or 1 when
+// w == NULL; zeros instead when `clear`.  Other slots are not written (A is
+// zero there).  The expert of route r is sorted_sel[inv[r]] when inv[r] <
+// *rows_end and rp[inv[r]] == r.  top_k <= 64, K % 8 == 0, 16-bit op.
 hipError_t launch_slot_rows(const void* src, int32_t src_dtype, int64_t src_ld, bool src_per_route,
                             const int32_t* sorted_sel, const int32_t* inv, const int64_t* rp, const int64_t* rows_end,
                             int64_t n_tokens, int64_t top_k, int32_t n_experts, int64_t K, const void* w,
-                            int32_t w_dtype, int32_t w_round, int32_t op_dtype, void* A, hipStream_t stream);
+                            int32_t w_dtype, int32_t w_round, bool clear, int32_t op_dtype, void* A,
+                            hipStream_t stream);
 // out[t][n] = sum_c A[t][c] B[c][n] (A [T][C], B [C][N] row-major, op dtype;
 // fp32 accumulation; rocBLAS, atomics off).  On a rocBLAS error returns
 // hipErrorUnknown with its status in *status.

@@ -47,6 +47,9 @@ extern "C" {
                                      instead of a route-ordered buffer + ordered row sum */
 #define CVMM_FLAG_COUNTERS_ZEROED 2 /* cvmm_bwd_w: the counter region at the start of the
                                        workspace is already zero (see cvmm_bwd_w) */
+#define CVMM_FLAG_WORKSPACE_ZEROED 8 /* cvmm_fwd / cvmm_bwd_x taking a dense top-k sum: the first
+                                        cvmm_topk_dense_zero_bytes() of the workspace are zero,
+                                        and the call leaves them zero (see cvmm_topk_dense) */
 
 /* kernel classes for the timing hooks */
 #define CVMM_KC_SORT 1        /* histogram + scan + scatter of cvmm_sort_routes */
@@ -117,8 +120,15 @@ int cvmm_tuning_set(int32_t knob, int64_t value);
  *     fastest as the op-dtype [E][d_in][d_out] copy (unit stride on d_out);
  *   cvmm_bwd_x, unweighted token input, top_k > 1: K = d_out, N = d_in; the
  *     weights as the op-dtype [E][d_out][d_in] copy (unit stride on d_in).
- * Other keys are cast into the workspace.  Returns 1 or 0. */
+ * Other keys are cast into the workspace.  Returns 1 or 0.
+ * The slotted rows take the first cvmm_topk_dense_zero_bytes() of the
+ * call's workspace.  The call zero-fills them first, unless the caller
+ * passes CVMM_FLAG_WORKSPACE_ZEROED: then they must be zero on entry, only
+ * the tokens' own slots are written, and the call clears those after the GEMM
+ * (a caller that keeps its workspace skips rewriting the zeros: at
+ * SwitchHead size 67 MB of slots instead of 268 MB of rows, twice). */
 int cvmm_topk_dense(int64_t n_tokens, int32_t n_experts, int64_t K, int64_t N, int64_t top_k, int32_t op_dtype);
+size_t cvmm_topk_dense_zero_bytes(int64_t n_tokens, int32_t n_experts, int64_t K, int32_t op_dtype);
 
 /* ------------------------------------------------------------------------ */
 /* Selector preparation                                                      */

@@ -175,3 +175,47 @@ def test_dense_topk_keys_cast_into_the_workspace(dense):
     y = C._forward(x2.cuda(), s2.sel_index, s2.sel, keys2.cuda(), s2.out_index, w2.cuda(), torch.bfloat16)
     exp2 = U.run_oracle(x2, keys2, sel2, w2, go2, True, True)
     assert U.norm_rel(U.to_np(y), exp2["out"]) <= 2e-2
+
+
+def test_dense_workspace_zeroed_flag(dense):
+    """Through the C ABI: without CVMM_FLAG_WORKSPACE_ZEROED the call fills
+    the slotted rows itself (the workspace may hold anything); with it the
+    call writes only the tokens' slots into a zero workspace and leaves that
+    region zero again.  All three calls give the same bits."""
+    x, keys, sel, _, go = _case(15, 2, 160, 64, 96, 16, 4, False, False)
+    E, D, H = keys.shape
+    s = C.cvmm_prepare_sel2(sel.cuda())
+    C.create_kernels()
+    s._resolve(E)
+    lib = N.lib()
+    st = N.stream_of(torch.device("cuda"))
+    kt = keys.cuda().transpose(1, 2).contiguous().to(torch.bfloat16)    # [E, d_out, d_in]
+    kv = kt.transpose(1, 2)                                              # logical [E, d_in, d_out]
+    g = go.cuda().reshape(-1, H).contiguous()
+    R, T = sel.numel(), sel.numel() // 4
+    offs = C._offsets_for(s.sel, E)
+    rpos = s.out_index._cvmm_route_pos
+    ws_b = lib.cvmm_bwd_x_workspace_bytes(R, E, D, H, T, 1, 0, 1, 4, N.BF16, N.BF16, 0, 0)
+    zb = lib.cvmm_topk_dense_zero_bytes(T, E, H, N.BF16)
+    assert 0 < zb <= ws_b
+
+    def call(ws, flags):
+        gx = torch.empty(T, D, dtype=torch.bfloat16, device="cuda")
+        N.check(lib.cvmm_bwd_x(N.ptr(g), N.BF16, g.shape[0], g.stride(0), N.ptr(kv), N.BF16, E, D, H,
+                               *kv.stride(), N.ptr(s.sel), N.ptr(s.sel_index), N.ptr(s.out_index), R, N.ptr(offs),
+                               N.ptr(rpos), None, 0, 4, None, 0, 0, 0, N.BF16, N.ptr(gx), N.BF16, T, D, None, 0,
+                               flags, N.ptr(ws), ws_b, st), "cvmm_bwd_x")
+        return gx
+
+    junk = torch.full((ws_b,), 0x5A, dtype=torch.uint8, device="cuda")
+    a = call(junk, 0)
+    ws = torch.zeros(ws_b, dtype=torch.uint8, device="cuda")
+    b = call(ws, N.FLAG_WORKSPACE_ZEROED)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(ws[:zb]) == 0
+    c = call(ws, N.FLAG_WORKSPACE_ZEROED)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(ws[:zb]) == 0
+    assert torch.equal(a, b) and torch.equal(b, c)
+    exp = U.run_oracle(x, keys, sel, None, go, False, True)
+    assert U.norm_rel(U.to_np(a), exp["x_grad"].reshape(T, D)) <= 2e-2
