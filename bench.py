@@ -507,6 +507,23 @@ def kernel_role(name: str):
     return None
 
 
+def kernel_class(name: str):
+    """kernel_role for the routed GEMMs and the weight gradient; the other
+    kernels of a step by name: the dense top-k GEMM (rocBLAS), its slot
+    writes, the combine, the sort and the weight cast."""
+    role = kernel_role(name)
+    if role is not None:
+        return role
+    base = name.split("<")[0].split("(")[0].split()[-1] if name else ""
+    if base.startswith("Cijk_") or "rocblas" in base:
+        return "dense_topk"
+    for key, cls in (("slot_rows", "slots"), ("combine_rows", "combine"), ("sort_", "sort"), ("cast_keys", "cast"),
+                     ("copy_ids", "sort"), ("sum_partials", "dgate"), ("fill_zero", "fill"), ("gelu", "gelu")):
+        if key in base:
+            return cls
+    return None
+
+
 def _short(name: str, width: int = 90) -> str:
     n = name.replace("__hip_bfloat16", "bf16").replace("_Float16", "f16").replace("cvmm::", "")
     n = n.split("(")[0] if n.startswith("void ") or "(" in n else n
@@ -582,7 +599,7 @@ def summarize(dirpath: str, copy_dir=None) -> str:
             avg_us[n] = float(r["AverageNs"]) / 1e3
             if float(r["Percentage"]) < 0.5:
                 continue
-            lines.append(f"| `{_short(n)}` | {kernel_role(n) or ''} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} "
+            lines.append(f"| `{_short(n)}` | {kernel_class(n) or ''} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} "
                          f"| {float(r['Percentage']):.1f} |")
         lines.append("")
     cnt = {}
@@ -594,7 +611,7 @@ def summarize(dirpath: str, copy_dir=None) -> str:
     if W_name in W.PROJECTIONS:
         proj = W.PROJECTIONS[W_name]()
     if cnt:
-        lines += ["## Counters per dispatch of the GEMM kernels (averages over the counter runs' dispatches)", "",
+        lines += ["## Counters per dispatch (averages over the counter runs' dispatches)", "",
                   "FETCH/WRITE: `FETCH_SIZE` / `WRITE_SIZE` (KiB) x 1024 x the copy factor "
                   f"(fetch {fac.get('FETCH_SIZE', float('nan')):.3f}, write {fac.get('WRITE_SIZE', float('nan')):.3f}: "
                   "bytes a 256 MiB device copy moves / what the counter reads for it).  MFMA busy = "
@@ -605,9 +622,12 @@ def summarize(dirpath: str, copy_dir=None) -> str:
                   "| kernel | class | trace us | FETCH MB | WRITE MB | alg. MB | traffic / alg. | L2 hit % | "
                   "MFMA busy % | MFMA GFLOP (alg.) | LDS confl. cyc/inst | LDS confl. % |",
                   "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
-        for k, d in cnt.items():
-            role = kernel_role(k)
-            if role is None:
+        def order(item):
+            c = kernel_class(item[0])
+            return (c not in PHASE, -avg_us.get(item[0], 0.0))
+        for k, d in sorted(cnt.items(), key=order):
+            role = kernel_class(k)
+            if role is None or avg_us.get(k, 0.0) < 1.0:
                 continue
             mean = lambda c: (sum(d[c]) / len(d[c])) if c in d and d[c] else float("nan")
             fetch = mean("FETCH_SIZE") * 1024 * fac.get("FETCH_SIZE", float("nan")) / 1e6
@@ -624,29 +644,51 @@ def summarize(dirpath: str, copy_dir=None) -> str:
             per_inst = conf / mean("SQ_INSTS_LDS") if mean("SQ_INSTS_LDS") else float("nan")
             conf_pct = conf / (grbm * CU_NUM) * 100
             us = avg_us.get(k, float("nan"))
-            lines.append(f"| `{_short(k, 70)}` | {role} | {us:.1f} | {fetch:.1f} | {write:.1f} | {alg:.1f} | "
-                         f"{(fetch + write) / alg:.2f} | {hit:.1f} | {busy:.1f} | {gflop:.2f} ({alg_gf:.2f}) | "
-                         f"{per_inst:.3f} | {conf_pct:.2f} |")
+            ratio = f"{(fetch + write) / alg:.2f}" if alg == alg else "-"
+            alg_s = f"{alg:.1f}" if alg == alg else "-"
+            gf = f"{gflop:.2f} ({alg_gf:.2f})" if alg_gf == alg_gf else f"{gflop:.2f}"
+            lines.append(f"| `{_short(k, 70)}` | {role} | {us:.1f} | {fetch:.1f} | {write:.1f} | {alg_s} | "
+                         f"{ratio} | {hit:.1f} | {busy:.1f} | {gf} | {per_inst:.3f} | {conf_pct:.2f} |")
         lines.append("")
     return "\n".join(lines)
 
 
-def traffic_json(dirpath: str, copy_dir: str, kernel_class: str):
+def traffic_json(dirpath: str, copy_dir: str, cls: str):
     """FETCH_SIZE + WRITE_SIZE bytes per launch of the class's kernel (the
-    `traffic` field of bench.py's roofline), from a profile.sh run."""
+    `traffic` field of bench.py's roofline), from a profile.sh run.  A GEMM
+    class that ran as the dense top-k path counts the dense GEMM plus its two
+    slot passes (write, clear)."""
     cnt = {}
     for pas in ("fetch", "write"):
         for k, d in _counters(os.path.join(dirpath, pas)).items():
             cnt.setdefault(k, {}).update(d)
     fac = _copy_factors(copy_dir)
+
+    def per_launch(d):
+        f = sum(d["FETCH_SIZE"]) / len(d["FETCH_SIZE"]) * 1024 * fac["FETCH_SIZE"]
+        w = sum(d["WRITE_SIZE"]) / len(d["WRITE_SIZE"]) * 1024 * fac["WRITE_SIZE"]
+        return f, w
+
+    base = {"kernel": cls, "workload": os.path.basename(os.path.normpath(dirpath)),
+            "copy_factor_fetch": fac["FETCH_SIZE"], "copy_factor_write": fac["WRITE_SIZE"]}
     for k, d in cnt.items():
-        if kernel_role(k) == kernel_class and "FETCH_SIZE" in d and "WRITE_SIZE" in d:
-            f = sum(d["FETCH_SIZE"]) / len(d["FETCH_SIZE"]) * 1024 * fac["FETCH_SIZE"]
-            w = sum(d["WRITE_SIZE"]) / len(d["WRITE_SIZE"]) * 1024 * fac["WRITE_SIZE"]
-            return {"kernel": kernel_class, "kernel_name": k, "workload": os.path.basename(os.path.normpath(dirpath)),
-                    "bytes_per_launch": int(f + w), "fetch_bytes": int(f), "write_bytes": int(w),
-                    "copy_factor_fetch": fac["FETCH_SIZE"], "copy_factor_write": fac["WRITE_SIZE"]}
+        if kernel_role(k) == cls and "FETCH_SIZE" in d and "WRITE_SIZE" in d:
+            f, w = per_launch(d)
+            return {**base, "kernel_name": k, "bytes_per_launch": int(f + w), "fetch_bytes": int(f),
+                    "write_bytes": int(w)}
+    if cls in ("gemm_fwd", "gemm_bwd_x"):
+        dense = [(k, d) for k, d in cnt.items() if kernel_class(k) in ("dense_topk", "slots")
+                 and "FETCH_SIZE" in d and "WRITE_SIZE" in d]
+        if any(kernel_class(k) == "dense_topk" for k, _ in dense):
+            f = w = 0.0
+            for k, d in dense:
+                n = 2 if kernel_class(k) == "slots" else 1
+                df, dw = per_launch(d)
+                f, w = f + n * df, w + n * dw
+            return {**base, "kernel_name": "dense top-k: " + ", ".join(k for k, _ in dense),
+                    "bytes_per_launch": int(f + w), "fetch_bytes": int(f), "write_bytes": int(w)}
     return None
+
 
 
 def main():
