@@ -117,9 +117,11 @@ std::map<std::pair<int, int64_t>, Scratch> g_sort_ws, g_wgrad_ws, g_dense_ws;
 
 // The workspace of a call that takes a dense top-k sum (cvmm_topk_dense):
 // kept per (device, stream) with its slotted-row region zero between calls
-// (zeroed once, when allocated; every call leaves it zero), so the call only
-// writes the tokens' own slots.  `run` makes the call with the flag to pass;
-// a failed call may leave slots written, so the region is re-zeroed next time.
+// (zeroed when it is not known to be; every call leaves it zero), so the call
+// only writes the tokens' own slots.  A call writes the bytes after its own
+// region, so afterwards exactly that region is known zero; a failed call may
+// leave slots written, so nothing is.  `run` makes the call with the flag to
+// pass.
 template <typename F>
 void with_dense_workspace(const Tensor& like, int64_t stream, size_t bytes, size_t zero_bytes, F&& run) {
   Tensor buf;
@@ -146,6 +148,8 @@ void with_dense_workspace(const Tensor& like, int64_t stream, size_t bytes, size
     sp->clean = 0;
     throw;
   }
+  std::lock_guard<std::mutex> lk(g_mu);
+  sp->clean = zero_bytes;
 }
 
 Tensor sort_workspace(const Tensor& like, int64_t stream, size_t bytes) {

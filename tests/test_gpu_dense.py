@@ -219,3 +219,22 @@ def test_dense_workspace_zeroed_flag(dense):
     assert torch.equal(a, b) and torch.equal(b, c)
     exp = U.run_oracle(x, keys, sel, None, go, False, True)
     assert U.norm_rel(U.to_np(a), exp["x_grad"].reshape(T, D)) <= 2e-2
+
+
+def test_dense_workspace_rezeroed_after_a_call_with_a_smaller_region(dense):
+    """The host glue keeps one workspace per stream with the slotted-row
+    region zero between calls.  A call writes the bytes after its own region
+    (here the fp32 keys cast into the workspace), so a later call with a
+    larger region must not take those bytes for zero: call A (32 tokens,
+    2048-wide weights cast behind a 64 KiB region) and then call B (1024
+    tokens, a 2 MiB region inside A's buffer) both match the oracle."""
+    outs = []
+    for seed, T, H in ((21, 16, 2048), (22, 512, 64)):
+        x, keys, sel, w, go = _case(seed, 2, T, 64, H, 16, 4, True, True)
+        s = C.cvmm_prepare_sel2(sel.cuda(), w.cuda(), route_input=True)
+        s._resolve(16)
+        y = C._forward(x.cuda(), s.sel_index, s.sel, keys.cuda(), s.out_index, w.cuda(), torch.bfloat16)
+        torch.cuda.synchronize()
+        exp = U.run_oracle(x, keys, sel, w, go, True, True, need_w=False)
+        outs.append(U.norm_rel(U.to_np(y), exp["out"]))
+    assert max(outs) <= 2e-2, outs
