@@ -322,6 +322,11 @@ int cvmm_tuning_set(int32_t knob, int64_t value) {
     g_gemm_order.store((int32_t)value);
     return CVMM_OK;
   }
+  if (knob == CVMM_TUNE_SORT_CHUNK) {
+    if (value < 0 || value > (1 << 24)) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: sort chunk out of range");
+    set_sort_chunk(value);
+    return CVMM_OK;
+  }
   if (knob == CVMM_TUNE_DENSE_TOPK) {
     if (value < 0 || value > 2) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: dense top-k choice must be 0, 1 or 2");
     g_dense_topk.store((int32_t)value);
@@ -558,6 +563,7 @@ int cvmm_sort_routes_cast_keys(const void* sel, int32_t sel_is_int64, int64_t n_
   const bool fuse = n_routes > 0 && n_routes <= 0x7fffffffll && n_experts > 0 && n_experts <= 32767 && top_k > 0 &&
                     sel && sorted_sel && perm && offsets && keys && (keys_t || keys_n) && d_in > 0 && d_out > 0 &&
                     n_experts <= 65535 && (int64_t)n_experts * (d_in / 64) * (d_out / 64) < 0x7f000000ll &&
+                    sort_cast_fusable(n_experts) &&
                     cast_vec_ok(keys, keys_dtype, k_se, k_si, k_sj, d_in, d_out, out_dtype, keys_t, keys_n) &&
                     workspace != nullptr && workspace_bytes >= sort_workspace_bytes(n_routes, n_experts);
   if (!fuse) {

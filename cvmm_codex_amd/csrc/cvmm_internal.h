@@ -171,6 +171,10 @@ int32_t wgrad_auto_tile(int64_t M, int64_t N, int64_t grid_chunks);
 // ---------------------------------------------------------------------------
 size_t sort_workspace_bytes(int64_t n_routes, int32_t n_experts);
 int64_t sort_chunk_size(int64_t n_routes, int32_t n_experts);
+// routes per chunk of the sort (0: the built-in choice)
+void set_sort_chunk(int64_t routes);
+// whether the selector scatter and the weight cast fit one launch
+bool sort_cast_fusable(int32_t n_experts);
 // bytes of a chunks x (E + 1) int32 count matrix, rounded up to 256
 size_t sort_counts_bytes(int64_t n_chunks, int32_t n_experts);
 // A weight cast to run in the sort's scatter launch (vectorised cast only).

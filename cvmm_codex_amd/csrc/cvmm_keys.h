@@ -22,9 +22,14 @@ struct CastArgs {
 // pieces of the same rows and, through a padded fp32 LDS tile, to kt as
 // 16-byte pieces of its rows (8 consecutive d_in values per thread).  RNE,
 // the rounding of the reference's in-register cast (cvmm.py:198-204).
+// LDS of one cast block: the fp32 tile, 64 rows of up to 128 columns plus
+// one padding column (the launches that cast provide it).
+constexpr int kCastTileFloats = 64 * 129;
+
 template <typename OutT>
-__device__ __forceinline__ void cast_tile_vec(const CastArgs<OutT>& a, int64_t e, int64_t ti, int64_t tj) {
-  __shared__ float tile[64][65];
+__device__ __forceinline__ void cast_tile_vec(const CastArgs<OutT>& a, int64_t e, int64_t ti, int64_t tj,
+                                              float* lds) {
+  float(*tile)[65] = reinterpret_cast<float(*)[65]>(lds);
   const int64_t i0 = ti * 64, j0 = tj * 64;
   const int t = threadIdx.x;
   const int c4 = (t & 15) * 4;
@@ -66,8 +71,9 @@ __device__ __forceinline__ void cast_tile_vec(const CastArgs<OutT>& a, int64_t e
 // reads (lane l: d_in 8 * (l % 8) + k, d_out l / 8) hit 64 distinct banks
 // with the 129-float row pitch; the row writes conflict two ways.
 template <typename OutT>
-__device__ __forceinline__ void cast_tile_vec128(const CastArgs<OutT>& a, int64_t e, int64_t ti, int64_t tj) {
-  __shared__ float tile[64][129];
+__device__ __forceinline__ void cast_tile_vec128(const CastArgs<OutT>& a, int64_t e, int64_t ti, int64_t tj,
+                                                 float* lds) {
+  float(*tile)[129] = reinterpret_cast<float(*)[129]>(lds);
   const int64_t i0 = ti * 64, j0 = tj * 128;
   const int t = threadIdx.x;
   const int c8 = (t & 15) * 8;
@@ -112,14 +118,14 @@ __host__ __device__ inline int64_t cast_blocks(int64_t n_experts, int64_t d_in, 
   return n_experts * (d_in / 64) * (d_out / cast_block_cols(d_out));
 }
 template <typename OutT>
-__device__ __forceinline__ void cast_block(const CastArgs<OutT>& a, int64_t t) {
+__device__ __forceinline__ void cast_block(const CastArgs<OutT>& a, int64_t t, float* lds) {
   const int64_t ti = a.d_in / 64;
   if (a.d_out % 128 == 0) {
     const int64_t tj = a.d_out / 128;
-    cast_tile_vec128(a, t / (ti * tj), (t / tj) % ti, t % tj);
+    cast_tile_vec128(a, t / (ti * tj), (t / tj) % ti, t % tj, lds);
   } else {
     const int64_t tj = a.d_out / 64;
-    cast_tile_vec(a, t / (ti * tj), (t / tj) % ti, t % tj);
+    cast_tile_vec(a, t / (ti * tj), (t / tj) % ti, t % tj, lds);
   }
 }
 

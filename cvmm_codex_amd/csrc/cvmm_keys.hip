@@ -40,7 +40,8 @@ __global__ __launch_bounds__(256) void cast_keys_kernel(const void* __restrict__
 // Vectorised fast path (see cast_block): one workgroup per block.
 template <typename OutT>
 __global__ __launch_bounds__(256) void cast_keys_vec_kernel(const CastArgs<OutT> a) {
-  cast_block(a, (int64_t)blockIdx.x);
+  __shared__ float tile[kCastTileFloats];
+  cast_block(a, (int64_t)blockIdx.x, tile);
 }
 
 hipError_t launch_cast_keys(const void* keys, int32_t keys_dtype, int64_t se, int64_t si, int64_t sj,

@@ -17,6 +17,8 @@
 //                  experts keep route order).
 // The chunk size keeps (E + 1) * n_chunks, the counts each workgroup reads,
 // at most 64K.
+#include <atomic>
+
 #include "cvmm_common.h"
 #include "cvmm_internal.h"
 #include "cvmm_keys.h"
@@ -128,9 +130,99 @@ __device__ void scatter_chunk(const IdxT* __restrict__ sel, int64_t n_routes, in
   }
 }
 
+// The chunks that scatter through LDS (scatter_chunk_local): up to this many
+// buckets (4 x (E + 1) positions in the dynamic LDS) and routes (a key and a
+// route offset each in the launch's 33 KB tile buffer), in selections of at
+// least this many routes.  Measured against the direct scatter (same box,
+// sort + cast per step): switch_v (524288 routes, 256 experts) 40.4 -> 33.2
+// us, switch_o 35.0 -> 31.8 us, ff_up (65536 routes, 64 chunks: the
+// scatter's latency, not its stores, is the limit) 16.1 -> 17.0 us.
+constexpr int32_t kSortLocalBuckets = 2048;
+constexpr int64_t kSortLocalChunk = kCastTileFloats / 2;
+constexpr int64_t kSortLocalMinRoutes = 1 << 18;
+
+// The same stable order through LDS: the rounds place each route at its
+// local position (the chunk's routes bucket by bucket, equal buckets in
+// route order) with its key and offset, writing route_pos on the way (route
+// order, coalesced); then the threads walk the local positions and write
+// sorted_sel, perm and token_index: each bucket's run of the chunk goes to
+// consecutive output positions, where the direct scatter stores one 4- or
+// 8-byte value per route and output at a scattered position (a partial line
+// written back per store).  lbase = the chunk's first local position of each
+// bucket, lpos its running copy, gpos the chunk's first output position.
+template <typename IdxT>
+__device__ void scatter_chunk_local(const IdxT* __restrict__ sel, int64_t n_routes, int32_t n_experts, int64_t chunk,
+                                    int32_t n_bits, int64_t top_k, const int32_t* gpos, int32_t* lpos,
+                                    const int32_t* lbase, int32_t* l_key, int32_t* l_route,
+                                    int32_t* __restrict__ sorted_sel, int64_t* __restrict__ perm,
+                                    int64_t* __restrict__ token_index, int32_t* __restrict__ route_pos, int64_t b,
+                                    const IdxT (&pre)[kSortPrefetch]) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = lane_id();
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int64_t lo = b * chunk;
+  const int64_t hi = min(lo + chunk, n_routes);
+  int round = 0;
+  for (int64_t base = lo; base < hi; base += kSortThreads, ++round) {
+    const int64_t i = base + threadIdx.x;
+    const bool valid = i < hi;
+    IdxT key = (IdxT)0;
+    if (round < kSortPrefetch) {
+#pragma unroll
+      for (int r = 0; r < kSortPrefetch; ++r)
+        if (r == round) key = pre[r];
+    } else if (valid) {
+      key = sel[i];
+    }
+    const int32_t bucket = valid ? bucket_of(key, n_experts) : 0;
+    uint64_t peers = __ballot(valid);
+    for (int bit = 0; bit < n_bits; ++bit) {
+      const bool set = (bucket >> bit) & 1;
+      const uint64_t bb = __ballot(set);
+      peers &= set ? bb : ~bb;
+    }
+    const int rank = __popcll(peers & lt_mask);
+    const int cnt = __popcll(peers);
+    for (int w = 0; w < kSortThreads / 64; ++w) {
+      if (wave == w && valid) {
+        const int32_t p0 = lpos[bucket];
+        const int32_t lp = p0 + rank;
+        if (rank == 0) lpos[bucket] = p0 + cnt;
+        l_key[lp] = (int32_t)key;
+        l_route[lp] = (int32_t)(i - lo);
+        if (route_pos != nullptr) route_pos[i] = gpos[bucket] + (lp - lbase[bucket]);
+      }
+      __syncthreads();
+    }
+  }
+  const int32_t n = (int32_t)(hi - lo);
+  for (int32_t lp = threadIdx.x; lp < n; lp += kSortThreads) {
+    const int32_t key = l_key[lp];
+    const int32_t e = bucket_of(key, n_experts);
+    const int64_t p = (int64_t)gpos[e] + (lp - lbase[e]);
+    const int64_t i = lo + l_route[lp];
+    sorted_sel[p] = key;
+    perm[p] = i;
+    if (token_index != nullptr) token_index[p] = i / top_k;
+  }
+}
+
+// Dynamic LDS of a scatter workgroup: its positions (and totals, local
+// positions and bases), plus, for the scatter launch of its own, the local
+// order (the launch that casts beside it lends the cast's tile instead).
 size_t scatter_lds_bytes(int32_t n_experts) {
   const int32_t nb = n_experts + 1;
+  if (nb <= kSortLocalBuckets) return (size_t)4 * nb * sizeof(int32_t);
   return (size_t)(nb <= kSortFastBuckets ? 2 : 1) * nb * sizeof(int32_t);
+}
+static size_t scatter_kernel_lds_bytes(int32_t n_experts) {
+  return scatter_lds_bytes(n_experts) + (n_experts + 1 <= kSortLocalBuckets ? kCastTileFloats * sizeof(float) : 0);
+}
+
+// Whether the scatter fits in one launch with the cast (its positions beside
+// the cast's 33 KB tile, within the 160 KB of LDS a workgroup may take).
+bool sort_cast_fusable(int32_t n_experts) {
+  return scatter_lds_bytes(n_experts) + kCastTileFloats * sizeof(float) + 1024 <= 160 * 1024;
 }
 
 template <typename IdxT>
@@ -156,7 +248,7 @@ struct ScatterArgs {
 // Chunk b: output positions from the histogram rows, then the stable scatter.
 // sh: n_experts + 1 positions (+ n_experts + 1 totals when <= kSortFastBuckets).
 template <typename IdxT>
-__device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b) {
+__device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b, float* tile) {
   const int64_t n_routes = a.n_routes, chunk = a.chunk, n_chunks = a.n_chunks, top_k = a.top_k;
   const int32_t n_experts = a.n_experts, n_bits = a.n_bits;
   const int32_t* __restrict__ counts = a.counts;
@@ -164,6 +256,11 @@ __device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b
   int32_t* __restrict__ n_invalid = a.n_invalid;
   int32_t* pos = sh;  // running output positions of this chunk
   const int32_t nb = n_experts + 1;
+  // through LDS (scatter_chunk_local): the chunk's own count of each bucket
+  // goes to lbase (then its exclusive scan) beside pos and the totals
+  const bool local = nb <= kSortLocalBuckets && chunk <= kSortLocalChunk && n_routes >= kSortLocalMinRoutes;
+  int32_t* lpos = sh + 2 * nb;
+  int32_t* lbase = sh + 3 * nb;
   // the first rounds' ids, loaded before the count-matrix pass so that their
   // latency overlaps it
   IdxT pre[kSortPrefetch];
@@ -182,6 +279,7 @@ __device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b
     for (int32_t e = threadIdx.x; e < nb; e += kSortThreads) {
       tot[e] = a.tot[e];
       pos[e] = counts[b * (int64_t)nb + e];
+      if (local) lbase[e] = (b + 1 < n_chunks ? counts[(b + 1) * (int64_t)nb + e] : a.tot[e]) - pos[e];
     }
     __syncthreads();
     if (b == 0 && threadIdx.x == 0 && n_invalid != nullptr) *n_invalid = tot[n_experts];
@@ -195,7 +293,10 @@ __device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b
     // consecutive elements belong to distinct buckets, so the LDS adds of one
     // wave instruction do not collide.
     int32_t* tot = sh + nb;
-    for (int32_t e = threadIdx.x; e < nb; e += kSortThreads) pos[e] = tot[e] = 0;
+    for (int32_t e = threadIdx.x; e < nb; e += kSortThreads) {
+      pos[e] = tot[e] = 0;
+      if (local) lbase[e] = 0;
+    }
     __syncthreads();
     const int32_t n = (int32_t)(n_chunks * nb);
     constexpr int U = 32;
@@ -213,6 +314,7 @@ __device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b
           const int32_t c = i / nb, e = i - c * nb;
           atomicAdd(&tot[e], v[u]);
           if (c < b) atomicAdd(&pos[e], v[u]);
+          if (local && c == b) lbase[e] = v[u];
         }
       }
     }
@@ -245,6 +347,15 @@ __device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b
     }
   }
   __syncthreads();
+  if (local) {
+    block_exclusive_scan(lbase, nb);
+    for (int32_t e = threadIdx.x; e < nb; e += kSortThreads) lpos[e] = lbase[e];
+    __syncthreads();
+    int32_t* l_key = reinterpret_cast<int32_t*>(tile);
+    scatter_chunk_local(a.sel, n_routes, n_experts, chunk, n_bits, top_k, pos, lpos, lbase, l_key,
+                        l_key + kSortLocalChunk, a.sorted_sel, a.perm, a.token_index, a.route_pos, b, pre);
+    return;
+  }
   scatter_chunk(a.sel, n_routes, n_experts, chunk, n_bits, top_k, pos, a.sorted_sel, a.perm, a.token_index,
                 a.route_pos, b, pre);
 }
@@ -252,7 +363,9 @@ __device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b
 template <typename IdxT>
 __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(const ScatterArgs<IdxT> a) {
   extern __shared__ int32_t sh[];
-  scatter_block(a, sh, blockIdx.x);
+  const int32_t nb = a.n_experts + 1;
+  // the local order after the positions (scatter_kernel_lds_bytes)
+  scatter_block(a, sh, blockIdx.x, reinterpret_cast<float*>(sh + (nb <= kSortLocalBuckets ? 4 * nb : 0)));
 }
 
 // The scatter and the per-step weight cast in one launch: workgroups
@@ -262,10 +375,11 @@ template <typename IdxT, typename OutT>
 __global__ __launch_bounds__(kSortThreads) void sort_scatter_cast_kernel(const ScatterArgs<IdxT> a,
                                                                          const CastArgs<OutT> c) {
   extern __shared__ int32_t sh[];
+  __shared__ float tile[kCastTileFloats];  // the cast's tile, or the scatter's local order
   if ((int64_t)blockIdx.x < a.n_chunks) {
-    scatter_block(a, sh, blockIdx.x);
+    scatter_block(a, sh, blockIdx.x, tile);
   } else {
-    cast_block(c, (int64_t)blockIdx.x - a.n_chunks);
+    cast_block(c, (int64_t)blockIdx.x - a.n_chunks, tile);
   }
 }
 
@@ -288,7 +402,12 @@ __global__ void expert_offsets_kernel(const int32_t* __restrict__ sorted_sel, in
 // host side
 // ---------------------------------------------------------------------------
 
+static std::atomic<int64_t> g_sort_chunk{0};
+void set_sort_chunk(int64_t routes) { g_sort_chunk.store(routes); }
+
 int64_t sort_chunk_size(int64_t n_routes, int32_t n_experts) {
+  const int64_t knob = g_sort_chunk.load();
+  if (knob > 0) return (knob + kSortThreads - 1) / kSortThreads * kSortThreads;
   // >= kSortMinChunk routes; (E + 1) * n_chunks <= 64K
   int64_t c = (n_routes * (int64_t)(n_experts + 1) + 65535) / 65536;
   if (c < kSortMinChunk) c = kSortMinChunk;
@@ -405,7 +524,7 @@ hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_rout
   const int64_t n_chunks = (n_routes + chunk - 1) / chunk;
   int32_t* counts = (int32_t*)ws;
   const size_t lds = (size_t)(n_experts + 1) * sizeof(int32_t);
-  const size_t lds_scatter = scatter_lds_bytes(n_experts);
+  const size_t lds_scatter = cast == nullptr ? scatter_kernel_lds_bytes(n_experts) : scatter_lds_bytes(n_experts);
   {
     hipError_t e = sel_is_int64 ? allow_lds(sort_hist_kernel<int64_t>, lds) : allow_lds(sort_hist_kernel<int32_t>, lds);
     if (e == hipSuccess)
@@ -446,8 +565,11 @@ hipError_t launch_sort_scatter(const int64_t* sel, int64_t n_routes, int32_t n_e
                                int64_t* offsets, int32_t* route_pos, int32_t* n_invalid_out, hipStream_t stream) {
   if (n_routes <= 0) return hipSuccess;
   const int64_t n_chunks = (n_routes + chunk - 1) / chunk;
-  const size_t lds = (size_t)(n_experts + 1) * sizeof(int32_t);
-  const size_t lds_scatter = scatter_lds_bytes(n_experts);
+  const size_t lds_scatter = scatter_kernel_lds_bytes(n_experts);
+  {
+    const hipError_t e = allow_lds(sort_scatter_kernel<int64_t>, lds_scatter);
+    if (e != hipSuccess) return e;
+  }
   int n_bits = 0;
   while ((1ll << n_bits) <= (int64_t)n_experts) ++n_bits;  // buckets 0..E
   const int32_t* tot = launch_colscan(counts, n_chunks, n_experts, stream);

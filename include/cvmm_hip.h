@@ -96,12 +96,18 @@ int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launche
  *     combine, the token gradient of a token-input selection): 1 = always
  *     the routed GEMM + route-ordered buffer, 2 = the dense GEMM over
  *     expert-slotted rows wherever its shapes fit (see cvmm_topk_dense).
- *     Built in: the cost model of cvmm_topk_dense. */
+ *     Built in: the cost model of cvmm_topk_dense.
+ *   CVMM_TUNE_SORT_CHUNK: routes per chunk of the selector sort (a multiple
+ *     of 256; larger chunks, fewer scatter workgroups).  Built in: >= 1024,
+ *     and the count matrix (chunks x (E + 1)) at most 64K entries.  A chunk
+ *     that makes the sort's workspace exceed 1 MiB fails
+ *     cvmm_sort_routes_noalloc. */
 #define CVMM_TUNE_PANEL_TILES_PER_WG 1
 #define CVMM_TUNE_WGRAD_ORDER 2
 #define CVMM_TUNE_GEMM_ORDER 3
 #define CVMM_TUNE_WGRAD_TILE 5
 #define CVMM_TUNE_DENSE_TOPK 6
+#define CVMM_TUNE_SORT_CHUNK 7
 int cvmm_tuning_set(int32_t knob, int64_t value);
 
 /* Whether a top-k sum -- out[t] = sum over the top_k routes (t, j) of

@@ -193,6 +193,9 @@ def test_weighted_route_input_reused_selector():
     ((1,), 1, torch.int64), ((13,), 7, torch.int64), ((3, 5, 3), 7, torch.int32),
     ((16, 512, 8), 64, torch.int64), ((8, 1024, 64), 256, torch.int64), ((2, 7, 1), 13, torch.int32),
     ((4, 4096, 8), 512, torch.int64), ((1, 5, 2), 32, torch.int64), ((64, 1000, 2), 2000, torch.int64),
+    # >= 2^18 routes: the scatter orders each chunk in LDS first
+    ((4, 65536, 1), 1, torch.int64), ((3, 30000, 4), 7, torch.int32), ((2, 40000, 4), 2047, torch.int64),
+    ((2, 40000, 4), 2048, torch.int64),
 ])
 def test_sort_routes_bit_exact(shape, E, dtype):
     g = torch.Generator().manual_seed(sum(shape) * 31 + E)
