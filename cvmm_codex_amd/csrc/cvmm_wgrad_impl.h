@@ -284,37 +284,49 @@ __global__ __launch_bounds__(kWgThreads, 2) void wgrad_kernel(const WgradParams 
     return;
   }
 
-  // partial tile of this chunk -> workspace (tile-contiguous fp32)
+  // partial tile of this chunk -> workspace (tile-contiguous fp32).  The
+  // partials and the counter are accessed with agent-scope relaxed atomics
+  // (coherent across the XCDs' L2s); each thread waits for its partial stores
+  // to complete before the barrier and the count, so the last arriver reads
+  // every chunk's partials.  Release/acquire fences would write back and
+  // invalidate the XCD's whole L2 instead.
   const int64_t slot = s_slot;
   if (slot >= p.max_slots) return;  // cannot happen: workspace sized for 2R/split slots
-  float* mine = p.partial + (slot * tiles + tile) * (int64_t)(BM * BN);
+  auto pack2 = [](float a, float b) {
+    return (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+  };
+  uint64_t* mine = reinterpret_cast<uint64_t*>(p.partial + (slot * tiles + tile) * (int64_t)(BM * BN));
   for (int r = tid / TPR; r < BM; r += RPP) {
-    float* d = mine + r * BN + cg * 8;
+    uint64_t* d = mine + (r * BN + cg * 8) / 2;
     const float* s = Cs + r * Cfg::C_LD + cg * 8;
-    *reinterpret_cast<float4*>(d) = make_float4(s[0], s[1], s[2], s[3]);
-    *reinterpret_cast<float4*>(d + 4) = make_float4(s[4], s[5], s[6], s[7]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __hip_atomic_store(d + j, pack2(s[2 * j], s[2 * j + 1]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __threadfence();  // release the partial to the device before signalling
+  // vmcnt(0) only (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] at [15:14])
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
   __syncthreads();
   if (tid == 0) {
     int32_t* ctr = p.counters + (int64_t)expert * tiles + tile;
-    const int32_t prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const int32_t prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == nch - 1);
     if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();  // acquire: see every chunk's partial
   // this expert's slots are consecutive; add them in chunk order
   const int64_t base_slot = s_base_slot;
   for (int r = tid / TPR; r < BM; r += RPP) {
     float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int32_t c = 0; c < nch; ++c) {
-      const float* src = p.partial + ((base_slot + c) * tiles + tile) * (int64_t)(BM * BN) + r * BN + cg * 8;
-      const float4 a = *reinterpret_cast<const float4*>(src);
-      const float4 b = *reinterpret_cast<const float4*>(src + 4);
-      v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
-      v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
+      const uint64_t* src = reinterpret_cast<const uint64_t*>(
+          p.partial + ((base_slot + c) * tiles + tile) * (int64_t)(BM * BN) + r * BN + cg * 8);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint64_t w = __hip_atomic_load(src + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v[2 * j] += __uint_as_float((uint32_t)w);
+        v[2 * j + 1] += __uint_as_float((uint32_t)(w >> 32));
+      }
     }
     write_dw(r, v);
   }

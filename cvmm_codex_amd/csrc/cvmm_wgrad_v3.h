@@ -382,39 +382,51 @@ __global__ __launch_bounds__(256, (BM / WM / 16) * (BN / WN / 16) <= 16 ? 2 : 1)
   }
 
   // ---- multi-chunk expert: fp32 partial tile in fragment order -> workspace;
-  // the last arriver sums the chunks in chunk order
+  // the last arriver sums the chunks in chunk order.  The partials and the
+  // counter are accessed with agent-scope (sc1) relaxed atomics, coherent
+  // across the XCDs' L2s: every thread waits for its partial stores to
+  // complete before the barrier and the count, so the last arriver reads
+  // every chunk's partials from the coherent level.  (Release/acquire fences
+  // write back and invalidate the whole L2 of the XCD under the feet of the
+  // other workgroups there: the FFN stack's weight gradient took 780 us per
+  // launch with them, 720 us with this exchange.)
   const int64_t slot = sched.slot;
   if (slot >= p.max_slots) return;  // cannot happen: workspace holds 2R/split + 1 slots
+  // float4 k of this lane's fragment list = two 8-byte words at 2k, 2k + 1
   auto frag_ptr = [&](int64_t sl) {
-    return reinterpret_cast<float4*>(p.partial) + ((sl * tiles + tile) * Cfg::NW + wave) * (IN * JM) * 64 + lane;
+    return reinterpret_cast<uint64_t*>(p.partial) +
+           2 * (((sl * tiles + tile) * Cfg::NW + wave) * (IN * JM) * 64 + lane);
+  };
+  auto pack2 = [](float a, float b) {
+    return (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
   };
   {
-    float4* d = frag_ptr(slot);
+    uint64_t* d = frag_ptr(slot);
 #pragma unroll
     for (int i = 0; i < IN; ++i)
 #pragma unroll
-      for (int j = 0; j < JM; ++j)
-      {
-        d[(i * JM + j) * 64] = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      for (int j = 0; j < JM; ++j) {
+        uint64_t* w = d + 2 * (i * JM + j) * 64;
+        __hip_atomic_store(w, pack2(acc[i][j][0], acc[i][j][1]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(w + 1, pack2(acc[i][j][2], acc[i][j][3]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_sched_barrier(0);
       }
   }
-  __threadfence();
+  vm_wait<0>();
   __syncthreads();
   if (tid == 0) {
     int32_t* ctr = p.counters + (int64_t)expert * tiles + tile;
-    const int32_t prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const int32_t prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     sched.last = (prev == nch - 1);
     if (sched.last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!sched.last) return;
-  __threadfence();
   // each of the wave's blocks: 0 + chunk 0 + chunk 1 + ... in chunk order,
   // GB blocks at a time (GB loads in flight per chunk); flat block index
   // b = i * JM + j, as the partials are laid out
-  const float4* src = frag_ptr(sched.base_slot);
-  const int64_t stride = tiles * Cfg::NW * (IN * JM) * 64;  // float4 between chunks
+  const uint64_t* src = frag_ptr(sched.base_slot);
+  const int64_t stride = 2 * tiles * Cfg::NW * (IN * JM) * 64;  // 8-byte words between chunks
   constexpr int NB = IN * JM, GB = NB < 16 ? NB : 16;
 #pragma unroll 1
   for (int g0 = 0; g0 < NB; g0 += GB) {
@@ -423,10 +435,15 @@ __global__ __launch_bounds__(256, (BM / WM / 16) * (BN / WN / 16) <= 16 ? 2 : 1)
     for (int b = 0; b < GB; ++b) t[b] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll 1
     for (int32_t c = 0; c < nch; ++c) {
-      const float4* q = src + c * stride + g0 * 64;
+      const uint64_t* q = src + c * stride + 2 * g0 * 64;
       float4 v[GB];
 #pragma unroll
-      for (int b = 0; b < GB; ++b) v[b] = q[b * 64];
+      for (int b = 0; b < GB; ++b) {
+        const uint64_t lo = __hip_atomic_load(q + 2 * b * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t hi = __hip_atomic_load(q + 2 * b * 64 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v[b] = make_float4(__uint_as_float((uint32_t)lo), __uint_as_float((uint32_t)(lo >> 32)),
+                           __uint_as_float((uint32_t)hi), __uint_as_float((uint32_t)(hi >> 32)));
+      }
 #pragma unroll
       for (int b = 0; b < GB; ++b) {
         t[b].x += v[b].x;
