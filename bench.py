@@ -128,24 +128,23 @@ def kernel_launchers(runner: Runner):
             None if runner.w is None else runner.w.detach())
     keys = runner.keys.detach()
     fast = C._fast_path(op, keys.shape[1], keys.shape[2])
-    kt, kn = C._cast_keys(keys, op, True, True) if fast else (None, None)
     k = runner.p.weights.shape[-1] if runner.w is not None else runner.p.sel.shape[-1]
-    fwd_t, bwd_t, _, _ = C._plan_copies(keys, op, runner.p.routes, k, runner.w is not None,
-                                        not runner.p.route_input, True)
+    plan = C._plan_copies(keys, op, runner.p.routes, k, runner.w is not None, not runner.p.route_input, True)
+    kt, kn = C._cast_keys(keys, op, plan) if fast else (None, None)
+    keys_f, fwd_t = C._copy_view(plan, kt, kn, True) if fast else (None, True)
+    keys_x, bwd_t = C._copy_view(plan, kt, kn, False) if fast else (None, False)
 
     def cast():
-        C._cast_keys(keys, op, True, True)
+        C._cast_keys(keys, op, plan)
 
     def fwd():
-        C._forward(runner.x.detach(), s.sel_index, s.sel, keys, s.out_index, args[6], op,
-                   (kt if fwd_t else kn) if fast else None, fwd_t)
+        C._forward(runner.x.detach(), s.sel_index, s.sel, keys, s.out_index, args[6], op, keys_f, fwd_t)
 
     def bwd_w():
         C._backward(Ctx, go, *args, False, True, False)
 
     def bwd_x():
-        C._backward(Ctx, go, *args, True, False, runner.w is not None,
-                    keys_x=(kt if bwd_t else kn) if fast else None, keys_x_is_t=bwd_t)
+        C._backward(Ctx, go, *args, True, False, runner.w is not None, keys_x=keys_x, keys_x_is_t=bwd_t)
 
     out = {"fwd": fwd, "bwd_w": bwd_w, "bwd_x": bwd_x}
     if fast:

@@ -19,6 +19,8 @@ F32, F16, BF16 = 0, 1, 2            # cvmm.py:36-44 dtype ids
 FLAG_ATOMIC_REDUCE = 1
 FLAG_COUNTERS_ZEROED = 2
 FLAG_WORKSPACE_ZEROED = 8
+CAST_T_INTERLEAVED = 1
+CAST_N_INTERLEAVED = 2
 TUNE_PANEL_TILES_PER_WG = 1
 TUNE_WGRAD_ORDER = 2
 TUNE_GEMM_ORDER = 3
@@ -52,8 +54,9 @@ _SIGS = {
     "cvmm_copy_ids": (ctypes.c_int, [_P, _I32, _I64, _P, _P]),
     "cvmm_expert_offsets": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
     "cvmm_sort_routes_cast_keys": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _SZ,
-                                                  _P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P]),
-    "cvmm_cast_keys": (ctypes.c_int, [_P, _I32, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P]),
+                                                  _P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _I32,
+                                                  _P]),
+    "cvmm_cast_keys": (ctypes.c_int, [_P, _I32, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _I32, _P]),
     "cvmm_route_topk_workspace_bytes": (_SZ, [_I64, _I32, _I64]),
     "cvmm_route_topk": (ctypes.c_int, [_P, _I32, _I64, _I64, _I32, _I64, _I32, _P, _P,
                                        _P, _P, _P, _P, _P, _P, _SZ, _P]),

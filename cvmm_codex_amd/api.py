@@ -29,7 +29,7 @@ from __future__ import annotations
 import os
 import threading
 from dataclasses import dataclass
-from typing import Dict, Optional, Tuple, Union
+from typing import Dict, NamedTuple, Optional, Tuple, Union
 
 import torch
 
@@ -119,30 +119,48 @@ def _sort_routes(raw_flat: torch.Tensor, n_experts: int, top_k: int):
 
 
 # Weight casts made together with a sort by cvmm(), for the CVMM.forward of
-# the same call: (keys, keys._version, op dtype, kt, kn).
+# the same call: (keys, keys._version, op dtype, layout, kt, kn).
 _cast_done = threading.local()
+
+
+class _CopyPlan(NamedTuple):
+    """The op-dtype weight copies a call reads.  The routed GEMMs read their K
+    dimension with unit stride: kt [E, d_out, d_in] for the forward, kn
+    [E, d_in, d_out] for the grad-input.  A top-k sum taken as a dense GEMM
+    (cvmm_topk_dense) reads the same orientation with the experts interleaved
+    between the rows (kt as [d_out, E, d_in], kn as [d_in, E, d_out]: the
+    GEMM's B^T rows).  Under torch.compile tracing the copies stay in the
+    routed layouts and a dense sum reads the other copy as [E*K, N] rows
+    (`fwd_t` / `bwd_t` say which copy each phase reads)."""
+    want_t: bool
+    want_n: bool
+    layout: int  # N.CAST_*_INTERLEAVED bits
+    fwd_t: bool
+    bwd_t: bool
 
 
 def _sort_routes_cast(raw_flat: torch.Tensor, n_experts: int, top_k: int, cast):
     """_sort_routes plus the step's weight cast in the same launches
-    (`cast` = (keys, op dtype, want kt, want kn)); the copies are left for
+    (`cast` = (keys, op dtype, _CopyPlan)); the copies are left for
     CVMM.forward."""
-    keys, op, want_t, want_n = cast
+    keys, op, plan = cast
     (ssel, perm, tok, offsets, route_pos), kt, kn = N.host().sort_routes_cast(
-        raw_flat, n_experts, top_k, keys, N.dtype_id(op), want_t, want_n, N.stream_of(raw_flat.device))
+        raw_flat, n_experts, top_k, keys, N.dtype_id(op), plan.want_t, plan.want_n, plan.layout,
+        N.stream_of(raw_flat.device))
     perm._cvmm_route_pos = route_pos
-    _cast_done.entry = (keys, keys._version, op, kt, kn)
+    _cast_done.entry = (keys, keys._version, op, plan.layout, kt, kn)
     return ssel, perm, tok, offsets
 
 
-def _take_cast(keys: torch.Tensor, op: torch.dtype, want_t: bool, want_n: bool):
+def _take_cast(keys: torch.Tensor, op: torch.dtype, plan: _CopyPlan):
     """The weight copies cast with this call's sort, if they still match."""
     entry = getattr(_cast_done, "entry", None)
     _cast_done.entry = None
     if entry is None:
         return None
-    k, version, eop, kt, kn = entry
-    if k is not keys or version != keys._version or eop != op or (want_t and kt is None) or (want_n and kn is None):
+    k, version, eop, layout, kt, kn = entry
+    if (k is not keys or version != keys._version or eop != op or layout != plan.layout
+            or (plan.want_t and kt is None) or (plan.want_n and kn is None)):
         return None
     return kt, kn
 
@@ -155,22 +173,35 @@ def _topk_dense(n_tokens: int, n_experts: int, K: int, N_: int, top_k: int, op_i
 
 
 def _plan_copies(keys: torch.Tensor, op: torch.dtype, n_routes: int, top_k: int, weighted: bool,
-                 token_input: bool, need_grad_input: bool):
-    """The op-dtype weight copies a call reads: (forward reads kt, grad-input
-    reads kt, want kt, want kn).  The routed GEMMs read their K dimension with
-    unit stride: kt [E, d_out, d_in] for the forward, kn [E, d_in, d_out] for
-    the grad-input.  A top-k sum taken as a dense GEMM (cvmm_topk_dense) reads
-    the weights as [E*K, N] rows instead: kn for the weighted forward, kt for
-    the token gradient."""
+                 token_input: bool, need_grad_input: bool) -> _CopyPlan:
+    """The copies of this call (_CopyPlan)."""
     E, d_in, d_out = keys.shape
     op_id = N.dtype_id(op)
     T = n_routes // top_k if top_k > 0 else 0
-    fwd_dense = weighted and top_k >= 2 and _topk_dense(T, E, d_in, d_out, top_k, op_id)
-    bwd_dense = not weighted and token_input and top_k >= 2 and _topk_dense(T, E, d_out, d_in, top_k, op_id)
-    fwd_t, bwd_t = not fwd_dense, bwd_dense
-    want_t = fwd_t or (need_grad_input and bwd_t)
-    want_n = (not fwd_t) or (need_grad_input and not bwd_t)
-    return fwd_t, bwd_t, want_t, want_n
+    fwd_dense = weighted and top_k >= 2 and not cvmm_atomic_reduce and _topk_dense(T, E, d_in, d_out, top_k, op_id)
+    bwd_dense = (need_grad_input and not weighted and token_input and top_k >= 2 and not cvmm_atomic_reduce
+                 and _topk_dense(T, E, d_out, d_in, top_k, op_id))
+    if _compiling():
+        fwd_t, bwd_t = not fwd_dense, bwd_dense
+        return _CopyPlan(fwd_t or (need_grad_input and bwd_t), (not fwd_t) or (need_grad_input and not bwd_t),
+                         0, fwd_t, bwd_t)
+    layout = (N.CAST_T_INTERLEAVED if fwd_dense else 0) | (N.CAST_N_INTERLEAVED if bwd_dense else 0)
+    return _CopyPlan(True, need_grad_input, layout, True, False)
+
+
+def _copy_view(plan: _CopyPlan, kt, kn, fwd: bool):
+    """(copy, is_t) for the host call of the forward (`fwd`) or the
+    grad-input: an interleaved copy goes as its logical [E, d_in, d_out]
+    view (is_t False); a routed-layout copy as it is."""
+    is_t = plan.fwd_t if fwd else plan.bwd_t
+    copy = kt if is_t else kn
+    if copy is None:
+        return None, is_t
+    if is_t and plan.layout & N.CAST_T_INTERLEAVED:
+        return copy.permute(1, 2, 0), False   # [d_out, E, d_in] -> [E, d_in, d_out]
+    if not is_t and plan.layout & N.CAST_N_INTERLEAVED:
+        return copy.permute(1, 0, 2), False   # [d_in, E, d_out] -> [E, d_in, d_out]
+    return copy, is_t
 
 
 def cvmm_expert_offsets(sorted_experts: torch.Tensor, n_experts: int) -> torch.Tensor:
@@ -484,14 +515,15 @@ def _flags() -> int:
     return N.FLAG_ATOMIC_REDUCE if cvmm_atomic_reduce else 0
 
 
-def _cast_keys(keys: torch.Tensor, op: torch.dtype, want_t: bool, want_n: bool):
-    """keys [E, d_in, d_out] -> op-dtype copies kt [E, d_out, d_in] (forward) and
-    kn [E, d_in, d_out] (grad-input), one pass."""
+def _cast_keys(keys: torch.Tensor, op: torch.dtype, plan: _CopyPlan):
+    """keys [E, d_in, d_out] -> the op-dtype copies kt (forward) and kn
+    (grad-input) of `plan`, one pass."""
     _require_device(keys, "keys")
     if _compiling():
         kt, kn = _ops.cast_keys(keys, op)
         return kt, kn
-    return N.host().cast_keys(keys, N.dtype_id(op), want_t, want_n, N.stream_of(keys.device))
+    return N.host().cast_keys(keys, N.dtype_id(op), plan.want_t, plan.want_n, plan.layout,
+                              N.stream_of(keys.device))
 
 
 def _forward(x, sel_index, sel, keys, out_index, rw, op_dtype, keys_op=None, keys_op_is_t=True):
@@ -532,15 +564,14 @@ def _backward(ctx, grad_output, x, keys, raw_sel, sel, sel_index, out_index, rw,
 
 
 def _copies_for_call(ctx, keys, op, n_routes, top_k, weighted, token_input, need_grad_input):
-    """The forward's weight copy for CVMM(.Gelu).forward, the grad-input's
-    kept on ctx: cast with the sort when cvmm() did that, else here."""
-    fwd_t, bwd_t, want_t, want_n = _plan_copies(keys, op, n_routes, top_k, weighted, token_input,
-                                                need_grad_input)
-    pre = None if _compiling() else _take_cast(keys, op, want_t, want_n)
-    kt, kn = pre if pre is not None else _cast_keys(keys, op, want_t, want_n)
-    ctx.keys_x = (kt if bwd_t else kn) if need_grad_input else None
-    ctx.keys_x_is_t = bwd_t
-    return (kt if fwd_t else kn), fwd_t
+    """The forward's weight copy (copy, is_t) for CVMM(.Gelu).forward, the
+    grad-input's kept on ctx: cast with the sort when cvmm() did that, else
+    here."""
+    plan = _plan_copies(keys, op, n_routes, top_k, weighted, token_input, need_grad_input)
+    pre = None if _compiling() else _take_cast(keys, op, plan)
+    kt, kn = pre if pre is not None else _cast_keys(keys, op, plan)
+    ctx.keys_x, ctx.keys_x_is_t = _copy_view(plan, kt, kn, False) if need_grad_input else (None, False)
+    return _copy_view(plan, kt, kn, True)
 
 
 class CVMM(torch.autograd.Function):
@@ -595,8 +626,9 @@ class CVMMGelu(torch.autograd.Function):
         ctx.keys_x, ctx.keys_x_is_t = None, False
         if _fast_path(out_type, keys.shape[1], keys.shape[2]):
             k = raw_sel.shape[-1] if raw_sel.ndim > 0 else 1
-            keys_t, _ = _copies_for_call(ctx, keys, out_type, sel.numel(), k, False, out_index is not None,
-                                         ctx.needs_input_grad[0])
+            keys_t, is_t = _copies_for_call(ctx, keys, out_type, sel.numel(), k, False, out_index is not None,
+                                            ctx.needs_input_grad[0])
+            assert is_t, "an unweighted forward reads the routed-layout kt copy"
         n_experts = keys.shape[0]
         R = sel.numel()
         y, h = N.host().forward_gelu(x, keys, keys_t, sel, sel_index, out_index, _offsets_for(sel, n_experts),
@@ -634,9 +666,9 @@ def cvmm_gelu(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.Te
     op = get_dtype()
     if sel._pending() and keys.is_cuda and _fast_path(op, keys.shape[1], keys.shape[2]):
         raw = sel._raw_shape_tensor()
-        _, _, want_t, want_n = _plan_copies(keys, op, raw.numel(), raw.shape[-1] if raw.ndim else 1, False,
-                                            not sel._route_mode, torch.is_grad_enabled() and x.requires_grad)
-        cast = (keys, op, want_t, want_n)
+        plan = _plan_copies(keys, op, raw.numel(), raw.shape[-1] if raw.ndim else 1, False,
+                            not sel._route_mode, torch.is_grad_enabled() and x.requires_grad)
+        cast = (keys, op, plan)
     sel._resolve(keys.shape[0], cast)
     return CVMMGelu.apply(x, sel._raw_shape_tensor(), sel.sel_index, sel.sel, keys, sel.out_index)
 
@@ -667,8 +699,7 @@ def cvmm(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.Tensor)
         raw = sel._raw_shape_tensor()
         k = rw.shape[-1] if rw is not None else (raw.shape[-1] if raw.ndim else 1)
         need = torch.is_grad_enabled() and (x.requires_grad or (rw is not None and rw.requires_grad))
-        _, _, want_t, want_n = _plan_copies(keys, op, raw.numel(), k, rw is not None, not sel._route_mode, need)
-        cast = (keys, op, want_t, want_n)
+        cast = (keys, op, _plan_copies(keys, op, raw.numel(), k, rw is not None, not sel._route_mode, need))
     sel._resolve(keys.shape[0], cast)
     if cvmm_log_shapes:
         sh = (x.shape, keys.shape)

@@ -65,7 +65,7 @@ def _(sorted_experts, n_experts):
 # ---------------------------------------------------------------------------
 @torch.library.custom_op(f"{NS}::cast_keys", mutates_args=())
 def cast_keys(keys: torch.Tensor, op_dtype: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
-    kt, kn = N.host().cast_keys(keys, N.dtype_id(op_dtype), True, True, N.stream_of(keys.device))
+    kt, kn = N.host().cast_keys(keys, N.dtype_id(op_dtype), True, True, 0, N.stream_of(keys.device))
     return kt, kn
 
 

@@ -238,30 +238,40 @@ DenseWs carve_dense(Carver& c, int64_t n_tokens, int32_t n_experts, int64_t K, i
   return w;
 }
 
-// The dense top-k sum: out[t] = sum_j s_tj src[row(t, j)] @ B_e.  `keys` (the
-// logical [E, d_in, d_out] view with its strides) is used as B when it is
-// already the op-dtype [E*K][N] row layout (kn_layout: K = d_in; otherwise K
-// = d_out), else cast into the workspace.
+// The dense top-k sum: out[t] = sum_j s_tj src[row(t, j)] @ B_e, with K =
+// d_in, N = d_out for the forward (`fwd`), K = d_out, N = d_in for the
+// grad-input.  `keys` (the logical [E, d_in, d_out] view with its strides) is
+// the GEMM's B as it stands when it is an op-dtype copy in one of the two row
+// layouts: B^T [N][E*K] (the cast's expert-interleaved copy: [d_out][E][d_in]
+// for the forward, [d_in][E][d_out] for the grad-input; both operands
+// k-contiguous, the faster GEMM) or B [E*K][N] ([E][d_in][d_out] for the
+// forward, [E][d_out][d_in] for the grad-input).  Other keys are cast into
+// the workspace's B^T.
 int run_dense_topk(const DenseWs& w, const void* src, int32_t src_dtype, int64_t src_ld, bool src_per_route,
                    const int32_t* sorted_sel, const int32_t* route_pos, const int64_t* rp, const int64_t* offs,
                    int64_t n_routes, int64_t n_tokens, int64_t top_k, int32_t n_experts, const void* keys,
                    int32_t keys_dtype, int64_t d_in, int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj,
-                   bool kn_layout, const void* rw, int32_t rw_dtype, int32_t w_round, int32_t op_dtype, void* out,
+                   bool fwd, const void* rw, int32_t rw_dtype, int32_t w_round, int32_t op_dtype, void* out,
                    int32_t out_dtype, int64_t out_ld, bool a_zeroed, uint32_t gemm_class, const char* what,
                    hipStream_t s) {
-  const int64_t K = kn_layout ? d_in : d_out, N = kn_layout ? d_out : d_in;
+  const int64_t K = fwd ? d_in : d_out, N = fwd ? d_out : d_in;
   const void* B = keys;
-  const bool direct = keys_dtype == op_dtype && k_se == d_in * d_out &&
-                      (kn_layout ? (k_sj == 1 && k_si == d_out) : (k_si == 1 && k_sj == d_in));
-  if (!direct) {
-    // kn_layout: the [E][d_in][d_out] copy; else the [E][d_out][d_in] copy
+  const bool same = keys_dtype == op_dtype;
+  const bool by_col = same && k_se == K && (fwd ? (k_si == 1 && k_sj == n_experts * d_in)
+                                                : (k_sj == 1 && k_si == n_experts * d_out));
+  const bool by_row = same && k_se == d_in * d_out &&
+                      (fwd ? (k_sj == 1 && k_si == d_out) : (k_si == 1 && k_sj == d_in));
+  if (!by_col && !by_row) {
+    // the expert-interleaved copy of this GEMM's orientation
     int r = check_launch(timed(CVMM_KC_CAST_KEYS, s, [&] {
       return launch_cast_keys(keys, keys_dtype, k_se, k_si, k_sj, n_experts, d_in, d_out, op_dtype,
-                              kn_layout ? nullptr : w.b, kn_layout ? w.b : nullptr, s);
+                              fwd ? w.b : nullptr, fwd ? nullptr : w.b,
+                              fwd ? kCastTInterleaved : kCastNInterleaved, s);
     }), what);
     if (r) return r;
     B = w.b;
   }
+  const bool b_by_col = !by_row;
   const int32_t* inv = route_pos;
   if (!inv) {
     int r = check_launch(timed_combine(s, [&] { return launch_invert_rows(rp, n_routes, w.inv, s); }), what);
@@ -285,7 +295,8 @@ int run_dense_topk(const DenseWs& w, const void* src, int32_t src_dtype, int64_t
   if (r) return r;
   int status = 0;
   const hipError_t e = timed(gemm_class, s, [&] {
-    return dense_rows_gemm(w.a, B, n_tokens, (int64_t)n_experts * K, N, op_dtype, out, out_dtype, out_ld, s, &status);
+    return dense_rows_gemm(w.a, B, b_by_col, n_tokens, (int64_t)n_experts * K, N, op_dtype, out, out_dtype, out_ld,
+                           s, &status);
   });
   if (e != hipSuccess) {
     if (status != 0) return fail(CVMM_ERR_LAUNCH, "%s: rocblas_gemm_ex failed (status %d)", what, status);
@@ -541,16 +552,20 @@ int cvmm_route_topk_backward(const void* logits, int32_t logits_dtype, int64_t n
 // ---------------------------------------------------------------------------
 int cvmm_cast_keys(const void* keys, int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out,
                    int64_t k_se, int64_t k_si, int64_t k_sj, int32_t out_dtype, void* keys_t, void* keys_n,
-                   void* stream) {
+                   int32_t layout, void* stream) {
   if (!valid_dtype(keys_dtype) || (out_dtype != kBF16 && out_dtype != kF16))
     return fail(CVMM_ERR_INVALID, "cvmm_cast_keys: keys dtype must be float, output bf16 or f16");
+  if (layout & ~(kCastTInterleaved | kCastNInterleaved))
+    return fail(CVMM_ERR_INVALID, "cvmm_cast_keys: unknown layout bits %d", layout);
   if (n_experts <= 0 || d_in <= 0 || d_out <= 0) return fail(CVMM_ERR_INVALID, "cvmm_cast_keys: bad sizes");
   if (n_experts > 65535 || (d_in + 63) / 64 > 65535)
     return fail(CVMM_ERR_UNSUPPORTED, "cvmm_cast_keys: too many experts / rows");
   if (!keys) return fail(CVMM_ERR_INVALID, "cvmm_cast_keys: keys NULL");
   if (!keys_t && !keys_n) return CVMM_OK;
-  return check_launch(timed(CVMM_KC_CAST_KEYS, (hipStream_t)stream, [&] { return launch_cast_keys(keys, keys_dtype, k_se, k_si, k_sj, n_experts, d_in, d_out, out_dtype,
-                                       keys_t, keys_n, (hipStream_t)stream); }),
+  return check_launch(timed(CVMM_KC_CAST_KEYS, (hipStream_t)stream, [&] {
+                        return launch_cast_keys(keys, keys_dtype, k_se, k_si, k_sj, n_experts, d_in, d_out,
+                                                out_dtype, keys_t, keys_n, layout, (hipStream_t)stream);
+                      }),
                       "cvmm_cast_keys");
 }
 
@@ -559,11 +574,11 @@ int cvmm_sort_routes_cast_keys(const void* sel, int32_t sel_is_int64, int64_t n_
                                int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* workspace,
                                size_t workspace_bytes, const void* keys, int32_t keys_dtype, int64_t d_in,
                                int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj, int32_t out_dtype,
-                               void* keys_t, void* keys_n, void* stream) {
+                               void* keys_t, void* keys_n, int32_t layout, void* stream) {
   const bool fuse = n_routes > 0 && n_routes <= 0x7fffffffll && n_experts > 0 && n_experts <= 32767 && top_k > 0 &&
                     sel && sorted_sel && perm && offsets && keys && (keys_t || keys_n) && d_in > 0 && d_out > 0 &&
                     n_experts <= 65535 && (int64_t)n_experts * (d_in / 64) * (d_out / 64) < 0x7f000000ll &&
-                    sort_cast_fusable(n_experts) &&
+                    sort_cast_fusable(n_experts) && !(layout & ~(kCastTInterleaved | kCastNInterleaved)) &&
                     cast_vec_ok(keys, keys_dtype, k_se, k_si, k_sj, d_in, d_out, out_dtype, keys_t, keys_n) &&
                     workspace != nullptr && workspace_bytes >= sort_workspace_bytes(n_routes, n_experts);
   if (!fuse) {
@@ -572,10 +587,10 @@ int cvmm_sort_routes_cast_keys(const void* sel, int32_t sel_is_int64, int64_t n_
                              route_pos, n_invalid, workspace, workspace_bytes, stream);
     if (r) return r;
     return cvmm_cast_keys(keys, keys_dtype, n_experts, d_in, d_out, k_se, k_si, k_sj, out_dtype, keys_t, keys_n,
-                          stream);
+                          layout, stream);
   }
   hipStream_t s = (hipStream_t)stream;
-  const CastRequest cr{keys, k_se, k_si, n_experts, d_in, d_out, out_dtype, keys_t, keys_n};
+  const CastRequest cr{keys, k_se, k_si, n_experts, d_in, d_out, out_dtype, keys_t, keys_n, layout};
   return check_launch(timed(CVMM_KC_SORT, s, [&] { return launch_sort_routes(sel, sel_is_int64 != 0, n_routes, n_experts, top_k, sorted_sel, perm,
                                          token_index, offsets, route_pos, n_invalid, workspace, s, &cr); }),
                       "cvmm_sort_routes_cast_keys");

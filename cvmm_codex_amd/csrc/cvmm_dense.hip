@@ -7,10 +7,11 @@
 // are placed in expert slots:
 //     A[t][e*K + k] = sum over the routes j of token t with expert e of
 //                     rnd_op(s_tj * src[row(t,j)][k])         (zero elsewhere)
-//     out[t] = A[t] @ Wk,   Wk[(e, k)][n] = W[e] as [E*K][N] rows
-// where Wk is the op-dtype weight copy whose rows are the product's K
-// dimension (the forward's [E][d_in][d_out] copy for the forward, the
-// transposed [E][d_out][d_in] copy for the grad-input).  A has E/top_k times
+//     out[t] = A[t] @ Wk,   Wk[(e, k)][n] = W[e][k][n] of the product
+// where Wk is an op-dtype weight copy, either as Wk^T [N][E*K] rows (the
+// cast's expert-interleaved copy of the phase's own orientation: both GEMM
+// operands k-contiguous, the faster form) or as [E*K][N] rows (the routed
+// copy of the other orientation).  A has E/top_k times
 // the product's useful flops, but no [R, N] route-ordered buffer is written
 // and read back: at high fan-out (SwitchHead, 64 of 256 experts, a 2.1 GB
 // buffer) the GEMM is the cheaper way.  The sum over a token's routes runs in
@@ -160,10 +161,12 @@ rocblas_datatype blas_type(int32_t dt) {
 }  // namespace
 
 // out[t][n] (row stride out_ld, out_dtype) = sum_c A[t][c] * B[c][n], with A
-// [T][C] and B [C][N] row-major in op_dtype, fp32 accumulation.  Returns a
-// HIP-style error: hipErrorUnknown with `status` set on a rocBLAS failure.
-hipError_t dense_rows_gemm(const void* A, const void* B, int64_t T, int64_t C, int64_t N, int32_t op_dtype, void* out,
-                           int32_t out_dtype, int64_t out_ld, hipStream_t stream, int* status) {
+// [T][C] row-major and B as [C][N] rows or (b_by_col) as B^T [N][C] rows, op
+// dtype, fp32 accumulation.  Returns a HIP-style error: hipErrorUnknown with
+// `status` set on a rocBLAS failure.
+hipError_t dense_rows_gemm(const void* A, const void* B, bool b_by_col, int64_t T, int64_t C, int64_t N,
+                           int32_t op_dtype, void* out, int32_t out_dtype, int64_t out_ld, hipStream_t stream,
+                           int* status) {
   *status = 0;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -183,11 +186,14 @@ hipError_t dense_rows_gemm(const void* A, const void* B, int64_t T, int64_t C, i
   rocblas_handle h = g_blas[dev];
   rocblas_status st = rocblas_set_stream(h, stream);
   // column-major view: out^T [N x T] = B^T [N x C] * A^T [C x T]; the
-  // row-major arrays are exactly those column-major matrices
+  // row-major arrays are those column-major matrices, B^T transposed when B
+  // comes as [N][C] rows (both operands k-contiguous: ~15 % faster at
+  // SwitchHead size on MI355X)
   const float alpha = 1.f, beta = 0.f;
   if (st == rocblas_status_success)
-    st = rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_none, (rocblas_int)N, (rocblas_int)T,
-                         (rocblas_int)C, &alpha, B, blas_type(op_dtype), (rocblas_int)N, A, blas_type(op_dtype),
+    st = rocblas_gemm_ex(h, b_by_col ? rocblas_operation_transpose : rocblas_operation_none, rocblas_operation_none,
+                         (rocblas_int)N, (rocblas_int)T, (rocblas_int)C, &alpha, B, blas_type(op_dtype),
+                         (rocblas_int)(b_by_col ? C : N), A, blas_type(op_dtype),
                          (rocblas_int)C, &beta, out, blas_type(out_dtype), (rocblas_int)out_ld, out,
                          blas_type(out_dtype), (rocblas_int)out_ld, rocblas_datatype_f32_r, rocblas_gemm_algo_standard,
                          0, rocblas_gemm_flags_none);

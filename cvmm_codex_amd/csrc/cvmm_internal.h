@@ -177,6 +177,11 @@ void set_sort_chunk(int64_t routes);
 bool sort_cast_fusable(int32_t n_experts);
 // bytes of a chunks x (E + 1) int32 count matrix, rounded up to 256
 size_t sort_counts_bytes(int64_t n_chunks, int32_t n_experts);
+// Layout bits of the cast's outputs (the C ABI's CVMM_CAST_T_INTERLEAVED /
+// CVMM_CAST_N_INTERLEAVED): kt as [d_out][E][d_in], kn as [d_in][E][d_out].
+constexpr int32_t kCastTInterleaved = 1;
+constexpr int32_t kCastNInterleaved = 2;
+
 // A weight cast to run in the sort's scatter launch (vectorised cast only).
 struct CastRequest {
   const void* keys;
@@ -186,6 +191,7 @@ struct CastRequest {
   int32_t out_dtype;
   void* kt;
   void* kn;
+  int32_t layout;
 };
 // The vectorised cast applies: fp32 keys with unit column stride, 16-byte
 // aligned rows, d_in and d_out multiples of 64, 16-bit output.
@@ -203,10 +209,11 @@ hipError_t launch_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, in
                                  int64_t* offsets, hipStream_t stream);
 
 // keys (any float storage / strides) -> op dtype copies kt [E][d_out][d_in]
-// and/or kn [E][d_in][d_out] (either may be null)
+// and/or kn [E][d_in][d_out] (either may be null; `layout` bits interleave
+// the experts between the rows instead)
 hipError_t launch_cast_keys(const void* keys, int32_t keys_dtype, int64_t se, int64_t si, int64_t sj,
                             int32_t n_experts, int64_t d_in, int64_t d_out, int32_t out_dtype, void* kt,
-                            void* kn, hipStream_t stream);
+                            void* kn, int32_t layout, hipStream_t stream);
 
 // ---------------------------------------------------------------------------
 // small kernels
@@ -255,11 +262,13 @@ hipError_t launch_slot_rows(const void* src, int32_t src_dtype, int64_t src_ld, 
                             int64_t n_tokens, int64_t top_k, int32_t n_experts, int64_t K, const void* w,
                             int32_t w_dtype, int32_t w_round, bool clear, int32_t op_dtype, void* A,
                             hipStream_t stream);
-// out[t][n] = sum_c A[t][c] B[c][n] (A [T][C], B [C][N] row-major, op dtype;
-// fp32 accumulation; rocBLAS, atomics off).  On a rocBLAS error returns
-// hipErrorUnknown with its status in *status.
-hipError_t dense_rows_gemm(const void* A, const void* B, int64_t T, int64_t C, int64_t N, int32_t op_dtype, void* out,
-                           int32_t out_dtype, int64_t out_ld, hipStream_t stream, int* status);
+// out[t][n] = sum_c A[t][c] B[c][n] (A [T][C] row-major; B as [C][N] rows,
+// or, when `b_by_col`, as B^T [N][C] rows; op dtype; fp32 accumulation;
+// rocBLAS, atomics off).  On a rocBLAS error returns hipErrorUnknown with its
+// status in *status.
+hipError_t dense_rows_gemm(const void* A, const void* B, bool b_by_col, int64_t T, int64_t C, int64_t N,
+                           int32_t op_dtype, void* out, int32_t out_dtype, int64_t out_ld, hipStream_t stream,
+                           int* status);
 constexpr int32_t kDenseMaxExperts = 4096;  // the slot kernel's per-wave LDS table
 // GELU (erf form) over rows: y = rnd(gelu(h)); its backward
 // dh = rnd(dy * gelu'(h)) (the formula of torch's gelu backward).

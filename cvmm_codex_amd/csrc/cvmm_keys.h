@@ -12,9 +12,29 @@ struct CastArgs {
   const float* keys;
   int64_t se, si;  // element strides of expert and d_in (d_out is unit-stride)
   int64_t d_in, d_out;
-  OutT* kt;        // [E][d_out][d_in] or nullptr
-  OutT* kn;        // [E][d_in][d_out] or nullptr
+  OutT* kt;        // rows of d_in values, one per (expert, d_out column), or nullptr
+  OutT* kn;        // rows of d_out values, one per (expert, d_in row), or nullptr
+  int64_t t_se, t_sr;  // kt element strides of expert and row (d_in is unit-stride)
+  int64_t n_se, n_sr;  // kn element strides of expert and row (d_out is unit-stride)
 };
+
+// The output strides of a cast layout (CVMM_CAST_*_INTERLEAVED bits):
+// kt [E][d_out][d_in] or, interleaved, [d_out][E][d_in]; kn [E][d_in][d_out]
+// or, interleaved, [d_in][E][d_out].  The interleaved copies are the
+// [N][E*K] row-major B^T of a dense top-k GEMM with both operands
+// k-contiguous.
+template <typename OutT>
+inline CastArgs<OutT> make_cast_args(const void* keys, int64_t se, int64_t si, int64_t n_experts, int64_t d_in,
+                                     int64_t d_out, void* kt, void* kn, int32_t layout) {
+  CastArgs<OutT> a{static_cast<const float*>(keys), se, si, d_in, d_out, static_cast<OutT*>(kt),
+                   static_cast<OutT*>(kn), 0, 0, 0, 0};
+  const bool ti = (layout & kCastTInterleaved) != 0, ni = (layout & kCastNInterleaved) != 0;
+  a.t_se = ti ? d_in : d_out * d_in;
+  a.t_sr = ti ? n_experts * d_in : d_in;
+  a.n_se = ni ? d_out : d_in * d_out;
+  a.n_sr = ni ? n_experts * d_out : d_out;
+  return a;
+}
 
 // One 64 x 64 tile (expert e, d_in tile ti, d_out tile tj) of fp32 keys with
 // unit column stride, 16-byte aligned rows, d_in and d_out multiples of 64:
@@ -47,7 +67,7 @@ __device__ __forceinline__ void cast_tile_vec(const CastArgs<OutT>& a, int64_t e
       pk.h[1] = from_f32<OutT>(v.y);
       pk.h[2] = from_f32<OutT>(v.z);
       pk.h[3] = from_f32<OutT>(v.w);
-      *reinterpret_cast<uint2*>(a.kn + (e * a.d_in + i0 + r) * a.d_out + j0 + c4) = pk.u;
+      *reinterpret_cast<uint2*>(a.kn + e * a.n_se + (i0 + r) * a.n_sr + j0 + c4) = pk.u;
     }
   }
   if (a.kt == nullptr) return;
@@ -59,7 +79,7 @@ __device__ __forceinline__ void cast_tile_vec(const CastArgs<OutT>& a, int64_t e
     union { uint4 u; OutT h[8]; } pk;
 #pragma unroll
     for (int k = 0; k < 8; ++k) pk.h[k] = from_f32<OutT>(tile[i8 + k][j]);
-    *reinterpret_cast<uint4*>(a.kt + (e * a.d_out + j0 + j) * a.d_in + i0 + i8) = pk.u;
+    *reinterpret_cast<uint4*>(a.kt + e * a.t_se + (j0 + j) * a.t_sr + i0 + i8) = pk.u;
   }
 }
 
@@ -93,7 +113,7 @@ __device__ __forceinline__ void cast_tile_vec128(const CastArgs<OutT>& a, int64_
       union { uint4 u; OutT h[8]; } pk;
 #pragma unroll
       for (int k = 0; k < 8; ++k) pk.h[k] = from_f32<OutT>(f[k]);
-      *reinterpret_cast<uint4*>(a.kn + (e * a.d_in + i0 + r) * a.d_out + j0 + c8) = pk.u;
+      *reinterpret_cast<uint4*>(a.kn + e * a.n_se + (i0 + r) * a.n_sr + j0 + c8) = pk.u;
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) tile[r][c8 + k] = f[k];
@@ -107,7 +127,7 @@ __device__ __forceinline__ void cast_tile_vec128(const CastArgs<OutT>& a, int64_
     union { uint4 u; OutT h[8]; } pk;
 #pragma unroll
     for (int k = 0; k < 8; ++k) pk.h[k] = from_f32<OutT>(tile[i8 + k][j]);
-    *reinterpret_cast<uint4*>(a.kt + (e * a.d_out + j0 + j) * a.d_in + i0 + i8) = pk.u;
+    *reinterpret_cast<uint4*>(a.kt + e * a.t_se + (j0 + j) * a.t_sr + i0 + i8) = pk.u;
   }
 }
 

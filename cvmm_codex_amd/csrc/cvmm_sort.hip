@@ -506,11 +506,13 @@ void launch_scatter_cast(const ScatterArgs<IdxT>& a, const CastRequest& cr, size
   allow_lds(sort_scatter_cast_kernel<IdxT, bf16_t>, lds);
   allow_lds(sort_scatter_cast_kernel<IdxT, f16_t>, lds);
   if (cr.out_dtype == kBF16) {
-    const CastArgs<bf16_t> c{(const float*)cr.keys, cr.se, cr.si, cr.d_in, cr.d_out, (bf16_t*)cr.kt, (bf16_t*)cr.kn};
+    const CastArgs<bf16_t> c =
+        make_cast_args<bf16_t>(cr.keys, cr.se, cr.si, cr.n_experts, cr.d_in, cr.d_out, cr.kt, cr.kn, cr.layout);
     hipLaunchKernelGGL((sort_scatter_cast_kernel<IdxT, bf16_t>), dim3((unsigned)grid), dim3(kSortThreads), lds, stream,
                        a, c);
   } else {
-    const CastArgs<f16_t> c{(const float*)cr.keys, cr.se, cr.si, cr.d_in, cr.d_out, (f16_t*)cr.kt, (f16_t*)cr.kn};
+    const CastArgs<f16_t> c =
+        make_cast_args<f16_t>(cr.keys, cr.se, cr.si, cr.n_experts, cr.d_in, cr.d_out, cr.kt, cr.kn, cr.layout);
     hipLaunchKernelGGL((sort_scatter_cast_kernel<IdxT, f16_t>), dim3((unsigned)grid), dim3(kSortThreads), lds, stream,
                        a, c);
   }

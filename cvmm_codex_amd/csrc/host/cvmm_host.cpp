@@ -185,11 +185,27 @@ std::vector<Tensor> sort_routes(const Tensor& raw, int64_t n_experts, int64_t to
   return {ssel, perm, tok, off, pos};
 }
 
+// The op-dtype weight copies of a cast (`layout`: CVMM_CAST_* bits): kt
+// [E, d_out, d_in] or, interleaved, [d_out, E, d_in]; kn [E, d_in, d_out] or
+// [d_in, E, d_out].
+std::tuple<OptT, OptT> cast_outputs(const Tensor& keys, at::ScalarType op, bool want_t, bool want_n,
+                                    int64_t layout) {
+  const int64_t E = keys.size(0), d_in = keys.size(1), d_out = keys.size(2);
+  OptT kt, kn;
+  if (want_t)
+    kt = (layout & CVMM_CAST_T_INTERLEAVED) ? at::empty({d_out, E, d_in}, opts(keys, op))
+                                            : at::empty({E, d_out, d_in}, opts(keys, op));
+  if (want_n)
+    kn = (layout & CVMM_CAST_N_INTERLEAVED) ? at::empty({d_in, E, d_out}, opts(keys, op))
+                                            : at::empty({E, d_in, d_out}, opts(keys, op));
+  return {kt, kn};
+}
+
 // The sort and the same step's weight cast in one call (the cast runs in the
 // scatter launch): (sorted, perm, perm // top_k, offsets, route_pos), kt, kn.
 std::tuple<std::vector<Tensor>, OptT, OptT> sort_routes_cast(const Tensor& raw, int64_t n_experts, int64_t top_k,
                                                              const Tensor& keys, int64_t op_id, bool want_t,
-                                                             bool want_n, int64_t stream) {
+                                                             bool want_n, int64_t layout, int64_t stream) {
   require_device(raw, "sel");
   require_device(keys, "keys");
   Tensor flat = raw.reshape({-1});
@@ -203,9 +219,7 @@ std::tuple<std::vector<Tensor>, OptT, OptT> sort_routes_cast(const Tensor& raw, 
   const auto op = dtype_of(op_id);
   const int64_t E = keys.size(0), d_in = keys.size(1), d_out = keys.size(2);
   if (E != n_experts) throw py::value_error("cvmm: keys.shape[0] differs from the expert count");
-  OptT kt, kn;
-  if (want_t) kt = at::empty({E, d_out, d_in}, opts(keys, op));
-  if (want_n) kn = at::empty({E, d_in, d_out}, opts(keys, op));
+  auto [kt, kn] = cast_outputs(keys, op, want_t, want_n, layout);
   const size_t ws_bytes = cvmm_sort_workspace_bytes(R, (int32_t)n_experts);
   Tensor ws = sort_workspace(flat, stream, ws_bytes);
   check(cvmm_sort_routes_cast_keys(ptr(flat), flat.scalar_type() == at::kLong ? 1 : 0, R, (int32_t)n_experts,
@@ -213,7 +227,7 @@ std::tuple<std::vector<Tensor>, OptT, OptT> sort_routes_cast(const Tensor& raw, 
                                    tptr<int64_t>(tok), tptr<int64_t>(off), tptr<int32_t>(pos), nullptr, ptr(ws),
                                    (size_t)ws.numel(), ptr(keys), dtype_id(keys.scalar_type()), d_in, d_out,
                                    keys.stride(0), keys.stride(1), keys.stride(2), (int32_t)op_id, ptr(kt), ptr(kn),
-                                   (void*)stream),
+                                   (int32_t)layout, (void*)stream),
         "cvmm_sort_routes_cast_keys");
   return {{ssel, perm, tok, off, pos}, kt, kn};
 }
@@ -286,17 +300,17 @@ Tensor expert_offsets(const Tensor& sorted, int64_t n_experts, int64_t stream) {
   return out;
 }
 
-// keys [E, d_in, d_out] -> op-dtype copies kt [E, d_out, d_in] (forward) and
-// kn [E, d_in, d_out] (grad-input), one pass.
-std::tuple<OptT, OptT> cast_keys(const Tensor& keys, int64_t op_id, bool want_t, bool want_n, int64_t stream) {
+// keys [E, d_in, d_out] -> op-dtype copies kt (forward) and kn (grad-input)
+// in the layouts of cast_outputs, one pass.
+std::tuple<OptT, OptT> cast_keys(const Tensor& keys, int64_t op_id, bool want_t, bool want_n, int64_t layout,
+                                 int64_t stream) {
   require_device(keys, "keys");
   const auto op = dtype_of(op_id);
   const int64_t E = keys.size(0), d_in = keys.size(1), d_out = keys.size(2);
-  OptT kt, kn;
-  if (want_t) kt = at::empty({E, d_out, d_in}, opts(keys, op));
-  if (want_n) kn = at::empty({E, d_in, d_out}, opts(keys, op));
+  auto [kt, kn] = cast_outputs(keys, op, want_t, want_n, layout);
   check(cvmm_cast_keys(ptr(keys), dtype_id(keys.scalar_type()), (int32_t)E, d_in, d_out, keys.stride(0),
-                       keys.stride(1), keys.stride(2), (int32_t)op_id, ptr(kt), ptr(kn), (void*)stream),
+                       keys.stride(1), keys.stride(2), (int32_t)op_id, ptr(kt), ptr(kn), (int32_t)layout,
+                       (void*)stream),
         "cvmm_cast_keys");
   return {kt, kn};
 }
@@ -305,7 +319,8 @@ std::tuple<OptT, OptT> cast_keys(const Tensor& keys, int64_t op_id, bool want_t,
 // forward (cvmm.py:1524-1550): returns [out_rows, d_out] in the op dtype
 // ---------------------------------------------------------------------------
 // The op-dtype weight copy a call reads, as the logical [E, d_in, d_out]
-// view: `copy` is the [E, d_out, d_in] copy when `is_t`, else [E, d_in, d_out].
+// view: `copy` is the [E, d_out, d_in] copy when `is_t`, else the view itself
+// (a [E, d_in, d_out] copy, or an interleaved copy already viewed so).
 Tensor copy_view(const Tensor& copy, bool is_t) { return is_t ? copy.transpose(1, 2) : copy; }
 
 Tensor forward(const Tensor& x, const Tensor& keys, const OptT& keys_op, bool keys_op_is_t, const Tensor& sel,
@@ -530,9 +545,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("route_topk_backward", &route_topk_backward, py::arg("logits"), py::arg("sel"), py::arg("grad_weights"),
         py::arg("top_k"), py::arg("renormalize"), py::arg("stream"));
   m.def("sort_routes_cast", &sort_routes_cast, py::arg("raw"), py::arg("n_experts"), py::arg("top_k"),
-        py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"), py::arg("stream"));
-  m.def("cast_keys", &cast_keys, py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"),
+        py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"), py::arg("layout"),
         py::arg("stream"));
+  m.def("cast_keys", &cast_keys, py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"),
+        py::arg("layout"), py::arg("stream"));
   m.def("forward", &forward);
   m.def("forward_gelu", &forward_gelu);
   m.def("gelu_backward", &gelu_backward, py::arg("grad"), py::arg("pre_act"), py::arg("stream"));

@@ -185,7 +185,7 @@ int cvmm_sort_routes_cast_keys(const void* sel, int32_t sel_is_int64, int64_t n_
                                int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* workspace,
                                size_t workspace_bytes, const void* keys, int32_t keys_dtype, int64_t d_in,
                                int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj, int32_t out_dtype,
-                               void* keys_t, void* keys_n, void* stream);
+                               void* keys_t, void* keys_n, int32_t layout, void* stream);
 
 /* Router (no counterpart in cvmm.py; replaces its callers' router lines,
  * benchmark_ffn_moe.py:91-97 and benchmark_framework_moe.py:129-135:
@@ -226,11 +226,18 @@ int cvmm_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_e
 /* Cast the expert weights once per step to the MFMA operand type (bf16/f16)
  * in the two k-contiguous layouts the routed GEMMs read:
  *   keys_t [E][d_out][d_in]  (forward)   keys_n [E][d_in][d_out]  (grad-input)
- * Either output may be NULL.  Replaces the per-tile in-register weight cast
+ * Either output may be NULL.  `layout` bits interleave the experts between
+ * the rows instead: CVMM_CAST_T_INTERLEAVED writes keys_t as
+ * [d_out][E][d_in], CVMM_CAST_N_INTERLEAVED keys_n as [d_in][E][d_out] -- the
+ * B^T rows of a dense top-k sum (cvmm_topk_dense), passed to cvmm_fwd /
+ * cvmm_bwd_x as the logical [E, d_in, d_out] view (strides (d_in, 1, E*d_in)
+ * and (d_out, E*d_out, 1)).  Replaces the per-tile in-register weight cast
  * of cvmm_kernel (cvmm.py:198-204) with one pass per step; RNE rounding. */
+#define CVMM_CAST_T_INTERLEAVED 1
+#define CVMM_CAST_N_INTERLEAVED 2
 int cvmm_cast_keys(const void* keys, int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out,
                    int64_t k_se, int64_t k_si, int64_t k_sj, int32_t out_dtype, void* keys_t, void* keys_n,
-                   void* stream);
+                   int32_t layout, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Forward: CVMM.forward (cvmm.py:1524-1550) = cvmm_triton (cvmm.py:814-867)  */

@@ -177,6 +177,40 @@ def test_dense_topk_keys_cast_into_the_workspace(dense):
     assert U.norm_rel(U.to_np(y), exp2["out"]) <= 2e-2
 
 
+def test_dense_topk_reads_either_weight_row_layout(dense):
+    """The dense GEMM's B as given: the expert-interleaved copy ([N][E*K]
+    rows, both operands k-contiguous; what cvmm() casts for a dense sum) or
+    the routed-layout copy of the other orientation ([E*K][N] rows), for the
+    token gradient and for the weighted forward, each against the oracle."""
+    class Ctx:
+        op_type = torch.bfloat16
+
+    x, keys, sel, _, go = _case(15, 2, 160, 64, 128, 16, 4, False, False)
+    s = C.cvmm_prepare_sel2(sel.cuda())
+    C.create_kernels()
+    s._resolve(16)
+    xd, kd, gd = x.cuda(), keys.cuda(), go.cuda()
+    exp = U.run_oracle(x, keys, sel, None, go, False, True)
+    kt, _ = C._cast_keys(kd, torch.bfloat16, C._CopyPlan(True, False, 0, True, False))
+    _, kn_i = C._cast_keys(kd, torch.bfloat16, C._CopyPlan(False, True, N.CAST_N_INTERLEAVED, True, False))
+    assert kn_i.shape == (64, 16, 128)
+    for keys_x, is_t in ((kt, True), (kn_i.permute(1, 0, 2), False)):
+        gx, _, _ = C._backward(Ctx, gd, xd, kd, s.raw_sel, s.sel, s.sel_index, s.out_index, None, True, False,
+                               False, keys_x=keys_x, keys_x_is_t=is_t)
+        assert U.norm_rel(U.to_np(gx), exp["x_grad"]) <= 2e-2, is_t
+
+    x2, keys2, sel2, w2, go2 = _case(16, 2, 160, 64, 128, 16, 4, True, True)
+    s2 = C.cvmm_prepare_sel2(sel2.cuda(), w2.cuda(), route_input=True)
+    s2._resolve(16)
+    k2 = keys2.cuda()
+    exp2 = U.run_oracle(x2, keys2, sel2, w2, go2, True, True)
+    kt_i, kn = C._cast_keys(k2, torch.bfloat16, C._CopyPlan(True, True, N.CAST_T_INTERLEAVED, True, False))
+    assert kt_i.shape == (128, 16, 64) and kn.shape == (16, 64, 128)
+    for keys_op in (kn, kt_i.permute(1, 2, 0)):
+        y = C._forward(x2.cuda(), s2.sel_index, s2.sel, k2, s2.out_index, w2.cuda(), torch.bfloat16, keys_op, False)
+        assert U.norm_rel(U.to_np(y), exp2["out"]) <= 2e-2
+
+
 def test_dense_workspace_zeroed_flag(dense):
     """Through the C ABI: without CVMM_FLAG_WORKSPACE_ZEROED the call fills
     the slotted rows itself (the workspace may hold anything); with it the

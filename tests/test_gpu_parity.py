@@ -244,10 +244,13 @@ def test_sort_int64_ids_wrap_like_int32_cast():
     (777, 300, 1, 256, 64, True), (4000, 16, 4, 96, 128, False), (5000, 5, 2, 192, 384, True),
     (524288, 256, 64, 2048, 64, True),   # SwitchHead size: the column-scan scatter beside the cast
 ])
-def test_sort_and_cast_in_one_call_match_the_separate_calls(R, E, k, d_in, d_out, fused):
+@pytest.mark.parametrize("layout", [0, 3])
+def test_sort_and_cast_in_one_call_match_the_separate_calls(R, E, k, d_in, d_out, fused, layout):
     """cvmm_sort_routes_cast_keys (scatter and weight cast in one launch where
     the vectorised cast applies, else the two calls) gives the bits of
-    cvmm_sort_routes + cvmm_cast_keys; out-of-range ids included."""
+    cvmm_sort_routes + cvmm_cast_keys; out-of-range ids included.  Both copy
+    layouts: routed ([E, d_out, d_in], [E, d_in, d_out]) and expert-interleaved
+    ([d_out, E, d_in], [d_in, E, d_out]), each against torch's own cast."""
     from cvmm_codex_amd import _native as N
     lib = N.lib()
     g = torch.Generator().manual_seed(R + E)
@@ -263,8 +266,10 @@ def test_sort_and_cast_in_one_call_match_the_separate_calls(R, E, k, d_in, d_out
                     off=torch.full((E,), -7, dtype=torch.int64, device="cuda"),
                     pos=torch.full((R,), -7, dtype=torch.int32, device="cuda"),
                     nin=torch.full((1,), -7, dtype=torch.int32, device="cuda"),
-                    kt=torch.zeros(E, d_out, d_in, dtype=torch.bfloat16, device="cuda"),
-                    kn=torch.zeros(E, d_in, d_out, dtype=torch.bfloat16, device="cuda"),
+                    kt=torch.zeros(*((d_out, E, d_in) if layout & 1 else (E, d_out, d_in)),
+                                   dtype=torch.bfloat16, device="cuda"),
+                    kn=torch.zeros(*((d_in, E, d_out) if layout & 2 else (E, d_in, d_out)),
+                                   dtype=torch.bfloat16, device="cuda"),
                     ws=torch.empty(ws_b, dtype=torch.uint8, device="cuda"))
 
     a, b = outputs(), outputs()
@@ -272,14 +277,15 @@ def test_sort_and_cast_in_one_call_match_the_separate_calls(R, E, k, d_in, d_out
                            N.ptr(o["off"]), N.ptr(o["pos"]), N.ptr(o["nin"]), N.ptr(o["ws"]), ws_b)
     key_args = (N.ptr(keys), N.F32)
     N.check(lib.cvmm_sort_routes(*sort_args(a), st), "sort")
-    N.check(lib.cvmm_cast_keys(*key_args, E, d_in, d_out, *keys.stride(), N.BF16, N.ptr(a["kt"]), N.ptr(a["kn"]), st),
-            "cast")
+    N.check(lib.cvmm_cast_keys(*key_args, E, d_in, d_out, *keys.stride(), N.BF16, N.ptr(a["kt"]), N.ptr(a["kn"]),
+                               layout, st), "cast")
     N.check(lib.cvmm_sort_routes_cast_keys(*sort_args(b), *key_args, d_in, d_out, *keys.stride(), N.BF16,
-                                           N.ptr(b["kt"]), N.ptr(b["kn"]), st), "sort+cast")
+                                           N.ptr(b["kt"]), N.ptr(b["kn"]), layout, st), "sort+cast")
     for n in ("ssel", "perm", "tok", "off", "pos", "nin", "kt", "kn"):
         assert torch.equal(a[n], b[n]), n
-    assert torch.equal(b["kn"], keys.to(torch.bfloat16))
-    assert torch.equal(b["kt"], keys.transpose(1, 2).contiguous().to(torch.bfloat16))
+    kb = keys.to(torch.bfloat16)
+    assert torch.equal(b["kn"], kb.permute(1, 0, 2) if layout & 2 else kb)
+    assert torch.equal(b["kt"], kb.permute(2, 0, 1) if layout & 1 else kb.transpose(1, 2))
     assert fused == (d_in % 64 == 0 and d_out % 64 == 0)
 
 
