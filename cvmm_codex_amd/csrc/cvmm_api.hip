@@ -1046,16 +1046,26 @@ int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, con
   p.M = d_in; p.N = d_out;
   p.offsets = offs; p.n_experts = n_experts; p.n_routes = n_routes;
   p.dw = grad_keys; p.dw_dtype = grad_keys_dtype; p.dw_se = gk_se; p.dw_sm = gk_si; p.dw_sn = gk_sj;
-  // tile-major by default: measured faster on every benchmark shape (the
-  // activation column slice of one tile, shared by the top-k experts of each
-  // token, stays in one XCD's L2)
-  const int32_t order = g_wgrad_order.load();
-  p.order = order == 1 ? kWgOrderChunk : order == 3 ? kWgOrderChunkXcd : kWgOrderTile;
   // dW tile: the knob, else 256 x 256 where both sides fill it and the grid
   // still holds >= 4 workgroups per CU (the FFN stack's 2048 x 512: 1.6 -> 0.8 ms per
   // launch; the gathered bytes per flop halve against 128 x 128)
   const int32_t tile = g_wgrad_tile.load();
   p.tile_choice = tile > 0 ? tile - 1 : wgrad_auto_tile(d_in, d_out, p.grid_chunks);
+  // Workgroup order: the knob, else chunk-xcd for the 16-bit kernel's 128 x
+  // 128 tile (ff_up 38.5 -> 35.0 us, ff_down 52.9 -> 50.8 us per launch: the
+  // eight dW tiles of a chunk share its routes' gradient rows in one L2) and
+  // tile-major for the other tiles (the activation column slice of one tile,
+  // shared by the top-k experts of each token, stays in one XCD's L2:
+  // switch_v 223 us against 249 with chunk-xcd, the FFN stack 4.49 against
+  // 4.55 ms).  Every order gives the same bits.
+  const int32_t order = g_wgrad_order.load();
+  if (order == 0) {
+    int bm, bn;
+    wgrad_fast_tile(d_in, d_out, p.tile_choice, &bm, &bn);
+    p.order = wgrad_fast_eligible(p, op_dtype) && bm == 128 && bn == 128 ? kWgOrderChunkXcd : kWgOrderTile;
+  } else {
+    p.order = order == 1 ? kWgOrderChunk : order == 3 ? kWgOrderChunkXcd : kWgOrderTile;
+  }
   return check_launch(timed(CVMM_KC_WGRAD, s, [&] { return launch_wgrad(p, op_dtype, s); }), "cvmm_bwd_w(gemm)");
 }
 

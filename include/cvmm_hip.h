@@ -82,8 +82,8 @@ int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launche
  *     routed GEMM (1..4096).
  *   CVMM_TUNE_WGRAD_ORDER: workgroup order of the weight-gradient kernel,
  *     1 = the tiles of one expert chunk on one XCD, 2 = one dW tile of every
- *     expert on one XCD (the built-in choice), 3 = expert chunk c on XCD
- *     c % 8 with all its tiles.
+ *     expert on one XCD, 3 = expert chunk c on XCD c % 8 with all its tiles.
+ *     Built in: 3 for the 16-bit kernel's 128 x 128 dW tile, else 2.
  *   CVMM_TUNE_WGRAD_TILE: dW tile of the 16-bit weight-gradient kernel where
  *     its base tile is 128 x 128 and dW is contiguous aligned fp32: 1 = 128 x
  *     128, 2 = 256 x 128, 3 = 128 x 256, 4 = 256 x 256.  Built in: 256 x 256
