@@ -95,6 +95,15 @@ inline FastDiv make_fast_div(int64_t d) {
   return FastDiv{m, 31 + l};
 }
 
+// The same constants computed on the device, for 1 <= d < 2^31: then
+// 2^(31+l) < 2^63 and 64-bit arithmetic suffices.
+__device__ __forceinline__ FastDiv make_fast_div_dev(int64_t d) {
+  int l = 0;
+  while ((1ll << l) < d) ++l;
+  const uint64_t num = 1ull << (31 + l);
+  return FastDiv{(num + (uint64_t)d - 1) / (uint64_t)d, 31 + l};
+}
+
 // Wave helpers (64-wide wavefronts).
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
@@ -106,6 +115,18 @@ __device__ __forceinline__ int64_t wave_incl_scan(int64_t v) {
     if (lane >= d) v += o;
   }
   return v;
+}
+
+// Workgroup barrier for a hand-over through LDS only: this wave's LDS
+// operations complete (lgkmcnt(0)), then s_barrier.  __syncthreads() would
+// also wait for the wave's outstanding global stores (its release fence),
+// which a hand-over of LDS data does not need when no thread of the launch
+// reads those stores.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt at their maxima
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // Map a linear workgroup id so that consecutive logical ids are dispatched to

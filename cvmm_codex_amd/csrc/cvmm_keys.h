@@ -71,7 +71,7 @@ __device__ __forceinline__ void cast_tile_vec(const CastArgs<OutT>& a, int64_t e
     }
   }
   if (a.kt == nullptr) return;
-  __syncthreads();
+  lds_barrier();  // the tile is complete; the kn stores need not have landed
   const int i8 = (t & 7) * 8;
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
@@ -119,7 +119,7 @@ __device__ __forceinline__ void cast_tile_vec128(const CastArgs<OutT>& a, int64_
     for (int k = 0; k < 8; ++k) tile[r][c8 + k] = f[k];
   }
   if (a.kt == nullptr) return;
-  __syncthreads();
+  lds_barrier();  // the tile is complete; the kn stores need not have landed
   const int i8 = (t & 7) * 8;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {

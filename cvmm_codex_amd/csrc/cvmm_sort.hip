@@ -125,7 +125,114 @@ __device__ void scatter_chunk(const IdxT* __restrict__ sel, int64_t n_routes, in
         if (token_index != nullptr) token_index[p] = i / top_k;
         if (route_pos != nullptr) route_pos[i] = (int32_t)p;
       }
-      __syncthreads();
+      lds_barrier();  // pos[] is handed to the next wave; the stores may still be in flight
+    }
+  }
+}
+
+// Routes per wave of the turn-free scatter: a quarter of the chunk, whole
+// 64-route rounds.
+__host__ __device__ inline int64_t scatter_wave_span(int64_t n) { return ((n + 3) / 4 + 63) / 64 * 64; }
+
+// Stable scatter of one chunk without turns between the waves: wave w owns
+// the routes [lo + w * span, lo + (w + 1) * span).  It counts them per
+// bucket (64 at a time: one ballot per bucket bit ranks the lanes of a
+// bucket, the lowest lane adds the count), an exclusive scan over the four
+// waves gives every wave its first output position per bucket, and each
+// wave then writes its routes.  Equal buckets keep route order: a wave's
+// routes precede the next wave's, and a wave goes through its rounds and
+// lanes in route order.  Two barriers per chunk, where the turns of
+// scatter_chunk take one per wave and 256-route round.  `pos`: the chunk's
+// first output position per bucket; `wpos`: 4 x (E + 1) LDS ints; `pre`: the
+// wave's first rounds' ids.
+template <typename IdxT>
+__device__ void scatter_chunk_waves(const IdxT* __restrict__ sel, int64_t n_routes, int32_t n_experts, int64_t chunk,
+                                    int32_t n_bits, int64_t top_k, const int32_t* pos, int32_t* wpos,
+                                    int32_t* __restrict__ sorted_sel, int64_t* __restrict__ perm,
+                                    int64_t* __restrict__ token_index, int32_t* __restrict__ route_pos, int64_t b,
+                                    const IdxT (&pre)[kSortPrefetch]) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = lane_id();
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int32_t nb = n_experts + 1;
+  const int64_t lo = b * chunk;
+  const int64_t hi = min(lo + chunk, n_routes);
+  const int64_t span = scatter_wave_span(hi - lo);
+  const int64_t w_lo = lo + wave * span;
+  const int64_t w_hi = min(w_lo + span, hi);
+  int32_t* mine = wpos + wave * nb;
+  for (int32_t e = lane; e < nb; e += 64) mine[e] = 0;
+  // route indices are < 2^31; a top_k at least that large puts every route in token 0
+  const bool huge_k = top_k >= (int64_t(1) << 31);
+  const FastDiv by_k = make_fast_div_dev(huge_k ? 1 : top_k);
+
+  // one 64-route round: the route's key, bucket, rank among its bucket's
+  // lanes and the bucket's lane count
+  auto round_of = [&](int r, int64_t base, IdxT& key, int32_t& bucket, int& rank, int& cnt) {
+    const int64_t i = base + lane;
+    const bool valid = i < w_hi;
+    key = (IdxT)0;
+    if (r < kSortPrefetch) {
+#pragma unroll
+      for (int q = 0; q < kSortPrefetch; ++q)
+        if (q == r) key = pre[q];
+    } else if (valid) {
+      key = sel[i];
+    }
+    bucket = valid ? bucket_of(key, n_experts) : 0;
+    uint64_t peers = __ballot(valid);
+    for (int bit = 0; bit < n_bits; ++bit) {
+      const bool set = (bucket >> bit) & 1;
+      const uint64_t bb = __ballot(set);
+      peers &= set ? bb : ~bb;
+    }
+    rank = valid ? __popcll(peers & lt_mask) : -1;
+    cnt = __popcll(peers);
+  };
+
+  // counts need no ranks: one LDS add per route
+  int r = 0;
+  for (int64_t base = w_lo; base < w_hi; base += 64, ++r) {
+    const int64_t i = base + lane;
+    if (i < w_hi) {
+      IdxT key = (IdxT)0;
+      if (r < kSortPrefetch) {
+#pragma unroll
+        for (int q = 0; q < kSortPrefetch; ++q)
+          if (q == r) key = pre[q];
+      } else {
+        key = sel[i];
+      }
+      atomicAdd(&mine[bucket_of(key, n_experts)], 1);
+    }
+  }
+  lds_barrier();
+  for (int32_t e = threadIdx.x; e < nb; e += kSortThreads) {
+    int32_t run = pos[e];
+#pragma unroll
+    for (int w = 0; w < kSortThreads / 64; ++w) {
+      const int32_t c = wpos[w * nb + e];
+      wpos[w * nb + e] = run;
+      run += c;
+    }
+  }
+  lds_barrier();
+  r = 0;
+  for (int64_t base = w_lo; base < w_hi; base += 64, ++r) {
+    IdxT key;
+    int32_t bucket;
+    int rank, cnt;
+    round_of(r, base, key, bucket, rank, cnt);
+    if (rank >= 0) {
+      const int64_t i = base + lane;
+      const int32_t p0 = mine[bucket];
+      const int64_t p = (int64_t)p0 + rank;
+      sorted_sel[p] = (int32_t)key;
+      perm[p] = i;
+      if (token_index != nullptr) token_index[p] = huge_k ? 0 : by_k.div(i);
+      if (route_pos != nullptr) route_pos[i] = (int32_t)p;
+      // after the wave's reads of this round (LDS operations of a wave run in order)
+      if (rank == 0) mine[bucket] = p0 + cnt;
     }
   }
 }
@@ -192,7 +299,7 @@ __device__ void scatter_chunk_local(const IdxT* __restrict__ sel, int64_t n_rout
         l_route[lp] = (int32_t)(i - lo);
         if (route_pos != nullptr) route_pos[i] = gpos[bucket] + (lp - lbase[bucket]);
       }
-      __syncthreads();
+      lds_barrier();  // lpos[] and the local order are handed on through LDS
     }
   }
   const int32_t n = (int32_t)(hi - lo);
@@ -212,7 +319,10 @@ __device__ void scatter_chunk_local(const IdxT* __restrict__ sel, int64_t n_rout
 // order (the launch that casts beside it lends the cast's tile instead).
 size_t scatter_lds_bytes(int32_t n_experts) {
   const int32_t nb = n_experts + 1;
-  if (nb <= kSortLocalBuckets) return (size_t)4 * nb * sizeof(int32_t);
+  // positions, then totals / local positions / local bases, or the
+  // turn-free scatter's 4 x nb wave positions (over the totals, which are
+  // dead by then)
+  if (nb <= kSortLocalBuckets) return (size_t)5 * nb * sizeof(int32_t);
   return (size_t)(nb <= kSortFastBuckets ? 2 : 1) * nb * sizeof(int32_t);
 }
 static size_t scatter_kernel_lds_bytes(int32_t n_experts) {
@@ -259,17 +369,22 @@ __device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b
   // through LDS (scatter_chunk_local): the chunk's own count of each bucket
   // goes to lbase (then its exclusive scan) beside pos and the totals
   const bool local = nb <= kSortLocalBuckets && chunk <= kSortLocalChunk && n_routes >= kSortLocalMinRoutes;
+  // the turn-free scatter (scatter_chunk_waves) where its wave positions fit
+  const bool waves = !local && nb <= kSortLocalBuckets;
   int32_t* lpos = sh + 2 * nb;
   int32_t* lbase = sh + 3 * nb;
   // the first rounds' ids, loaded before the count-matrix pass so that their
-  // latency overlaps it
+  // latency overlaps it: 256-route rounds in thread order, or the wave's own
+  // 64-route rounds
   IdxT pre[kSortPrefetch];
   {
     const int64_t lo = b * chunk, hi = min(lo + chunk, n_routes);
+    const int64_t w_lo = lo + (threadIdx.x >> 6) * scatter_wave_span(hi - lo);
+    const int64_t w_hi = min(w_lo + scatter_wave_span(hi - lo), hi);
 #pragma unroll
     for (int r = 0; r < kSortPrefetch; ++r) {
-      const int64_t i = lo + r * kSortThreads + threadIdx.x;
-      pre[r] = i < hi ? a.sel[i] : (IdxT)0;
+      const int64_t i = waves ? w_lo + r * 64 + lane_id() : lo + r * kSortThreads + threadIdx.x;
+      pre[r] = a.sel[i < hi ? i : hi - 1];  // unconditional (see the count pass); masked by index later
     }
   }
   if (a.tot != nullptr) {
@@ -297,28 +412,31 @@ __device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b
       pos[e] = tot[e] = 0;
       if (local) lbase[e] = 0;
     }
-    __syncthreads();
+    lds_barrier();  // (the prefetched ids may still be in flight)
     const int32_t n = (int32_t)(n_chunks * nb);
+    const FastDiv by_nb = make_fast_div_dev(nb);
     constexpr int U = 32;
     for (int32_t i0 = threadIdx.x; i0 < n; i0 += U * kSortThreads) {
       int32_t v[U];
+      // unconditional loads (a clamped index, masked below): a load under a
+      // branch makes the compiler wait for it before the next one
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int32_t i = i0 + u * kSortThreads;
-        v[u] = i < n ? counts[i] : 0;
+        v[u] = counts[i < n ? i : n - 1];
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int32_t i = i0 + u * kSortThreads;
         if (i < n) {
-          const int32_t c = i / nb, e = i - c * nb;
+          const int32_t c = (int32_t)by_nb.div(i), e = i - c * nb;
           atomicAdd(&tot[e], v[u]);
           if (c < b) atomicAdd(&pos[e], v[u]);
           if (local && c == b) lbase[e] = v[u];
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (b == 0 && threadIdx.x == 0 && n_invalid != nullptr) *n_invalid = tot[n_experts];
     block_exclusive_scan(tot, nb);  // tot[e] = first output position of bucket e
     if (b == 0) {
@@ -354,6 +472,11 @@ __device__ void scatter_block(const ScatterArgs<IdxT>& a, int32_t* sh, int64_t b
     int32_t* l_key = reinterpret_cast<int32_t*>(tile);
     scatter_chunk_local(a.sel, n_routes, n_experts, chunk, n_bits, top_k, pos, lpos, lbase, l_key,
                         l_key + kSortLocalChunk, a.sorted_sel, a.perm, a.token_index, a.route_pos, b, pre);
+    return;
+  }
+  if (waves) {
+    scatter_chunk_waves(a.sel, n_routes, n_experts, chunk, n_bits, top_k, pos, sh + nb, a.sorted_sel, a.perm,
+                        a.token_index, a.route_pos, b, pre);
     return;
   }
   scatter_chunk(a.sel, n_routes, n_experts, chunk, n_bits, top_k, pos, a.sorted_sel, a.perm, a.token_index,
