@@ -734,7 +734,7 @@ def main():
     knobs = {"panel_tiles_per_wg": N.TUNE_PANEL_TILES_PER_WG, "wgrad_order": N.TUNE_WGRAD_ORDER,
              "gemm_order": N.TUNE_GEMM_ORDER,
              "wgrad_tile": N.TUNE_WGRAD_TILE, "dense_topk": N.TUNE_DENSE_TOPK,
-             "sort_chunk": N.TUNE_SORT_CHUNK}
+             "sort_chunk": N.TUNE_SORT_CHUNK, "ring_tile": N.TUNE_RING_TILE}
     for kv in args.tune:
         name, _, value = kv.partition("=")
         if name not in knobs:

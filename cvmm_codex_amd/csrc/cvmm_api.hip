@@ -115,6 +115,7 @@ std::atomic<int32_t> g_wgrad_order{0};
 std::atomic<int32_t> g_wgrad_tile{0};
 std::atomic<int32_t> g_gemm_order{0};
 std::atomic<int32_t> g_dense_topk{0};
+std::atomic<int32_t> g_ring_tile{0};
 
 // m-tile order of the routed GEMMs (see GemmParams::token_major): the knob's
 // choice, or -1 to let the kernel launcher decide
@@ -341,6 +342,11 @@ int cvmm_tuning_set(int32_t knob, int64_t value) {
   if (knob == CVMM_TUNE_DENSE_TOPK) {
     if (value < 0 || value > 2) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: dense top-k choice must be 0, 1 or 2");
     g_dense_topk.store((int32_t)value);
+    return CVMM_OK;
+  }
+  if (knob == CVMM_TUNE_RING_TILE) {
+    if (value < 0 || value > 2) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: long-K tile choice must be 0, 1 or 2");
+    g_ring_tile.store((int32_t)value);
     return CVMM_OK;
   }
   if (knob == CVMM_TUNE_WGRAD_ORDER) {
@@ -681,6 +687,7 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
   p.prod_dtype = -1;
   p.w_idx = rp;
   p.panel_tpw = g_panel_tpw.load();
+  p.ring_tile = g_ring_tile.load();
   p.token_major = gemm_token_major(n_experts);
 
   if (!weighted) {
@@ -888,6 +895,7 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
   p.prod_dtype = -1;
   p.role = 1;
   p.panel_tpw = g_panel_tpw.load();
+  p.ring_tile = g_ring_tile.load();
   p.token_major = gemm_token_major(n_experts);
 
   void* route_buf = nullptr;

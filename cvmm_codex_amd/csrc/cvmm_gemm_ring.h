@@ -50,8 +50,10 @@ struct RingCfg {
   static constexpr int SLICE_BYTES = A_BYTES + B_BYTES;
   static constexpr int D = SLICE_BYTES / 4096;         // DMA instructions per wave per slice
   static constexpr int DA = A_BYTES / 4096;            // ... of which for A
-  static constexpr int WN = BN / 64, WM = BM / 64;     // wave grid, 64 x 64 per wave
-  static_assert(WM * WN == 4, "4 waves of 64x64");
+  static constexpr int WN = BN / 64, WM = 4 / WN;      // wave grid: 64 columns per wave
+  static constexpr int WROWS = BM / WM;                // rows per wave: 64, or 80 (160-row tiles)
+  static constexpr int MB = WROWS / 16;                // 16-row MFMA blocks per wave
+  static_assert(WM * WN == 4 && WM * WROWS == BM && WROWS % 16 == 0, "4 waves of whole 16-row blocks");
   static_assert(SLICE_BYTES % 4096 == 0, "whole DMA instructions per wave");
   static_assert(STAGES >= 2 && STAGES <= 5, "ring depth");
   static_assert((STAGES - 2) * D < 64, "vmcnt range");
@@ -64,9 +66,21 @@ __device__ __forceinline__ int ring_swz(int row) {
   else return row & 7;
 }
 
+// lgkmcnt(0) tied to the registers of the fragment reads of one k step (NB
+// B fragments, NA A fragments): no use of them is scheduled before the wait.
+template <int NB, int NA>
+__device__ __forceinline__ void lds_wait_tied_n(lds_u32x4 (&x)[NB], lds_u32x4 (&y)[NA]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x[0]), "+v"(y[0]));
+#pragma unroll
+  for (int i = 1; i < NB; ++i) asm volatile("" : "+v"(x[i]));
+#pragma unroll
+  for (int i = 1; i < NA; ++i) asm volatile("" : "+v"(y[i]));
+}
+
 template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int Role, int BK, bool DG = false>
 __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(const GemmParams p) {
   using Cfg = RingCfg<BM, BN, STAGES, BK>;
+  constexpr int MB = Cfg::MB, WR = Cfg::WROWS;
   static_assert(!RA || Cfg::KSS == 1, "read-ahead keeps one k step per slice");
   __shared__ __attribute__((aligned(1024))) char ring[STAGES * Cfg::SLICE_BYTES];
   __shared__ RouteMeta<BM> meta;
@@ -118,32 +132,36 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   // ---- fragments: lane reads row (l % 16) of each 16-row block, chunk l / 16
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   const int fr = lane & 15, fq = lane >> 4;
-  int a_off[Cfg::KSS][4], b_off[Cfg::KSS][4];  // per k step of a slice
+  int a_off[Cfg::KSS][MB], b_off[Cfg::KSS][4];  // per k step of a slice
 #pragma unroll
-  for (int kk = 0; kk < Cfg::KSS; ++kk)
+  for (int kk = 0; kk < Cfg::KSS; ++kk) {
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int ra = wm * WR + j * 16 + fr;
+      a_off[kk][j] = ra * Cfg::ROWB + (((kk * 4 + fq) ^ ring_swz<Cfg::CPR>(ra)) << 4);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int ra = wm * 64 + i * 16 + fr;
       const int rb = BM + wn * 64 + i * 16 + fr;
-      a_off[kk][i] = ra * Cfg::ROWB + (((kk * 4 + fq) ^ ring_swz<Cfg::CPR>(ra)) << 4);
       b_off[kk][i] = rb * Cfg::ROWB + (((kk * 4 + fq) ^ ring_swz<Cfg::CPR>(rb)) << 4);
     }
-  f32x4_t acc[4][4];  // acc[i][j]: n-block i, m-block j (C^T orientation)
+  }
+  f32x4_t acc[4][MB];  // acc[i][j]: n-block i, m-block j (C^T orientation)
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  auto read_frags = [&](const char* buf, lds_u32x4 (&af)[4], lds_u32x4 (&bf)[4], int kk = 0) {
+    for (int j = 0; j < MB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto read_frags = [&](const char* buf, lds_u32x4 (&af)[MB], lds_u32x4 (&bf)[4], int kk = 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) bf[i] = lds_read128(buf + b_off[kk][i]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) af[j] = lds_read128(buf + a_off[kk][j]);
+    for (int j = 0; j < MB; ++j) af[j] = lds_read128(buf + a_off[kk][j]);
   };
-  auto mfma = [&](lds_u32x4 (&af)[4], lds_u32x4 (&bf)[4]) {
+  auto mfma = [&](lds_u32x4 (&af)[MB], lds_u32x4 (&bf)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) MfmaOp<OpT>::step(acc[i][j], as_uint4(bf[i]), as_uint4(af[j]));
+      for (int j = 0; j < MB; ++j) MfmaOp<OpT>::step(acc[i][j], as_uint4(bf[i]), as_uint4(af[j]));
   };
 
   const int64_t nk = (p.K + Cfg::BK - 1) / Cfg::BK;
@@ -157,13 +175,13 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
       issue(s0, ring + s0 * Cfg::SLICE_BYTES);
       issue_fence();
     }
-    lds_u32x4 a0[4], b0[4], a1[4], b1[4];
+    lds_u32x4 a0[MB], b0[4], a1[MB], b1[4];
     vm_wait<(STAGES - 1) * Cfg::D>();
     wg_barrier();
     read_frags(ring, a0, b0);
-    lds_wait_tied(b0, a0);
+    lds_wait_tied_n(b0, a0);
     int buf = 0;  // buffer of slice s
-    auto step = [&](int64_t s, lds_u32x4 (&ac)[4], lds_u32x4 (&bc)[4], lds_u32x4 (&an)[4], lds_u32x4 (&bn)[4]) {
+    auto step = [&](int64_t s, lds_u32x4 (&ac)[MB], lds_u32x4 (&bc)[4], lds_u32x4 (&an)[MB], lds_u32x4 (&bn)[4]) {
       const int nxt = buf + 1 == STAGES ? 0 : buf + 1;
       vm_wait<(STAGES - 2) * Cfg::D>();  // slice s + 1 has landed (only DMA is in flight)
       wg_barrier();
@@ -171,7 +189,7 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
       issue_fence();
       read_frags(ring + nxt * Cfg::SLICE_BYTES, an, bn);
       mfma(ac, bc);
-      lds_wait_tied(bn, an);
+      lds_wait_tied_n(bn, an);
       buf = nxt;
     };
     for (int64_t s = 0; s < nk; s += 2) {
@@ -195,9 +213,9 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
       issue_fence();
 #pragma unroll
       for (int kk = 0; kk < Cfg::KSS; ++kk) {
-        lds_u32x4 af[4], bf[4];
+        lds_u32x4 af[MB], bf[4];
         read_frags(ring + cur * Cfg::SLICE_BYTES, af, bf, kk);
-        lds_wait_tied(bf, af);
+        lds_wait_tied_n(bf, af);
         mfma(af, bf);
       }
       cur = cur + 1 == STAGES ? 0 : cur + 1;
@@ -208,7 +226,7 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   // workgroup can end and its LDS be handed to another
   vm_wait<0>();
 
-  // ---- epilogue from registers: lane holds C[m = wm*64 + j*16 + fr]
+  // ---- epilogue from registers: lane holds C[m = wm*WR + j*16 + fr]
   // [n = n0 + wn*64 + i*16 + 4*fq + {0..3}]
   const bool has_w = p.w != nullptr;
   // plain: the value is the product rounded once to the output type, which
@@ -218,14 +236,14 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   // DG with 16-bit x: every x piece this lane needs (4 rows x 4 blocks of 4
   // columns, 8 bytes each) is requested before the output stores, so the
   // gathers' latency overlaps them
-  uint2 xpre[4][4];
+  uint2 xpre[MB][4];
   bool xpre_ok = false;
   if constexpr (DG) {
     xpre_ok = p.dg_x_dtype != kF32 && (reinterpret_cast<uintptr_t>(p.dg_x) & 7) == 0 && p.dg_x_ld % 4 == 0;
     if (xpre_ok) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t xr = meta.dgrow[wm * 64 + j * 16 + fr];
+      for (int j = 0; j < MB; ++j) {
+        const int64_t xr = meta.dgrow[wm * WR + j * 16 + fr];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int64_t n = nwave + i * 16 + 4 * fq;
@@ -272,8 +290,8 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
     }
   };
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int m = wm * 64 + j * 16 + fr;
+  for (int j = 0; j < MB; ++j) {
+    const int m = wm * WR + j * 16 + fr;
     const int64_t orow = meta.orow[m];
     float v[4][4];
     if (plain) {
@@ -324,10 +342,10 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
     // x pieces of 4 columns as one 8-byte (16-bit x) or 16-byte (fp32 x) load
     const bool x16 = p.dg_x_dtype != kF32;
     const bool xvec = (reinterpret_cast<uintptr_t>(p.dg_x) & (x16 ? 7 : 15)) == 0 && p.dg_x_ld % 4 == 0;
-    float part[4];
+    float part[MB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = wm * 64 + j * 16 + fr;
+    for (int j = 0; j < MB; ++j) {
+      const int m = wm * WR + j * 16 + fr;
       const int64_t xr = meta.dgrow[m];
       float xv[4][4];
 #pragma unroll
@@ -374,8 +392,8 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
     }
     if constexpr (Cfg::WN == 1) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int m = wm * 64 + j * 16 + fr;
+      for (int j = 0; j < MB; ++j) {
+        const int m = wm * WR + j * 16 + fr;
         if (fq == 0 && meta.dgrow[m] >= 0 && meta.widx[m] >= 0) p.dg[meta.widx[m] * p.dg_ntiles + ntile] = part[j];
       }
     } else {
@@ -385,13 +403,13 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
       wg_barrier();
       if (fq == 0) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) red[wn * BM + wm * 64 + j * 16 + fr] = part[j];
+        for (int j = 0; j < MB; ++j) red[wn * BM + wm * WR + j * 16 + fr] = part[j];
       }
       __syncthreads();
       if (wn == 0 && fq == 0) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = wm * 64 + j * 16 + fr;
+        for (int j = 0; j < MB; ++j) {
+          const int m = wm * WR + j * 16 + fr;
           float sum = red[m];
 #pragma unroll
           for (int w = 1; w < Cfg::WN; ++w) sum += red[w * BM + m];
@@ -443,9 +461,32 @@ hipError_t launch_routed_gemm_ring_t(const GemmParams& p_in, hipStream_t stream)
 // benchmark's spread of expert loads: 35.9 us, against 45.7 us for three
 // 16 KB slices of 32 k at three workgroups per CU.
 // 256 x 64 tiles: 3 slices of 20 KB + 9 KB = 69 KB, two per CU, read-ahead.
+// 160 x 128 tiles (two waves of 80 rows along m: 5 MFMA blocks each; two
+// 36 KB slices + metadata = 78 KB, two per CU) unless they cost more than
+// 5 % over 128-row tiles in round count x tile height, with the tile count
+// estimated as R / BM + E / 2 (an expert's last tile half full on average)
+// on 256 CUs x 2 workgroups.  At the ff_up forward shape 128-row tiles need
+// 544 tiles on 512 slots -- 32 run as a second round alone -- while 160-row
+// tiles need ~442: one round (42.4 -> 32.0 us; the ff_down grad-input 74.6
+// -> 50.3 us).  Over many rounds a tile's weight slices serve 25 % more rows
+// (the FFN stack's long-K products 522 -> 508 and 540 -> 523 us per
+// launch).  A single round of a small product keeps 128-row tiles (more
+// workgroups).
+inline bool ring_tall_tiles(const GemmParams& p) {
+  constexpr int64_t kSlots = 2 * 256;
+  const int64_t nt = (p.N + 127) / 128;
+  auto rounds = [&](int64_t bm) {
+    const int64_t tiles = (p.n_routes + bm - 1) / bm + p.n_experts / 2;
+    return (tiles * nt + kSlots - 1) / kSlots;
+  };
+  return 20 * 160 * rounds(160) <= 21 * 128 * rounds(128);
+}
+
 template <typename OpT, typename OutT>
 hipError_t launch_routed_gemm_ring_out(const GemmParams& p, hipStream_t stream) {
   if (p.N <= 64) return launch_routed_gemm_ring_t<OpT, OutT, 256, 64, 3, 2, true, 32>(p, stream);
+  if (p.ring_tile == 2 || (p.ring_tile == 0 && ring_tall_tiles(p)))
+    return launch_routed_gemm_ring_t<OpT, OutT, 160, 128, 2, 2, false, 64>(p, stream);
   return launch_routed_gemm_ring_t<OpT, OutT, 128, 128, 2, 2, false, 64>(p, stream);
 }
 

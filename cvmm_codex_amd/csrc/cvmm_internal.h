@@ -76,6 +76,9 @@ struct GemmParams {
   // (erf form): out = gelu(h), and h (the product in the output type) to aux
   int32_t act;
   void* aux;
+  // m-tile height of the long-K kernel with 128-column tiles: 0 = the
+  // launcher's choice, 1 = 128 rows, 2 = 160 rows
+  int32_t ring_tile;
   // zero the output rows (and aux rows) of the routes no tile covers: those
   // whose expert id is outside [0, E), sorted past offsets[E - 1]; done by the
   // workgroups past the last m-tile (direct per-route stores only)

@@ -101,13 +101,19 @@ int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launche
  *     of 256; larger chunks, fewer scatter workgroups).  Built in: >= 1024,
  *     and the count matrix (chunks x (E + 1)) at most 64K entries.  A chunk
  *     that makes the sort's workspace exceed 1 MiB fails
- *     cvmm_sort_routes_noalloc. */
+ *     cvmm_sort_routes_noalloc.
+ *   CVMM_TUNE_RING_TILE: m-tile height of the long-K routed GEMM (K > 128)
+ *     with 128-column tiles: 1 = 128 rows, 2 = 160 rows.  Built in: 160 rows
+ *     unless the estimated dispatch rounds times the tile height come out
+ *     more than 5 % higher (the ff_up forward: one round of ~442 tiles
+ *     instead of 544 tiles on 512 slots).  Both give the same bits. */
 #define CVMM_TUNE_PANEL_TILES_PER_WG 1
 #define CVMM_TUNE_WGRAD_ORDER 2
 #define CVMM_TUNE_GEMM_ORDER 3
 #define CVMM_TUNE_WGRAD_TILE 5
 #define CVMM_TUNE_DENSE_TOPK 6
 #define CVMM_TUNE_SORT_CHUNK 7
+#define CVMM_TUNE_RING_TILE 8
 int cvmm_tuning_set(int32_t knob, int64_t value);
 
 /* Whether a top-k sum -- out[t] = sum over the top_k routes (t, j) of

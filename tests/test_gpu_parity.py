@@ -472,6 +472,56 @@ def test_gemm_order_does_not_change_bits(weighted, route_input, skew):
     U.compare(b, exp, 2e-2)
 
 
+@pytest.mark.parametrize("weighted,route_input,D,H,skew", [
+    (False, False, 256, 128, None),   # long-K forward, one n tile
+    (True, True, 128, 256, 0.7),      # long-K weighted grad-input with the routing-weight gradient, hot expert
+    (False, False, 384, 256, None),   # long-K forward, two n tiles
+    (True, False, 256, 384, 0.0),     # both products long-K
+])
+def test_long_k_tile_height_does_not_change_bits(weighted, route_input, D, H, skew):
+    """128- and 160-row m-tiles of the long-K routed GEMM run every row's
+    k slices in the same order: identical bits, and the oracle's values."""
+    from cvmm_codex_amd import _native as N
+    x, keys, sel, w, go = _rand_case(35, 4, 384, D, H, 12, 6, weighted, route_input, skew=skew)
+    lib = N.lib()
+    try:
+        assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 1) == 0
+        a = U.run_hip(x, keys, sel, w, go, route_input, True)
+        assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 2) == 0
+        b = U.run_hip(x, keys, sel, w, go, route_input, True)
+    finally:
+        lib.cvmm_tuning_set(N.TUNE_RING_TILE, 0)
+    for n in ("out", "x_grad", "keys_grad", "weights_grad"):
+        if a[n] is None:
+            assert b[n] is None
+        else:
+            assert torch.equal(a[n], b[n]), n
+    exp = U.run_oracle(x, keys, sel, w, go, route_input, True)
+    U.compare(b, exp, 2e-2)
+
+
+def test_long_k_gelu_epilogue_tile_height_does_not_change_bits():
+    """The GELU epilogue of the long-K forward at both tile heights."""
+    from cvmm_codex_amd import _native as N
+    import cvmm_codex_amd.api as C
+    x, keys, sel, _, go = _rand_case(36, 4, 384, 256, 128, 12, 6)
+    lib = N.lib()
+    outs = []
+    try:
+        for t in (1, 2):
+            assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, t) == 0
+            xd, kd = x.cuda().requires_grad_(True), keys.cuda().requires_grad_(True)
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                y = C.cvmm_gelu(xd, C.cvmm_prepare_sel2(sel.cuda()), kd)
+            y.backward(go.cuda().to(y.dtype))
+            torch.cuda.synchronize()
+            outs.append((y.detach(), xd.grad, kd.grad))
+    finally:
+        lib.cvmm_tuning_set(N.TUNE_RING_TILE, 0)
+    for u, v in zip(*outs):
+        assert torch.equal(u, v)
+
+
 @pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True), (True, False)])
 def test_route_positions_from_sort_or_computed(weighted, route_input):
     """The route-ordered rows are gathered per token through the sort's

@@ -112,6 +112,9 @@ def test_tuning_knob_rejects_bad_values(lib):
     assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 0) == 0
     assert lib.cvmm_tuning_set(N.TUNE_GEMM_ORDER, 3) != 0
     assert lib.cvmm_tuning_set(N.TUNE_GEMM_ORDER, 0) == 0
+    assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 3) != 0
+    assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 2) == 0
+    assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 0) == 0
     assert lib.cvmm_tuning_set(4, 32) != 0               # the retired reduce-GEMM threshold knob
 
 
