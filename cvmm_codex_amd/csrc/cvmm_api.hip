@@ -941,9 +941,10 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
   float* dg_part = nullptr;
   const int64_t dg_nt = ntiles_of(d_in, gemm_bn(d_in));
   if (weighted && grad_rw) {
+    // no fill: the GEMM writes every (route, n tile) partial -- covered
+    // routes from their tile's epilogue, out-of-range expert ids as zeros
+    // from the workgroups past the last m-tile
     dg_part = (float*)c.take((size_t)n_routes * dg_nt * 4);
-    int r = check_launch(timed_fill(s, [&] { return launch_fill_zero(dg_part, (size_t)n_routes * dg_nt * 4, s); }), "cvmm_bwd_x(zero dg)");
-    if (r) return r;
     p.dg = dg_part; p.dg_ntiles = (int32_t)dg_nt;
     p.dg_x = x; p.dg_x_dtype = x_dtype; p.dg_x_ld = x_ld; p.dg_x_rows = x_rows; p.dg_x_idx = sel_index;
     p.dg_val_dtype = op_dtype;

@@ -166,22 +166,32 @@ __device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& 
 }
 
 // Called by a workgroup past the last m-tile (gemm_schedule returned false,
-// leaving the tile count in m.row0): when the call asks for it, zero the
-// columns [c0, c1) of the output rows (and GELU pre-activation rows) of the
-// routes no tile covers -- expert id outside [0, E), sorted at or past
-// offsets[E - 1].  Surplus m-tile j of the n_surplus launched takes every
-// n_surplus-th such route; a launch of ceil(R / BM) + min(E, R) m-tiles has at
-// least one surplus m-tile whenever such routes exist.
+// leaving the tile count in m.row0), for the routes no tile covers -- expert
+// id outside [0, E), sorted at or past offsets[E - 1]: when the call asks
+// for it, zero the columns [c0, c1) of their output rows (and GELU
+// pre-activation rows); and zero their routing-weight gradient partial of
+// n tile `dg_tile` (>= 0 when the caller covers exactly that n tile), so the
+// partials need no fill before the launch.  Surplus m-tile j of the
+// n_surplus launched takes every n_surplus-th such route; a launch of
+// ceil(R / BM) + min(E, R) m-tiles has at least one surplus m-tile whenever
+// such routes exist.
 template <int BM>
 __device__ void zero_unrouted_cols(const GemmParams& p, const RouteMeta<BM>& m, int64_t tile, int64_t m_tiles,
-                                   int64_t c0, int64_t c1) {
-  if (!p.zero_unrouted || p.out == nullptr) return;
+                                   int64_t c0, int64_t c1, int64_t dg_tile) {
+  const bool zero_out = p.zero_unrouted && p.out != nullptr;
+  const bool zero_dg = p.dg != nullptr && dg_tile >= 0;
+  if (!zero_out && !zero_dg) return;
   const int64_t j = tile - m.row0, n_surplus = m_tiles - m.row0;
   if (j < 0 || n_surplus <= 0) return;
   int64_t q0 = p.offsets[p.n_experts - 1];
   q0 = q0 < 0 ? 0 : q0;
   if (c1 > p.N) c1 = p.N;
   for (int64_t q = q0 + j; q < p.n_routes; q += n_surplus) {
+    if (zero_dg && threadIdx.x == 0) {
+      const int64_t wi = p.w_idx[q];
+      if (wi >= 0 && wi < p.n_routes) p.dg[wi * p.dg_ntiles + dg_tile] = 0.f;
+    }
+    if (!zero_out) continue;
     const int64_t oi = p.o_idx != nullptr ? p.o_idx[q] / p.o_div : q;
     if (oi < 0 || oi >= p.out_rows) continue;
     for (int64_t c = c0 + threadIdx.x; c < c1; c += kGemmThreads) {
@@ -279,7 +289,9 @@ __device__ void gemm_epilogue(const GemmParams& p, const float* C0, const float*
       // fixed-order butterfly over the TPR lanes of the row (deterministic)
 #pragma unroll
       for (int d = 1; d < TPR; d <<= 1) s += __shfl_xor(s, d, 64);
-      if (cg == 0 && r < rows && xr >= 0 && m.widx[r] >= 0)
+      // every covered route writes its partial (0 without an x row): the
+      // partials are not zero-filled before the launch
+      if (cg == 0 && r < rows && m.widx[r] >= 0)
         p.dg[m.widx[r] * p.dg_ntiles + ntile] = s;
     }
   }

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void routed_gemm_kernel(const Gemm
   const int64_t n0 = ntile * BN;
 
   if (!gemm_schedule<BM>(p, tile, meta)) {
-    zero_unrouted_cols<BM>(p, meta, tile, gridDim.x / n_ntiles, n0, n0 + BN);
+    zero_unrouted_cols<BM>(p, meta, tile, gridDim.x / n_ntiles, n0, n0 + BN, ntile);
     return;
   }
   const int32_t expert = meta.expert;

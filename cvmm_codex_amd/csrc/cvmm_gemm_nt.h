@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void routed_gemm_nt_kernel(const G
   const int64_t n0 = ntile * BN;
 
   if (!gemm_schedule<BM>(p, tile, meta)) {
-    zero_unrouted_cols<BM>(p, meta, tile, gridDim.x / n_ntiles, n0, n0 + BN);
+    zero_unrouted_cols<BM>(p, meta, tile, gridDim.x / n_ntiles, n0, n0 + BN, ntile);
     return;
   }
   const int32_t expert = meta.expert;
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void routed_gemm_nloop_kernel(cons
   const int64_t nt_end = nt_begin + ng < n_ntiles ? nt_begin + ng : n_ntiles;
 
   if (!gemm_schedule<BM>(p, tile, meta)) {
-    zero_unrouted_cols<BM>(p, meta, tile, gridDim.x / n_groups, nt_begin * BN, nt_end * BN);
+    zero_unrouted_cols<BM>(p, meta, tile, gridDim.x / n_groups, nt_begin * BN, nt_end * BN, -1);
     return;
   }
   const int32_t expert = meta.expert;

@@ -194,7 +194,7 @@ __global__ __launch_bounds__(kGemmThreads, (PanelCfg<KP, BN, WM>::OCC)) void rou
   const int T = (int)((n_ntiles - nt0) < tpw ? (n_ntiles - nt0) : tpw);
 
   if (!gemm_schedule<Cfg::BM>(p, tile, meta)) {
-    zero_unrouted_cols<Cfg::BM>(p, meta, tile, gridDim.x / n_groups, nt0 * BN, (nt0 + T) * BN);
+    zero_unrouted_cols<Cfg::BM>(p, meta, tile, gridDim.x / n_groups, nt0 * BN, (nt0 + T) * BN, -1);
     return;
   }
   const int32_t expert = meta.expert;

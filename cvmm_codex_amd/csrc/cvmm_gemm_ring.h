@@ -95,7 +95,7 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   const int64_t n0 = ntile * BN;
 
   if (!gemm_schedule<BM>(p, tile, meta)) {
-    zero_unrouted_cols<BM>(p, meta, tile, gridDim.x / n_ntiles, n0, n0 + BN);
+    zero_unrouted_cols<BM>(p, meta, tile, gridDim.x / n_ntiles, n0, n0 + BN, ntile);
     return;
   }
   const int32_t expert = meta.expert;
@@ -394,7 +394,7 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
 #pragma unroll
       for (int j = 0; j < MB; ++j) {
         const int m = wm * WR + j * 16 + fr;
-        if (fq == 0 && meta.dgrow[m] >= 0 && meta.widx[m] >= 0) p.dg[meta.widx[m] * p.dg_ntiles + ntile] = part[j];
+        if (fq == 0 && meta.widx[m] >= 0) p.dg[meta.widx[m] * p.dg_ntiles + ntile] = part[j];
       }
     } else {
       // every wave is past its last LDS read of the ring (the DMA drained
@@ -413,7 +413,7 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
           float sum = red[m];
 #pragma unroll
           for (int w = 1; w < Cfg::WN; ++w) sum += red[w * BM + m];
-          if (meta.dgrow[m] >= 0 && meta.widx[m] >= 0) p.dg[meta.widx[m] * p.dg_ntiles + ntile] = sum;
+          if (meta.widx[m] >= 0) p.dg[meta.widx[m] * p.dg_ntiles + ntile] = sum;
         }
       }
     }

@@ -297,8 +297,9 @@ def test_invalid_ids_contribute_nothing(weighted, route_input):
     unwritten rows.  Checked against the oracle with those routes sent to
     expert 0 with a zero grad row (token input) or a zero routing weight
     (weighted), which contribute exact zeros; outputs that belong to an
-    invalid route itself (its forward row, its route-input gradient row, its
-    weight gradient) have no defined value and are left out."""
+    invalid route itself (its forward row, its route-input gradient row) have
+    no defined value and are left out; its weight gradient is zero (the GEMM's
+    surplus workgroups write its partials, which are not pre-filled)."""
     x, keys, sel, w, go = _rand_case(51, 2, 256, 128, 192, 8, 4, weighted, route_input)
     g = torch.Generator().manual_seed(52)
     bad = torch.rand(sel.shape, generator=g) < 0.1
@@ -315,6 +316,7 @@ def test_invalid_ids_contribute_nothing(weighted, route_input):
         if route_input:  # per-route input rows: only the valid routes' are defined
             got["x_grad"] = got["x_grad"].reshape(-1, x.shape[-1])[torch.from_numpy(keep).cuda()]
             exp["x_grad"] = exp["x_grad"].reshape(-1, x.shape[-1])[keep]
+        assert torch.all(got["weights_grad"].reshape(-1)[torch.from_numpy(~keep).cuda()] == 0)
         got["weights_grad"] = got["weights_grad"].reshape(-1)[torch.from_numpy(keep).cuda()]
         exp["weights_grad"] = exp["weights_grad"].reshape(-1)[keep]
         U.compare(got, exp, 2e-2)
@@ -324,6 +326,74 @@ def test_invalid_ids_contribute_nothing(weighted, route_input):
         exp = U.run_oracle(x, keys, sel_ok, None, go_ok, route_input, True)
         got["out"] = exp["out"] = None
         U.compare(got, exp, 2e-2, names=("x_grad", "keys_grad"))
+
+
+@pytest.mark.parametrize("D,H,amp,ring_tile", [(128, 256, True, 1), (1024, 320, True, 1), (1024, 320, True, 2),
+                                               (64, 256, True, 0), (256, 64, True, 0), (48, 96, True, 0),
+                                               (96, 80, False, 0)])
+def test_weight_grad_partials_need_no_filled_workspace(D, H, amp, ring_tile):
+    """Through the C ABI, weighted route-input grad-input with grad_rw: the
+    per-(route, n tile) partials are written by the GEMM itself (covered
+    routes by their tile, routes with out-of-range expert ids as zeros by the
+    surplus workgroups), so a workspace of 0xFF bytes (NaN as fp32) gives the
+    same bits as a zeroed one.  Shapes: the long-K ring kernel (128- and
+    160-row tiles, and its 256 x 64 tile for N <= 64), the short-K tiled
+    kernel (128 x 128 and 256 x 64) and the general kernel (fp32 op)."""
+    from cvmm_codex_amd import _native as N
+    E, K, T = 8, 4, 192
+    dt = torch.bfloat16 if amp else torch.float32
+    x, keys, sel, w, go = _rand_case(61 + D + H, 2, T, D, H, E, K, True, True,
+                                     x_dt=dt, k_dt=torch.float32)
+    g = torch.Generator().manual_seed(62)
+    bad = torch.rand(sel.shape, generator=g) < 0.1
+    sel_bad = sel.clone()
+    sel_bad[bad] = torch.where(torch.rand(sel.shape, generator=g) < 0.5, -1, E + 3)[bad]
+    s = C.cvmm_prepare_sel2(sel_bad.cuda(), w.cuda(), route_input=True)
+    s._resolve(E)
+    lib = N.lib()
+    st = N.stream_of(torch.device("cuda"))
+    op = N.BF16 if amp else N.F32
+    kv = keys.cuda().to(dt)                                  # [E, d_in, d_out]
+    gd = go.cuda().to(dt).reshape(-1, H).contiguous()
+    xd = x.cuda().reshape(-1, D).contiguous()
+    rw = w.cuda().reshape(-1).contiguous()
+    R = sel.numel()
+    offs = C._offsets_for(s.sel, E)
+    rp = s.out_index if s.out_index is not None else s.sel_index
+    rpos = C._route_pos(rp, R)
+    ws_b = lib.cvmm_bwd_x_workspace_bytes(R, E, D, H, R, 1, 1, 1 if s.out_index is not None else 0, K,
+                                          N.dtype_id(dt), op, 1, 0)
+
+    def call(fill):
+        ws = torch.full((max(ws_b, 1),), fill, dtype=torch.uint8, device="cuda")
+        gx = torch.empty(R, D, dtype=dt, device="cuda")
+        grw = torch.empty(R, dtype=torch.float32, device="cuda")
+        N.check(lib.cvmm_bwd_x(N.ptr(gd), N.dtype_id(dt), gd.shape[0], gd.stride(0), N.ptr(kv), N.dtype_id(dt), E,
+                               D, H, *kv.stride(), N.ptr(s.sel), N.ptr(s.sel_index), N.ptr(s.out_index), R,
+                               N.ptr(offs), N.ptr(rpos), N.ptr(rw), N.F32, K, N.ptr(xd), N.dtype_id(dt), R, D, op,
+                               N.ptr(gx), N.dtype_id(dt), R, D, N.ptr(grw), N.F32, 0, N.ptr(ws), ws_b, st),
+                "cvmm_bwd_x")
+        torch.cuda.synchronize()
+        return gx, grw
+
+    assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, ring_tile) == 0
+    try:
+        gx0, grw0 = call(0)
+        gx1, grw1 = call(0xFF)
+    finally:
+        lib.cvmm_tuning_set(N.TUNE_RING_TILE, 0)
+    assert torch.equal(grw0, grw1) and torch.equal(gx0, gx1)
+    assert torch.isfinite(grw1).all()
+    badc = bad.reshape(-1).cuda()
+    assert torch.all(grw1[badc] == 0)
+    sel_ok = sel.clone()
+    sel_ok[bad] = 0
+    w_ok = w.clone()
+    w_ok[bad] = 0
+    exp = U.run_oracle(x, keys, sel_ok, w_ok, go, True, amp)
+    keep = ~bad.reshape(-1).numpy()
+    err = U.norm_rel(U.to_np(grw1)[keep], exp["weights_grad"].reshape(-1)[keep])
+    assert err <= (2e-2 if amp else 1e-4), err
 
 
 @pytest.mark.parametrize("R,E", [(4000, 16), (524288, 256), (262144, 1000)])
