@@ -514,7 +514,7 @@ def kernel_class(name: str):
     if role is not None:
         return role
     base = name.split("<")[0].split("(")[0].split()[-1] if name else ""
-    if base.startswith("Cijk_") or "rocblas" in base:
+    if "Cijk_" in base or "rocblas" in base:
         return "dense_topk"
     for key, cls in (("slot_rows", "slots"), ("combine_rows", "combine"), ("sort_", "sort"), ("cast_keys", "cast"),
                      ("copy_ids", "sort"), ("sum_partials", "dgate"), ("fill_zero", "fill"), ("gelu", "gelu")):
@@ -713,7 +713,7 @@ def main():
                     help="with --summarize: print the traffic JSON of this kernel class (gemm_fwd, gemm_bwd_x, wgrad)")
     ap.add_argument("--tune", action="append", default=[], metavar="KNOB=VALUE",
                     help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, wgrad_tile, gemm_order, "
-                         "dense_topk) before running")
+                         "dense_topk, sort_chunk, ring_tile) before running")
     args = ap.parse_args()
 
     if args.summarize:

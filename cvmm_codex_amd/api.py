@@ -706,5 +706,36 @@ def cvmm(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.Tensor)
         if sh not in known_shapes:
             print("New shape:", sh)
             known_shapes.add(sh)
+    if not _compiling():
+        return _cvmm_native(x, sel, keys)
     return CVMM.apply(x, sel._raw_shape_tensor(), sel.sel_index, sel.sel, keys, sel.out_index,
                       sel.reduction_weight)
+
+
+def _cvmm_native(x: torch.Tensor, sel: CVMMSel, keys: torch.Tensor) -> torch.Tensor:
+    """CVMM.apply for eager calls, as one C++ autograd function (the host
+    glue's ``cvmm_apply``): the same forward and backward host calls as
+    CVMM.forward / CVMM.backward, with the backward node run by the autograd
+    engine without Python (no GIL taken on its device thread)."""
+    rw = sel.reduction_weight
+    raw = sel._raw_shape_tensor()
+    s, sel_index, out_index = sel.sel, sel.sel_index, sel.out_index
+    top_k = raw.shape[-1] if raw.ndim > 0 else 1
+    op = get_dtype()
+    keys_op = keys_x = None
+    fwd_t, keys_x_is_t = True, False
+    weighted = rw is not None
+    if _fast_path(op, keys.shape[1], keys.shape[2]):
+        k = rw.shape[-1] if weighted else top_k
+        need = torch.is_grad_enabled() and (x.requires_grad or (weighted and rw.requires_grad))
+        plan = _plan_copies(keys, op, s.numel(), k, weighted, out_index is not None, need)
+        pre = _take_cast(keys, op, plan)
+        kt, kn = pre if pre is not None else _cast_keys(keys, op, plan)
+        if need:
+            keys_x, keys_x_is_t = _copy_view(plan, kt, kn, False)
+        keys_op, fwd_t = _copy_view(plan, kt, kn, True)
+    _require_device(s, "sel")
+    shape = [*rw.shape[:-1], keys.shape[2]] if weighted else [*s.shape, keys.shape[2]]
+    return N.host().cvmm_apply(x, keys, rw, s, sel_index, out_index, _offsets_for(s, keys.shape[0]),
+                               _route_pos(out_index if out_index is not None else sel_index, s.numel()),
+                               keys_op, fwd_t, keys_x, keys_x_is_t, top_k, N.dtype_id(op), _flags(), shape)

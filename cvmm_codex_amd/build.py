@@ -56,9 +56,11 @@ def _host_flags():
 
     cflags = ["-O2", "-std=c++17", "-fPIC", f"-DTORCH_EXTENSION_NAME={HOST_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H",
               f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}", "-I" + INCLUDE,
-              "-I" + sysconfig.get_paths()["include"], *["-I" + p for p in include_paths()]]
+              "-I" + sysconfig.get_paths()["include"], *["-I" + p for p in include_paths()],
+              # torch's current HIP stream (c10/hip/HIPStream.h) for the C++ autograd function
+              "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "include")]
     ldflags = [*["-L" + p for p in library_paths()], *["-Wl,-rpath," + p for p in library_paths()],
-               "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-L" + HERE, "-lcvmm_hip",
+               "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-L" + HERE, "-lcvmm_hip",
                "-Wl,-rpath,$ORIGIN"]
     return cflags, ldflags, sysconfig.get_config_var("EXT_SUFFIX")
 

@@ -10,6 +10,7 @@
 // (cvmm.py:1796-1803), cvmm_triton (cvmm.py:814-867) with the weighted combine
 // (cvmm.py:1543-1545), and CVMM.backward's products (cvmm.py:1552-1755).
 #include <torch/extension.h>
+#include <c10/hip/HIPStream.h>
 
 #include <map>
 #include <mutex>
@@ -323,7 +324,7 @@ std::tuple<OptT, OptT> cast_keys(const Tensor& keys, int64_t op_id, bool want_t,
 // (a [E, d_in, d_out] copy, or an interleaved copy already viewed so).
 Tensor copy_view(const Tensor& copy, bool is_t) { return is_t ? copy.transpose(1, 2) : copy; }
 
-Tensor forward(const Tensor& x, const Tensor& keys, const OptT& keys_op, bool keys_op_is_t, const Tensor& sel,
+Tensor cvmm_forward_impl(const Tensor& x, const Tensor& keys, const OptT& keys_op, bool keys_op_is_t, const Tensor& sel,
                const Tensor& sel_index, const OptT& out_index, const Tensor& offsets, const OptT& route_pos,
                const OptT& rw, int64_t op_id, int64_t out_id, int64_t flags, int64_t stream) {
   require_device(x, "x");
@@ -448,7 +449,7 @@ Tensor gelu_backward(const Tensor& grad, const Tensor& pre, int64_t stream) {
 // ---------------------------------------------------------------------------
 // backward (cvmm.py:1552-1755): (grad_x, grad_keys, grad_reduction_weight)
 // ---------------------------------------------------------------------------
-std::tuple<OptT, OptT, OptT> backward(const Tensor& grad_output, const Tensor& x, const Tensor& keys,
+std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const Tensor& x, const Tensor& keys,
                                       const OptT& keys_x, bool keys_x_is_t, const Tensor& sel, const Tensor& sel_index,
                                       const OptT& out_index, const Tensor& offsets, const OptT& route_pos,
                                       const OptT& rw, int64_t top_k, int64_t op_id, bool need_grad_x,
@@ -534,6 +535,67 @@ std::tuple<OptT, OptT, OptT> backward(const Tensor& grad_output, const Tensor& x
   return {grad_x, grad_w, grad_rw};
 }
 
+// ---------------------------------------------------------------------------
+// CVMM as a C++ autograd function (cvmm.py:1521-1755): the forward above, and
+// a backward node that runs the backward above on the autograd engine's
+// device thread without Python.  A Python autograd.Function's node takes the
+// GIL on that thread to run its backward and again to free its context,
+// which stalls the caller's next step.
+// ---------------------------------------------------------------------------
+int64_t current_stream(const Tensor& like) {
+  return (int64_t)(uintptr_t)c10::hip::getCurrentHIPStream(like.get_device()).stream();
+}
+
+Tensor opt_or_undef(const OptT& t) { return t.has_value() ? *t : Tensor(); }
+OptT undef_or_opt(const Tensor& t) { return t.defined() ? OptT(t) : std::nullopt; }
+
+struct CvmmFunction : public torch::autograd::Function<CvmmFunction> {
+  // x, keys and reduction_weight (optional) are the differentiable inputs;
+  // the rest is routing, the op-dtype weight copies and settings.
+  static Tensor forward(torch::autograd::AutogradContext* ctx, const Tensor& x, const Tensor& keys, const OptT& rw,
+                        const Tensor& sel, const Tensor& sel_index, const OptT& out_index, const Tensor& offsets,
+                        const OptT& route_pos, const OptT& keys_op, bool keys_op_is_t, const OptT& keys_x,
+                        bool keys_x_is_t, int64_t top_k, int64_t op_id, int64_t flags,
+                        const std::vector<int64_t>& out_shape) {
+    const bool need_x = x.requires_grad(), need_keys = keys.requires_grad();
+    const bool need_rw = rw.has_value() && rw->requires_grad();
+    ctx->save_for_backward({x, keys, opt_or_undef(rw), sel, sel_index, opt_or_undef(out_index), offsets,
+                            opt_or_undef(route_pos), need_x || need_rw ? opt_or_undef(keys_x) : Tensor()});
+    ctx->saved_data["keys_x_is_t"] = keys_x_is_t;
+    ctx->saved_data["top_k"] = top_k;
+    ctx->saved_data["op_id"] = op_id;
+    ctx->saved_data["flags"] = flags;
+    ctx->saved_data["need"] = (int64_t)((need_x ? 1 : 0) | (need_keys ? 2 : 0) | (need_rw ? 4 : 0));
+    Tensor out = cvmm_forward_impl(x, keys, keys_op, keys_op_is_t, sel, sel_index, out_index, offsets, route_pos,
+                                   rw, op_id, -1, flags, current_stream(x));
+    // not a view in autograd's sense (its base is no input and is never seen)
+    return at::_unsafe_view(out, out_shape);
+  }
+
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    const auto v = ctx->get_saved_variables();
+    const Tensor& x = v[0];
+    const int64_t need = ctx->saved_data["need"].toInt();
+    auto [gx, gw, grw] = cvmm_backward_impl(
+        grads[0], x, v[1], undef_or_opt(v[8]), ctx->saved_data["keys_x_is_t"].toBool(), v[3], v[4],
+        undef_or_opt(v[5]), v[6], undef_or_opt(v[7]), undef_or_opt(v[2]), ctx->saved_data["top_k"].toInt(),
+        ctx->saved_data["op_id"].toInt(), (need & 1) != 0, (need & 2) != 0, (need & 4) != 0,
+        ctx->saved_data["flags"].toInt(), current_stream(x));
+    // one entry per forward argument
+    return {opt_or_undef(gx), opt_or_undef(gw), opt_or_undef(grw), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(),
+            Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+  }
+};
+
+Tensor cvmm_apply(const Tensor& x, const Tensor& keys, const OptT& rw, const Tensor& sel, const Tensor& sel_index,
+                  const OptT& out_index, const Tensor& offsets, const OptT& route_pos, const OptT& keys_op,
+                  bool keys_op_is_t, const OptT& keys_x, bool keys_x_is_t, int64_t top_k, int64_t op_id,
+                  int64_t flags, const std::vector<int64_t>& out_shape) {
+  return CvmmFunction::apply(x, keys, rw, sel, sel_index, out_index, offsets, route_pos, keys_op, keys_op_is_t,
+                             keys_x, keys_x_is_t, top_k, op_id, flags, out_shape);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -549,10 +611,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("stream"));
   m.def("cast_keys", &cast_keys, py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"),
         py::arg("layout"), py::arg("stream"));
-  m.def("forward", &forward);
+  m.def("forward", &cvmm_forward_impl);
   m.def("forward_gelu", &forward_gelu);
   m.def("gelu_backward", &gelu_backward, py::arg("grad"), py::arg("pre_act"), py::arg("stream"));
-  m.def("backward", &backward);
+  m.def("backward", &cvmm_backward_impl);
+  m.def("cvmm_apply", &cvmm_apply);
   // operand rules, exposed for tests
   m.def("storage_for", [](const Tensor& t, int64_t op_id) { return storage_for(t, dtype_of(op_id)); });
   m.def("keys_view", &keys_view);
