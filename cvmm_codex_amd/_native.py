@@ -19,6 +19,7 @@ F32, F16, BF16 = 0, 1, 2            # cvmm.py:36-44 dtype ids
 FLAG_ATOMIC_REDUCE = 1
 FLAG_COUNTERS_ZEROED = 2
 FLAG_WORKSPACE_ZEROED = 8
+FLAG_COUNTS_READY = 16
 CAST_T_INTERLEAVED = 1
 CAST_N_INTERLEAVED = 2
 TUNE_PANEL_TILES_PER_WG = 1
@@ -53,10 +54,14 @@ _SIGS = {
     "cvmm_sort_routes": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "cvmm_sort_routes_noalloc": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P]),
     "cvmm_copy_ids": (ctypes.c_int, [_P, _I32, _I64, _P, _P]),
+    "cvmm_copy_ids_count": (ctypes.c_int, [_P, _I32, _I64, _I32, _P, _P, _SZ, _P]),
     "cvmm_expert_offsets": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
     "cvmm_sort_routes_cast_keys": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _SZ,
                                                   _P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _I32,
                                                   _P]),
+    "cvmm_sort_routes_cast_keys_ex": (ctypes.c_int, [_P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _SZ,
+                                                     _P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _I32,
+                                                     _I32, _P]),
     "cvmm_cast_keys": (ctypes.c_int, [_P, _I32, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _I32, _P]),
     "cvmm_route_topk_workspace_bytes": (_SZ, [_I64, _I32, _I64]),
     "cvmm_route_topk": (ctypes.c_int, [_P, _I32, _I64, _I64, _I32, _I64, _I32, _P, _P,

@@ -102,7 +102,7 @@ def dtype_to_type_id(dtype: torch.dtype) -> int:
 # native selector preparation
 # ----------------------------------------------------------------------------
 
-def _sort_routes(raw_flat: torch.Tensor, n_experts: int, top_k: int):
+def _sort_routes(raw_flat: torch.Tensor, n_experts: int, top_k: int, counted_ws=None):
     """Stable counting sort on the device: (sorted int32, perm int64,
     perm // top_k int64, inclusive offsets int64[E]).  `raw_flat` holds int32
     or int64 ids (int64 read as their low 32 bits, like an int32 cast).  The
@@ -113,7 +113,7 @@ def _sort_routes(raw_flat: torch.Tensor, n_experts: int, top_k: int):
         ssel, perm, tok, offsets, _ = _ops.sort_routes(raw_flat, n_experts, top_k)
         return ssel, perm, tok, offsets
     ssel, perm, tok, offsets, route_pos = N.host().sort_routes(raw_flat, n_experts, top_k,
-                                                               N.stream_of(raw_flat.device))
+                                                               N.stream_of(raw_flat.device), counted_ws)
     perm._cvmm_route_pos = route_pos
     return ssel, perm, tok, offsets
 
@@ -139,14 +139,14 @@ class _CopyPlan(NamedTuple):
     bwd_t: bool
 
 
-def _sort_routes_cast(raw_flat: torch.Tensor, n_experts: int, top_k: int, cast):
+def _sort_routes_cast(raw_flat: torch.Tensor, n_experts: int, top_k: int, cast, counted_ws=None):
     """_sort_routes plus the step's weight cast in the same launches
     (`cast` = (keys, op dtype, _CopyPlan)); the copies are left for
     CVMM.forward."""
     keys, op, plan = cast
     (ssel, perm, tok, offsets, route_pos), kt, kn = N.host().sort_routes_cast(
         raw_flat, n_experts, top_k, keys, N.dtype_id(op), plan.want_t, plan.want_n, plan.layout,
-        N.stream_of(raw_flat.device))
+        N.stream_of(raw_flat.device), counted_ws)
     perm._cvmm_route_pos = route_pos
     _cast_done.entry = (keys, keys._version, op, plan.layout, kt, kn)
     return ssel, perm, tok, offsets
@@ -241,20 +241,37 @@ def _offsets_for(sel: torch.Tensor, n_experts: int) -> torch.Tensor:
     return off
 
 
-class _Routing:
-    """One recorded selection; sorted on the device on first use, per expert count."""
+# The expert count the last sort of a selection of (routes, top_k) used:
+# cvmm_prepare_sel2 builds the sort's histogram for it together with the id
+# copy (cvmm_copy_ids_count), and the sort skips that launch when cvmm()
+# brings the same count.
+_expert_guess: Dict[Tuple[int, int], int] = {}
 
-    def __init__(self, raw_flat: torch.Tensor, top_k: int):
+
+class _Routing:
+    """One recorded selection; sorted on the device on first use, per expert count.
+    `counted` = (expert count, sort workspace holding the ids' histogram for it)."""
+
+    def __init__(self, raw_flat: torch.Tensor, top_k: int, counted=None):
         self.raw = raw_flat
         self.k = top_k
         self.by_e: Dict[int, Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]] = {}
         self.first_e: Optional[int] = None
+        self.counted = counted
 
     def get(self, n_experts: int, cast=None):
         hit = self.by_e.get(n_experts)
         if hit is None:
-            hit = (_sort_routes_cast(self.raw, n_experts, self.k, cast) if cast is not None
-                   else _sort_routes(self.raw, n_experts, self.k))
+            ws = None
+            if self.counted is not None:   # one use: the sort turns the counts into prefixes
+                ws = self.counted[1] if self.counted[0] == n_experts else None
+                self.counted = None
+            if not _compiling():
+                if len(_expert_guess) > 64:
+                    _expert_guess.clear()
+                _expert_guess[(self.raw.numel(), self.k)] = n_experts
+            hit = (_sort_routes_cast(self.raw, n_experts, self.k, cast, ws) if cast is not None
+                   else _sort_routes(self.raw, n_experts, self.k, ws))
             self.by_e[n_experts] = hit
             if self.first_e is None:
                 self.first_e = n_experts
@@ -413,9 +430,17 @@ def cvmm_prepare_sel2(sel: Union[torch.Tensor, CVMMSel], w: Optional[torch.Tenso
     if _compiling():
         fsel = sel.reshape(-1)
         fsel = fsel.clone() if fsel.dtype == torch.int32 else fsel.to(torch.int32)
+        routing = _Routing(fsel, n_per_batch)
     else:
-        fsel = N.host().copy_ids(sel, N.stream_of(sel.device)).reshape(-1)
-    out = CVMMSel._deferred(fsel.view(sel.shape), _Routing(fsel, n_per_batch), route_input, w)
+        guess = _expert_guess.get((sel.numel(), n_per_batch))
+        if guess is not None:
+            fsel, ws = N.host().copy_ids_count(sel, guess, N.stream_of(sel.device))
+            fsel = fsel.reshape(-1)
+            routing = _Routing(fsel, n_per_batch, (guess, ws))
+        else:
+            fsel = N.host().copy_ids(sel, N.stream_of(sel.device)).reshape(-1)
+            routing = _Routing(fsel, n_per_batch)
+    out = CVMMSel._deferred(fsel.view(sel.shape), routing, route_input, w)
     out._raw_sel = out._raw_src
     return out
 

@@ -311,11 +311,16 @@ int64_t gemm_bn(int64_t n) { return n <= 64 ? 64 : 128; }
 
 }  // namespace
 
+static int sort_routes_checked(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts,
+                               int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                               int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* workspace,
+                               size_t workspace_bytes, void* stream, bool counts_ready);
+
 extern "C" {
 
 const char* cvmm_last_error(void) { return g_err.c_str(); }
 
-int cvmm_abi_version(void) { return 10; }
+int cvmm_abi_version(void) { return 11; }
 
 int cvmm_timing_enable(uint32_t class_mask) {
   std::lock_guard<std::mutex> lk(g_timing_mu);
@@ -402,6 +407,18 @@ int cvmm_sort_routes(const void* sel, int32_t sel_is_int64, int64_t n_routes, in
                      int32_t* sorted_sel, int64_t* perm, int64_t* token_index, int64_t* offsets,
                      int32_t* route_pos, int32_t* n_invalid, void* workspace, size_t workspace_bytes,
                      void* stream) {
+  return sort_routes_checked(sel, sel_is_int64, n_routes, n_experts, top_k, sorted_sel, perm, token_index, offsets,
+                             route_pos, n_invalid, workspace, workspace_bytes, stream, false);
+}
+
+}  // extern "C"
+
+// cvmm_sort_routes; `counts_ready`: the workspace already holds the count
+// matrix of these ids for n_experts (cvmm_copy_ids_count).
+static int sort_routes_checked(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts,
+                               int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                               int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* workspace,
+                               size_t workspace_bytes, void* stream, bool counts_ready) {
   if (n_experts <= 0) return fail(CVMM_ERR_INVALID, "cvmm_sort_routes: n_experts must be > 0 (got %d)", n_experts);
   if (n_experts > 32767) return fail(CVMM_ERR_UNSUPPORTED, "cvmm_sort_routes: at most 32767 experts (got %d)", n_experts);
   if (n_routes < 0 || n_routes > 0x7fffffffll)
@@ -418,11 +435,10 @@ int cvmm_sort_routes(const void* sel, int32_t sel_is_int64, int64_t n_routes, in
     return fail(CVMM_ERR_WORKSPACE, "cvmm_sort_routes: workspace too small (%zu < %zu)", workspace_bytes,
                 sort_workspace_bytes(n_routes, n_experts));
   return check_launch(timed(CVMM_KC_SORT, s, [&] { return launch_sort_routes(sel, sel_is_int64 != 0, n_routes, n_experts, top_k, sorted_sel, perm,
-                                         token_index, offsets, route_pos, n_invalid, workspace, s); }),
+                                         token_index, offsets, route_pos, n_invalid, workspace, s, nullptr,
+                                         counts_ready); }),
                       "cvmm_sort_routes");
 }
-
-}  // extern "C"
 
 // ---------------------------------------------------------------------------
 // cvmm_sort_routes_noalloc: the sort with its histogram scratch in a
@@ -581,6 +597,37 @@ int cvmm_sort_routes_cast_keys(const void* sel, int32_t sel_is_int64, int64_t n_
                                size_t workspace_bytes, const void* keys, int32_t keys_dtype, int64_t d_in,
                                int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj, int32_t out_dtype,
                                void* keys_t, void* keys_n, int32_t layout, void* stream) {
+  return cvmm_sort_routes_cast_keys_ex(sel, sel_is_int64, n_routes, n_experts, top_k, sorted_sel, perm, token_index,
+                                       offsets, route_pos, n_invalid, workspace, workspace_bytes, keys, keys_dtype,
+                                       d_in, d_out, k_se, k_si, k_sj, out_dtype, keys_t, keys_n, layout, 0, stream);
+}
+
+int cvmm_copy_ids_count(const void* sel, int32_t sel_is_int64, int64_t n, int32_t n_experts, int32_t* out,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  if (n_experts <= 0 || n_experts > 32767)
+    return fail(CVMM_ERR_INVALID, "cvmm_copy_ids_count: n_experts must be in 1 .. 32767 (got %d)", n_experts);
+  if (n < 0 || n > 0x7fffffffll) return fail(CVMM_ERR_INVALID, "cvmm_copy_ids_count: n out of range");
+  if (n > 0 && (!sel || !out)) return fail(CVMM_ERR_INVALID, "cvmm_copy_ids_count: NULL pointer");
+  if (n > 0 && (workspace == nullptr || workspace_bytes < sort_workspace_bytes(n, n_experts)))
+    return fail(CVMM_ERR_WORKSPACE, "cvmm_copy_ids_count: workspace too small (%zu < %zu)", workspace_bytes,
+                sort_workspace_bytes(n, n_experts));
+  return check_launch(timed(CVMM_KC_SORT, (hipStream_t)stream, [&] {
+    return launch_copy_ids_count(sel, sel_is_int64 != 0, n, n_experts, out, workspace, (hipStream_t)stream);
+  }), "cvmm_copy_ids_count");
+}
+
+int cvmm_sort_routes_cast_keys_ex(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts,
+                                  int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                                  int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* workspace,
+                                  size_t workspace_bytes, const void* keys, int32_t keys_dtype, int64_t d_in,
+                                  int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj, int32_t out_dtype,
+                                  void* keys_t, void* keys_n, int32_t layout, int32_t flags, void* stream) {
+  if (flags & ~CVMM_FLAG_COUNTS_READY)
+    return fail(CVMM_ERR_INVALID, "cvmm_sort_routes_cast_keys_ex: unknown flags %d", flags);
+  const bool counts_ready = (flags & CVMM_FLAG_COUNTS_READY) != 0;
+  if (!keys || (!keys_t && !keys_n))  // no cast asked for: the sort alone
+    return sort_routes_checked(sel, sel_is_int64, n_routes, n_experts, top_k, sorted_sel, perm, token_index,
+                               offsets, route_pos, n_invalid, workspace, workspace_bytes, stream, counts_ready);
   const bool fuse = n_routes > 0 && n_routes <= 0x7fffffffll && n_experts > 0 && n_experts <= 32767 && top_k > 0 &&
                     sel && sorted_sel && perm && offsets && keys && (keys_t || keys_n) && d_in > 0 && d_out > 0 &&
                     n_experts <= 65535 && (int64_t)n_experts * (d_in / 64) * (d_out / 64) < 0x7f000000ll &&
@@ -589,8 +636,8 @@ int cvmm_sort_routes_cast_keys(const void* sel, int32_t sel_is_int64, int64_t n_
                     workspace != nullptr && workspace_bytes >= sort_workspace_bytes(n_routes, n_experts);
   if (!fuse) {
     // separate calls, each with its own argument checks
-    int r = cvmm_sort_routes(sel, sel_is_int64, n_routes, n_experts, top_k, sorted_sel, perm, token_index, offsets,
-                             route_pos, n_invalid, workspace, workspace_bytes, stream);
+    int r = sort_routes_checked(sel, sel_is_int64, n_routes, n_experts, top_k, sorted_sel, perm, token_index,
+                                offsets, route_pos, n_invalid, workspace, workspace_bytes, stream, counts_ready);
     if (r) return r;
     return cvmm_cast_keys(keys, keys_dtype, n_experts, d_in, d_out, k_se, k_si, k_sj, out_dtype, keys_t, keys_n,
                           layout, stream);
@@ -598,7 +645,8 @@ int cvmm_sort_routes_cast_keys(const void* sel, int32_t sel_is_int64, int64_t n_
   hipStream_t s = (hipStream_t)stream;
   const CastRequest cr{keys, k_se, k_si, n_experts, d_in, d_out, out_dtype, keys_t, keys_n, layout};
   return check_launch(timed(CVMM_KC_SORT, s, [&] { return launch_sort_routes(sel, sel_is_int64 != 0, n_routes, n_experts, top_k, sorted_sel, perm,
-                                         token_index, offsets, route_pos, n_invalid, workspace, s, &cr); }),
+                                         token_index, offsets, route_pos, n_invalid, workspace, s, &cr,
+                                         counts_ready); }),
                       "cvmm_sort_routes_cast_keys");
 }
 

@@ -207,7 +207,11 @@ inline bool cast_vec_ok(const void* keys, int32_t keys_dtype, int64_t se, int64_
 hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_routes, int32_t n_experts,
                               int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
                               int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* ws,
-                              hipStream_t stream, const CastRequest* cast = nullptr);
+                              hipStream_t stream, const CastRequest* cast = nullptr, bool counts_ready = false);
+// The int32 copy of the ids plus the sort's count matrix for n_experts
+// (written into the sort workspace `ws`, as the histogram launch would).
+hipError_t launch_copy_ids_count(const void* sel, bool sel_is_int64, int64_t n_routes, int32_t n_experts,
+                                 int32_t* out, void* ws, hipStream_t stream);
 hipError_t launch_expert_offsets(const int32_t* sorted_sel, int64_t n_routes, int32_t n_experts,
                                  int64_t* offsets, hipStream_t stream);
 

@@ -55,6 +55,28 @@ __global__ __launch_bounds__(kSortThreads) void sort_hist_kernel(
   for (int e = threadIdx.x; e <= n_experts; e += kSortThreads) counts[b * (int64_t)(n_experts + 1) + e] = hist[e];
 }
 
+// The histogram launch fused with the int32 copy of the ids that selector
+// preparation takes anyway: chunk b's ids are copied and counted by bucket
+// (int64 ids by their low 32 bits, the value the copy keeps).
+template <typename IdxT>
+__global__ __launch_bounds__(kSortThreads) void copy_ids_count_kernel(
+    const IdxT* __restrict__ sel, int64_t n_routes, int32_t n_experts, int64_t chunk,
+    int32_t* __restrict__ out, int32_t* __restrict__ counts) {
+  extern __shared__ int32_t hist[];  // n_experts + 1
+  const int64_t b = blockIdx.x;
+  for (int e = threadIdx.x; e <= n_experts; e += kSortThreads) hist[e] = 0;
+  __syncthreads();
+  const int64_t lo = b * chunk;
+  const int64_t hi = min(lo + chunk, n_routes);
+  for (int64_t i = lo + threadIdx.x; i < hi; i += kSortThreads) {
+    const int32_t v = (int32_t)sel[i];
+    out[i] = v;
+    atomicAdd(&hist[bucket_of(v, n_experts)], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e <= n_experts; e += kSortThreads) counts[b * (int64_t)(n_experts + 1) + e] = hist[e];
+}
+
 // Exclusive scan, in place, of the n values a[0, n) in LDS (whole workgroup).
 __device__ void block_exclusive_scan(int32_t* a, int32_t n) {
   __shared__ int64_t wave_total[kSortThreads / 64];
@@ -641,10 +663,33 @@ void launch_scatter_cast(const ScatterArgs<IdxT>& a, const CastRequest& cr, size
   }
 }
 
+hipError_t launch_copy_ids_count(const void* sel, bool sel_is_int64, int64_t n_routes, int32_t n_experts,
+                                 int32_t* out, void* ws, hipStream_t stream) {
+  if (n_routes <= 0) return hipSuccess;
+  const int64_t chunk = sort_chunk_size(n_routes, n_experts);
+  const int64_t n_chunks = (n_routes + chunk - 1) / chunk;
+  const size_t lds = (size_t)(n_experts + 1) * sizeof(int32_t);
+  int32_t* counts = (int32_t*)ws;
+  if (sel_is_int64) {
+    const hipError_t e = allow_lds(copy_ids_count_kernel<int64_t>, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(copy_ids_count_kernel<int64_t>, dim3((unsigned)n_chunks), dim3(kSortThreads), lds, stream,
+                       (const int64_t*)sel, n_routes, n_experts, chunk, out, counts);
+  } else {
+    const hipError_t e = allow_lds(copy_ids_count_kernel<int32_t>, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(copy_ids_count_kernel<int32_t>, dim3((unsigned)n_chunks), dim3(kSortThreads), lds, stream,
+                       (const int32_t*)sel, n_routes, n_experts, chunk, out, counts);
+  }
+  return hipGetLastError();
+}
+
+// `counts_ready`: the workspace already holds these ids' count matrix for
+// n_experts (launch_copy_ids_count); the histogram launch is skipped.
 hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_routes, int32_t n_experts,
                               int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
                               int64_t* offsets, int32_t* route_pos, int32_t* n_invalid_out, void* ws,
-                              hipStream_t stream, const CastRequest* cast) {
+                              hipStream_t stream, const CastRequest* cast, bool counts_ready) {
   const int64_t chunk = sort_chunk_size(n_routes, n_experts);
   const int64_t n_chunks = (n_routes + chunk - 1) / chunk;
   int32_t* counts = (int32_t*)ws;
@@ -659,12 +704,13 @@ hipError_t launch_sort_routes(const void* sel, bool sel_is_int64, int64_t n_rout
   }
   int n_bits = 0;
   while ((1ll << n_bits) <= (int64_t)n_experts) ++n_bits;  // buckets 0..E
-  if (sel_is_int64) {
-    hipLaunchKernelGGL(sort_hist_kernel<int64_t>, dim3(n_chunks), dim3(kSortThreads), lds, stream,
-                       (const int64_t*)sel, n_routes, n_experts, chunk, n_chunks, counts);
-  } else {
-    hipLaunchKernelGGL(sort_hist_kernel<int32_t>, dim3(n_chunks), dim3(kSortThreads), lds, stream,
-                       (const int32_t*)sel, n_routes, n_experts, chunk, n_chunks, counts);
+  if (!counts_ready) {
+    if (sel_is_int64)
+      hipLaunchKernelGGL(sort_hist_kernel<int64_t>, dim3(n_chunks), dim3(kSortThreads), lds, stream,
+                         (const int64_t*)sel, n_routes, n_experts, chunk, n_chunks, counts);
+    else
+      hipLaunchKernelGGL(sort_hist_kernel<int32_t>, dim3(n_chunks), dim3(kSortThreads), lds, stream,
+                         (const int32_t*)sel, n_routes, n_experts, chunk, n_chunks, counts);
   }
   const int32_t* tot = launch_colscan(counts, n_chunks, n_experts, stream);
   if (sel_is_int64) {

@@ -166,7 +166,8 @@ Tensor sort_workspace(const Tensor& like, int64_t stream, size_t bytes) {
 // returns (sorted int32, perm int64, perm // top_k int64, offsets int64[E],
 // route_pos int32 = inverse of perm)
 // ---------------------------------------------------------------------------
-std::vector<Tensor> sort_routes(const Tensor& raw, int64_t n_experts, int64_t top_k, int64_t stream) {
+std::vector<Tensor> sort_routes(const Tensor& raw, int64_t n_experts, int64_t top_k, int64_t stream,
+                                const OptT& counted_ws) {
   require_device(raw, "sel");
   Tensor flat = raw.reshape({-1});
   if (flat.scalar_type() != at::kInt && flat.scalar_type() != at::kLong) flat = flat.to(at::kInt);
@@ -177,11 +178,12 @@ std::vector<Tensor> sort_routes(const Tensor& raw, int64_t n_experts, int64_t to
   Tensor ssel = i32.narrow(0, 0, R), pos = i32.narrow(0, R, R);
   Tensor perm = i64.narrow(0, 0, R), tok = i64.narrow(0, R, R), off = i64.narrow(0, 2 * R, n_experts);
   const size_t ws_bytes = cvmm_sort_workspace_bytes(R, (int32_t)n_experts);
-  Tensor ws = sort_workspace(flat, stream, ws_bytes);
-  check(cvmm_sort_routes(ptr(flat), flat.scalar_type() == at::kLong ? 1 : 0, R, (int32_t)n_experts,
-                         std::max<int64_t>(top_k, 1), tptr<int32_t>(ssel), tptr<int64_t>(perm), tptr<int64_t>(tok),
-                         tptr<int64_t>(off), tptr<int32_t>(pos), nullptr, ptr(ws), (size_t)ws.numel(),
-                         (void*)stream),
+  Tensor ws = counted_ws.has_value() ? *counted_ws : sort_workspace(flat, stream, ws_bytes);
+  check(cvmm_sort_routes_cast_keys_ex(ptr(flat), flat.scalar_type() == at::kLong ? 1 : 0, R, (int32_t)n_experts,
+                                      std::max<int64_t>(top_k, 1), tptr<int32_t>(ssel), tptr<int64_t>(perm),
+                                      tptr<int64_t>(tok), tptr<int64_t>(off), tptr<int32_t>(pos), nullptr, ptr(ws),
+                                      (size_t)ws.numel(), nullptr, 0, 0, 0, 0, 0, 0, 0, nullptr, nullptr, 0,
+                                      counted_ws.has_value() ? CVMM_FLAG_COUNTS_READY : 0, (void*)stream),
         "cvmm_sort_routes");
   return {ssel, perm, tok, off, pos};
 }
@@ -206,7 +208,8 @@ std::tuple<OptT, OptT> cast_outputs(const Tensor& keys, at::ScalarType op, bool 
 // scatter launch): (sorted, perm, perm // top_k, offsets, route_pos), kt, kn.
 std::tuple<std::vector<Tensor>, OptT, OptT> sort_routes_cast(const Tensor& raw, int64_t n_experts, int64_t top_k,
                                                              const Tensor& keys, int64_t op_id, bool want_t,
-                                                             bool want_n, int64_t layout, int64_t stream) {
+                                                             bool want_n, int64_t layout, int64_t stream,
+                                                             const OptT& counted_ws) {
   require_device(raw, "sel");
   require_device(keys, "keys");
   Tensor flat = raw.reshape({-1});
@@ -222,13 +225,14 @@ std::tuple<std::vector<Tensor>, OptT, OptT> sort_routes_cast(const Tensor& raw, 
   if (E != n_experts) throw py::value_error("cvmm: keys.shape[0] differs from the expert count");
   auto [kt, kn] = cast_outputs(keys, op, want_t, want_n, layout);
   const size_t ws_bytes = cvmm_sort_workspace_bytes(R, (int32_t)n_experts);
-  Tensor ws = sort_workspace(flat, stream, ws_bytes);
-  check(cvmm_sort_routes_cast_keys(ptr(flat), flat.scalar_type() == at::kLong ? 1 : 0, R, (int32_t)n_experts,
-                                   std::max<int64_t>(top_k, 1), tptr<int32_t>(ssel), tptr<int64_t>(perm),
-                                   tptr<int64_t>(tok), tptr<int64_t>(off), tptr<int32_t>(pos), nullptr, ptr(ws),
-                                   (size_t)ws.numel(), ptr(keys), dtype_id(keys.scalar_type()), d_in, d_out,
-                                   keys.stride(0), keys.stride(1), keys.stride(2), (int32_t)op_id, ptr(kt), ptr(kn),
-                                   (int32_t)layout, (void*)stream),
+  Tensor ws = counted_ws.has_value() ? *counted_ws : sort_workspace(flat, stream, ws_bytes);
+  check(cvmm_sort_routes_cast_keys_ex(ptr(flat), flat.scalar_type() == at::kLong ? 1 : 0, R, (int32_t)n_experts,
+                                      std::max<int64_t>(top_k, 1), tptr<int32_t>(ssel), tptr<int64_t>(perm),
+                                      tptr<int64_t>(tok), tptr<int64_t>(off), tptr<int32_t>(pos), nullptr, ptr(ws),
+                                      (size_t)ws.numel(), ptr(keys), dtype_id(keys.scalar_type()), d_in, d_out,
+                                      keys.stride(0), keys.stride(1), keys.stride(2), (int32_t)op_id, ptr(kt),
+                                      ptr(kn), (int32_t)layout, counted_ws.has_value() ? CVMM_FLAG_COUNTS_READY : 0,
+                                      (void*)stream),
         "cvmm_sort_routes_cast_keys");
   return {{ssel, perm, tok, off, pos}, kt, kn};
 }
@@ -290,6 +294,23 @@ Tensor copy_ids(const Tensor& sel, int64_t stream) {
                       (void*)stream),
         "cvmm_copy_ids");
   return out;
+}
+
+// copy_ids plus the sort's count matrix for an expected expert count, in a
+// sort workspace of its own: (ids, workspace).  A sort of the copy for that
+// count passes the workspace and CVMM_FLAG_COUNTS_READY.
+std::tuple<Tensor, Tensor> copy_ids_count(const Tensor& sel, int64_t n_experts, int64_t stream) {
+  require_device(sel, "sel");
+  Tensor flat = sel.reshape({-1});
+  if (flat.scalar_type() != at::kInt && flat.scalar_type() != at::kLong) flat = flat.to(at::kLong);
+  flat = flat.contiguous();
+  Tensor out = at::empty(sel.sizes(), opts(flat, at::kInt));
+  const size_t ws_bytes = cvmm_sort_workspace_bytes(flat.numel(), (int32_t)n_experts);
+  Tensor ws = at::empty({(int64_t)std::max<size_t>(ws_bytes, 1)}, opts(flat, at::kByte));
+  check(cvmm_copy_ids_count(ptr(flat), flat.scalar_type() == at::kLong ? 1 : 0, flat.numel(), (int32_t)n_experts,
+                            tptr<int32_t>(out), ptr(ws), (size_t)ws.numel(), (void*)stream),
+        "cvmm_copy_ids_count");
+  return {out, ws};
 }
 
 Tensor expert_offsets(const Tensor& sorted, int64_t n_experts, int64_t stream) {
@@ -600,15 +621,17 @@ Tensor cvmm_apply(const Tensor& x, const Tensor& keys, const OptT& rw, const Ten
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "Host glue of cvmm_codex_amd: one call per CVMM phase into libcvmm_hip.so";
-  m.def("sort_routes", &sort_routes, py::arg("raw"), py::arg("n_experts"), py::arg("top_k"), py::arg("stream"));
+  m.def("sort_routes", &sort_routes, py::arg("raw"), py::arg("n_experts"), py::arg("top_k"), py::arg("stream"),
+        py::arg("counted_ws") = py::none());
   m.def("expert_offsets", &expert_offsets, py::arg("sorted"), py::arg("n_experts"), py::arg("stream"));
   m.def("copy_ids", &copy_ids, py::arg("sel"), py::arg("stream"));
+  m.def("copy_ids_count", &copy_ids_count, py::arg("sel"), py::arg("n_experts"), py::arg("stream"));
   m.def("route_topk", &route_topk, py::arg("logits"), py::arg("top_k"), py::arg("renormalize"), py::arg("stream"));
   m.def("route_topk_backward", &route_topk_backward, py::arg("logits"), py::arg("sel"), py::arg("grad_weights"),
         py::arg("top_k"), py::arg("renormalize"), py::arg("stream"));
   m.def("sort_routes_cast", &sort_routes_cast, py::arg("raw"), py::arg("n_experts"), py::arg("top_k"),
         py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"), py::arg("layout"),
-        py::arg("stream"));
+        py::arg("stream"), py::arg("counted_ws") = py::none());
   m.def("cast_keys", &cast_keys, py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"),
         py::arg("layout"), py::arg("stream"));
   m.def("forward", &cvmm_forward_impl);

@@ -50,6 +50,9 @@ extern "C" {
 #define CVMM_FLAG_WORKSPACE_ZEROED 8 /* cvmm_fwd / cvmm_bwd_x taking a dense top-k sum: the first
                                         cvmm_topk_dense_zero_bytes() of the workspace are zero,
                                         and the call leaves them zero (see cvmm_topk_dense) */
+#define CVMM_FLAG_COUNTS_READY 16 /* cvmm_sort_routes_cast_keys_ex: the workspace already holds the
+                                     count matrix of these ids for n_experts, written by
+                                     cvmm_copy_ids_count (see there) */
 
 /* kernel classes for the timing hooks */
 #define CVMM_KC_SORT 1        /* histogram + scan + scatter of cvmm_sort_routes */
@@ -193,6 +196,19 @@ int cvmm_sort_routes_cast_keys(const void* sel, int32_t sel_is_int64, int64_t n_
                                int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj, int32_t out_dtype,
                                void* keys_t, void* keys_n, int32_t layout, void* stream);
 
+/* cvmm_sort_routes_cast_keys with flags: CVMM_FLAG_COUNTS_READY skips the
+ * sort's histogram launch, whose count matrix the workspace already holds
+ * (cvmm_copy_ids_count of the same ids for the same n_experts, with the
+ * sort-chunk tuning knob unchanged in between).  keys == NULL (or both
+ * outputs NULL): the sort alone, as cvmm_sort_routes.  No counterpart in the
+ * reference. */
+int cvmm_sort_routes_cast_keys_ex(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts,
+                                  int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
+                                  int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* workspace,
+                                  size_t workspace_bytes, const void* keys, int32_t keys_dtype, int64_t d_in,
+                                  int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj, int32_t out_dtype,
+                                  void* keys_t, void* keys_n, int32_t layout, int32_t flags, void* stream);
+
 /* Router (no counterpart in cvmm.py; replaces its callers' router lines,
  * benchmark_ffn_moe.py:91-97 and benchmark_framework_moe.py:129-135:
  *   probs = softmax(logits.float()); weights, sel = probs.topk(top_k)
@@ -223,6 +239,17 @@ int cvmm_route_topk_backward(const void* logits, int32_t logits_dtype, int64_t n
  * the `fsel = sel.flatten().to(torch.int32)` copy cvmm_prepare_sel2 takes
  * (cvmm.py:1796), which fixes the routing when the selector is prepared. */
 int cvmm_copy_ids(const void* sel, int32_t sel_is_int64, int64_t n, int32_t* out, void* stream);
+
+/* cvmm_copy_ids that also writes, into a sort workspace (size
+ * cvmm_sort_workspace_bytes(n, n_experts)), the per-chunk expert histogram
+ * the sort of the copy would compute first for n_experts; a later
+ * cvmm_sort_routes_cast_keys_ex with CVMM_FLAG_COUNTS_READY and that
+ * workspace skips its histogram launch.  The copy is what cvmm_copy_ids
+ * writes (cvmm.py:1796); the histogram has no counterpart in the reference:
+ * cvmm_prepare_sel2 does not know the expert count, so the caller passes the
+ * count it expects and sorts without the flag when the call uses another. */
+int cvmm_copy_ids_count(const void* sel, int32_t sel_is_int64, int64_t n, int32_t n_experts, int32_t* out,
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* offsets[e] = #{i : sorted_sel[i] <= e}; replaces cvmm_expert_offsets
  * (cvmm.py:1108-1120, kernel cvmm.py:315-335). */

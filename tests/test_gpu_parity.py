@@ -289,6 +289,79 @@ def test_sort_and_cast_in_one_call_match_the_separate_calls(R, E, k, d_in, d_out
     assert fused == (d_in % 64 == 0 and d_out % 64 == 0)
 
 
+@pytest.mark.parametrize("R,E,k,d_in,d_out,is64", [
+    (65536, 64, 8, 1024, 128, True), (4000, 16, 4, 128, 192, False), (777, 300, 1, 256, 64, True),
+    (4000, 16, 4, 96, 128, True),        # cast not fusable: separate cast launch
+    (524288, 256, 64, 2048, 64, True),   # column-scan scatter
+    (3000, 9000, 2, 64, 64, False),      # many-bucket scatter
+])
+def test_sort_with_counts_from_the_id_copy(R, E, k, d_in, d_out, is64):
+    """cvmm_copy_ids_count (the id copy plus the sort's histogram) followed by
+    cvmm_sort_routes_cast_keys_ex with CVMM_FLAG_COUNTS_READY gives the bits
+    of cvmm_copy_ids + cvmm_sort_routes + cvmm_cast_keys, out-of-range ids
+    included; keys NULL gives the sort alone."""
+    from cvmm_codex_amd import _native as N
+    lib = N.lib()
+    g = torch.Generator().manual_seed(R + E + 1)
+    raw = torch.randint(-1, E + 1, (R,), generator=g).cuda()
+    if not is64:
+        raw = raw.to(torch.int32)
+    keys = torch.randn(E, d_in, d_out, generator=g).cuda() if E * d_in * d_out <= 1 << 26 else None
+    st = N.stream_of(raw.device)
+    ws_b = lib.cvmm_sort_workspace_bytes(R, E)
+
+    def outputs():
+        o = dict(ids=torch.full((R,), -7, dtype=torch.int32, device="cuda"),
+                 ssel=torch.full((R,), -7, dtype=torch.int32, device="cuda"),
+                 perm=torch.full((R,), -7, dtype=torch.int64, device="cuda"),
+                 tok=torch.full((R,), -7, dtype=torch.int64, device="cuda"),
+                 off=torch.full((E,), -7, dtype=torch.int64, device="cuda"),
+                 pos=torch.full((R,), -7, dtype=torch.int32, device="cuda"),
+                 nin=torch.full((1,), -7, dtype=torch.int32, device="cuda"),
+                 ws=torch.full((ws_b,), 0xA5, dtype=torch.uint8, device="cuda"))
+        if keys is not None:
+            o["kt"] = torch.zeros(E, d_out, d_in, dtype=torch.bfloat16, device="cuda")
+            o["kn"] = torch.zeros(E, d_in, d_out, dtype=torch.bfloat16, device="cuda")
+        return o
+
+    a, b = outputs(), outputs()
+    sort_args = lambda o: (N.ptr(o["ids"]), 0, R, E, k, N.ptr(o["ssel"]), N.ptr(o["perm"]), N.ptr(o["tok"]),
+                           N.ptr(o["off"]), N.ptr(o["pos"]), N.ptr(o["nin"]), N.ptr(o["ws"]), ws_b)
+    N.check(lib.cvmm_copy_ids(N.ptr(raw), int(is64), R, N.ptr(a["ids"]), st), "copy")
+    N.check(lib.cvmm_sort_routes(*sort_args(a), st), "sort")
+    N.check(lib.cvmm_copy_ids_count(N.ptr(raw), int(is64), R, E, N.ptr(b["ids"]), N.ptr(b["ws"]), ws_b, st),
+            "copy+count")
+    if keys is not None:
+        N.check(lib.cvmm_cast_keys(N.ptr(keys), N.F32, E, d_in, d_out, *keys.stride(), N.BF16, N.ptr(a["kt"]),
+                                   N.ptr(a["kn"]), 0, st), "cast")
+        N.check(lib.cvmm_sort_routes_cast_keys_ex(*sort_args(b), N.ptr(keys), N.F32, d_in, d_out, *keys.stride(),
+                                                  N.BF16, N.ptr(b["kt"]), N.ptr(b["kn"]), 0, N.FLAG_COUNTS_READY,
+                                                  st), "sort+cast, counted")
+    else:
+        N.check(lib.cvmm_sort_routes_cast_keys_ex(*sort_args(b), None, 0, 0, 0, 0, 0, 0, 0, None, None, 0,
+                                                  N.FLAG_COUNTS_READY, st), "sort, counted")
+    torch.cuda.synchronize()
+    for n in ("ids", "ssel", "perm", "tok", "off", "pos", "nin") + (("kt", "kn") if keys is not None else ()):
+        assert torch.equal(a[n], b[n]), n
+
+
+def test_prepared_selection_sorts_with_the_expected_expert_count():
+    """cvmm_prepare_sel2 counts the ids for the expert count the last sort of
+    a same-sized selection used, and cvmm() sorts without the histogram launch
+    when its keys bring that count; another count sorts from scratch.  Three
+    calls (no expectation yet, the expected count, a different count) each
+    match the oracle."""
+    x, keys, sel, w, go = _rand_case(71, 2, 96, 64, 80, 8, 4, False, False)
+    key = (sel.numel(), sel.shape[-1])
+    C._expert_guess.pop(key, None)
+    for E in (8, 8, 12):
+        keys_e = keys if E == 8 else (torch.randn(E, 64, 80, generator=torch.Generator().manual_seed(E)) / 8)
+        got = U.run_hip(x, keys_e, sel, w, go, False, True)
+        exp = U.run_oracle(x, keys_e, sel, w, go, False, True)
+        U.compare(got, exp, 2e-2)
+        assert C._expert_guess[key] == E
+
+
 @pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True), (True, False)])
 def test_invalid_ids_contribute_nothing(weighted, route_input):
     """Routes whose expert id is outside [0, E) sort last and no GEMM writes

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.cvmm_abi_version() == 10
+    assert lib.cvmm_abi_version() == 11
 
 
 def test_workspace_queries(lib):
@@ -76,6 +76,11 @@ def test_invalid_arguments_fail_before_launch(lib):
     assert rc == 1 and b"n_experts" in lib.cvmm_last_error()
     rc = lib.cvmm_sort_routes_noalloc(None, 0, 10, 100000, 1, None, None, None, None, None, None, None)
     assert rc == 2
+    # the id copy with the sort's histogram: expert count, workspace; the sort with unknown flags
+    assert lib.cvmm_copy_ids_count(None, 0, 10, 0, None, None, 0, None) == 1
+    assert lib.cvmm_copy_ids_count(ctypes.c_void_p(16), 0, 10, 8, ctypes.c_void_p(16), None, 0, None) == 3
+    assert lib.cvmm_sort_routes_cast_keys_ex(None, 0, 10, 8, 1, None, None, None, None, None, None, None, 0, None,
+                                             0, 0, 0, 0, 0, 0, 0, None, None, 0, 64, None) == 1
     args = [None, 7, 1, 16, None, 0, 4, 16, 8, 128, 8, 1, None, None, None, 1, None, None, None, 0, 1,
             0, None, 0, 1, 8, 0, None, 0, None]
     assert lib.cvmm_fwd(*args) == 1 and b"dtype" in lib.cvmm_last_error()
