@@ -987,13 +987,16 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
   }
 
   float* dg_part = nullptr;
+  bool dg_direct = false;
   const int64_t dg_nt = ntiles_of(d_in, gemm_bn(d_in));
   if (weighted && grad_rw) {
     // no fill: the GEMM writes every (route, n tile) partial -- covered
     // routes from their tile's epilogue, out-of-range expert ids as zeros
-    // from the workgroups past the last m-tile
+    // from the workgroups past the last m-tile.  One n tile and an fp32
+    // gradient: the partial is the gradient, written in place.
     dg_part = (float*)c.take((size_t)n_routes * dg_nt * 4);
-    p.dg = dg_part; p.dg_ntiles = (int32_t)dg_nt;
+    dg_direct = dg_nt == 1 && grad_rw_dtype == kF32;
+    p.dg = dg_direct ? (float*)grad_rw : dg_part; p.dg_ntiles = (int32_t)dg_nt;
     p.dg_x = x; p.dg_x_dtype = x_dtype; p.dg_x_ld = x_ld; p.dg_x_rows = x_rows; p.dg_x_idx = sel_index;
     p.dg_val_dtype = op_dtype;
   }
@@ -1014,7 +1017,7 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
     }
     if (r) return r;
   }
-  if (dg_part) {
+  if (dg_part && !dg_direct) {
     r = check_launch(timed_combine(s, [&] { return launch_sum_partials(dg_part, n_routes, (int32_t)dg_nt, grad_rw, grad_rw_dtype, s); }),
                      "cvmm_bwd_x(dgate)");
     if (r) return r;
