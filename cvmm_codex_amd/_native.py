@@ -180,6 +180,13 @@ def ptr(t) -> int | None:
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
+def stream_of_tensor(t: torch.Tensor) -> int:
+    """Raw handle of the current HIP stream of `t`'s device."""
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
+    return stream_of(t.device)
+
+
 def stream_of(device: torch.device) -> int:
     """Raw handle of the current HIP stream of `device` (the kernels launch on it)."""
     idx = device.index if device.index is not None else torch.cuda.current_device()

@@ -431,17 +431,20 @@ def cvmm_prepare_sel2(sel: Union[torch.Tensor, CVMMSel], w: Optional[torch.Tenso
         fsel = sel.reshape(-1)
         fsel = fsel.clone() if fsel.dtype == torch.int32 else fsel.to(torch.int32)
         routing = _Routing(fsel, n_per_batch)
+        shaped = fsel.view(sel.shape)
     else:
         guess = _expert_guess.get((sel.numel(), n_per_batch))
+        stream = N.stream_of_tensor(sel)
         if guess is not None:
-            fsel, ws = N.host().copy_ids_count(sel, guess, N.stream_of(sel.device))
-            fsel = fsel.reshape(-1)
+            shaped, ws = N.host().copy_ids_count(sel, guess, stream)
+            fsel = shaped.reshape(-1)
             routing = _Routing(fsel, n_per_batch, (guess, ws))
         else:
-            fsel = N.host().copy_ids(sel, N.stream_of(sel.device)).reshape(-1)
+            shaped = N.host().copy_ids(sel, stream)
+            fsel = shaped.reshape(-1)
             routing = _Routing(fsel, n_per_batch)
-    out = CVMMSel._deferred(fsel.view(sel.shape), routing, route_input, w)
-    out._raw_sel = out._raw_src
+    out = CVMMSel._deferred(shaped, routing, route_input, w)
+    out._raw_sel = shaped
     return out
 
 
@@ -711,56 +714,76 @@ def create_kernels() -> None:
 
 def cvmm(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.Tensor) -> torch.Tensor:
     """cvmm.py:1759-1783."""
-    if not _compiling():  # the ops load the library when they run
-        create_kernels()
+    if not _compiling():
+        return _cvmm_eager(x, sel, keys)
     if not isinstance(sel, CVMMSel):
         sel = cvmm_prepare_sel(sel, keys.shape[0])
-    # a selection still to be sorted is sorted in the launches that also cast
-    # this step's weights (consumed by CVMM.forward below)
-    cast = None
-    op = get_dtype()
-    if sel._pending() and keys.is_cuda and _fast_path(op, keys.shape[1], keys.shape[2]) and not _compiling():
-        rw = sel.reduction_weight
-        raw = sel._raw_shape_tensor()
-        k = rw.shape[-1] if rw is not None else (raw.shape[-1] if raw.ndim else 1)
-        need = torch.is_grad_enabled() and (x.requires_grad or (rw is not None and rw.requires_grad))
-        cast = (keys, op, _plan_copies(keys, op, raw.numel(), k, rw is not None, not sel._route_mode, need))
-    sel._resolve(keys.shape[0], cast)
+    sel._resolve(keys.shape[0])
+    _log_shape(x, keys)
+    return CVMM.apply(x, sel._raw_shape_tensor(), sel.sel_index, sel.sel, keys, sel.out_index,
+                      sel.reduction_weight)
+
+
+def _log_shape(x: torch.Tensor, keys: torch.Tensor) -> None:
     if cvmm_log_shapes:
         sh = (x.shape, keys.shape)
         if sh not in known_shapes:
             print("New shape:", sh)
             known_shapes.add(sh)
-    if not _compiling():
-        return _cvmm_native(x, sel, keys)
-    return CVMM.apply(x, sel._raw_shape_tensor(), sel.sel_index, sel.sel, keys, sel.out_index,
-                      sel.reduction_weight)
 
 
-def _cvmm_native(x: torch.Tensor, sel: CVMMSel, keys: torch.Tensor) -> torch.Tensor:
-    """CVMM.apply for eager calls, as one C++ autograd function (the host
-    glue's ``cvmm_apply``): the same forward and backward host calls as
-    CVMM.forward / CVMM.backward, with the backward node run by the autograd
-    engine without Python (no GIL taken on its device thread)."""
-    rw = sel.reduction_weight
-    raw = sel._raw_shape_tensor()
-    s, sel_index, out_index = sel.sel, sel.sel_index, sel.out_index
-    top_k = raw.shape[-1] if raw.ndim > 0 else 1
+def _cvmm_eager(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.Tensor) -> torch.Tensor:
+    """cvmm() outside torch.compile tracing: CVMM.apply as one C++ autograd
+    function (the host glue's ``cvmm_apply``) with the same forward and
+    backward host calls as CVMM.forward / CVMM.backward; its backward node
+    runs in the autograd engine without Python (no GIL taken on the engine's
+    device thread).  A selection still to be sorted is sorted in the launches
+    that also cast this step's weights."""
+    if N._host is None:
+        create_kernels()
+    if not isinstance(sel, CVMMSel):
+        sel = cvmm_prepare_sel(sel, keys.shape[0])
+    E, d_in, d_out = keys.shape
     op = get_dtype()
+    rw = sel.reduction_weight
+    weighted = rw is not None
+    raw = sel._raw_shape_tensor()
+    top_k = raw.shape[-1] if raw.ndim > 0 else 1
+    pending = sel._pending()
+    plan = None
+    if keys.is_cuda and _fast_path(op, d_in, d_out):
+        # the eager branch of _plan_copies
+        need = torch.is_grad_enabled() and (x.requires_grad or (weighted and rw.requires_grad))
+        token_input = (not sel._route_mode) if pending else sel._out_index is not None
+        k = rw.shape[-1] if weighted else top_k
+        op_id = _DTYPE_IDS[op]
+        T = raw.numel() // k if k > 0 else 0
+        fwd_dense = weighted and k >= 2 and not cvmm_atomic_reduce and _topk_dense(T, E, d_in, d_out, k, op_id)
+        bwd_dense = (need and not weighted and token_input and k >= 2 and not cvmm_atomic_reduce
+                     and _topk_dense(T, E, d_out, d_in, k, op_id))
+        layout = (N.CAST_T_INTERLEAVED if fwd_dense else 0) | (N.CAST_N_INTERLEAVED if bwd_dense else 0)
+        plan = _CopyPlan(True, need, layout, True, False)
+    if pending:
+        sel._resolve(E, (keys, op, plan) if plan is not None else None)
+    _log_shape(x, keys)
+    s, sel_index, out_index = sel._sel, sel._sel_index, sel._out_index
     keys_op = keys_x = None
     fwd_t, keys_x_is_t = True, False
-    weighted = rw is not None
-    if _fast_path(op, keys.shape[1], keys.shape[2]):
-        k = rw.shape[-1] if weighted else top_k
-        need = torch.is_grad_enabled() and (x.requires_grad or (weighted and rw.requires_grad))
-        plan = _plan_copies(keys, op, s.numel(), k, weighted, out_index is not None, need)
+    if plan is not None:
         pre = _take_cast(keys, op, plan)
         kt, kn = pre if pre is not None else _cast_keys(keys, op, plan)
-        if need:
+        if plan.want_n:
             keys_x, keys_x_is_t = _copy_view(plan, kt, kn, False)
         keys_op, fwd_t = _copy_view(plan, kt, kn, True)
-    _require_device(s, "sel")
-    shape = [*rw.shape[:-1], keys.shape[2]] if weighted else [*s.shape, keys.shape[2]]
-    return N.host().cvmm_apply(x, keys, rw, s, sel_index, out_index, _offsets_for(s, keys.shape[0]),
-                               _route_pos(out_index if out_index is not None else sel_index, s.numel()),
-                               keys_op, fwd_t, keys_x, keys_x_is_t, top_k, N.dtype_id(op), _flags(), shape)
+    if not s.is_cuda:
+        _require_device(s, "sel")
+    shape = [*rw.shape[:-1], d_out] if weighted else [*s.shape, d_out]
+    rp = out_index if out_index is not None else sel_index
+    pos = getattr(rp, "_cvmm_route_pos", None)
+    if pos is not None and pos.numel() != s.numel():
+        pos = None
+    return N._host.cvmm_apply(x, keys, rw, s, sel_index, out_index, _offsets_for(s, E), pos, keys_op, fwd_t,
+                              keys_x, keys_x_is_t, top_k, _DTYPE_IDS[op], _flags(), shape)
+
+
+_DTYPE_IDS = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
