@@ -185,8 +185,25 @@ def _plan_copies(keys: torch.Tensor, op: torch.dtype, n_routes: int, top_k: int,
         fwd_t, bwd_t = not fwd_dense, bwd_dense
         return _CopyPlan(fwd_t or (need_grad_input and bwd_t), (not fwd_t) or (need_grad_input and not bwd_t),
                          0, fwd_t, bwd_t)
+    return _eager_plan(d_in, d_out, fwd_dense, bwd_dense, need_grad_input)
+
+
+def _eager_plan(d_in: int, d_out: int, fwd_dense: bool, bwd_dense: bool, need_grad_input: bool) -> _CopyPlan:
+    """Eager copies: one copy where one product runs the long-K routed GEMM
+    (K > 128), which reads the weights in either orientation, and the other
+    product needs that copy's own orientation (the short-K kernel's, or a
+    dense top-k sum's interleaved rows); else kt for the forward and kn for
+    the grad-input."""
     layout = (N.CAST_T_INTERLEAVED if fwd_dense else 0) | (N.CAST_N_INTERLEAVED if bwd_dense else 0)
-    return _CopyPlan(True, need_grad_input, layout, True, False)
+    if not need_grad_input:
+        return _CopyPlan(True, False, layout, True, False)
+    fwd_ring = d_in > 128 and not fwd_dense
+    bwd_ring = d_out > 128 and not bwd_dense
+    if fwd_ring:       # kn only: the forward reads it n-contiguous
+        return _CopyPlan(False, True, layout, False, False)
+    if bwd_ring:       # kt only: the grad-input reads it n-contiguous
+        return _CopyPlan(True, False, layout, True, True)
+    return _CopyPlan(True, True, layout, True, False)
 
 
 def _copy_view(plan: _CopyPlan, kt, kn, fwd: bool):
@@ -650,16 +667,15 @@ class CVMMGelu(torch.autograd.Function):
     def forward(ctx, x: torch.Tensor, raw_sel: torch.Tensor, sel_index: torch.Tensor, sel: torch.Tensor,
                 keys: torch.Tensor, out_index: Optional[torch.Tensor] = None):
         out_type = get_dtype()
-        keys_t = None
+        keys_t, is_t = None, True
         ctx.keys_x, ctx.keys_x_is_t = None, False
         if _fast_path(out_type, keys.shape[1], keys.shape[2]):
             k = raw_sel.shape[-1] if raw_sel.ndim > 0 else 1
             keys_t, is_t = _copies_for_call(ctx, keys, out_type, sel.numel(), k, False, out_index is not None,
                                             ctx.needs_input_grad[0])
-            assert is_t, "an unweighted forward reads the routed-layout kt copy"
         n_experts = keys.shape[0]
         R = sel.numel()
-        y, h = N.host().forward_gelu(x, keys, keys_t, sel, sel_index, out_index, _offsets_for(sel, n_experts),
+        y, h = N.host().forward_gelu(x, keys, keys_t, is_t, sel, sel_index, out_index, _offsets_for(sel, n_experts),
                                      _route_pos(out_index if out_index is not None else sel_index, R),
                                      N.dtype_id(out_type), _flags(), N.stream_of(x.device))
         ctx.save_for_backward(x, keys, raw_sel, sel, sel_index, out_index, h)
@@ -761,8 +777,7 @@ def _cvmm_eager(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.
         fwd_dense = weighted and k >= 2 and not cvmm_atomic_reduce and _topk_dense(T, E, d_in, d_out, k, op_id)
         bwd_dense = (need and not weighted and token_input and k >= 2 and not cvmm_atomic_reduce
                      and _topk_dense(T, E, d_out, d_in, k, op_id))
-        layout = (N.CAST_T_INTERLEAVED if fwd_dense else 0) | (N.CAST_N_INTERLEAVED if bwd_dense else 0)
-        plan = _CopyPlan(True, need, layout, True, False)
+        plan = _eager_plan(d_in, d_out, fwd_dense, bwd_dense, need)
     if pending:
         sel._resolve(E, (keys, op, plan) if plan is not None else None)
     _log_shape(x, keys)
@@ -772,7 +787,7 @@ def _cvmm_eager(x: torch.Tensor, sel: Union[torch.Tensor, CVMMSel], keys: torch.
     if plan is not None:
         pre = _take_cast(keys, op, plan)
         kt, kn = pre if pre is not None else _cast_keys(keys, op, plan)
-        if plan.want_n:
+        if need:
             keys_x, keys_x_is_t = _copy_view(plan, kt, kn, False)
         keys_op, fwd_t = _copy_view(plan, kt, kn, True)
     if not s.is_cuda:

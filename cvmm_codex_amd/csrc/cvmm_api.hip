@@ -26,10 +26,15 @@ bool routed_gemm_ring_applies(const GemmParams& p, int32_t op);
 
 // Fast path (DMA-staged, 16-bit k-contiguous operands) when eligible, else the
 // general kernel (any storage type / stride / width).
+// Weights k-contiguous, or n-contiguous ([k][n] rows of the other
+// orientation's copy) where the long-K ring kernel takes them.
 static bool nt_eligible(const GemmParams& p, int32_t op) {
   auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-  return (op == kBF16 || op == kF16) && p.a_dtype == op && p.b_dtype == op && p.b_sk == 1 && p.K % 8 == 0 &&
-         p.epi == kEpiStore && al(p.a) && al(p.b) && p.a_ld % 8 == 0 && p.b_sn % 8 == 0 && p.b_se % 8 == 0;
+  const bool common = (op == kBF16 || op == kF16) && p.a_dtype == op && p.b_dtype == op && p.K % 8 == 0 &&
+                      p.epi == kEpiStore && al(p.a) && al(p.b) && p.a_ld % 8 == 0 && p.b_se % 8 == 0;
+  if (!common) return false;
+  if (p.b_sk == 1) return p.b_sn % 8 == 0;
+  return p.b_sn == 1 && p.b_sk % 8 == 0 && p.N % 8 == 0 && routed_gemm_ring_applies(p, op);
 }
 
 hipError_t launch_routed_gemm(const GemmParams& p, int32_t op, hipStream_t s) {

@@ -143,6 +143,18 @@ __device__ __forceinline__ void lgkm_wait_w(lds_u32x4 (&w)[2]) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(w[0]), "+v"(w[1]));
 }
 
+// 16-byte chunk swizzle of [k][column] rows read by ds_read_b64_tr_b16 (lane
+// L of a 16-lane group reads 8 bytes of row L / 4 at column 4 * (L % 4); the
+// group's 4 rows x 32 bytes land on distinct banks).  The rule sees row bits
+// 0, 1 and 3 only, so rows r and r + 4, r + 32 share it.  CPR = chunks per
+// row: 16 or 32 (256- or 512-byte rows: the 256-byte rule within each half)
+// or 8 (128-byte rows).
+template <int CPR>
+__device__ __forceinline__ int tr_row_swz(int row) {
+  if constexpr (CPR >= 16) return 2 * ((row & 3) | (((row >> 3) & 1) << 2));
+  else return 2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1));
+}
+
 // Wait until at most `ahead` slices (D DMA instructions each) are in flight.
 template <int D, int K>
 __device__ __forceinline__ void vm_wait_slices(int ahead) {
@@ -359,7 +371,8 @@ __global__ __launch_bounds__(kGemmThreads, (PanelCfg<KP, BN, WM>::OCC)) void rou
 inline bool panel_eligible(const GemmParams& p, int32_t op) {
   const size_t osz = p.out_dtype == kF32 ? 16 : 8;
   const size_t esz = p.out_dtype == kF32 ? 4 : 2;
-  return p.K <= 128 && p.act == 0 && p.epi == kEpiStore && p.dg == nullptr && p.w == nullptr && p.out != nullptr &&
+  return p.K <= 128 && p.b_sk == 1 && p.act == 0 && p.epi == kEpiStore && p.dg == nullptr && p.w == nullptr &&
+         p.out != nullptr &&
          p.val_dtype == p.out_dtype && (p.out_dtype == op || p.out_dtype == kF32) && p.N % 64 == 0 &&
          (reinterpret_cast<uintptr_t>(p.out) % osz) == 0 && ((size_t)p.out_ld * esz) % osz == 0;
 }

@@ -34,6 +34,8 @@
 // chunk ^ ((r >> 2) & 3) or no swizzle.
 #pragma once
 
+#include <type_traits>
+
 #include "cvmm_gemm_panel.h"
 
 namespace cvmm {
@@ -77,10 +79,34 @@ __device__ __forceinline__ void lds_wait_tied_n(lds_u32x4 (&x)[NB], lds_u32x4 (&
   for (int i = 1; i < NA; ++i) asm volatile("" : "+v"(y[i]));
 }
 
-template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int Role, int BK, bool DG = false>
+// lgkmcnt(0) tied to the registers of one k step's transposed B reads (two
+// 8-byte reads per 16-column block) and its A fragment reads.
+template <int NA>
+__device__ __forceinline__ void lds_wait_tied_tr(lds_u32x2 (&x)[4][2], lds_u32x4 (&y)[NA]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x[0][0]), "+v"(y[0]));
+  asm volatile("" : "+v"(x[0][1]));
+#pragma unroll
+  for (int i = 1; i < 4; ++i) asm volatile("" : "+v"(x[i][0]), "+v"(x[i][1]));
+#pragma unroll
+  for (int i = 1; i < NA; ++i) asm volatile("" : "+v"(y[i]));
+}
+
+// BNC: the weights are n-contiguous in memory (B[k][n] rows of N values, as
+// the other orientation's copy holds them).  Their slices then sit in LDS as
+// BK rows of BN columns, and ds_read_b64_tr_b16 hands each lane 4 k values of
+// one column per read; two reads make the 8 consecutive k values of an MFMA
+// operand (the weight gradient's transposed reads).  One weight copy then
+// serves both products of a step.
+template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int Role, int BK, bool DG = false,
+          bool BNC = false>
 __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(const GemmParams p) {
   using Cfg = RingCfg<BM, BN, STAGES, BK>;
   constexpr int MB = Cfg::MB, WR = Cfg::WROWS;
+  constexpr int ROWB_B = BNC ? BN * 2 : Cfg::ROWB;  // bytes per LDS row of a B slice
+  constexpr int CPR_B = ROWB_B / 16;
+  constexpr int A_INSTS = Cfg::A_BYTES / 1024;     // DMA instructions of a slice's A rows
+  static_assert(Cfg::A_BYTES % 1024 == 0, "A and B rows in separate DMA instructions");
+  static_assert(!BNC || CPR_B == 8 || CPR_B == 16, "128- or 256-byte B rows");
   static_assert(!RA || Cfg::KSS == 1, "read-ahead keeps one k step per slice");
   __shared__ __attribute__((aligned(1024))) char ring[STAGES * Cfg::SLICE_BYTES];
   __shared__ RouteMeta<BM> meta;
@@ -101,30 +127,45 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   const int32_t expert = meta.expert;
 
   // ---- per-lane DMA sources: instruction j of wave w fills LDS bytes
-  // [(w * D + j) * 1024, +1024) of a slice = 16 rows of 64 bytes; A rows first
+  // [(w * D + j) * 1024, +1024) of a slice; A rows first, then B rows ([n][k]
+  // rows of BK values, or with BNC [k][n] rows of BN values)
   const char* zero = reinterpret_cast<const char*>(g_cvmm_zero_page);
   const char* src[Cfg::D];
-  int kc[Cfg::D];  // element offset of this lane's chunk within a slice
+  int kc[Cfg::D];  // k of this lane's chunk within a slice: its first element, or (BNC B) its row
 #pragma unroll
   for (int j = 0; j < Cfg::D; ++j) {
     const int q = (wave * Cfg::D + j) * 64 + lane;  // 16-byte chunk index within the slice
-    const int row = q / Cfg::CPR;
-    const int c = (q % Cfg::CPR) ^ ring_swz<Cfg::CPR>(row);
-    kc[j] = c * 8;
-    if (row < BM) {
+    if (wave * Cfg::D + j < A_INSTS) {
+      const int row = q / Cfg::CPR;
+      const int c = (q % Cfg::CPR) ^ ring_swz<Cfg::CPR>(row);
+      kc[j] = c * 8;
       const int64_t ar = meta.arow[row];
       src[j] = ar >= 0 ? reinterpret_cast<const char*>(p.a) + (ar * p.a_ld + c * 8) * 2 : nullptr;
-    } else {
+    } else if constexpr (!BNC) {
+      const int row = q / Cfg::CPR;
+      const int c = (q % Cfg::CPR) ^ ring_swz<Cfg::CPR>(row);
+      kc[j] = c * 8;
       const int64_t gn = n0 + (row - BM);
       src[j] = gn < p.N ? reinterpret_cast<const char*>(p.b) + ((int64_t)expert * p.b_se + gn * p.b_sn + c * 8) * 2
                         : nullptr;
+    } else {
+      const int qb = q - A_INSTS * 64;
+      const int krow = qb / CPR_B;
+      const int c = (qb % CPR_B) ^ tr_row_swz<CPR_B>(krow);
+      kc[j] = krow;
+      const int64_t gn = n0 + c * 8;
+      src[j] = gn < p.N ? reinterpret_cast<const char*>(p.b) + ((int64_t)expert * p.b_se + krow * p.b_sk + gn) * 2
+                        : nullptr;
     }
   }
+  // bytes a chunk's source moves per k: 2 along a row, a row stride for BNC B
+  const int64_t b_adv = BNC ? p.b_sk * 2 : 2;
   auto issue = [&](int64_t s, char* buf) {
     const int64_t k0 = s * Cfg::BK;
 #pragma unroll
     for (int j = 0; j < Cfg::D; ++j) {
-      const char* sp = (src[j] != nullptr && k0 + kc[j] < p.K) ? src[j] + k0 * 2 : zero;
+      const int64_t adv = wave * Cfg::D + j < A_INSTS ? 2 : b_adv;
+      const char* sp = (src[j] != nullptr && k0 + kc[j] < p.K) ? src[j] + k0 * adv : zero;
       dma16(sp, buf + (wave * Cfg::D + j) * 1024);
     }
   };
@@ -132,6 +173,10 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   // ---- fragments: lane reads row (l % 16) of each 16-row block, chunk l / 16
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   const int fr = lane & 15, fq = lane >> 4;
+  // B fragment of n-block i, k step kk: lane l holds B[n = 16 i + l % 16]
+  // [k = 32 kk + 8 (l / 16) .. + 8].  [n][k] rows: one 16-byte read.  BNC
+  // [k][n] rows: two transposed reads of rows 8 (l / 16) + (l % 16) / 4 and
+  // + 4, at column 4 (l % 4) of the 16-column block.
   int a_off[Cfg::KSS][MB], b_off[Cfg::KSS][4];  // per k step of a slice
 #pragma unroll
   for (int kk = 0; kk < Cfg::KSS; ++kk) {
@@ -142,8 +187,14 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int rb = BM + wn * 64 + i * 16 + fr;
-      b_off[kk][i] = rb * Cfg::ROWB + (((kk * 4 + fq) ^ ring_swz<Cfg::CPR>(rb)) << 4);
+      if constexpr (BNC) {
+        const int r = kk * 32 + fq * 8 + (fr >> 2);
+        const int lane_lo = ((fr & 1) << 3) + (((fr >> 1) & 1) << 4);
+        b_off[kk][i] = Cfg::A_BYTES + r * ROWB_B + lane_lo + (((wn * 8 + 2 * i) ^ tr_row_swz<CPR_B>(r)) << 4);
+      } else {
+        const int rb = BM + wn * 64 + i * 16 + fr;
+        b_off[kk][i] = rb * Cfg::ROWB + (((kk * 4 + fq) ^ ring_swz<Cfg::CPR>(rb)) << 4);
+      }
     }
   }
   f32x4_t acc[4][MB];  // acc[i][j]: n-block i, m-block j (C^T orientation)
@@ -151,17 +202,35 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < MB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  auto read_frags = [&](const char* buf, lds_u32x4 (&af)[MB], lds_u32x4 (&bf)[4], int kk = 0) {
+  using BFrag = std::conditional_t<BNC, lds_u32x2[4][2], lds_u32x4[4]>;
+  auto read_frags = [&](const char* buf, lds_u32x4 (&af)[MB], BFrag& bf, int kk = 0) {
+    if constexpr (BNC) {
+      const uint32_t base = lds_addr(buf);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) bf[i] = lds_read128(buf + b_off[kk][i]);
+      for (int i = 0; i < 4; ++i) {
+        bf[i][0] = lds_read_tr<0>(base + b_off[kk][i]);
+        bf[i][1] = lds_read_tr<4 * ROWB_B>(base + b_off[kk][i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bf[i] = lds_read128(buf + b_off[kk][i]);
+    }
 #pragma unroll
     for (int j = 0; j < MB; ++j) af[j] = lds_read128(buf + a_off[kk][j]);
   };
-  auto mfma = [&](lds_u32x4 (&af)[MB], lds_u32x4 (&bf)[4]) {
+  auto wait_frags = [&](BFrag& bf, lds_u32x4 (&af)[MB]) {
+    if constexpr (BNC) lds_wait_tied_tr(bf, af);
+    else lds_wait_tied_n(bf, af);
+  };
+  auto mfma = [&](lds_u32x4 (&af)[MB], BFrag& bf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
+      uint4 b;
+      if constexpr (BNC) b = make_uint4(bf[i][0].x, bf[i][0].y, bf[i][1].x, bf[i][1].y);
+      else b = as_uint4(bf[i]);
 #pragma unroll
-      for (int j = 0; j < MB; ++j) MfmaOp<OpT>::step(acc[i][j], as_uint4(bf[i]), as_uint4(af[j]));
+      for (int j = 0; j < MB; ++j) MfmaOp<OpT>::step(acc[i][j], b, as_uint4(af[j]));
+    }
   };
 
   const int64_t nk = (p.K + Cfg::BK - 1) / Cfg::BK;
@@ -175,13 +244,14 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
       issue(s0, ring + s0 * Cfg::SLICE_BYTES);
       issue_fence();
     }
-    lds_u32x4 a0[MB], b0[4], a1[MB], b1[4];
+    lds_u32x4 a0[MB], a1[MB];
+    BFrag b0, b1;
     vm_wait<(STAGES - 1) * Cfg::D>();
     wg_barrier();
     read_frags(ring, a0, b0);
-    lds_wait_tied_n(b0, a0);
+    wait_frags(b0, a0);
     int buf = 0;  // buffer of slice s
-    auto step = [&](int64_t s, lds_u32x4 (&ac)[MB], lds_u32x4 (&bc)[4], lds_u32x4 (&an)[MB], lds_u32x4 (&bn)[4]) {
+    auto step = [&](int64_t s, lds_u32x4 (&ac)[MB], BFrag& bc, lds_u32x4 (&an)[MB], BFrag& bn) {
       const int nxt = buf + 1 == STAGES ? 0 : buf + 1;
       vm_wait<(STAGES - 2) * Cfg::D>();  // slice s + 1 has landed (only DMA is in flight)
       wg_barrier();
@@ -189,7 +259,7 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
       issue_fence();
       read_frags(ring + nxt * Cfg::SLICE_BYTES, an, bn);
       mfma(ac, bc);
-      lds_wait_tied_n(bn, an);
+      wait_frags(bn, an);
       buf = nxt;
     };
     for (int64_t s = 0; s < nk; s += 2) {
@@ -213,9 +283,10 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
       issue_fence();
 #pragma unroll
       for (int kk = 0; kk < Cfg::KSS; ++kk) {
-        lds_u32x4 af[MB], bf[4];
+        lds_u32x4 af[MB];
+        BFrag bf;
         read_frags(ring + cur * Cfg::SLICE_BYTES, af, bf, kk);
-        lds_wait_tied_n(bf, af);
+        wait_frags(bf, af);
         mfma(af, bf);
       }
       cur = cur + 1 == STAGES ? 0 : cur + 1;
@@ -426,15 +497,18 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
 // multiple of 8 with 16-byte aligned output rows.
 inline bool ring_eligible(const GemmParams& p, int32_t op) {
   const size_t esz = p.out_dtype == kF32 ? 4 : 2;
-  return p.K > 128 && p.epi == kEpiStore && p.out != nullptr &&
+  // weights k-contiguous, or n-contiguous with 16-byte aligned k rows
+  const bool b_ok = p.b_sk == 1 || (p.b_sn == 1 && p.b_sk % 8 == 0 && p.b_se % 8 == 0 &&
+                                     (reinterpret_cast<uintptr_t>(p.b) & 15) == 0);
+  return p.K > 128 && p.epi == kEpiStore && p.out != nullptr && b_ok &&
          (p.dg == nullptr || (p.act == 0 && p.dg_ntiles == (p.N + (p.N <= 64 ? 63 : 127)) / (p.N <= 64 ? 64 : 128))) &&
          (p.act == 0 || (p.aux != nullptr && (reinterpret_cast<uintptr_t>(p.aux) % 16) == 0)) &&
          (p.out_dtype == op || p.out_dtype == kF32) && p.N % 8 == 0 &&
          (reinterpret_cast<uintptr_t>(p.out) % 16) == 0 && ((size_t)p.out_ld * esz) % 16 == 0;
 }
 
-template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int BK>
-hipError_t launch_routed_gemm_ring_t(const GemmParams& p_in, hipStream_t stream) {
+template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int BK, bool BNC>
+hipError_t launch_routed_gemm_ring_b(const GemmParams& p_in, hipStream_t stream) {
   GemmParams p = p_in;
   p.token_major = resolve_token_major(p);
   const int64_t m_tiles = (p.n_routes + BM - 1) / BM + (p.n_experts < p.n_routes ? p.n_experts : p.n_routes);
@@ -444,15 +518,22 @@ hipError_t launch_routed_gemm_ring_t(const GemmParams& p_in, hipStream_t stream)
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
   // the routing-weight gradient only ever comes with the grad-input product
   if (p.role == 0 && p.dg == nullptr)
-    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 0, BK>), dim3((unsigned)grid),
-                       dim3(kGemmThreads), 0, stream, p);
+    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 0, BK, false, BNC>),
+                       dim3((unsigned)grid), dim3(kGemmThreads), 0, stream, p);
   else if (p.dg == nullptr)
-    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1, BK>), dim3((unsigned)grid),
-                       dim3(kGemmThreads), 0, stream, p);
+    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1, BK, false, BNC>),
+                       dim3((unsigned)grid), dim3(kGemmThreads), 0, stream, p);
   else
-    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1, BK, true>),
+    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1, BK, true, BNC>),
                        dim3((unsigned)grid), dim3(kGemmThreads), 0, stream, p);
   return hipGetLastError();
+}
+
+// k-contiguous weights ([n][k] rows), or n-contiguous ones (BNC, b_sn == 1)
+template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int BK>
+hipError_t launch_routed_gemm_ring_t(const GemmParams& p, hipStream_t stream) {
+  if (p.b_sk == 1) return launch_routed_gemm_ring_b<OpT, OutT, BM, BN, STAGES, OCC, RA, BK, false>(p, stream);
+  return launch_routed_gemm_ring_b<OpT, OutT, BM, BN, STAGES, OCC, RA, BK, true>(p, stream);
 }
 
 // 128 x 128 tiles: two 32 KB slices of 64 k (128-byte rows: each gathered A

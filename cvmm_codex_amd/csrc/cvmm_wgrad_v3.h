@@ -54,10 +54,7 @@ struct RouteSlice {
   static constexpr int BYTES = 32 * ROWB;
   static constexpr int INSTS = BYTES / 1024;
   static_assert(CPR == 8 || CPR == 16 || CPR == 32, "64, 128 or 256 columns");
-  __device__ static __forceinline__ int swz(int row) {
-    if constexpr (CPR >= 16) return 2 * ((row & 3) | (((row >> 3) & 1) << 2));
-    else return 2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1));
-  }
+  __device__ static __forceinline__ int swz(int row) { return tr_row_swz<CPR>(row); }
 };
 
 // A BM x BN tile on a WM x WN grid of waves; each wave owns JM x IN blocks of

@@ -413,7 +413,8 @@ Tensor cvmm_forward_impl(const Tensor& x, const Tensor& keys, const OptT& keys_o
 // benchmark_ffn_moe.py:96), unweighted selections: (gelu(h), h), [R, d_out]
 // in the op dtype
 // ---------------------------------------------------------------------------
-std::tuple<Tensor, Tensor> forward_gelu(const Tensor& x, const Tensor& keys, const OptT& keys_t, const Tensor& sel,
+std::tuple<Tensor, Tensor> forward_gelu(const Tensor& x, const Tensor& keys, const OptT& keys_t, bool keys_t_is_t,
+                                        const Tensor& sel,
                                         const Tensor& sel_index, const OptT& out_index, const Tensor& offsets,
                                         const OptT& route_pos, int64_t op_id, int64_t flags, int64_t stream) {
   require_device(x, "x");
@@ -426,7 +427,7 @@ std::tuple<Tensor, Tensor> forward_gelu(const Tensor& x, const Tensor& keys, con
   Tensor xf, kv;
   if (keys_t.has_value()) {
     xf = rows_of(x.scalar_type() == op ? x : x.to(op), d_in);
-    kv = keys_t->transpose(1, 2);
+    kv = copy_view(*keys_t, keys_t_is_t);
   } else {
     xf = rows_of(storage_for(x, op), d_in);
     kv = keys_view(storage_for(keys, op));

@@ -283,7 +283,10 @@ int cvmm_cast_keys(const void* keys, int32_t keys_dtype, int32_t n_experts, int6
  *                                                       (out: [R/reduce_k, d_out])
  * keys element (e, i, j) is at keys[e*k_se + i*k_si + j*k_sj]; x rows are
  * contiguous with row stride x_ld.  op_dtype is the MFMA operand type
- * (autocast dtype or F32); x/keys are converted to it in-kernel.
+ * (autocast dtype or F32); x/keys are converted to it in-kernel.  Op-dtype
+ * keys with either inner stride 1 take the DMA-staged kernels where the
+ * product's k dimension (d_in here, d_out in cvmm_bwd_x) exceeds 128; so one
+ * cast copy (cvmm_cast_keys) can serve both products of a step.
  * route_pos (optional): the inverse of rp = out_index or sel_index, as
  * cvmm_sort_routes writes it; computed in the workspace when NULL.
  * Top-k sums (weighted here, token-input in cvmm_bwd_x) are taken in one of
