@@ -377,15 +377,17 @@ inline bool panel_eligible(const GemmParams& p, int32_t op) {
          (reinterpret_cast<uintptr_t>(p.out) % osz) == 0 && ((size_t)p.out_ld * esz) % osz == 0;
 }
 
-// n-tiles per workgroup: enough workgroups for about 1.5 per slot
-// (occ per CU x 256 CUs), n-tiles split evenly over the groups of an m-tile.
+// n-tiles per workgroup: enough workgroups for about one per slot (occ per
+// CU x 256 CUs), n-tiles split evenly over the groups of an m-tile.
 // Measured with 128-row tiles (n-tiles per workgroup 2/4/6/8/16): ff_up
 // grad-input 70.9 / 52.6 / 50.6 / 47.6 / 49.2 us, ff_down forward 70.7 / 52.1
-// / 51.4 / 46.7 / 48.7 us; the SwitchHead shapes (4352 m-tiles) are best with
-// all n-tiles in one group.
+// / 51.4 / 46.7 / 48.7 us; with 256-row tiles 4/5/6/8/11/16: 44.5 / 48.8 /
+// 44.5 / 43.5 / 51.9 / 51.1 us (ff_up; ff_down forward 45.0 -> 43.9 us from
+// 6 to 8); the SwitchHead shapes (4352 m-tiles) are best with all n-tiles in
+// one group.
 inline int32_t panel_tiles_per_wg(int64_t m_tiles, int64_t n_ntiles, int occ) {
   const int64_t slots = occ * 256;
-  int64_t groups = (3 * slots / 2 + m_tiles - 1) / (m_tiles > 0 ? m_tiles : 1);
+  int64_t groups = (slots + m_tiles - 1) / (m_tiles > 0 ? m_tiles : 1);
   if (groups < 1) groups = 1;
   if (groups > n_ntiles) groups = n_ntiles;
   return (int32_t)((n_ntiles + groups - 1) / groups);
