@@ -643,6 +643,7 @@ def test_long_k_tile_height_does_not_change_bits(weighted, route_input, D, H, sk
     U.compare(b, exp, 2e-2)
 
 
+@pytest.mark.parametrize("op", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("D,H,weighted,route_input,tile", [
     (1024, 128, False, False, 2),   # forward 160 x 128 (ff_up); grad-input: short K
     (256, 128, False, False, 1),    # forward 128 x 128
@@ -652,7 +653,7 @@ def test_long_k_tile_height_does_not_change_bits(weighted, route_input, D, H, sk
     (512, 256, False, False, 1),    # both products long-K
     (200, 96, True, False, 0),      # d_in % 64 != 0: the last k slice part-filled
 ])
-def test_long_k_reads_either_weight_orientation(D, H, weighted, route_input, tile):
+def test_long_k_reads_either_weight_orientation(D, H, weighted, route_input, tile, op):
     """The long-K routed GEMM reads the weights k-contiguous ([n][k] rows: the
     copy in its own orientation) or n-contiguous ([k][n] rows: the other
     orientation's copy, through transposed LDS reads).  Both give the same
@@ -661,24 +662,24 @@ def test_long_k_reads_either_weight_orientation(D, H, weighted, route_input, til
     from cvmm_codex_amd import _native as N
 
     class Ctx:
-        op_type = torch.bfloat16
+        op_type = op
 
     lib = N.lib()
     E, K = 8, 4
-    x, keys, sel, w, go = _rand_case(91 + D + H, 2, 160, D, H, E, K, weighted, route_input)
+    x, keys, sel, w, go = _rand_case(91 + D + H, 2, 160, D, H, E, K, weighted, route_input, x_dt=op)
     s = C.cvmm_prepare_sel2(sel.cuda(), w.cuda() if weighted else None, route_input=route_input)
     s._resolve(E)
     xd, kd, gd = x.cuda(), keys.cuda(), go.cuda()
     wd = w.cuda() if weighted else None
-    kt = kd.transpose(1, 2).contiguous().to(torch.bfloat16)   # [E, d_out, d_in]: k-contiguous forward rows
-    kn = kd.to(torch.bfloat16)                                 # [E, d_in, d_out]: k-contiguous grad-input rows
+    kt = kd.transpose(1, 2).contiguous().to(op)   # [E, d_out, d_in]: k-contiguous forward rows
+    kn = kd.to(op)                                 # [E, d_in, d_out]: k-contiguous grad-input rows
     outs = {}
     try:
         assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, tile) == 0
         assert lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 1) == 0   # the routed GEMMs, not a dense top-k sum
         for name, (k_fwd, fwd_t, k_bwd, bwd_t) in {"own": (kt, True, kn, False),
                                                    "other": (kn, False, kt, True)}.items():
-            y = C._forward(xd, s.sel_index, s.sel, kd, s.out_index, wd, torch.bfloat16, k_fwd, fwd_t)
+            y = C._forward(xd, s.sel_index, s.sel, kd, s.out_index, wd, op, k_fwd, fwd_t)
             gx, _, grw = C._backward(Ctx, gd, xd, kd, s.raw_sel, s.sel, s.sel_index, s.out_index, wd, True, False,
                                      weighted, keys_x=k_bwd, keys_x_is_t=bwd_t)
             torch.cuda.synchronize()
@@ -694,7 +695,8 @@ def test_long_k_reads_either_weight_orientation(D, H, weighted, route_input, til
             assert b is None
         elif long_k:
             assert torch.equal(a, b), what
-    exp = U.run_oracle(x, keys, sel, w, go, route_input, True)
+    exp = U.run_oracle(x, keys, sel, w, go, route_input, True,
+                       amp_dtype="bfloat16" if op == torch.bfloat16 else "float16")
     y, gx, grw = outs["other"]
     assert U.norm_rel(U.to_np(y), exp["out"].reshape(y.shape)) <= 2e-2
     assert U.norm_rel(U.to_np(gx).reshape(exp["x_grad"].shape), exp["x_grad"]) <= 2e-2
