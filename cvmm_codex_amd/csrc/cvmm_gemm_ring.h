@@ -233,6 +233,26 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
     }
   };
 
+  // DG (16-bit x with 8-byte aligned rows, ring_eligible): every x piece
+  // this lane needs for the routing-weight gradient (MB rows x 4 blocks of 4
+  // columns, 8 bytes each) is requested early, so the gathers' latency
+  // overlaps the last MFMAs (or at least the output stores)
+  uint2 xpre[MB][4];
+  auto load_x = [&]() {
+    const int64_t nw = n0 + wn * 64;
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int64_t xr = meta.dgrow[wm * WR + j * 16 + fr];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t n = nw + i * 16 + 4 * fq;
+        xpre[j][i] = xr >= 0 && n < p.N
+                         ? *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.dg_x) + xr * p.dg_x_ld + n)
+                         : make_uint2(0, 0);
+      }
+    }
+  };
+
   const int64_t nk = (p.K + Cfg::BK - 1) / Cfg::BK;
   if constexpr (RA) {
     // ---- k loop with fragment read-ahead: the fragments of slice s + 1 are
@@ -276,11 +296,7 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
       issue_fence();
     }
     int cur = 0, refill = STAGES - 1;
-    for (int64_t s = 0; s < nk; ++s) {
-      vm_wait<(STAGES - 2) * Cfg::D>();
-      wg_barrier();
-      issue(s + STAGES - 1, ring + refill * Cfg::SLICE_BYTES);
-      issue_fence();
+    auto multiply = [&]() {
 #pragma unroll
       for (int kk = 0; kk < Cfg::KSS; ++kk) {
         lds_u32x4 af[MB];
@@ -289,13 +305,33 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
         wait_frags(bf, af);
         mfma(af, bf);
       }
+    };
+    // DG: the last slice is peeled (K > 128, so nk >= 2)
+    static_assert(!DG || STAGES == 2, "the peeled DG slice leaves no DMA in flight");
+    const int64_t n_loop = DG ? nk - 1 : nk;
+    for (int64_t s = 0; s < n_loop; ++s) {
+      vm_wait<(STAGES - 2) * Cfg::D>();
+      wg_barrier();
+      issue(s + STAGES - 1, ring + refill * Cfg::SLICE_BYTES);
+      issue_fence();
+      multiply();
       cur = cur + 1 == STAGES ? 0 : cur + 1;
       refill = refill + 1 == STAGES ? 0 : refill + 1;
     }
+    if constexpr (DG) {
+      // the last slice: the x pieces take the place of its refill, which
+      // would only bring zeros from past K
+      vm_wait<(STAGES - 2) * Cfg::D>();
+      wg_barrier();
+      load_x();
+      issue_fence();
+      multiply();
+    }
   }
   // slices past K may still be landing in LDS: drain them before the
-  // workgroup can end and its LDS be handed to another
-  vm_wait<0>();
+  // workgroup can end and its LDS be handed to another (the peeled DG loop
+  // issues none; its x loads are waited for where they are used)
+  if constexpr (RA || !DG) vm_wait<0>();
 
   // ---- epilogue from registers: lane holds C[m = wm*WR + j*16 + fr]
   // [n = n0 + wn*64 + i*16 + 4*fq + {0..3}]
@@ -304,27 +340,8 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   // the conversion at the store does by itself
   const bool plain = !has_w && p.val_dtype == DTypeOf<OutT>::value;
   const int64_t nwave = n0 + wn * 64;
-  // DG with 16-bit x: every x piece this lane needs (4 rows x 4 blocks of 4
-  // columns, 8 bytes each) is requested before the output stores, so the
-  // gathers' latency overlaps them
-  uint2 xpre[MB][4];
-  bool xpre_ok = false;
-  if constexpr (DG) {
-    xpre_ok = p.dg_x_dtype != kF32 && (reinterpret_cast<uintptr_t>(p.dg_x) & 7) == 0 && p.dg_x_ld % 4 == 0;
-    if (xpre_ok) {
-#pragma unroll
-      for (int j = 0; j < MB; ++j) {
-        const int64_t xr = meta.dgrow[wm * WR + j * 16 + fr];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int64_t n = nwave + i * 16 + 4 * fq;
-          xpre[j][i] = xr >= 0 && n + 3 < p.N
-                           ? *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.dg_x) + xr * p.dg_x_ld + n)
-                           : make_uint2(0, 0);
-        }
-      }
-    }
-  }
+  // DG without a peeled last slice (the read-ahead loop): the x pieces now
+  if constexpr (DG && RA) load_x();
   // one row piece of 4 x 16 columns: lane values -> 16-byte (or 4 x 16-byte
   // fp32) stores of row rowp
   auto store_row = [&](char* rowp, const float (&v)[4][4]) {
@@ -410,52 +427,23 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
     // sum_n rnd(acc, dg_val) * x[dgrow][n].  Fixed order: each lane its 16
     // columns (blocks i, then the 4 columns), the 4 lanes of a row (xor 16,
     // then xor 32), then the waves of the tile row in wn order through LDS.
-    // x pieces of 4 columns as one 8-byte (16-bit x) or 16-byte (fp32 x) load
-    const bool x16 = p.dg_x_dtype != kF32;
-    const bool xvec = (reinterpret_cast<uintptr_t>(p.dg_x) & (x16 ? 7 : 15)) == 0 && p.dg_x_ld % 4 == 0;
+    // (N % 8 == 0: a 4-column piece is wholly inside or outside the row)
+    const bool xbf = p.dg_x_dtype == kBF16;
     float part[MB];
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
-      const int m = wm * WR + j * 16 + fr;
-      const int64_t xr = meta.dgrow[m];
-      float xv[4][4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t n = nwave + i * 16 + 4 * fq;
-        const int64_t o = xr * p.dg_x_ld + n;
-        if (xr < 0) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) xv[i][q] = 0.f;
-        } else if (xpre_ok && n + 3 < p.N) {
-          union { uint2 u; bf16_t b[4]; f16_t h[4]; } c;
-          c.u = xpre[j][i];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) xv[i][q] = p.dg_x_dtype == kBF16 ? (float)c.b[q] : (float)c.h[q];
-        } else if (xvec && n + 3 < p.N) {
-          if (x16) {
-            union { uint2 u; bf16_t b[4]; f16_t h[4]; } c;
-            c.u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.dg_x) + o);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) xv[i][q] = p.dg_x_dtype == kBF16 ? (float)c.b[q] : (float)c.h[q];
-          } else {
-            const float4 f = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.dg_x) + o);
-            xv[i][0] = f.x;
-            xv[i][1] = f.y;
-            xv[i][2] = f.z;
-            xv[i][3] = f.w;
-          }
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) xv[i][q] = n + q < p.N ? load_as_f32(p.dg_x, p.dg_x_dtype, o + q) : 0.f;
-        }
-      }
+      const int64_t xr = meta.dgrow[wm * WR + j * 16 + fr];
       float sum = 0.f;
       if (xr >= 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+          if (nwave + i * 16 + 4 * fq >= p.N) continue;
+          union { uint2 u; bf16_t b[4]; f16_t h[4]; } c;
+          c.u = xpre[j][i];
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            if (nwave + i * 16 + 4 * fq + q < p.N) sum += round_to(acc[i][j][q], p.dg_val_dtype) * xv[i][q];
+            sum += round_to(acc[i][j][q], p.dg_val_dtype) * (xbf ? (float)c.b[q] : (float)c.h[q]);
+        }
       }
       sum += __shfl_xor(sum, 16, 64);
       sum += __shfl_xor(sum, 32, 64);
@@ -493,15 +481,18 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
 
 // The ring kernel applies: plain stores (optionally scaled by a per-row
 // routing weight, optionally with the routing-weight gradient partials of
-// its n tile, of gemm_bn(N) columns), output in the op type or fp32, N a
-// multiple of 8 with 16-byte aligned output rows.
+// its n tile, of gemm_bn(N) columns, against 16-bit x with 8-byte aligned
+// rows), output in the op type or fp32, N a multiple of 8 with 16-byte
+// aligned output rows.
 inline bool ring_eligible(const GemmParams& p, int32_t op) {
   const size_t esz = p.out_dtype == kF32 ? 4 : 2;
   // weights k-contiguous, or n-contiguous with 16-byte aligned k rows
   const bool b_ok = p.b_sk == 1 || (p.b_sn == 1 && p.b_sk % 8 == 0 && p.b_se % 8 == 0 &&
                                      (reinterpret_cast<uintptr_t>(p.b) & 15) == 0);
   return p.K > 128 && p.epi == kEpiStore && p.out != nullptr && b_ok &&
-         (p.dg == nullptr || (p.act == 0 && p.dg_ntiles == (p.N + (p.N <= 64 ? 63 : 127)) / (p.N <= 64 ? 64 : 128))) &&
+         (p.dg == nullptr || (p.act == 0 && p.dg_ntiles == (p.N + (p.N <= 64 ? 63 : 127)) / (p.N <= 64 ? 64 : 128) &&
+                              (p.dg_x_dtype == kBF16 || p.dg_x_dtype == kF16) &&
+                              (reinterpret_cast<uintptr_t>(p.dg_x) & 7) == 0 && p.dg_x_ld % 4 == 0)) &&
          (p.act == 0 || (p.aux != nullptr && (reinterpret_cast<uintptr_t>(p.aux) % 16) == 0)) &&
          (p.out_dtype == op || p.out_dtype == kF32) && p.N % 8 == 0 &&
          (reinterpret_cast<uintptr_t>(p.out) % 16) == 0 && ((size_t)p.out_ld * esz) % 16 == 0;
