@@ -773,8 +773,8 @@ def test_routing_weight_grad_with_misaligned_x_rows(route_input):
     """x as a view one element into rows of 257: neither its address nor its
     row stride is 8-byte aligned.  The forward and the weight gradient take
     the general kernels; the grad-input GEMM (aligned grad operand, d_out =
-    320) keeps the long-K kernel, whose routing-weight gradient then reads x
-    element by element instead of in prefetched 8-byte pieces."""
+    320) with its routing-weight gradient takes the tiled kernel, which reads
+    x element by element (the long-K kernel reads only 8-byte pieces)."""
     x, keys, sel, w, go = _rand_case(16, 2, 128, 256, 320, 8, 4, True, route_input)
     dev = torch.device("cuda")
     base = torch.zeros(*x.shape[:-1], x.shape[-1] + 1, dtype=x.dtype, device=dev)
@@ -792,11 +792,14 @@ def test_routing_weight_grad_with_misaligned_x_rows(route_input):
     U.compare(got, U.run_oracle(x, keys, sel, w, go, route_input, True), 2e-2)
 
 
-def test_fp32_x_under_autocast():
-    """fp32 activations with bf16 autocast: cast to bf16 inside the kernels."""
-    x, keys, sel, w, go = _rand_case(14, 2, 64, 96, 80, 6, 3, True, False, x_dt=torch.float32)
-    got = U.run_hip(x, keys, sel, w, go, False, True)
-    exp = U.run_oracle(x, keys, sel, w, go, False, True)
+@pytest.mark.parametrize("D,H,route_input", [(96, 80, False), (128, 320, True), (64, 256, True)])
+def test_fp32_x_under_autocast(D, H, route_input):
+    """fp32 activations with bf16 autocast: cast to bf16 inside the kernels.
+    With route input and d_out > 128 the grad-input GEMM is long-K and its
+    routing-weight gradient reads fp32 x rows (the tiled kernel's path)."""
+    x, keys, sel, w, go = _rand_case(14, 2, 64, D, H, 6, 3, True, route_input, x_dt=torch.float32)
+    got = U.run_hip(x, keys, sel, w, go, route_input, True)
+    exp = U.run_oracle(x, keys, sel, w, go, route_input, True)
     U.compare(got, exp, 2e-2)
 
 
