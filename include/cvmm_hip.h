@@ -347,7 +347,9 @@ int cvmm_gelu_backward(const void* grad, int32_t grad_dtype, int64_t grad_ld, co
  *  weighted (both)                          : grad_rw[rp] = <rnd_op(g_i), x[sel_index[i]]>
  * grad_x and/or grad_rw may be NULL when not needed; route_pos and the
  * top-k sum's flags as for cvmm_fwd (here K = d_out, N = d_in; the reduce
- * GEMM is not taken for a weighted call that asks for grad_rw). */
+ * GEMM is not taken for a weighted call that asks for grad_rw).  With
+ * grad_rw and d_out > 128, 16-bit x with 8-byte aligned rows (x pointer and
+ * x_ld) keeps the DMA-staged kernel; other x takes the slower tiled one. */
 size_t cvmm_bwd_x_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out,
                                   int64_t grad_x_rows, int32_t has_offsets, int32_t weighted, int32_t token_input,
                                   int64_t top_k, int32_t grad_x_dtype, int32_t op_dtype, int32_t need_grad_rw,
