@@ -155,6 +155,16 @@ __device__ __forceinline__ int tr_row_swz(int row) {
   else return 2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1));
 }
 
+// 16-byte chunk swizzle of the panel kernel's [n][k] weight tiles, whose
+// 16-lane fragment reads take one chunk of 16 consecutive rows: 256-byte rows
+// put chunk c of row n at c ^ (n & 15), 128-byte rows (two per 256 bytes) at
+// c ^ ((n >> 1) & 7), so those 16 chunks fill 16 distinct 16-byte bank groups.
+template <int CPR>
+__device__ __forceinline__ int panel_swz(int row) {
+  if constexpr (CPR >= 16) return row & 15;
+  else return (row >> 1) & 7;
+}
+
 // Wait until at most `ahead` slices (D DMA instructions each) are in flight.
 template <int D, int K>
 __device__ __forceinline__ void vm_wait_slices(int ahead) {
@@ -179,7 +189,7 @@ struct PanelCfg {
   static constexpr int NI = BN / (16 * WN);           // 16-column blocks per wave (wave: 64 x BN/WN)
   static constexpr int KS = KP / 32;                  // MFMA k steps
   static constexpr int OCC = WM == 2 ? 3 : 2;         // workgroups per CU (LDS 52.8 / 57.5 KB)
-  static_assert(CPR >= 8, "swizzle needs >= 8 chunks per row");
+  static_assert(CPR == 8 || CPR == 16, "swizzle for 128- or 256-byte rows");
   static_assert(WM == 2 || WM == 4, "128- or 256-row tiles");
 };
 
@@ -233,7 +243,7 @@ __global__ __launch_bounds__(kGemmThreads, (PanelCfg<KP, BN, WM>::OCC)) void rou
   }
   issue_fence();
 
-  // ---- weight tile t -> LDS buffer (row = n, 16-byte chunk c at c ^ (n & 7)) --
+  // ---- weight tile t -> LDS buffer (row = n, 16-byte chunk c at c ^ panel_swz(n))
   const char* bexp = reinterpret_cast<const char*>(p.b) + (int64_t)expert * p.b_se * 2;
   auto issue = [&](int t, char* buf) {
     const int64_t nb = (nt0 + t) * BN;
@@ -241,7 +251,7 @@ __global__ __launch_bounds__(kGemmThreads, (PanelCfg<KP, BN, WM>::OCC)) void rou
     for (int j = 0; j < Cfg::D; ++j) {
       const int q = (wave * Cfg::D + j) * 64 + lane;
       const int row = q / Cfg::CPR;
-      const int c = (q % Cfg::CPR) ^ lds_swz(row);
+      const int c = (q % Cfg::CPR) ^ panel_swz<Cfg::CPR>(row);
       const char* src = c * 8 < p.K ? bexp + ((nb + row) * p.b_sn + c * 8) * 2 : zero + lane * 16;
       dma16(src, buf + (wave * Cfg::D + j) * 1024);
     }
@@ -267,7 +277,7 @@ __global__ __launch_bounds__(kGemmThreads, (PanelCfg<KP, BN, WM>::OCC)) void rou
       for (int i = 0; i < Cfg::NI; ++i) {
         const int n = wn * (BN / Cfg::WN) + i * 16 + fr;
         const int c = ks * 4 + fq;
-        bf[i] = *reinterpret_cast<const uint4*>(buf + n * (Cfg::CPR * 16) + ((c ^ lds_swz(n)) << 4));
+        bf[i] = *reinterpret_cast<const uint4*>(buf + n * (Cfg::CPR * 16) + ((c ^ panel_swz<Cfg::CPR>(n)) << 4));
       }
 #pragma unroll
       for (int i = 0; i < Cfg::NI; ++i)
