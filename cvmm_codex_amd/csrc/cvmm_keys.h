@@ -57,10 +57,12 @@ __device__ __forceinline__ void cast_tile_vec(const CastArgs<OutT>& a, int64_t e
   for (int q = 0; q < 4; ++q) {
     const int r = (t >> 4) + 16 * q;
     const float4 v = *reinterpret_cast<const float4*>(a.keys + e * a.se + (i0 + r) * a.si + j0 + c4);
-    tile[r][c4] = v.x;
-    tile[r][c4 + 1] = v.y;
-    tile[r][c4 + 2] = v.z;
-    tile[r][c4 + 3] = v.w;
+    if (a.kt != nullptr) {  // the tile only feeds the transposed copy
+      tile[r][c4] = v.x;
+      tile[r][c4 + 1] = v.y;
+      tile[r][c4 + 2] = v.z;
+      tile[r][c4 + 3] = v.w;
+    }
     if (a.kn != nullptr) {
       union { uint2 u; OutT h[4]; } pk;
       pk.h[0] = from_f32<OutT>(v.x);
@@ -115,8 +117,10 @@ __device__ __forceinline__ void cast_tile_vec128(const CastArgs<OutT>& a, int64_
       for (int k = 0; k < 8; ++k) pk.h[k] = from_f32<OutT>(f[k]);
       *reinterpret_cast<uint4*>(a.kn + e * a.n_se + (i0 + r) * a.n_sr + j0 + c8) = pk.u;
     }
+    if (a.kt != nullptr) {  // the tile only feeds the transposed copy
 #pragma unroll
-    for (int k = 0; k < 8; ++k) tile[r][c8 + k] = f[k];
+      for (int k = 0; k < 8; ++k) tile[r][c8 + k] = f[k];
+    }
   }
   if (a.kt == nullptr) return;
   lds_barrier();  // the tile is complete; the kn stores need not have landed
