@@ -18,7 +18,6 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcvmm_hip
 F32, F16, BF16 = 0, 1, 2            # cvmm.py:36-44 dtype ids
 FLAG_ATOMIC_REDUCE = 1
 FLAG_COUNTERS_ZEROED = 2
-FLAG_WORKSPACE_ZEROED = 8
 FLAG_COUNTS_READY = 16
 CAST_T_INTERLEAVED = 1
 CAST_N_INTERLEAVED = 2
@@ -47,7 +46,6 @@ _SIGS = {
     "cvmm_timing_enable": (ctypes.c_int, [ctypes.c_uint32]),
     "cvmm_tuning_set": (ctypes.c_int, [_I32, _I64]),
     "cvmm_topk_dense": (ctypes.c_int, [_I64, _I32, _I64, _I64, _I64, _I32]),
-    "cvmm_topk_dense_zero_bytes": (_SZ, [_I64, _I32, _I64, _I32]),
     "cvmm_timing_result": (ctypes.c_int, [ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
                                           ctypes.POINTER(ctypes.c_int64)]),
     "cvmm_sort_workspace_bytes": (_SZ, [_I64, _I32]),

@@ -83,9 +83,7 @@ def build(verbose: bool = True, jobs: int | None = None) -> str:
         objs = list(ex.map(_compile, srcs))
         host_obj = host_obj.result()
     tmp = LIB + ".tmp"
-    # rocBLAS (the dense top-k GEMM): torch loads the same SONAME first when both are used
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-soname,libcvmm_hip.so", *objs, "-o", tmp,
-           "-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-soname,libcvmm_hip.so", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

@@ -201,114 +201,146 @@ bool reduce_needed(int32_t weighted, int32_t token_input, int64_t top_k) {
 
 int64_t ntiles_of(int64_t n, int64_t bn) { return (n + bn - 1) / bn; }
 
-// Dense top-k sum (cvmm_dense.hip) for a sum over top_k routes per token of
-// [K] x [K, N] products: the shapes it handles ...
+// Dense top-k sum (cvmm_topk_gemm.hip) for a sum over top_k routes per token
+// of [K] x [K, N] products: the shapes it handles ...
 bool dense_topk_shape_ok(int32_t op_dtype, int64_t n_tokens, int32_t n_experts, int64_t K, int64_t N,
                          int64_t top_k) {
   const int64_t lim = 0x7fffffffll;
-  return (op_dtype == kBF16 || op_dtype == kF16) && K % 8 == 0 && top_k >= 2 && top_k <= 64 &&
-         n_experts <= kDenseMaxExperts && n_tokens > 0 && n_tokens <= lim && N <= lim &&
-         (int64_t)n_experts * K <= lim && n_tokens * top_k <= lim;
+  if (!((op_dtype == kBF16 || op_dtype == kF16) && K % 8 == 0 && N % 8 == 0 && top_k >= 2 && top_k <= 64 &&
+        n_experts <= kTopkMaxExperts && n_tokens > 0 && n_tokens <= lim && N <= lim &&
+        (int64_t)n_experts * K <= lim && n_tokens * top_k <= lim))
+    return false;
+  // the GEMM's 32-bit offsets reach the workspace copies (rows of K, weights
+  // [E][N][K]) and the slot table
+  return topk_gemm_a_fits(n_tokens * top_k, K, K) && topk_gemm_b_fits(n_experts, K * N, K, K) &&
+         topk_gemm_table_fits(n_experts, n_tokens);
 }
-// ... and when it is the faster way (rates measured on MI355X: the library
-// GEMM at ~1.2 PFLOP/s over E/top_k times the useful flops plus the slotted
-// rows written and read at ~6 TB/s, against the routed GEMM at ~0.5 PFLOP/s
-// plus the [R, N] route buffer written and read at ~5 TB/s); the
-// CVMM_TUNE_DENSE_TOPK knob overrides it (1 never, 2 whenever the shapes fit).
+// ... and when it is the faster way (rates measured on MI355X: the dense GEMM
+// at ~1.2 PFLOP/s over E/top_k times the useful flops, against the routed
+// GEMM at ~0.5 PFLOP/s plus the [R, N] route buffer written and read at ~5
+// TB/s); the CVMM_TUNE_DENSE_TOPK knob overrides it (1 never, 2 whenever the
+// shapes fit).
 bool use_dense_topk(int32_t op_dtype, int64_t n_tokens, int32_t n_experts, int64_t K, int64_t N, int64_t top_k) {
   if (!dense_topk_shape_ok(op_dtype, n_tokens, n_experts, K, N, top_k)) return false;
   const int32_t knob = g_dense_topk.load();
   if (knob == 1) return false;
   if (knob == 2) return true;
   const double T = (double)n_tokens, R = T * (double)top_k;
-  const double t_dense = 2.0 * T * n_experts * K * N / 1.2e15 + 2.0 * T * n_experts * K * 2 / 6e12;
+  const double t_dense = 2.0 * T * n_experts * K * N / 1.2e15;
   const double t_route = R * N * 2 * 2 / 5e12 + 2.0 * R * K * N / 0.5e15;
   return t_dense < t_route;
 }
 
-// Workspace of a dense top-k sum: the slotted rows (first, so that a caller
-// can keep them zero between calls: CVMM_FLAG_WORKSPACE_ZEROED), a weight
-// copy in the [E*K][N] layout (used when the caller's keys are not already
-// that copy) and the inverse route permutation (when not given).
+// Workspace of a dense top-k sum: a weight copy in a layout the GEMM reads
+// (used when the caller's keys are not one), the inverse route permutation
+// (when not given), the slot table, and [R][K] op-dtype operand rows (the
+// weight-scaled route rows of a weighted sum, or a copy of rows that cannot
+// be moved 16 bytes at a time).
 struct DenseWs {
-  void* a;
   void* b;
   int32_t* inv;
+  uint32_t* offs;
+  uint8_t* slots;
+  uint8_t* nxt;
+  uint8_t* mult;
+  void* src;
 };
 DenseWs carve_dense(Carver& c, int64_t n_tokens, int32_t n_experts, int64_t K, int64_t N, int64_t n_routes,
                     int32_t op_dtype) {
+  const size_t esz = dtype_size(op_dtype), e16 = (size_t)topk_e16(n_experts);
   DenseWs w;
-  w.a = c.take((size_t)n_tokens * n_experts * K * dtype_size(op_dtype));
-  w.b = c.take((size_t)n_experts * K * N * dtype_size(op_dtype));
+  w.b = c.take((size_t)n_experts * K * N * esz);
   w.inv = (int32_t*)c.take((size_t)n_routes * 4);
+  w.offs = (uint32_t*)c.take((size_t)topk_slot_rows(n_tokens) * e16 * 4);
+  w.slots = (uint8_t*)c.take((size_t)topk_slot_rows(n_tokens) * e16);
+  w.nxt = (uint8_t*)c.take((size_t)n_routes);
+  w.mult = (uint8_t*)c.take((size_t)n_tokens);
+  w.src = c.take((size_t)n_routes * K * esz);
   return w;
 }
 
 // The dense top-k sum: out[t] = sum_j s_tj src[row(t, j)] @ B_e, with K =
 // d_in, N = d_out for the forward (`fwd`), K = d_out, N = d_in for the
 // grad-input.  `keys` (the logical [E, d_in, d_out] view with its strides) is
-// the GEMM's B as it stands when it is an op-dtype copy in one of the two row
-// layouts: B^T [N][E*K] (the cast's expert-interleaved copy: [d_out][E][d_in]
-// for the forward, [d_in][E][d_out] for the grad-input; both operands
-// k-contiguous, the faster GEMM) or B [E*K][N] ([E][d_in][d_out] for the
-// forward, [E][d_out][d_in] for the grad-input).  Other keys are cast into
-// the workspace's B^T.
+// read as it stands when it is an op-dtype copy whose K dimension has unit
+// stride (the per-expert copy of this product's orientation, or its
+// expert-interleaved form); other keys are cast into the workspace.
 int run_dense_topk(const DenseWs& w, const void* src, int32_t src_dtype, int64_t src_ld, bool src_per_route,
                    const int32_t* sorted_sel, const int32_t* route_pos, const int64_t* rp, const int64_t* offs,
                    int64_t n_routes, int64_t n_tokens, int64_t top_k, int32_t n_experts, const void* keys,
                    int32_t keys_dtype, int64_t d_in, int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj,
                    bool fwd, const void* rw, int32_t rw_dtype, int32_t w_round, int32_t op_dtype, void* out,
-                   int32_t out_dtype, int64_t out_ld, bool a_zeroed, uint32_t gemm_class, const char* what,
-                   hipStream_t s) {
+                   int32_t out_dtype, int64_t out_ld, uint32_t gemm_class, const char* what, hipStream_t s) {
   const int64_t K = fwd ? d_in : d_out, N = fwd ? d_out : d_in;
+  const int64_t esz = (int64_t)dtype_size(op_dtype);
+  // B_e[k][n] = b[e * b_se + n * b_sn + k]: keys[e][k][n] for the forward,
+  // keys[e][n][k] for the grad-input
   const void* B = keys;
-  const bool same = keys_dtype == op_dtype;
-  const bool by_col = same && k_se == K && (fwd ? (k_si == 1 && k_sj == n_experts * d_in)
-                                                : (k_sj == 1 && k_si == n_experts * d_out));
-  const bool by_row = same && k_se == d_in * d_out &&
-                      (fwd ? (k_sj == 1 && k_si == d_out) : (k_si == 1 && k_sj == d_in));
-  if (!by_col && !by_row) {
-    // the expert-interleaved copy of this GEMM's orientation
+  int64_t b_se = k_se, b_sn = fwd ? k_sj : k_si;
+  const int64_t k_unit = fwd ? k_si : k_sj;
+  if (!(keys_dtype == op_dtype && k_unit == 1 && aligned16(keys) && (k_se * esz) % 16 == 0 &&
+        (b_sn * esz) % 16 == 0 && topk_gemm_b_fits(n_experts, b_se, b_sn, K))) {
+    // the per-expert copy of this orientation: kt [E][d_out][d_in] or kn [E][d_in][d_out]
     int r = check_launch(timed(CVMM_KC_CAST_KEYS, s, [&] {
       return launch_cast_keys(keys, keys_dtype, k_se, k_si, k_sj, n_experts, d_in, d_out, op_dtype,
-                              fwd ? w.b : nullptr, fwd ? nullptr : w.b,
-                              fwd ? kCastTInterleaved : kCastNInterleaved, s);
+                              fwd ? w.b : nullptr, fwd ? nullptr : w.b, 0, s);
     }), what);
     if (r) return r;
     B = w.b;
+    b_se = K * N;
+    b_sn = K;
   }
-  const bool b_by_col = !by_row;
   const int32_t* inv = route_pos;
   if (!inv) {
     int r = check_launch(timed_combine(s, [&] { return launch_invert_rows(rp, n_routes, w.inv, s); }), what);
     if (r) return r;
     inv = w.inv;
   }
-  // the slotted rows: into an A the caller keeps zero (and the call leaves
-  // zero again), else into a zero-filled A
-  const size_t a_bytes = (size_t)n_tokens * n_experts * K * dtype_size(op_dtype);
-  if (!a_zeroed) {
-    int r = check_launch(timed_fill(s, [&] { return launch_fill_zero(w.a, a_bytes, s); }), what);
-    if (r) return r;
-  }
-  auto slots = [&](bool clear) {
-    return check_launch(timed_combine(s, [&] {
-      return launch_slot_rows(src, src_dtype, src_ld, src_per_route, sorted_sel, inv, rp, offs + (n_experts - 1),
-                              n_tokens, top_k, n_experts, K, rw, rw_dtype, w_round, clear, op_dtype, w.a, s);
+  // operand rows: with routing weights the scaled route rows, written by the
+  // slot-table launch; else the rows as given when they are 16-byte pieces
+  // of the op dtype, or an op-dtype copy
+  const void* A = src;
+  int64_t a_ld = src_ld;
+  if (rw != nullptr) {
+    A = w.src;
+    a_ld = K;
+  } else if (!(src_dtype == op_dtype && src_per_route && aligned16(src) && (src_ld * esz) % 16 == 0 &&
+                topk_gemm_a_fits(n_routes, src_ld, K))) {
+    // (an unweighted sum always comes with route rows: the token gradient)
+    int r = check_launch(timed_combine(s, [&] {
+      return launch_copy_rows_op(src, src_dtype, src_ld, n_routes, K, op_dtype, w.src, s);
     }), what);
-  };
-  int r = slots(false);
-  if (r) return r;
-  int status = 0;
-  const hipError_t e = timed(gemm_class, s, [&] {
-    return dense_rows_gemm(w.a, B, b_by_col, n_tokens, (int64_t)n_experts * K, N, op_dtype, out, out_dtype, out_ld,
-                           s, &status);
-  });
-  if (e != hipSuccess) {
-    if (status != 0) return fail(CVMM_ERR_LAUNCH, "%s: rocblas_gemm_ex failed (status %d)", what, status);
-    return check_launch(e, what);
+    if (r) return r;
+    A = w.src;
+    a_ld = K;
   }
-  return a_zeroed ? slots(true) : CVMM_OK;
+  int r = check_launch(timed_combine(s, [&] {
+    return launch_topk_slot_table(sorted_sel, inv, rp, offs + (n_experts - 1), n_tokens, top_k, n_experts, rw,
+                                  rw_dtype, w_round, src, src_dtype, src_ld, src_per_route, K, op_dtype, w.src,
+                                  a_ld, w.offs, w.slots, w.nxt, w.mult, s);
+  }), what);
+  if (r) return r;
+  TopkGemmParams p{};
+  p.src = A;
+  p.src_ld = a_ld;
+  p.offs = w.offs;
+  p.slots = w.slots;
+  p.t_pad = topk_slot_rows(n_tokens);
+  p.nxt = w.nxt;
+  p.mult = w.mult;
+  p.b = B;
+  p.b_se = b_se;
+  p.b_sn = b_sn;
+  p.n_tokens = n_tokens;
+  p.top_k = top_k;
+  p.K = K;
+  p.N = N;
+  p.n_experts = n_experts;
+  p.e16 = topk_e16(n_experts);
+  p.out = out;
+  p.out_ld = out_ld;
+  p.out_vec = aligned16(out) && (out_ld * (int64_t)dtype_size(out_dtype)) % 16 == 0;
+  return check_launch(timed(gemm_class, s, [&] { return launch_topk_gemm(p, op_dtype, out_dtype, s); }), what);
 }
 
 // n-tile width of the routed GEMM for output width n (256x64 tiles when narrow).
@@ -325,7 +357,7 @@ extern "C" {
 
 const char* cvmm_last_error(void) { return g_err.c_str(); }
 
-int cvmm_abi_version(void) { return 11; }
+int cvmm_abi_version(void) { return 12; }
 
 int cvmm_timing_enable(uint32_t class_mask) {
   std::lock_guard<std::mutex> lk(g_timing_mu);
@@ -374,11 +406,6 @@ int cvmm_tuning_set(int32_t knob, int64_t value) {
 
 int cvmm_topk_dense(int64_t n_tokens, int32_t n_experts, int64_t K, int64_t N, int64_t top_k, int32_t op_dtype) {
   return use_dense_topk(op_dtype, n_tokens, n_experts, K, N, top_k) ? 1 : 0;
-}
-
-size_t cvmm_topk_dense_zero_bytes(int64_t n_tokens, int32_t n_experts, int64_t K, int32_t op_dtype) {
-  if (n_tokens <= 0 || n_experts <= 0 || K <= 0) return 0;
-  return align_up((size_t)n_tokens * n_experts * K * dtype_size(op_dtype), 256);
 }
 
 int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launches) {
@@ -762,12 +789,12 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
     return check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
   }
   if (dense) {
-    // high fan-out: expert-slotted x rows (scaled by rnd_out(w)) and one GEMM
-    // against the [E*d_in][d_out] weight rows, no route buffer
+    // high fan-out: one GEMM over expert slots of the x rows (scaled by
+    // rnd_out(w)), no route buffer
     return run_dense_topk(dws, x, x_dtype, x_ld, out_index == nullptr, sorted_sel, route_pos, rp, offs, n_routes,
                           out_rows, reduce_k, n_experts, keys, keys_dtype, d_in, d_out, k_se, k_si, k_sj, true, rw,
-                          rw_dtype, out_dtype, op_dtype, out, out_dtype, out_ld,
-                          (flags & CVMM_FLAG_WORKSPACE_ZEROED) != 0, CVMM_KC_GEMM_FWD, "cvmm_fwd(dense)", s);
+                          rw_dtype, out_dtype, op_dtype, out, out_dtype, out_ld, CVMM_KC_GEMM_FWD,
+                          "cvmm_fwd(dense)", s);
   }
   if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
     // fused combine: y rounded to the output dtype, times rnd_out(w), fp32 atomics per token row
@@ -922,12 +949,11 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
   const int64_t* rp = token_input ? out_index : sel_index;
 
   if (dense && grad_x) {
-    // high fan-out: expert-slotted dY rows and one GEMM against the
-    // [E*d_out][d_in] weight rows, no route buffer
+    // high fan-out: one GEMM over expert slots of the dY rows, no route buffer
     return run_dense_topk(dws, grad, grad_dtype, grad_ld, true, sorted_sel, route_pos, rp, offs, n_routes,
                           grad_x_rows, top_k, n_experts, keys, keys_dtype, d_in, d_out, k_se, k_si, k_sj, false,
-                          nullptr, 0, 0, op_dtype, grad_x, grad_x_dtype, grad_x_ld,
-                          (flags & CVMM_FLAG_WORKSPACE_ZEROED) != 0, CVMM_KC_GEMM_BWDX, "cvmm_bwd_x(dense)", s);
+                          nullptr, 0, 0, op_dtype, grad_x, grad_x_dtype, grad_x_ld, CVMM_KC_GEMM_BWDX,
+                          "cvmm_bwd_x(dense)", s);
   }
 
   // grad @ keys[e]^T: K = d_out, N = d_in, B[k][n] = keys[e][n][k]

@@ -6,6 +6,7 @@
 #include <stddef.h>
 
 #include "cvmm_common.h"
+#include "cvmm_topk_gemm.h"
 
 namespace cvmm {
 
@@ -255,28 +256,6 @@ hipError_t launch_route_topk_backward(const void* logits, int32_t logits_dtype, 
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 // out[i] = (int32) sel[i] (int64 ids: their low 32 bits)
 hipError_t launch_copy_ids(const void* sel, bool sel_is_int64, int64_t n, int32_t* out, hipStream_t stream);
-// ---------------------------------------------------------------------------
-// dense top-k sums (cvmm_dense.hip): expert-slotted rows + one library GEMM
-// ---------------------------------------------------------------------------
-// The slots of A used by each token: A[t][e*K + k] = sum over the routes j
-// of token t with expert e of rnd_op(s_tj * src[row][k]), row = t*top_k + j
-// (src per route) or t, s_tj = rnd(w[t*top_k + j], w_round) or 1 when
-// w == NULL; zeros instead when `clear`.  Other slots are not written (A is
-// zero there).  The expert of route r is sorted_sel[inv[r]] when inv[r] <
-// *rows_end and rp[inv[r]] == r.  top_k <= 64, K % 8 == 0, 16-bit op.
-hipError_t launch_slot_rows(const void* src, int32_t src_dtype, int64_t src_ld, bool src_per_route,
-                            const int32_t* sorted_sel, const int32_t* inv, const int64_t* rp, const int64_t* rows_end,
-                            int64_t n_tokens, int64_t top_k, int32_t n_experts, int64_t K, const void* w,
-                            int32_t w_dtype, int32_t w_round, bool clear, int32_t op_dtype, void* A,
-                            hipStream_t stream);
-// out[t][n] = sum_c A[t][c] B[c][n] (A [T][C] row-major; B as [C][N] rows,
-// or, when `b_by_col`, as B^T [N][C] rows; op dtype; fp32 accumulation;
-// rocBLAS, atomics off).  On a rocBLAS error returns hipErrorUnknown with its
-// status in *status.
-hipError_t dense_rows_gemm(const void* A, const void* B, bool b_by_col, int64_t T, int64_t C, int64_t N,
-                           int32_t op_dtype, void* out, int32_t out_dtype, int64_t out_ld, hipStream_t stream,
-                           int* status);
-constexpr int32_t kDenseMaxExperts = 4096;  // the slot kernel's per-wave LDS table
 // GELU (erf form) over rows: y = rnd(gelu(h)); its backward
 // dh = rnd(dy * gelu'(h)) (the formula of torch's gelu backward).
 hipError_t launch_gelu_rows(const void* h, int32_t h_dtype, int64_t h_ld, int64_t rows, int64_t cols, void* y,

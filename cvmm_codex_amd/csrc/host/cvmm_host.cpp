@@ -114,44 +114,7 @@ struct Scratch {
   size_t clean = 0;  // length of the prefix known to be zero
 };
 std::mutex g_mu;
-std::map<std::pair<int, int64_t>, Scratch> g_sort_ws, g_wgrad_ws, g_dense_ws;
-
-// The workspace of a call that takes a dense top-k sum (cvmm_topk_dense):
-// kept per (device, stream) with its slotted-row region zero between calls
-// (zeroed when it is not known to be; every call leaves it zero), so the call
-// only writes the tokens' own slots.  A call writes the bytes after its own
-// region, so afterwards exactly that region is known zero; a failed call may
-// leave slots written, so nothing is.  `run` makes the call with the flag to
-// pass.
-template <typename F>
-void with_dense_workspace(const Tensor& like, int64_t stream, size_t bytes, size_t zero_bytes, F&& run) {
-  Tensor buf;
-  bool zeroed;
-  Scratch* sp;
-  {
-    std::lock_guard<std::mutex> lk(g_mu);
-    Scratch& s = g_dense_ws[{(int)like.get_device(), stream}];
-    if (!s.buf.defined() || (size_t)s.buf.numel() < bytes) {
-      s.buf = at::zeros({(int64_t)std::max<size_t>(bytes, 1)}, opts(like, at::kByte));
-      s.clean = (size_t)s.buf.numel();
-    } else if (s.clean < zero_bytes) {
-      s.buf.narrow(0, 0, (int64_t)zero_bytes).zero_();
-      s.clean = zero_bytes;
-    }
-    zeroed = zero_bytes <= s.clean;
-    buf = s.buf;
-    sp = &s;
-  }
-  try {
-    run(buf, zeroed ? CVMM_FLAG_WORKSPACE_ZEROED : 0);
-  } catch (...) {
-    std::lock_guard<std::mutex> lk(g_mu);
-    sp->clean = 0;
-    throw;
-  }
-  std::lock_guard<std::mutex> lk(g_mu);
-  sp->clean = zero_bytes;
-}
+std::map<std::pair<int, int64_t>, Scratch> g_sort_ws, g_wgrad_ws;
 
 Tensor sort_workspace(const Tensor& like, int64_t stream, size_t bytes) {
   std::lock_guard<std::mutex> lk(g_mu);
@@ -388,23 +351,14 @@ Tensor cvmm_forward_impl(const Tensor& x, const Tensor& keys, const OptT& keys_o
   Tensor out = at::empty({out_rows, d_out}, opts(x, dtype_of(outd)));
   const size_t ws_bytes = cvmm_fwd_workspace_bytes(R, (int32_t)E, d_in, d_out, out_rows, outd, od, 1,
                                                    rw.has_value() ? 1 : 0, (int32_t)flags);
-  auto call = [&](const OptT& ws, int64_t extra_flags) {
-    check(cvmm_fwd(ptr(xf), dtype_id(xf.scalar_type()), xf.size(0), xf.stride(0), ptr(kv),
-                   dtype_id(kv.scalar_type()), (int32_t)E, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2),
-                   tptr<int32_t>(s32), tptr<int64_t>(si), tptr<int64_t>(oi), R, tptr<int64_t>(offsets),
-                   tptr<int32_t>(route_pos), ptr(rwf), rwf.has_value() ? dtype_id(rwf->scalar_type()) : 0, k, od,
-                   ptr(out), outd, out_rows, d_out, (int32_t)(flags | extra_flags), ptr(ws), ws_bytes, (void*)stream),
-          "cvmm_fwd");
-  };
-  if (rw.has_value() && !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
-      cvmm_topk_dense(out_rows, (int32_t)E, d_in, d_out, k, od)) {
-    with_dense_workspace(x, stream, ws_bytes, cvmm_topk_dense_zero_bytes(out_rows, (int32_t)E, d_in, od),
-                         [&](const Tensor& ws, int64_t f) { call(ws, f); });
-  } else {
-    OptT ws;
-    if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(x, at::kByte));
-    call(ws, 0);
-  }
+  OptT ws;
+  if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(x, at::kByte));
+  check(cvmm_fwd(ptr(xf), dtype_id(xf.scalar_type()), xf.size(0), xf.stride(0), ptr(kv),
+                 dtype_id(kv.scalar_type()), (int32_t)E, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2),
+                 tptr<int32_t>(s32), tptr<int64_t>(si), tptr<int64_t>(oi), R, tptr<int64_t>(offsets),
+                 tptr<int32_t>(route_pos), ptr(rwf), rwf.has_value() ? dtype_id(rwf->scalar_type()) : 0, k, od,
+                 ptr(out), outd, out_rows, d_out, (int32_t)flags, ptr(ws), ws_bytes, (void*)stream),
+        "cvmm_fwd");
   return out;
 }
 
@@ -533,25 +487,16 @@ std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const
     const size_t ws_bytes = cvmm_bwd_x_workspace_bytes(R, (int32_t)E, d_in, d_out, gx_rows, 1, rw.has_value() ? 1 : 0,
                                                        oi.has_value() ? 1 : 0, k, dtype_id(x.scalar_type()), od,
                                                        need_grad_rw ? 1 : 0, (int32_t)flags);
-    auto call = [&](const OptT& ws, int64_t extra_flags) {
-      check(cvmm_bwd_x(ptr(g), dtype_id(g.scalar_type()), g.size(0), g.stride(0), ptr(kv),
-                       dtype_id(kv.scalar_type()), (int32_t)E, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2),
-                       tptr<int32_t>(s32), tptr<int64_t>(si), tptr<int64_t>(oi), R, tptr<int64_t>(offsets),
-                       tptr<int32_t>(route_pos), ptr(rwf), rwd, k, ptr(xr), dtype_id(xr.scalar_type()), xr.size(0),
-                       xr.stride(0), od, ptr(gx), dtype_id(x.scalar_type()), gx_rows, d_in, ptr(grad_rw),
-                       rw.has_value() ? dtype_id(rw->scalar_type()) : 0, (int32_t)(flags | extra_flags), ptr(ws),
-                       ws_bytes, (void*)stream),
-            "cvmm_bwd_x");
-    };
-    if (gx.has_value() && !rw.has_value() && oi.has_value() && top_k > 1 && !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
-        cvmm_topk_dense(gx_rows, (int32_t)E, d_out, d_in, top_k, od)) {
-      with_dense_workspace(x, stream, ws_bytes, cvmm_topk_dense_zero_bytes(gx_rows, (int32_t)E, d_out, od),
-                           [&](const Tensor& ws, int64_t f) { call(ws, f); });
-    } else {
-      OptT ws;
-      if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(x, at::kByte));
-      call(ws, 0);
-    }
+    OptT ws;
+    if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(x, at::kByte));
+    check(cvmm_bwd_x(ptr(g), dtype_id(g.scalar_type()), g.size(0), g.stride(0), ptr(kv),
+                     dtype_id(kv.scalar_type()), (int32_t)E, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2),
+                     tptr<int32_t>(s32), tptr<int64_t>(si), tptr<int64_t>(oi), R, tptr<int64_t>(offsets),
+                     tptr<int32_t>(route_pos), ptr(rwf), rwd, k, ptr(xr), dtype_id(xr.scalar_type()), xr.size(0),
+                     xr.stride(0), od, ptr(gx), dtype_id(x.scalar_type()), gx_rows, d_in, ptr(grad_rw),
+                     rw.has_value() ? dtype_id(rw->scalar_type()) : 0, (int32_t)flags, ptr(ws), ws_bytes,
+                     (void*)stream),
+          "cvmm_bwd_x");
     if (gx.has_value()) grad_x = gx->view(x.sizes());
   }
   return {grad_x, grad_w, grad_rw};

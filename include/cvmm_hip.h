@@ -47,9 +47,6 @@ extern "C" {
                                      instead of a route-ordered buffer + ordered row sum */
 #define CVMM_FLAG_COUNTERS_ZEROED 2 /* cvmm_bwd_w: the counter region at the start of the
                                        workspace is already zero (see cvmm_bwd_w) */
-#define CVMM_FLAG_WORKSPACE_ZEROED 8 /* cvmm_fwd / cvmm_bwd_x taking a dense top-k sum: the first
-                                        cvmm_topk_dense_zero_bytes() of the workspace are zero,
-                                        and the call leaves them zero (see cvmm_topk_dense) */
 #define CVMM_FLAG_COUNTS_READY 16 /* cvmm_sort_routes_cast_keys_ex: the workspace already holds the
                                      count matrix of these ids for n_experts, written by
                                      cvmm_copy_ids_count (see there) */
@@ -123,27 +120,24 @@ int cvmm_tuning_set(int32_t knob, int64_t value);
  * [K]-row x [K, N] expert products, for n_tokens tokens over n_experts
  * experts -- is taken as one dense GEMM (no counterpart in the reference,
  * which writes every route's product and sums them afterwards,
- * cvmm.py:1204-1223, :1541-1545).  The dense form places each token's K-wide
- * operand rows in expert slots, A[t][e*K + k], and multiplies A [T, E*K] by
- * the weights as [E*K, N] rows (a library GEMM, fp32 accumulation, one
- * rounding, deterministic): E / top_k times the useful flops, but no [R, N]
+ * cvmm.py:1204-1223, :1541-1545).  The dense form is the GEMM of A [T, E*K]
+ * (each token's K-wide operand rows in the slots of its experts, zero
+ * elsewhere) and the weights as [E*K, N] rows, with A's tiles gathered into
+ * LDS on the fly from a per-(token, expert) table of first routes (a token's
+ * further routes on one expert run as extra passes): fp32 accumulation, one
+ * rounding, deterministic; E / top_k times the useful flops, but no [R, N]
  * route-ordered buffer (2.1 GB at SwitchHead size).  It is taken when the
- * shapes fit (16-bit op, K % 8 == 0, 2 <= top_k <= 64, <= 4096 experts) and,
- * unless CVMM_TUNE_DENSE_TOPK says otherwise, a cost model of the two ways
- * (measured rates) favours it: at high fan-out (top_k / E >= ~1/4).
+ * shapes fit (16-bit op, K % 8 == 0, N % 8 == 0, 2 <= top_k <= 64, <= 1024
+ * experts) and, unless CVMM_TUNE_DENSE_TOPK says otherwise, a cost model of
+ * the two ways (measured rates) favours it: at high fan-out (top_k / E >=
+ * ~1/4).
  *   cvmm_fwd, weighted:          K = d_in,  N = d_out; the weights are read
- *     fastest as the op-dtype [E][d_in][d_out] copy (unit stride on d_out);
+ *     as they stand when an op-dtype copy with unit stride on d_in (the
+ *     [E][d_out][d_in] copy, or its expert-interleaved [d_out][E][d_in] form);
  *   cvmm_bwd_x, unweighted token input, top_k > 1: K = d_out, N = d_in; the
- *     weights as the op-dtype [E][d_out][d_in] copy (unit stride on d_in).
- * Other keys are cast into the workspace.  Returns 1 or 0.
- * The slotted rows take the first cvmm_topk_dense_zero_bytes() of the
- * call's workspace.  The call zero-fills them first, unless the caller
- * passes CVMM_FLAG_WORKSPACE_ZEROED: then they must be zero on entry, only
- * the tokens' own slots are written, and the call clears those after the GEMM
- * (a caller that keeps its workspace skips rewriting the zeros: at
- * SwitchHead size 67 MB of slots instead of 268 MB of rows, twice). */
+ *     weights with unit stride on d_out ([E][d_in][d_out] or [d_in][E][d_out]).
+ * Other keys are cast into the workspace.  Returns 1 or 0. */
 int cvmm_topk_dense(int64_t n_tokens, int32_t n_experts, int64_t K, int64_t N, int64_t top_k, int32_t op_dtype);
-size_t cvmm_topk_dense_zero_bytes(int64_t n_tokens, int32_t n_experts, int64_t K, int32_t op_dtype);
 
 /* ------------------------------------------------------------------------ */
 /* Selector preparation                                                      */

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.cvmm_abi_version() == 11
+    assert lib.cvmm_abi_version() == 12
 
 
 def test_workspace_queries(lib):
@@ -141,7 +141,8 @@ def test_router_arguments_fail_before_launch(lib):
 def test_dense_topk_choice(lib):
     """The top-k sum's dense form is chosen at SwitchHead fan-out (64 of 256
     experts, K = 64, N = 2048), not at top-8 of 64 (ff_up / ff_down) or of 128
-    (the FFN stack); only for 16-bit ops, 2 <= top_k <= 64 and K % 8 == 0;
+    (the FFN stack); only for 16-bit ops, 2 <= top_k <= 64, K % 8 == 0,
+    N % 8 == 0 and at most 1024 experts;
     the knob forces either way."""
     BF, F32 = N.BF16, N.F32
     assert lib.cvmm_topk_dense(8192, 256, 64, 2048, 64, BF) == 1        # switch_v grad-input, switch_o forward
@@ -156,14 +157,22 @@ def test_dense_topk_choice(lib):
         assert lib.cvmm_topk_dense(8192, 64, 128, 1024, 8, BF) == 1
         assert lib.cvmm_topk_dense(100, 7, 16, 24, 2, N.F16) == 1
         assert lib.cvmm_topk_dense(100, 7, 16, 24, 1, N.F16) == 0        # top-1 has no sum
+        # the GEMM addresses weights, operand rows and table with 32-bit offsets
+        assert lib.cvmm_topk_dense(8192, 1024, 1024, 2048, 8, BF) == 0   # 4 GiB of weights
+        assert lib.cvmm_topk_dense(1 << 20, 16, 1024, 512, 64, BF) == 0  # 128 GiB of operand rows
+        assert lib.cvmm_topk_dense(1 << 20, 1024, 8, 512, 2, BF) == 0    # 4 GiB slot table
         assert lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 1) == 0
         assert lib.cvmm_topk_dense(8192, 256, 64, 2048, 64, BF) == 0
         assert lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 3) != 0
     finally:
         lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 0)
-    # workspace: the dense form needs the slotted rows (T x E*K), not the [R, N] route buffer
+    assert lib.cvmm_topk_dense(8192, 2000, 64, 2048, 64, BF) == 0        # more experts than the table's rows hold
+    assert lib.cvmm_topk_dense(8192, 256, 64, 2044, 64, BF) == 0         # N % 8 != 0
+    # workspace: the dense form needs a weight copy, the slot tables (5 bytes
+    # per token and expert) and an operand copy (each at most E*K*N or R*K
+    # values), not the [R, N] route buffer
     R, T, E = 524288, 8192, 256
     ws = lib.cvmm_bwd_x_workspace_bytes(R, E, 2048, 64, T, 1, 0, 1, 64, BF, BF, 0, 0)
-    assert T * E * 64 * 2 <= ws < R * 2048 * 2 // 4
+    assert E * 64 * 2048 * 2 + T * E * 5 <= ws < R * 2048 * 2 // 4
     ws = lib.cvmm_fwd_workspace_bytes(R, E, 64, 2048, T, BF, BF, 1, 1, 0)
-    assert T * E * 64 * 2 <= ws < R * 2048 * 2 // 4
+    assert E * 64 * 2048 * 2 + T * E * 5 + R * 64 * 2 <= ws < R * 2048 * 2 // 4
