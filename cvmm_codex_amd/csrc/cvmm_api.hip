@@ -296,12 +296,17 @@ int run_dense_topk(const DenseWs& w, const void* src, int32_t src_dtype, int64_t
     if (r) return r;
     inv = w.inv;
   }
-  // operand rows: with routing weights the scaled route rows, written by the
-  // slot-table launch; else the rows as given when they are 16-byte pieces
-  // of the op dtype, or an op-dtype copy
+  // operand rows: with routing weights the scaled route rows (a launch of
+  // their own); else the rows as given when they are 16-byte pieces of the op
+  // dtype, or an op-dtype copy
   const void* A = src;
   int64_t a_ld = src_ld;
   if (rw != nullptr) {
+    int r = check_launch(timed_combine(s, [&] {
+      return launch_scale_rows(src, src_dtype, src_ld, src_per_route, rw, rw_dtype, w_round, n_routes, top_k, K,
+                               op_dtype, w.src, s);
+    }), what);
+    if (r) return r;
     A = w.src;
     a_ld = K;
   } else if (!(src_dtype == op_dtype && src_per_route && aligned16(src) && (src_ld * esz) % 16 == 0 &&
@@ -315,9 +320,8 @@ int run_dense_topk(const DenseWs& w, const void* src, int32_t src_dtype, int64_t
     a_ld = K;
   }
   int r = check_launch(timed_combine(s, [&] {
-    return launch_topk_slot_table(sorted_sel, inv, rp, offs + (n_experts - 1), n_tokens, top_k, n_experts, rw,
-                                  rw_dtype, w_round, src, src_dtype, src_ld, src_per_route, K, op_dtype, w.src,
-                                  a_ld, w.offs, w.slots, w.nxt, w.mult, s);
+    return launch_topk_slot_table(sorted_sel, inv, rp, offs + (n_experts - 1), n_tokens, top_k, n_experts, a_ld,
+                                  K, w.offs, w.slots, w.nxt, w.mult, s);
   }), what);
   if (r) return r;
   TopkGemmParams p{};

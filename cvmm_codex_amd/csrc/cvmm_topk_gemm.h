@@ -43,16 +43,17 @@ struct TopkGemmParams {
 // topk_slot_rows(n_tokens) bytes, offs as many 32-bit offsets, those of
 // operand rows a_ld elements apart): the expert of route r is
 // sorted_sel[inv[r]] when inv[r] < *rows_end and rp[inv[r]] == r, with an id in
-// [0, E).  With routing weights `w`, also the scaled operand rows of the valid
-// routes: xs[r][k] = rnd_op(rnd(w[r], w_round) * rnd_op(x[row][k])), row = r
-// (x_per_route) or r / top_k, xs contiguous [R][K].  top_k <= 64,
-// n_experts <= kTopkMaxExperts, 16-bit op dtype, K % 8 == 0.
+// [0, E).  top_k <= 64, n_experts <= kTopkMaxExperts.
 hipError_t launch_topk_slot_table(const int32_t* sorted_sel, const int32_t* inv, const int64_t* rp,
                                   const int64_t* rows_end, int64_t n_tokens, int64_t top_k, int32_t n_experts,
-                                  const void* w, int32_t w_dtype, int32_t w_round, const void* x, int32_t x_dtype,
-                                  int64_t x_ld, bool x_per_route, int64_t K, int32_t op_dtype, void* xs,
-                                  int64_t a_ld, uint32_t* offs, uint8_t* slots, uint8_t* nxt, uint8_t* mult,
+                                  int64_t a_ld, int64_t K, uint32_t* offs, uint8_t* slots, uint8_t* nxt, uint8_t* mult,
                                   hipStream_t stream);
+// The operand rows of a weighted sum: xs[r][k] = rnd_op(rnd(w[r], w_round) *
+// rnd_op(x[row][k])), row = r (x_per_route) or r / top_k, xs contiguous
+// [n_routes][K]; 16-bit op dtype, K % 8 == 0.
+hipError_t launch_scale_rows(const void* x, int32_t x_dtype, int64_t x_ld, bool x_per_route, const void* w,
+                             int32_t w_dtype, int32_t w_round, int64_t n_routes, int64_t top_k, int64_t K,
+                             int32_t op_dtype, void* xs, hipStream_t stream);
 // dst[r][k] = rnd_op(src[r * src_ld + k]), contiguous rows of K values
 hipError_t launch_copy_rows_op(const void* src, int32_t src_dtype, int64_t src_ld, int64_t rows, int64_t K,
                                int32_t op_dtype, void* dst, hipStream_t stream);

@@ -12,25 +12,27 @@
 //
 // A is never stored.  A workgroup owns 256 tokens x 256 output columns and
 // walks the experts in order, one 32-wide k slice at a time.  Each slice moves
-// straight into LDS by global_load_lds (16 bytes per lane, 4 lanes per
-// 64-byte row piece, one request each): the rows of the slice's A half are
-// the tokens' route rows for expert e -- found in a byte table of first routes
-// per (expert, token) that a small launch builds beforehand -- or the zero
-// page when a token has no route there; the B half holds the weight rows of
-// expert e for the tile's columns.  A token that picks one expert several
-// times gets its further routes as further passes over the experts (the
-// table's next-route links), so each product term is one operand row, as in
-// the reference's per-route products.  The weighted forward's routing
-// weights are applied to the route rows beforehand (the slot-table launch
-// writes the scaled rows), so the GEMM has no per-element work besides the
-// MFMAs.
+// straight into LDS by buffer loads (16 bytes per lane, 4 lanes per 64-byte
+// row piece, one request each): the rows of the slice's A half are the
+// tokens' route rows for expert e -- their byte offsets come from a table of
+// first routes per (expert, token) that a small launch builds beforehand --
+// or zeros (an offset past the descriptor's range) when a token has no route
+// there; the B half holds the weight rows of expert e for the tile's columns.
+// A token that picks one expert several times gets its further routes as
+// further passes over the experts (the table's next-route links), so each
+// product term is one operand row, as in the reference's per-route products.
+// The weighted forward's routing weights are applied to the route rows
+// beforehand (a scaling launch writes them), so the GEMM has no per-element
+// work besides the MFMAs.
 //
 // Pipeline.  The operand rows are gathered from L2 in 64-byte requests, so a
 // CU needs many requests in flight: slices rotate through a ring of four
 // 32 KB LDS buffers with three in flight while one is multiplied, and every
 // wait is an exact vmcnt (each slice is the same nine DMA instructions per
 // wave: four A pieces, four B pieces and the 256 table bytes of the slice
-// three ahead, which its issue needs).  The fragments of slice s + 1 are read
+// three ahead, which its issue needs).  The descriptors stay fixed: the
+// lane offsets come from the table (A) or are constant (B), and the slice's
+// k and expert move a uniform soffset.  The fragments of slice s + 1 are read
 // while the MFMAs of slice s run (two register sets), and the DMA of slice
 // s + 4 is issued between those MFMAs.
 //
@@ -58,104 +60,77 @@ constexpr int kTkTokens = 16;            // slot table launch: tokens per workgr
 // ---------------------------------------------------------------------------
 // slot table
 // ---------------------------------------------------------------------------
-// A workgroup of 4 waves takes 16 tokens, a wave one token at a time.  Lane
-// j < top_k resolves the expert e_j of route r = t * top_k + j (sorted
-// position q = inv[r], valid when q < *rows_end and rp[q] == r, with an
-// expert id in [0, E)); over the token's routes:
+// A workgroup of 4 waves takes 16 tokens; wave w takes tokens w, w + 4, w + 8
+// and w + 12 of them, lane j route j of each.  Lane j < top_k resolves the
+// expert e_j of route r = t * top_k + j (sorted position q = inv[r], valid
+// when q < *rows_end and rp[q] == r, with an expert id in [0, E)); the loads
+// of all four tokens are issued together.  Over the token's routes:
 //   slots[e][t] = 1 + the first j with e_j = e, else 0   (expert-major rows of
 //                 t_pad = n_tokens rounded up to 256 bytes; 0 past n_tokens)
 //   offs[e][t]  = the byte offset (t * top_k + j) * a_row_bytes of that
 //                 route's operand row, or kTopkOob
 //   nxt[r]      = 1 + the next j' > j with e_j' = e_j, else 0
 //   mult[t]     = the most routes of t on one expert (0: none valid)
-// Weighted (W): the operand rows of the token's valid routes, scaled by the
-// rounded routing weight as the reference's weighted combine has it
-// (cvmm.py:1545: rnd_out(w) applied to the route's product; here to its
-// operand row): xs[r][k] = rnd_op(rnd(w[r], w_round) * rnd_op(x[row][k])),
-// row = r for route input, t for token input.
-template <typename OpT, bool W>
+// The routes of a token that share an expert are found through a per-wave
+// LDS word per expert: each lane ORs in its bit, then reads back the set of
+// routes on its expert (first = lowest bit, next = lowest bit above its own,
+// count = population).
 __global__ __launch_bounds__(256) void topk_slot_table_kernel(
     const int32_t* __restrict__ sorted_sel, const int32_t* __restrict__ inv, const int64_t* __restrict__ rp,
     const int64_t* __restrict__ rows_end, int64_t n_tokens, int64_t t_pad, int32_t top_k, int32_t n_experts,
-    int32_t e16, const void* __restrict__ w, int32_t w_dtype, int32_t w_round, const void* __restrict__ x,
-    int32_t x_dtype, int64_t x_ld, int32_t x_per_route, int64_t K, OpT* __restrict__ xs, uint32_t a_row_bytes,
-    uint32_t* __restrict__ offs, uint8_t* __restrict__ slots, uint8_t* __restrict__ nxt,
-    uint8_t* __restrict__ mult) {
-  constexpr int32_t kOp = DTypeOf<OpT>::value;
+    int32_t e16, uint32_t a_row_bytes, uint32_t* __restrict__ offs, uint8_t* __restrict__ slots,
+    uint8_t* __restrict__ nxt, uint8_t* __restrict__ mult) {
+  constexpr int kPer = kTkTokens / 4;  // tokens per wave
   __shared__ __attribute__((aligned(16))) uint8_t tile[kTopkMaxExperts][kTkTokens];
-  __shared__ int32_t s_e[4][64];
-  __shared__ float s_w[4][W ? 64 : 1];
+  __shared__ unsigned long long s_set[4][kTopkMaxExperts];  // per wave: routes of the token on expert e
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int64_t tok0 = (int64_t)blockIdx.x * kTkTokens;
   for (int i = tid * 16; i < e16 * kTkTokens; i += 256 * 16)
     *reinterpret_cast<uint4*>(&tile[0][0] + i) = make_uint4(0, 0, 0, 0);
-  __syncthreads();
   const int64_t valid_end = *rows_end;
-  for (int tl = wave; tl < kTkTokens; tl += 4) {
+  // ---- the experts of the wave's routes, loads issued together
+  int64_t q[kPer];
+  int32_t e[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int64_t t = tok0 + wave + 4 * u;
+    q[u] = (t < n_tokens && lane < top_k) ? (int64_t)inv[t * top_k + lane] : -1;
+  }
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int64_t t = tok0 + wave + 4 * u;
+    e[u] = -1;
+    if (q[u] >= 0 && q[u] < valid_end && rp[q[u]] == t * top_k + lane) {
+      const int32_t id = sorted_sel[q[u]];
+      if (id >= 0 && id < n_experts) e[u] = id;
+    }
+  }
+  __syncthreads();  // the tile is zero
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int tl = wave + 4 * u;
     const int64_t t = tok0 + tl;
-    const bool active = t < n_tokens;  // wave-uniform
-    int32_t e = -1;
-    float sc = 0.f;
-    if (active && lane < top_k) {
-      const int64_t r = t * top_k + lane;
-      const int64_t q = inv[r];
-      if (q >= 0 && q < valid_end && rp[q] == r) {
-        const int32_t id = sorted_sel[q];
-        if (id >= 0 && id < n_experts) e = id;
-      }
-      if constexpr (W)
-        if (e >= 0) sc = round_to(load_as_f32(w, w_dtype, r), w_round);
-    }
-    int first = 64, next = 64, cnt = 0;
-    for (int i = 0; i < top_k; ++i) {
-      const int32_t ei = __shfl(e, i, 64);
-      if (e >= 0 && ei == e) {
-        ++cnt;
-        if (i < first) first = i;
-        if (i > lane && next == 64) next = i;
-      }
-    }
+    if (t >= n_tokens) break;  // wave-uniform; later tokens are further out
+    const int32_t eu = e[u];
+    unsigned long long* cell = &s_set[wave][eu >= 0 ? eu : 0];
+    if (eu >= 0) *cell = 0ull;
+    __builtin_amdgcn_wave_barrier();
+    if (eu >= 0) atomicOr(cell, 1ull << lane);
+    __builtin_amdgcn_wave_barrier();
+    const unsigned long long set = eu >= 0 ? *cell : 0ull;
+    __builtin_amdgcn_wave_barrier();
+    const int cnt = __popcll(set);
+    const unsigned long long above = lane == 63 ? 0ull : (set >> (lane + 1)) << (lane + 1);
     int m = cnt;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       const int v = __shfl_xor(m, o, 64);
       m = v > m ? v : m;
     }
-    if (!active) continue;
-    if (e >= 0 && first == lane) tile[e][tl] = (uint8_t)(lane + 1);
-    if (lane < top_k) nxt[t * top_k + lane] = (uint8_t)(e >= 0 && next < 64 ? next + 1 : 0);
+    if (eu >= 0 && __ffsll((long long)set) - 1 == lane) tile[eu][tl] = (uint8_t)(lane + 1);
+    if (lane < top_k) nxt[t * top_k + lane] = (uint8_t)(above != 0ull ? __ffsll((long long)above) : 0);
     if (lane == 0) mult[t] = (uint8_t)m;
-    if constexpr (W) {
-      s_e[wave][lane] = e;
-      s_w[wave][lane] = sc;
-      __builtin_amdgcn_wave_barrier();
-      const int64_t cpr = K / 8, total = top_k * cpr;
-      const bool vec = x_dtype == kOp && x_ld % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-      for (int64_t it = lane; it < total; it += 64) {
-        const int32_t jr = (int32_t)(it / cpr);
-        const int64_t c = it - jr * cpr;
-        if (s_e[wave][jr] < 0) continue;
-        const float sj = s_w[wave][jr];
-        const int64_t r = t * top_k + jr;
-        const int64_t off = (x_per_route ? r : t) * x_ld + c * 8;
-        float v[8];
-        if (vec) {
-          Chunk16 in;
-          in.u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + off);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) v[i] = to_f32(reinterpret_cast<const OpT*>(&in)[i]);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) v[i] = round_to(load_as_f32(x, x_dtype, off + i), kOp);
-        }
-        Chunk16 o;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) reinterpret_cast<OpT*>(&o)[i] = from_f32<OpT>(sj * v[i]);
-        *reinterpret_cast<uint4*>(xs + r * K + c * 8) = o.u;
-      }
-      __builtin_amdgcn_wave_barrier();
-    }
   }
   __syncthreads();
   // one thread per expert: the row piece of the 16 tokens in both tables
@@ -172,6 +147,58 @@ __global__ __launch_bounds__(256) void topk_slot_table_kernel(
     uint4* dst = reinterpret_cast<uint4*>(offs + (int64_t)e * t_pad + tok0);
 #pragma unroll
     for (int q = 0; q < 4; ++q) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// the weighted sum's operand rows, scaled by the rounded routing weight as the
+// reference's weighted combine has it (cvmm.py:1545: rnd_out(w) applied to
+// the route's product; here to its operand row):
+//   xs[r][k] = rnd_op(rnd(w[r], w_round) * rnd_op(x[row][k])),
+// row = r for route input, r / top_k for token input.  Every route is
+// scaled: the GEMM reads only the rows of valid routes (the table's), so no
+// route needs resolving here.  16-byte chunks, four loads in flight per
+// thread; IDX32: chunk indices fit 32 bits (cheaper division).
+// ---------------------------------------------------------------------------
+template <typename OpT, typename IdxT>
+__global__ __launch_bounds__(256) void scale_rows_kernel(const void* __restrict__ x, int32_t x_dtype, int64_t x_ld,
+                                                         int32_t x_per_route, const void* __restrict__ w,
+                                                         int32_t w_dtype, int32_t w_round, int64_t n_routes,
+                                                         int64_t top_k, int64_t K, OpT* __restrict__ xs) {
+  constexpr int32_t kOp = DTypeOf<OpT>::value;
+  constexpr int kU = 4;
+  const IdxT cpr = (IdxT)(K / 8);
+  const IdxT total = (IdxT)n_routes * cpr;
+  const bool vec = x_dtype == kOp && x_ld % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  for (IdxT base = (IdxT)blockIdx.x * (256 * kU); base < total; base += (IdxT)gridDim.x * (256 * kU)) {
+    Chunk16 in[kU];
+    float sc[kU];
+    IdxT it[kU];
+#pragma unroll
+    for (int v = 0; v < kU; ++v) {
+      it[v] = base + (IdxT)(v * 256) + (IdxT)threadIdx.x;
+      if (it[v] >= total) continue;
+      const IdxT r = it[v] / cpr, c = it[v] - r * cpr;
+      const int64_t row = x_per_route ? (int64_t)r : (int64_t)r / top_k;
+      const int64_t off = row * x_ld + (int64_t)c * 8;
+      sc[v] = round_to(load_as_f32(w, w_dtype, (int64_t)r), w_round);
+      if (vec) {
+        in[v].u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + off);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          reinterpret_cast<OpT*>(&in[v])[i] = from_f32<OpT>(round_to(load_as_f32(x, x_dtype, off + i), kOp));
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < kU; ++v) {
+      if (it[v] >= total) continue;
+      Chunk16 o;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        reinterpret_cast<OpT*>(&o)[i] = from_f32<OpT>(sc[v] * to_f32(reinterpret_cast<const OpT*>(&in[v])[i]));
+      *reinterpret_cast<uint4*>(xs + (int64_t)it[v] * 8) = o.u;
+    }
   }
 }
 
@@ -567,28 +594,42 @@ bool topk_gemm_table_fits(int32_t n_experts, int64_t n_tokens) {
 
 hipError_t launch_topk_slot_table(const int32_t* sorted_sel, const int32_t* inv, const int64_t* rp,
                                   const int64_t* rows_end, int64_t n_tokens, int64_t top_k, int32_t n_experts,
-                                  const void* w, int32_t w_dtype, int32_t w_round, const void* x, int32_t x_dtype,
-                                  int64_t x_ld, bool x_per_route, int64_t K, int32_t op_dtype, void* xs,
-                                  int64_t a_ld, uint32_t* offs, uint8_t* slots, uint8_t* nxt, uint8_t* mult,
+                                  int64_t a_ld, int64_t K, uint32_t* offs, uint8_t* slots, uint8_t* nxt, uint8_t* mult,
                                   hipStream_t stream) {
   if (n_tokens <= 0) return hipSuccess;
-  if (!topk_gemm_a_fits(n_tokens * top_k, a_ld, K) || !topk_gemm_table_fits(n_experts, n_tokens))
+  if (top_k > 64 || n_experts > kTopkMaxExperts || !topk_gemm_a_fits(n_tokens * top_k, a_ld, K) ||
+      !topk_gemm_table_fits(n_experts, n_tokens))
     return hipErrorInvalidValue;
   const int32_t e16 = topk_e16(n_experts);
   const int64_t t_pad = topk_slot_rows(n_tokens);
   const unsigned grid = (unsigned)(t_pad / kTkTokens);
-#define CVMM_TK_SLOTS(OP, WT)                                                                                   \
-  hipLaunchKernelGGL((topk_slot_table_kernel<OP, WT>), dim3(grid), dim3(256), 0, stream, sorted_sel, inv, rp,  \
-                     rows_end, n_tokens, t_pad, (int32_t)top_k, n_experts, e16, w, w_dtype, w_round, x, x_dtype, \
-                     x_ld, x_per_route ? 1 : 0, K, (OP*)xs, (uint32_t)(a_ld * 2), offs, slots, nxt, mult)
+  hipLaunchKernelGGL(topk_slot_table_kernel, dim3(grid), dim3(256), 0, stream, sorted_sel, inv, rp, rows_end,
+                     n_tokens, t_pad, (int32_t)top_k, n_experts, e16, (uint32_t)(a_ld * 2), offs, slots, nxt, mult);
+  return hipGetLastError();
+}
+
+hipError_t launch_scale_rows(const void* x, int32_t x_dtype, int64_t x_ld, bool x_per_route, const void* w,
+                             int32_t w_dtype, int32_t w_round, int64_t n_routes, int64_t top_k, int64_t K,
+                             int32_t op_dtype, void* xs, hipStream_t stream) {
+  const int64_t total = n_routes * (K / 8);
+  if (total <= 0) return hipSuccess;
+  if (K % 8 != 0 || top_k <= 0) return hipErrorInvalidValue;
+  int64_t blocks = (total + 1023) / 1024;
+  if (blocks > 8192) blocks = 8192;
+  const bool i32 = total + 8192 * 1024 < (1ll << 32);
+#define CVMM_SCALE(OP, IDX)                                                                                 \
+  hipLaunchKernelGGL((scale_rows_kernel<OP, IDX>), dim3((unsigned)blocks), dim3(256), 0, stream, x, x_dtype, \
+                     x_ld, x_per_route ? 1 : 0, w, w_dtype, w_round, n_routes, top_k, K, (OP*)xs)
   if (op_dtype == kBF16) {
-    if (w) CVMM_TK_SLOTS(bf16_t, true);
-    else CVMM_TK_SLOTS(bf16_t, false);
+    if (i32) CVMM_SCALE(bf16_t, uint32_t);
+    else CVMM_SCALE(bf16_t, int64_t);
+  } else if (op_dtype == kF16) {
+    if (i32) CVMM_SCALE(f16_t, uint32_t);
+    else CVMM_SCALE(f16_t, int64_t);
   } else {
-    if (w) CVMM_TK_SLOTS(f16_t, true);
-    else CVMM_TK_SLOTS(f16_t, false);
+    return hipErrorInvalidValue;
   }
-#undef CVMM_TK_SLOTS
+#undef CVMM_SCALE
   return hipGetLastError();
 }
 
