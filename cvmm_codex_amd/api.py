@@ -12,8 +12,10 @@ counterpart in cvmm.py) fuse the router lines its callers write before
 
 All arithmetic runs in the HIP kernels of ``libcvmm_hip.so`` (C ABI in
 ``include/cvmm_hip.h``), launched on torch's current stream; nothing here
-synchronises with the host.  There is no CPU or PyTorch fallback: CPU tensors
-and a missing library raise.
+synchronises with the host.  There is no CPU or PyTorch fallback: CPU operands
+and a missing library raise.  (Selectors may be prepared from ids in host
+memory, as the reference's pure-torch preparation allows; that makes only the
+sorted index metadata.)
 
 Selector sorting is deferred: ``cvmm_prepare_sel2`` takes the int32 copy of
 the ids the reference takes (cvmm.py:1796), so later writes to the caller's
@@ -413,9 +415,22 @@ for _name in ("sel", "sel_index", "out_index"):
 del _name
 
 
+def _host_sel(sel: torch.Tensor):
+    """A selection held in host memory, prepared with torch ops as the
+    reference prepares every selection (cvmm.py:25-26, :1796-1797): the int32
+    ids (a copy, so later writes to `sel` change nothing, as on the device),
+    their stable sort and its permutation.  Only the metadata is made here;
+    cvmm() itself takes GPU tensors."""
+    fsel = sel.reshape(-1).to(torch.int32, copy=True)
+    ssel, perm = fsel.sort(stable=True)
+    return fsel.view(sel.shape), ssel.view(sel.shape), perm
+
+
 def cvmm_prepare_sel(sel: torch.Tensor, n_experts: int) -> CVMMSel:
     """cvmm.py:24-27: sort the flattened ids; sel_index = sorting permutation."""
-    _require_device(sel, "sel")
+    if not sel.is_cuda:
+        raw, ssel, perm = _host_sel(sel)
+        return CVMMSel(raw, ssel, perm, None)
     ssel, perm, _, offsets = _Routing(sel.reshape(-1), 1).get(n_experts)
     s = ssel.view(sel.shape)
     s._cvmm_offsets = {n_experts: offsets}
@@ -440,8 +455,12 @@ def cvmm_prepare_sel2(sel: Union[torch.Tensor, CVMMSel], w: Optional[torch.Tenso
             return CVMMSel(sel.raw_sel, sel.sel, route_index, None, w)
         return CVMMSel(sel.raw_sel, sel.sel, sel.sel_index, sel.out_index, w)
 
-    _require_device(sel, "sel")
     n_per_batch = sel.shape[-1]
+    if not sel.is_cuda:
+        raw, ssel, perm = _host_sel(sel)
+        if route_input:
+            return CVMMSel(raw, ssel, perm, None, w)
+        return CVMMSel(raw, ssel, perm // n_per_batch, perm, w)
     # the reference's `fsel = sel.flatten().to(torch.int32)` (cvmm.py:1796):
     # the routing is fixed here, whatever later happens to `sel`
     if _compiling():

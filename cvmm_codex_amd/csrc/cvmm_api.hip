@@ -638,6 +638,50 @@ int cvmm_sort_routes_cast_keys(const void* sel, int32_t sel_is_int64, int64_t n_
                                        d_in, d_out, k_se, k_si, k_sj, out_dtype, keys_t, keys_n, layout, 0, stream);
 }
 
+}  // extern "C"
+
+// Count matrices cvmm_copy_ids_count has written: a workspace, the ids'
+// count and the expert count it counted for, and the sort chunk it used.  A
+// sort with CVMM_FLAG_COUNTS_READY trusts the workspace only while a record
+// matches its own call and its current chunk (the chunk knob may have changed
+// in between); the record is used up, as the sort turns the counts into
+// prefixes.  Without a matching record the sort counts again.
+namespace {
+struct CountedRecord {
+  const void* ws;
+  int64_t n_routes;
+  int32_t n_experts;
+  int64_t chunk;
+};
+std::mutex g_counted_mu;
+std::vector<CountedRecord> g_counted;  // the most recent last, at most kCountedKeep
+constexpr size_t kCountedKeep = 64;
+
+void counted_record(const void* ws, int64_t n_routes, int32_t n_experts) {
+  std::lock_guard<std::mutex> lk(g_counted_mu);
+  for (size_t i = 0; i < g_counted.size(); ++i)
+    if (g_counted[i].ws == ws) {
+      g_counted.erase(g_counted.begin() + (std::ptrdiff_t)i);
+      break;
+    }
+  if (g_counted.size() == kCountedKeep) g_counted.erase(g_counted.begin());
+  g_counted.push_back({ws, n_routes, n_experts, sort_chunk_size(n_routes, n_experts)});
+}
+
+bool counted_take(const void* ws, int64_t n_routes, int32_t n_experts) {
+  std::lock_guard<std::mutex> lk(g_counted_mu);
+  for (size_t i = 0; i < g_counted.size(); ++i) {
+    const CountedRecord r = g_counted[i];
+    if (r.ws != ws) continue;
+    g_counted.erase(g_counted.begin() + (std::ptrdiff_t)i);
+    return r.n_routes == n_routes && r.n_experts == n_experts && r.chunk == sort_chunk_size(n_routes, n_experts);
+  }
+  return false;
+}
+}  // namespace
+
+extern "C" {
+
 int cvmm_copy_ids_count(const void* sel, int32_t sel_is_int64, int64_t n, int32_t n_experts, int32_t* out,
                         void* workspace, size_t workspace_bytes, void* stream) {
   if (n_experts <= 0 || n_experts > 32767)
@@ -647,9 +691,11 @@ int cvmm_copy_ids_count(const void* sel, int32_t sel_is_int64, int64_t n, int32_
   if (n > 0 && (workspace == nullptr || workspace_bytes < sort_workspace_bytes(n, n_experts)))
     return fail(CVMM_ERR_WORKSPACE, "cvmm_copy_ids_count: workspace too small (%zu < %zu)", workspace_bytes,
                 sort_workspace_bytes(n, n_experts));
-  return check_launch(timed(CVMM_KC_SORT, (hipStream_t)stream, [&] {
+  const int r = check_launch(timed(CVMM_KC_SORT, (hipStream_t)stream, [&] {
     return launch_copy_ids_count(sel, sel_is_int64 != 0, n, n_experts, out, workspace, (hipStream_t)stream);
   }), "cvmm_copy_ids_count");
+  if (r == 0 && n > 0) counted_record(workspace, n, n_experts);
+  return r;
 }
 
 int cvmm_sort_routes_cast_keys_ex(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts,
@@ -660,7 +706,8 @@ int cvmm_sort_routes_cast_keys_ex(const void* sel, int32_t sel_is_int64, int64_t
                                   void* keys_t, void* keys_n, int32_t layout, int32_t flags, void* stream) {
   if (flags & ~CVMM_FLAG_COUNTS_READY)
     return fail(CVMM_ERR_INVALID, "cvmm_sort_routes_cast_keys_ex: unknown flags %d", flags);
-  const bool counts_ready = (flags & CVMM_FLAG_COUNTS_READY) != 0;
+  const bool counts_ready =
+      (flags & CVMM_FLAG_COUNTS_READY) != 0 && counted_take(workspace, n_routes, n_experts);
   if (!keys || (!keys_t && !keys_n))  // no cast asked for: the sort alone
     return sort_routes_checked(sel, sel_is_int64, n_routes, n_experts, top_k, sorted_sel, perm, token_index,
                                offsets, route_pos, n_invalid, workspace, workspace_bytes, stream, counts_ready);

@@ -129,6 +129,58 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Split-K hand-over of fp32 partial tiles between the workgroups of one
+// output tile, which may run on different XCDs (each with its own L2): each
+// writes its partials, counts itself in at the tile's counter, and the last to
+// arrive adds every chunk's partials.  The partials are stored and loaded as
+// agent-scope relaxed atomics and the counter is a relaxed agent-scope
+// fetch_add.
+//
+// gfx942 / gfx950: agent-scope atomic stores and loads are issued with sc1
+// (LLVM AMDGPUUsage, "Memory Model GFX942": stores write through the XCD's L2
+// to the agent's coherent level, loads do not hit stale L2 lines), and a
+// store leaves vmcnt only once that level has acknowledged it.  So a vmcnt(0)
+// wait after the partial stores, before the workgroup barrier and the count,
+// orders every partial before the count, and the last arriver's loads see
+// them -- without the whole-L2 writeback and invalidate that release/acquire
+// fences would cost.  Other targets use device-scope fences around the count
+// (release before it, acquire after it), the memory model's own protocol.
+#if defined(__gfx942__) || defined(__gfx950__)
+#define CVMM_SPLITK_SC1_PROTOCOL 1
+#else
+#define CVMM_SPLITK_SC1_PROTOCOL 0
+#endif
+
+// after this thread's partial stores, before the workgroup barrier
+__device__ __forceinline__ void splitk_published() {
+#if CVMM_SPLITK_SC1_PROTOCOL
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0) (gfx9 encoding)
+#else
+  __threadfence();
+#endif
+}
+
+// one thread per workgroup, after the barrier: count in; true for the last
+// of n arrivals (the counter is reset for the next launch)
+__device__ __forceinline__ bool splitk_arrive(int32_t* ctr, int32_t n) {
+#if CVMM_SPLITK_SC1_PROTOCOL
+  const int32_t prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#else
+  const int32_t prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+#endif
+  const bool last = prev == n - 1;
+  if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return last;
+}
+
+// the last arriver, before reading the other chunks' partials (after the
+// workgroup barrier that shares the arrival's outcome)
+__device__ __forceinline__ void splitk_acquired() {
+#if !CVMM_SPLITK_SC1_PROTOCOL
+  __threadfence();
+#endif
+}
+
 // Map a linear workgroup id so that consecutive logical ids are dispatched to
 // the same XCD (the hardware places workgroup i on XCD i % 8).  Bijective for
 // any grid size.

@@ -284,12 +284,8 @@ __global__ __launch_bounds__(kWgThreads, 2) void wgrad_kernel(const WgradParams 
     return;
   }
 
-  // partial tile of this chunk -> workspace (tile-contiguous fp32).  The
-  // partials and the counter are accessed with agent-scope relaxed atomics
-  // (coherent across the XCDs' L2s); each thread waits for its partial stores
-  // to complete before the barrier and the count, so the last arriver reads
-  // every chunk's partials.  Release/acquire fences would write back and
-  // invalidate the XCD's whole L2 instead.
+  // partial tile of this chunk -> workspace (tile-contiguous fp32), handed
+  // over by the split-K protocol of cvmm_common.h (splitk_*)
   const int64_t slot = s_slot;
   if (slot >= p.max_slots) return;  // cannot happen: workspace sized for 2R/split slots
   auto pack2 = [](float a, float b) {
@@ -303,17 +299,12 @@ __global__ __launch_bounds__(kWgThreads, 2) void wgrad_kernel(const WgradParams 
     for (int j = 0; j < 4; ++j)
       __hip_atomic_store(d + j, pack2(s[2 * j], s[2 * j + 1]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // vmcnt(0) only (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] at [15:14])
-  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+  splitk_published();
   __syncthreads();
-  if (tid == 0) {
-    int32_t* ctr = p.counters + (int64_t)expert * tiles + tile;
-    const int32_t prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == nch - 1);
-    if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (tid == 0) s_last = splitk_arrive(p.counters + (int64_t)expert * tiles + tile, nch);
   __syncthreads();
   if (!s_last) return;
+  splitk_acquired();
   // this expert's slots are consecutive; add them in chunk order
   const int64_t base_slot = s_base_slot;
   for (int r = tid / TPR; r < BM; r += RPP) {

@@ -379,14 +379,11 @@ __global__ __launch_bounds__(256, (BM / WM / 16) * (BN / WN / 16) <= 16 ? 2 : 1)
   }
 
   // ---- multi-chunk expert: fp32 partial tile in fragment order -> workspace;
-  // the last arriver sums the chunks in chunk order.  The partials and the
-  // counter are accessed with agent-scope (sc1) relaxed atomics, coherent
-  // across the XCDs' L2s: every thread waits for its partial stores to
-  // complete before the barrier and the count, so the last arriver reads
-  // every chunk's partials from the coherent level.  (Release/acquire fences
-  // write back and invalidate the whole L2 of the XCD under the feet of the
-  // other workgroups there: the FFN stack's weight gradient took 780 us per
-  // launch with them, 720 us with this exchange.)
+  // the last arriver sums the chunks in chunk order, by the split-K protocol
+  // of cvmm_common.h (splitk_*: on gfx942/gfx950 without release/acquire
+  // fences, which write back and invalidate the whole L2 of the XCD under the
+  // feet of the other workgroups there: the FFN stack's weight gradient took
+  // 780 us per launch with them, 720 us without).
   const int64_t slot = sched.slot;
   if (slot >= p.max_slots) return;  // cannot happen: workspace holds 2R/split + 1 slots
   // float4 k of this lane's fragment list = two 8-byte words at 2k, 2k + 1
@@ -409,16 +406,12 @@ __global__ __launch_bounds__(256, (BM / WM / 16) * (BN / WN / 16) <= 16 ? 2 : 1)
         __builtin_amdgcn_sched_barrier(0);
       }
   }
-  vm_wait<0>();
+  splitk_published();
   __syncthreads();
-  if (tid == 0) {
-    int32_t* ctr = p.counters + (int64_t)expert * tiles + tile;
-    const int32_t prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sched.last = (prev == nch - 1);
-    if (sched.last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (tid == 0) sched.last = splitk_arrive(p.counters + (int64_t)expert * tiles + tile, nch);
   __syncthreads();
   if (!sched.last) return;
+  splitk_acquired();
   // each of the wave's blocks: 0 + chunk 0 + chunk 1 + ... in chunk order,
   // GB blocks at a time (GB loads in flight per chunk); flat block index
   // b = i * JM + j, as the partials are laid out

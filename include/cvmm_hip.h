@@ -192,10 +192,12 @@ int cvmm_sort_routes_cast_keys(const void* sel, int32_t sel_is_int64, int64_t n_
 
 /* cvmm_sort_routes_cast_keys with flags: CVMM_FLAG_COUNTS_READY skips the
  * sort's histogram launch, whose count matrix the workspace already holds
- * (cvmm_copy_ids_count of the same ids for the same n_experts, with the
- * sort-chunk tuning knob unchanged in between).  keys == NULL (or both
- * outputs NULL): the sort alone, as cvmm_sort_routes.  No counterpart in the
- * reference. */
+ * (cvmm_copy_ids_count of the same ids for the same n_experts).  The library
+ * keeps a record of each such count (workspace, ids, experts, sort chunk)
+ * and honours the flag only when the record matches this call and the
+ * sort-chunk tuning knob still gives the same chunk; the record is used up.
+ * Otherwise the sort counts again.  keys == NULL (or both outputs NULL): the
+ * sort alone, as cvmm_sort_routes.  No counterpart in the reference. */
 int cvmm_sort_routes_cast_keys_ex(const void* sel, int32_t sel_is_int64, int64_t n_routes, int32_t n_experts,
                                   int64_t top_k, int32_t* sorted_sel, int64_t* perm, int64_t* token_index,
                                   int64_t* offsets, int32_t* route_pos, int32_t* n_invalid, void* workspace,

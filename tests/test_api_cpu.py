@@ -43,11 +43,51 @@ def test_prepare_sel2_rewraps_cvmmsel():
     assert rr.sel_index is r.sel_index
 
 
-def test_cpu_tensors_are_rejected():
+@pytest.mark.parametrize("route_input", [False, True])
+@pytest.mark.parametrize("dtype", [torch.int64, torch.int32])
+def test_host_selectors_match_oracle(route_input, dtype):
+    """cvmm_prepare_sel / cvmm_prepare_sel2 accept ids in host memory, as the
+    reference's pure-torch versions do (cvmm.py:24-27, :1786-1803): the
+    fields equal the oracle's (stable order among equal ids), with many ties."""
+    import numpy as np
+    from oracle import cvmm_oracle as O
+    g = torch.Generator().manual_seed(5)
+    sel = torch.randint(0, 7, (3, 11, 4), generator=g).to(dtype)
+    w = torch.rand(3, 11, 4, generator=g)
+    got = C.cvmm_prepare_sel2(sel, w, route_input=route_input)
+    exp = O.prepare_sel2(sel.numpy(), w.numpy(), route_input=route_input)
+    assert got.raw_sel.dtype == torch.int32 and got.sel.dtype == torch.int32
+    np.testing.assert_array_equal(got.raw_sel.numpy(), exp.raw_sel)
+    np.testing.assert_array_equal(got.sel.numpy(), exp.sel)
+    np.testing.assert_array_equal(got.sel_index.numpy(), exp.sel_index)
+    if route_input:
+        assert got.out_index is None
+    else:
+        np.testing.assert_array_equal(got.out_index.numpy(), exp.out_index)
+    assert got.reduction_weight is w
+    one = C.cvmm_prepare_sel(sel, 7)
+    e1 = O.prepare_sel(sel.numpy(), 7)
+    np.testing.assert_array_equal(one.sel.numpy(), e1.sel)
+    np.testing.assert_array_equal(one.sel_index.numpy(), e1.sel_index)
+    assert one.out_index is None
+
+
+def test_host_selector_is_a_snapshot():
+    """Writing to the caller's ids after preparation changes nothing, as for a
+    device selector."""
+    sel = torch.tensor([[3, 1], [1, 0]], dtype=torch.int32)
+    s = C.cvmm_prepare_sel2(sel)
+    sel.fill_(9)
+    assert s.raw_sel.tolist() == [[3, 1], [1, 0]]
+    assert s.sel.tolist() == [[0, 1], [1, 3]]
+
+
+def test_cpu_operands_are_rejected():
+    """Only the selector metadata is made on the host: the product itself has
+    no CPU path."""
+    sel = C.cvmm_prepare_sel2(torch.zeros(3, 2, dtype=torch.int64))
     with pytest.raises(RuntimeError, match="no CPU fallback"):
-        C.cvmm_prepare_sel2(torch.zeros(3, 2, dtype=torch.int64))
-    with pytest.raises(RuntimeError, match="no CPU fallback"):
-        C.cvmm_prepare_sel(torch.zeros(3, 2, dtype=torch.int64), 4)
+        C.cvmm(torch.zeros(3, 4), sel, torch.zeros(2, 4, 5))
 
 
 def test_dtype_ids_match_reference():

@@ -125,10 +125,20 @@ def _full_check(tag, x, sel, keys, w, gy, route_input, got):
     return errs
 
 
+@pytest.mark.parametrize("dense", [0, 1], ids=["default", "route_buffer"])
 @pytest.mark.parametrize("name", ["switch_v_2048", "switch_o_2048_weighted"])
-def test_c4_full_size_every_token_and_expert(name):
+def test_c4_full_size_every_token_and_expert(name, dense):
+    """dense=0: the default path (the top-k sums as the dense expert-slot
+    GEMM); dense=1: CVMM_TUNE_DENSE_TOPK=1, the hand-written route-buffer
+    path (routed GEMM into [R, N] rows, then the ordered top-k row sum)."""
+    from cvmm_codex_amd import _native as N
+    lib = N.lib()
     p = W.PROJECTIONS[name]()
-    got = _run_projection(p)
+    try:
+        assert lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, dense) == 0
+        got = _run_projection(p)
+    finally:
+        lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 0)
     _full_check(name, p.x, p.sel, p.keys, p.weights, p.grad_out, p.route_input, got)
 
 
@@ -220,3 +230,61 @@ def test_c5_ffn_stack_full_size_sampled():
     _full_check("up", x, sel.cpu(), w_up, None, h_pre.grad, False, (h_pre, x.grad, w_up.grad, None))
     _full_check("down", hidden.view(B, Tn, k, H), sel.cpu(), w_down, weights, s.grad_out, True,
                 (y, hidden.grad, w_down.grad, weights.grad))
+
+
+def test_c5_fused_stack_full_size_every_token_and_expert():
+    """The path the C5 bench line times, workloads.ffn_forward_fused (the
+    native router cvmm_route_topk and the up projection with its GELU in the
+    GEMM epilogue, cvmm_gelu), at full size.  The router's choice is checked
+    to be a top-k of the softmax in probability order; then, with that
+    routing, the whole stack is restated in float32 on the GPU (the torch
+    path of oracle/torch_cpu_path.py, torch autograd for the gradients,
+    router included) and every output row, x and gate gradient, and every
+    expert's weight gradients must agree."""
+    dev = torch.device("cuda")
+    s = W.c5_ffn_stack().to(dev)
+    B, Tn, D = s.x.shape
+    E, _, H = s.w_up.shape
+    k, T = s.k, B * Tn
+    x = s.x.clone().requires_grad_(True)
+    gate = s.gate.clone().requires_grad_(True)
+    w_up = s.w_up.clone().requires_grad_(True)
+    w_down = s.w_down.clone().requires_grad_(True)
+    y = W.ffn_forward_fused(s, C, x, gate, w_up, w_down)
+    y.backward(s.grad_out.to(y.dtype))
+    torch.cuda.synchronize()
+
+    # the routing the fused router chose: the same launch on the same logits
+    with torch.no_grad(), torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        logits = s.x @ s.gate + s.bias
+        w_got, sel, _ = C.cvmm_route_topk(logits, k, True)
+    sel = sel.reshape(T, k)
+    probs = torch.softmax(logits.float(), dim=-1).reshape(T, E)
+    assert float((probs.gather(1, sel) - probs.topk(k, dim=-1).values).abs().max()) <= 1e-6
+    counts = torch.bincount(sel.reshape(-1), minlength=E)
+    assert counts.max() > 10 * counts.float().mean()          # Zipf-skewed loads, as configured
+
+    # float32 restatement with that routing
+    xf = s.x.float().reshape(T, D).clone().requires_grad_(True)
+    gf = s.gate.float().clone().requires_grad_(True)
+    wuf = s.w_up.float().clone().requires_grad_(True)
+    wdf = s.w_down.float().clone().requires_grad_(True)
+    pw = torch.softmax(xf @ gf + s.bias.float(), dim=-1).gather(1, sel)
+    wr = pw / pw.sum(-1, keepdim=True).clamp_min(1e-20)
+    hidden = F.gelu(P.forward(xf, P.Routes(sel, E, False), wuf, None))
+    yr = P.forward(hidden, P.Routes(sel, E, True), wdf, wr)
+    yr.backward(s.grad_out.float().reshape(T, D))
+    torch.cuda.synchronize()
+
+    _check("weights", _np(w_got).reshape(T, k), _np(wr))
+    _check("out", _np(y).reshape(T, D), _np(yr))
+    _check("x_grad", _np(x.grad).reshape(T, D), _np(xf.grad))
+    _check("gate_grad", _np(gate.grad), _np(gf.grad))
+    for name, got, exp in (("w_up.grad", w_up.grad, wuf.grad), ("w_down.grad", w_down.grad, wdf.grad)):
+        for e in range(E):
+            if counts[e] == 0:
+                assert torch.count_nonzero(got[e]) == 0, f"{name}[{e}] of an empty expert"
+                continue
+            a, b = got[e].float(), exp[e]
+            err = float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+            assert err <= TOL, f"{name}[{e}] ({int(counts[e])} routes): {err:.3e}"

@@ -345,6 +345,49 @@ def test_sort_with_counts_from_the_id_copy(R, E, k, d_in, d_out, is64):
         assert torch.equal(a[n], b[n]), n
 
 
+def test_counted_sort_ignores_counts_of_another_chunk():
+    """A count matrix made by cvmm_copy_ids_count for one sort chunk is not
+    trusted once the sort-chunk knob has changed (the sort counts again), nor
+    a second time (the sort turned it into prefixes): both flagged sorts give
+    the bits of a plain sort under the new chunk."""
+    from cvmm_codex_amd import _native as N
+    lib = N.lib()
+    R, E, k = 30000, 64, 4
+    g = torch.Generator().manual_seed(77)
+    raw = torch.randint(0, E, (R,), generator=g).to(torch.int32).cuda()
+    st = N.stream_of(raw.device)
+    ws_b = lib.cvmm_sort_workspace_bytes(R, E)
+
+    def outputs():
+        return dict(ids=torch.full((R,), -7, dtype=torch.int32, device="cuda"),
+                    ssel=torch.full((R,), -7, dtype=torch.int32, device="cuda"),
+                    perm=torch.full((R,), -7, dtype=torch.int64, device="cuda"),
+                    tok=torch.full((R,), -7, dtype=torch.int64, device="cuda"),
+                    off=torch.full((E,), -7, dtype=torch.int64, device="cuda"),
+                    pos=torch.full((R,), -7, dtype=torch.int32, device="cuda"),
+                    nin=torch.full((1,), -7, dtype=torch.int32, device="cuda"),
+                    ws=torch.full((ws_b,), 0xA5, dtype=torch.uint8, device="cuda"))
+
+    sort_args = lambda o: (N.ptr(o["ids"]), 0, R, E, k, N.ptr(o["ssel"]), N.ptr(o["perm"]), N.ptr(o["tok"]),
+                           N.ptr(o["off"]), N.ptr(o["pos"]), N.ptr(o["nin"]), N.ptr(o["ws"]), ws_b)
+    a, b = outputs(), outputs()
+    try:
+        N.check(lib.cvmm_copy_ids_count(N.ptr(raw), 0, R, E, N.ptr(b["ids"]), N.ptr(b["ws"]), ws_b, st), "count")
+        # default chunk here: 1024 routes; larger chunks need less workspace,
+        # so the stale counts would pass the size check
+        assert lib.cvmm_tuning_set(N.TUNE_SORT_CHUNK, 2048) == 0
+        N.check(lib.cvmm_copy_ids(N.ptr(raw), 0, R, N.ptr(a["ids"]), st), "copy")
+        N.check(lib.cvmm_sort_routes(*sort_args(a), st), "plain sort")
+        for _ in range(2):
+            N.check(lib.cvmm_sort_routes_cast_keys_ex(*sort_args(b), None, 0, 0, 0, 0, 0, 0, 0, None, None, 0,
+                                                      N.FLAG_COUNTS_READY, st), "flagged sort")
+            torch.cuda.synchronize()
+            for n in ("ids", "ssel", "perm", "tok", "off", "pos", "nin"):
+                assert torch.equal(a[n], b[n]), n
+    finally:
+        lib.cvmm_tuning_set(N.TUNE_SORT_CHUNK, 0)
+
+
 def test_prepared_selection_sorts_with_the_expected_expert_count():
     """cvmm_prepare_sel2 counts the ids for the expert count the last sort of
     a same-sized selection used, and cvmm() sorts without the histogram launch
