@@ -53,6 +53,7 @@ class Runner:
         self.keys = self.p.keys.detach().requires_grad_(True)
         self.w = None if self.p.weights is None else self.p.weights.detach().requires_grad_(True)
         self.E = self.keys.shape[0]
+        self.n_steps = 0    # steps run by this process (profile summaries divide trace counts by it)
 
     def prepare(self):
         # the public call pattern (benchmark_ffn_moe.py:95-98): the selection
@@ -78,6 +79,7 @@ class Runner:
         s = self.prepare()
         y = self.forward(s)
         self.backward(y)
+        self.n_steps += 1
 
 
 def time_steps(runner: Runner, steps: int, warmup: int):
@@ -92,11 +94,13 @@ def time_steps(runner: Runner, steps: int, warmup: int):
 
 
 def time_phases(runner: Runner, iters: int):
-    """HIP events between the phases of a step (current stream).  "sel" is the
-    selector bookkeeping; the sort itself runs in "fwd" (inside cvmm())."""
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-    acc = np.zeros(3)
-    for _ in range(iters):
+    """GPU time of the phases of a step, from HIP events on torch's stream
+    between them: selector preparation, forward (which runs the selector's
+    sort), backward.  The iterations run back to back with no synchronisation
+    (the host stays ahead of the GPU), so the events time the GPU's work, not
+    host submission; call it after warm-up steps."""
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(iters)]
+    for ev in evs:
         runner.zero()
         ev[0].record()
         s = runner.prepare()
@@ -105,9 +109,23 @@ def time_phases(runner: Runner, iters: int):
         ev[2].record()
         runner.backward(y)
         ev[3].record()
-        torch.cuda.synchronize()
+        runner.n_steps += 1
+    torch.cuda.synchronize()
+    acc = np.zeros(3)
+    for ev in evs:
         acc += [ev[i].elapsed_time(ev[i + 1]) for i in range(3)]
-    return dict(zip(("sel", "fwd", "bwd"), (acc / iters).tolist()))
+    return dict(zip(("prepare", "fwd", "bwd"), (acc / iters).tolist()))
+
+
+def breakdown(phases, kt):
+    """The step's GPU time split as the reference's benchmark reports it
+    (benchmark_moe_shapes.py:100-124: sel, forward, backward): "sel" is the
+    device time of the selector launches (the id copy and the stable sort;
+    the sort runs inside cvmm(), in the same launches as the step's weight
+    cast when the shapes allow), "fwd" the rest of the forward, "bwd" the
+    backward.  Sums to the phases' GPU time."""
+    sel = kt["sort"]["ms_per_step"] if "sort" in kt else 0.0
+    return {"sel": sel, "fwd": phases["prepare"] + phases["fwd"] - sel, "bwd": phases["bwd"]}
 
 
 def kernel_launchers(runner: Runner):
@@ -319,6 +337,20 @@ def load_traffic(kernel: str, workload: str):
     return None
 
 
+def fabric_of(workload: str, ms: float):
+    """The fabric side of a step: FETCH_SIZE + WRITE_SIZE bytes of every
+    kernel of a step (profiles/traffic_step_<workload>.json, from a profile.sh
+    run) over the measured step time, as a fraction of 8 TB/s -- beside the
+    route-byte model's fraction, which counts gathers that L2 and MALL serve."""
+    path = os.path.join(ROOT, "profiles", f"traffic_step_{workload}.json")
+    if not os.path.exists(path):
+        return {"fabric_frac": None}
+    with open(path) as f:
+        b = json.load(f)["fabric_bytes_per_step"]
+    return {"fabric_bytes_per_step": b, "fabric_gbs": round(b / (ms * 1e-3) / 1e9, 1),
+            "fabric_frac": round(b / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)}
+
+
 def router_times(iters: int = 50, T: int = 16384, E: int = 128, k: int = 8):
     """The router of the FFN stack ([16384, 128]
     bf16 logits, top-8, renormalised) two ways: the reference callers' torch
@@ -377,21 +409,26 @@ class _Shape:
         return self.sel.numel()
 
 
-def ffn_line(steps: int = 10, warmup: int = 3, kernel_iters: int = 10):
+def ffn_line(steps: int = 10, warmup: int = 3, kernel_iters: int = 10, variant: str = "both"):
     """The FFN stack of BASELINE.json configs[4] (16384 tokens, 2048 -> 512 ->
     2048, 128 experts, top-8, Zipf-skewed gate; benchmark_ffn_moe.py:89-98),
     forward + backward, as one bench line: the library's fused router and up
     projection + GELU (``value``), beside the stack written as the
-    reference's callers write it (torch router lines, F.gelu around cvmm)."""
+    reference's callers write it (torch router lines, F.gelu around cvmm).
+    variant "fused" runs the fused stack only (profile runs: one stack per
+    trace)."""
     s = W.c5_ffn_stack().to(torch.device("cuda"))
     params = [t.clone().requires_grad_(True) for t in (s.x, s.gate, s.w_up, s.w_down)]
     import cvmm_codex_amd as C
+
+    n_steps = [0]
 
     def step(fwd):
         for t in params:
             t.grad = None
         out = fwd(s, C, *params)
         out.backward(s.grad_out)
+        n_steps[0] += 1
 
     def timed(fwd, n):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -402,8 +439,9 @@ def ffn_line(steps: int = 10, warmup: int = 3, kernel_iters: int = 10):
         b.synchronize()
         return a.elapsed_time(b) / n
 
-    res = {}
-    for name, fwd in (("composed", W.ffn_forward), ("fused", W.ffn_forward_fused)):
+    res = {"composed": None}
+    stacks = (("composed", W.ffn_forward), ("fused", W.ffn_forward_fused))
+    for name, fwd in stacks if variant == "both" else stacks[1:]:
         for _ in range(warmup):
             step(fwd)
         torch.cuda.synchronize()
@@ -415,6 +453,7 @@ def ffn_line(steps: int = 10, warmup: int = 3, kernel_iters: int = 10):
             step(W.ffn_forward_fused)
 
     kt = kernel_times(_Runner(), kernel_iters)
+    log(f"steps run: {n_steps[0]}")
     T, D = s.x.shape[0] * s.x.shape[1], s.x.shape[2]
     E, _, H = s.w_up.shape
     R = T * s.k
@@ -438,7 +477,7 @@ def ffn_line(steps: int = 10, warmup: int = 3, kernel_iters: int = 10):
         "config": {"workload": "ffn_stack", "tokens": T, "d_model": D, "hidden": H, "n_experts": E,
                    "top_k": s.k, "gate": "softmax top-8, Zipf(1.1) bias", "step": "router+up+gelu+down fwd+bwd",
                    "gflop_per_step": round(s.flops / 1e9, 3), "gate_gflop": round(gate_flops / 1e9, 3)},
-        "composed_ms_per_step": round(res["composed"], 5),
+        "composed_ms_per_step": None if res["composed"] is None else round(res["composed"], 5),
         "step_roofline": step_roof,
         "kernel_ms_per_launch": {k: round(v["avg_ms"], 5) for k, v in kt.items()},
         "kernel_launches_per_step": {k: v["launches_per_step"] for k, v in kt.items()},
@@ -508,18 +547,25 @@ def kernel_role(name: str):
 
 def kernel_class(name: str):
     """kernel_role for the routed GEMMs and the weight gradient; the other
-    kernels of a step by name: the dense top-k GEMM (rocBLAS), its slot
-    writes, the combine, the sort and the weight cast."""
+    kernels of a step by name: the dense top-k GEMM, its preparation (slot
+    table, weighted row scaling, operand copy), the combine, the sort, the
+    weight cast; torch's own kernels (the gate GEMMs of the FFN stack, its
+    elementwise ops) are "torch"."""
     role = kernel_role(name)
     if role is not None:
         return role
     base = name.split("<")[0].split("(")[0].split()[-1] if name else ""
-    if "Cijk_" in base or "rocblas" in base:
-        return "dense_topk"
-    for key, cls in (("slot_rows", "slots"), ("combine_rows", "combine"), ("sort_", "sort"), ("cast_keys", "cast"),
-                     ("copy_ids", "sort"), ("sum_partials", "dgate"), ("fill_zero", "fill"), ("gelu", "gelu")):
-        if key in base:
-            return cls
+    if base.startswith("cvmm::"):
+        for key, cls in (("topk_gemm", "dense_topk"), ("topk_slot_table", "dense_prep"),
+                         ("scale_rows", "dense_prep"), ("copy_rows_op", "dense_prep"),
+                         ("combine_rows", "combine"), ("sort_", "sort"), ("cast_keys", "cast"),
+                         ("copy_ids", "sort"), ("sum_partials", "dgate"), ("fill_zero", "fill"), ("gelu", "gelu"),
+                         ("route", "router")):
+            if key in base:
+                return cls
+        return "cvmm"
+    if name:
+        return "torch"
     return None
 
 
@@ -562,6 +608,45 @@ def _copy_factors(copy_dir):
     return f
 
 
+def step_fabric(dirpath: str, copy_dir: str):
+    """FETCH_SIZE + WRITE_SIZE bytes of one step on the fabric side: every
+    traced kernel's bytes per dispatch (counter runs, copy-calibrated) times
+    its dispatches in the kernel-trace run, over the steps that run made
+    (its "steps run: N" log line).  Kernels without counters are left out;
+    `covered` is the share of traced kernel time that has them."""
+    import glob
+    import re
+    stats = glob.glob(os.path.join(dirpath, "trace", "**", "*kernel_stats.csv"), recursive=True)
+    log_path = os.path.join(dirpath, "trace.log")
+    if not stats or not os.path.exists(log_path) or not copy_dir:
+        return None
+    runs = re.findall(r"steps run: (\d+)", open(log_path).read())
+    if not runs:
+        return None
+    n = int(runs[-1])
+    cnt = {}
+    for pas in ("fetch", "write"):
+        for k, d in _counters(os.path.join(dirpath, pas)).items():
+            cnt.setdefault(k, {}).update(d)
+    fac = _copy_factors(copy_dir)
+    rows = _read_csv(stats[0])
+    names = _demangle([r["Name"] for r in rows])
+    total_b = covered_t = all_t = 0.0
+    for r, name in zip(rows, names):
+        t = float(r["TotalDurationNs"])
+        all_t += t
+        d = cnt.get(name)
+        if not d or not d.get("FETCH_SIZE") or not d.get("WRITE_SIZE"):
+            continue
+        per = (sum(d["FETCH_SIZE"]) / len(d["FETCH_SIZE"]) * fac["FETCH_SIZE"] +
+               sum(d["WRITE_SIZE"]) / len(d["WRITE_SIZE"]) * fac["WRITE_SIZE"]) * 1024
+        total_b += per * int(r["Calls"])
+        covered_t += t
+    return {"kernel": "step", "workload": os.path.basename(os.path.normpath(dirpath)), "steps_traced": n,
+            "fabric_bytes_per_step": int(total_b / n), "covered": round(covered_t / all_t, 4) if all_t else None,
+            "copy_factor_fetch": fac["FETCH_SIZE"], "copy_factor_write": fac["WRITE_SIZE"]}
+
+
 def summarize(dirpath: str, copy_dir=None) -> str:
     import glob
     W_name = os.path.basename(os.path.normpath(dirpath))
@@ -586,7 +671,19 @@ def summarize(dirpath: str, copy_dir=None) -> str:
                   f"{rf['achieved']} {rf['unit']} = frac {rf['frac']:.4f} of {rf['peak']} ({rf['bound']}); "
                   f"MFMA frac {rf['mfma_frac']:.4f}, HBM frac {rf['hbm_frac']:.4f}",
                   f"- kernel us per launch: " + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in
-                                                          bench["kernel_ms_per_launch"].items()), ""]
+                                                          bench["kernel_ms_per_launch"].items())]
+        if "breakdown_ms" in bench:
+            lines.append("- step breakdown (GPU time): " + ", ".join(
+                f"{k} {v * 1e3:.1f} us" for k, v in bench["breakdown_ms"].items()) +
+                f" (sum {sum(bench['breakdown_ms'].values()) * 1e3:.1f} us)")
+        fab = step_fabric(dirpath, copy_dir)
+        if fab:
+            gbs = fab["fabric_bytes_per_step"] / (bench["ms_per_step"] * 1e-3) / 1e9
+            lines.append(f"- fabric side: FETCH + WRITE {fab['fabric_bytes_per_step'] / 1e6:.1f} MB per step "
+                         f"({fab['steps_traced']} traced steps, {fab['covered'] * 100:.1f} % of kernel time "
+                         f"counted) = {gbs:.0f} GB/s = frac {gbs / HBM_PEAK_GBS:.4f} of 8 TB/s, beside the "
+                         f"route-byte model's {sr['hbm_frac']:.4f}")
+        lines.append("")
     stats = glob.glob(os.path.join(dirpath, "trace", "**", "*kernel_stats.csv"), recursive=True)
     avg_us = {}
     if stats:
@@ -653,10 +750,16 @@ def summarize(dirpath: str, copy_dir=None) -> str:
 
 
 def traffic_json(dirpath: str, copy_dir: str, cls: str):
+    if cls == "step":
+        return step_fabric(dirpath, copy_dir)
+    return _traffic_json(dirpath, copy_dir, cls)
+
+
+def _traffic_json(dirpath: str, copy_dir: str, cls: str):
     """FETCH_SIZE + WRITE_SIZE bytes per launch of the class's kernel (the
     `traffic` field of bench.py's roofline), from a profile.sh run.  A GEMM
-    class that ran as the dense top-k path counts the dense GEMM plus its two
-    slot passes (write, clear)."""
+    class that ran as the dense top-k path counts the dense GEMM plus its
+    preparation launches (slot table, and the row scaling when weighted)."""
     cnt = {}
     for pas in ("fetch", "write"):
         for k, d in _counters(os.path.join(dirpath, pas)).items():
@@ -676,14 +779,13 @@ def traffic_json(dirpath: str, copy_dir: str, cls: str):
             return {**base, "kernel_name": k, "bytes_per_launch": int(f + w), "fetch_bytes": int(f),
                     "write_bytes": int(w)}
     if cls in ("gemm_fwd", "gemm_bwd_x"):
-        dense = [(k, d) for k, d in cnt.items() if kernel_class(k) in ("dense_topk", "slots")
+        dense = [(k, d) for k, d in cnt.items() if kernel_class(k) in ("dense_topk", "dense_prep")
                  and "FETCH_SIZE" in d and "WRITE_SIZE" in d]
         if any(kernel_class(k) == "dense_topk" for k, _ in dense):
             f = w = 0.0
             for k, d in dense:
-                n = 2 if kernel_class(k) == "slots" else 1
                 df, dw = per_launch(d)
-                f, w = f + n * df, w + n * dw
+                f, w = f + df, w + dw
             return {**base, "kernel_name": "dense top-k: " + ", ".join(k for k, _ in dense),
                     "bytes_per_launch": int(f + w), "fetch_bytes": int(f), "write_bytes": int(w)}
     return None
@@ -703,6 +805,8 @@ def main():
     ap.add_argument("--ffn", action="store_true",
                     help="time the FFN stack (configs[4]) with the fused router and GELU, beside the composed "
                          "stack (one JSON line) and exit")
+    ap.add_argument("--ffn-variant", choices=["both", "fused"], default="both",
+                    help="with --ffn: time the composed stack too (both) or the fused one only")
     ap.add_argument("--router", action="store_true",
                     help="time the fused router against the torch router lines (one JSON line) and exit")
     ap.add_argument("--summarize", metavar="DIR", default=None,
@@ -710,7 +814,8 @@ def main():
     ap.add_argument("--copy-dir", metavar="DIR", default=None,
                     help="with --summarize: the profile.sh copy-calibration directory")
     ap.add_argument("--traffic", metavar="CLASS", default=None,
-                    help="with --summarize: print the traffic JSON of this kernel class (gemm_fwd, gemm_bwd_x, wgrad)")
+                    help="with --summarize: print the traffic JSON of this kernel class (gemm_fwd, gemm_bwd_x, "
+                         "wgrad), or of the whole step (step)")
     ap.add_argument("--tune", action="append", default=[], metavar="KNOB=VALUE",
                     help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, wgrad_tile, gemm_order, "
                          "dense_topk, sort_chunk, ring_tile) before running")
@@ -750,7 +855,7 @@ def main():
     import cvmm_codex_amd.api as C
     C.cvmm_log_shapes = False   # stdout carries the one JSON line
     if args.ffn:
-        print(json.dumps(ffn_line(args.steps, args.warmup, args.kernel_iters)), flush=True)
+        print(json.dumps(ffn_line(args.steps, args.warmup, args.kernel_iters, args.ffn_variant)), flush=True)
         return
     if args.only == "copy":
         copy_calibration(iters=args.steps)
@@ -771,10 +876,12 @@ def main():
 
     log(f"workload {proj.name}: R={proj.routes} d_in={proj.keys.shape[1]} d_out={proj.keys.shape[2]} "
         f"E={proj.keys.shape[0]}")
-    # the per-phase and per-kernel passes first: a fresh process runs its
-    # first ~100 steps up to 8 % slower on the GPU (per-step GPU time falls
-    # from ~160 to ~149 us at ff_up; host submission stays ~90 us ahead), so
-    # the timed steps come after them and the W warm-up steps
+    # W warm-up steps, then the per-phase and per-kernel passes, then the
+    # timed steps (after W more): a fresh process runs its first ~100 steps
+    # up to 8 % slower on the GPU (per-step GPU time falls from ~160 to ~149
+    # us at ff_up; host submission stays ~90 us ahead)
+    for _ in range(args.warmup):
+        runner.step()
     phases = time_phases(runner, max(10, args.steps // 2))
     log(f"phases {phases}")
     kt = kernel_times(runner, args.kernel_iters)
@@ -790,6 +897,8 @@ def main():
     roofline.update({"kernel": dom, "avg_launch_ms": round(kt[dom]["avg_ms"], 5)})
     sflops, sbytes = step_work(proj)
     step_roof = roofline_of(bound, dtype, sflops, sbytes, ms * 1e-3)
+    step_roof.update(fabric_of(proj.name, ms))
+    log(f"steps run: {runner.n_steps}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -807,8 +916,9 @@ def main():
                    "top_k": proj.sel.shape[-1], "weighted": proj.weights is not None,
                    "step": "sel+fwd+bwd", "gflop_per_step": round(proj.flops / 1e9, 3)},
         "step_roofline": step_roof,
-        "breakdown_ms": {k: round(v, 5) for k, v in phases.items()},
+        "breakdown_ms": {k: round(v, 5) for k, v in breakdown(phases, kt).items()},
         "kernel_ms_per_launch": {k: round(v["avg_ms"], 5) for k, v in kt.items()},
+        "kernel_ms_per_step": {k: round(v["ms_per_step"], 5) for k, v in kt.items()},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

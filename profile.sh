@@ -15,6 +15,8 @@
 # usage:  bash profile.sh WORKLOAD [OUTDIR]
 #   WORKLOAD: a bench.py --workload name, `ffn` (the FFN stack) or `copy`
 #   then:   python bench.py --summarize OUTDIR/WORKLOAD [--copy-dir OUTDIR/copy]
+#           python bench.py --summarize OUTDIR/WORKLOAD --copy-dir OUTDIR/copy --traffic CLASS
+#             (CLASS: gemm_fwd, gemm_bwd_x, wgrad, or step for the whole step's fabric bytes)
 set -o pipefail
 W=${1:?usage: profile.sh WORKLOAD [OUTDIR]}
 ROOT=$(cd "$(dirname "$0")" && pwd)
@@ -33,9 +35,11 @@ if [ "$W" = copy ]; then
   exit 0
 fi
 
-if [ "$W" = ffn ]; then ARGS="--ffn"; else ARGS="--workload $W"; fi
+# ffn: the bench line times the fused and the composed stack; the trace and
+# the counter runs take the fused stack (the bench line's value) alone
+if [ "$W" = ffn ]; then ARGS="--ffn --ffn-variant fused"; LINE="--ffn"; else ARGS="--workload $W"; LINE=$ARGS; fi
 step "bench line"
-timeout -k 10 300 python3 bench.py $ARGS --no-cpu-baseline > "$OUT/bench.json" 2> "$OUT/bench.err" || exit $?
+timeout -k 10 300 python3 bench.py $LINE --no-cpu-baseline > "$OUT/bench.json" 2> "$OUT/bench.err" || exit $?
 step "kernel trace"
 timeout -k 10 300 rocprofv3 --kernel-trace --stats --output-format csv -d "$OUT/trace" -o run -- \
   python3 bench.py $ARGS --no-cpu-baseline --steps 20 --kernel-iters 10 > "$OUT/trace.log" 2>&1 || exit $?
