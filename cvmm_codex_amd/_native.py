@@ -97,6 +97,7 @@ _SIGS = {
         _I32, _P, _SZ, _P]),
     "cvmm_bwd_w_counter_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I32]),
     "cvmm_bwd_w_workspace_bytes": (_SZ, [_I64, _I32, _I64, _I64, _I32, _I32]),
+    "cvmm_bwd_w_workspace_bytes_ex": (_SZ, [_I64, _I32, _I64, _I64, _I32, _I32, _I32]),
     "cvmm_bwd_w": (ctypes.c_int, [
         _P, _I32, _I64, _I64,                 # x
         _P, _I32, _I64, _I64,                 # grad

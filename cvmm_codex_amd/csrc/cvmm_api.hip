@@ -1117,6 +1117,16 @@ size_t cvmm_bwd_w_counter_bytes(int64_t n_routes, int32_t n_experts, int64_t d_i
   return c.used;
 }
 
+}  // extern "C"
+
+// The weight gradient of a weighted route-input selection scales the route
+// rows beforehand (16-bit op, rows of whole 16-byte pieces).
+static bool wgrad_scales_rows(int32_t op_dtype, int64_t d_in) {
+  return (op_dtype == kBF16 || op_dtype == kF16) && d_in % 8 == 0;
+}
+
+extern "C" {
+
 size_t cvmm_bwd_w_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out,
                                   int32_t op_dtype, int32_t has_offsets) {
   int64_t split, grid_chunks, max_slots, tiles;
@@ -1126,6 +1136,14 @@ size_t cvmm_bwd_w_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d
   if (!has_offsets) c.take((size_t)n_experts * 8);
   c.take((size_t)max_slots * wgrad_partial_elems(d_in, d_out) * 4);
   return c.used;
+}
+
+size_t cvmm_bwd_w_workspace_bytes_ex(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out,
+                                     int32_t op_dtype, int32_t has_offsets, int32_t weighted_route_input) {
+  size_t need = cvmm_bwd_w_workspace_bytes(n_routes, n_experts, d_in, d_out, op_dtype, has_offsets);
+  if (weighted_route_input && wgrad_scales_rows(op_dtype, d_in))
+    need = align_up(need, 256) + (size_t)n_routes * d_in * dtype_size(op_dtype);
+  return need;
 }
 
 int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const void* grad, int32_t grad_dtype,
@@ -1177,6 +1195,26 @@ int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, con
   p.partial = (float*)c.take((size_t)p.max_slots * wgrad_partial_elems(d_in, d_out) * 4);
 
   const int64_t* rp = out_index ? out_index : sel_index;
+  // A weighted selection with route input (x row = route) whose workspace
+  // holds the rows: x scaled by its routes' weights once, rnd_op(rnd_op(w_r)
+  // * rnd_op(x_r)), then the unweighted kernel with the token's gradient row
+  // (the weight moves from the d_out-wide gradient slices of every dW tile to
+  // one pass over the d_in-wide route rows).
+  const size_t rows_bytes = (size_t)x_rows * d_in * dtype_size(op_dtype);
+  const bool scale_rows = weighted && out_index == nullptr && x_rows <= n_routes && n_routes > 0 &&
+                          wgrad_scales_rows(op_dtype, d_in) && align_up(c.used, 256) + rows_bytes <= workspace_bytes;
+  if (scale_rows) {
+    void* xs = c.take(rows_bytes);
+    int r = check_launch(timed(CVMM_KC_WGRAD, s, [&] {
+      return launch_scale_rows(x, x_dtype, x_ld, true, rw, rw_dtype, op_dtype, x_rows, top_k, d_in, op_dtype, xs,
+                               s);
+    }), "cvmm_bwd_w(scale)");
+    if (r) return r;
+    x = xs;
+    x_dtype = op_dtype;
+    x_ld = d_in;
+    rw = nullptr;
+  }
   p.x = x; p.x_dtype = x_dtype; p.x_ld = x_ld; p.x_rows = x_rows;
   p.x_vec = aligned16(x) && (x_ld * (int64_t)dtype_size(x_dtype)) % 16 == 0;
   p.x_idx = sel_index;

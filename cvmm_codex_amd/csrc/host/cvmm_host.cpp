@@ -449,7 +449,9 @@ std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const
   if (need_grad_keys) {
     Tensor xs = rows_of(fast && x.scalar_type() != op ? x.to(op) : storage_for(x, op), d_in);
     grad_w = at::empty(keys.sizes(), opts(keys, keys.scalar_type()));
-    const size_t ws_bytes = cvmm_bwd_w_workspace_bytes(R, (int32_t)E, d_in, d_out, od, 1);
+    // a weighted route-input selection gets room for its scaled route rows
+    const size_t ws_bytes =
+        cvmm_bwd_w_workspace_bytes_ex(R, (int32_t)E, d_in, d_out, od, 1, rw.has_value() && !oi.has_value() ? 1 : 0);
     const size_t ctr_bytes = cvmm_bwd_w_counter_bytes(R, (int32_t)E, d_in, d_out, od);
     Tensor ws;
     bool zeroed;

@@ -379,6 +379,17 @@ size_t cvmm_bwd_w_counter_bytes(int64_t n_routes, int32_t n_experts, int64_t d_i
                                 int32_t op_dtype);
 size_t cvmm_bwd_w_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out,
                                   int32_t op_dtype, int32_t has_offsets);
+/* The workspace of a weighted selection with route input (x row = route,
+ * out_index NULL) given room for its scaled rows: with at least this many
+ * bytes, cvmm_bwd_w scales each route row once, x'_r = rnd_op(rnd_op(w_r) *
+ * rnd_op(x_r)) (16-bit op, d_in % 8 == 0), and runs the unweighted product
+ * sum_i x'_i^T rnd_op(grad[rp(i)/top_k]) -- the weight applied to the route
+ * row instead of the gradient row (the rounding point moves; the product is
+ * the same).  With cvmm_bwd_w_workspace_bytes' size the weight is applied to
+ * the gradient rows inside the kernel.  weighted_route_input = 0: the same as
+ * cvmm_bwd_w_workspace_bytes.  No counterpart in the reference. */
+size_t cvmm_bwd_w_workspace_bytes_ex(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out,
+                                     int32_t op_dtype, int32_t has_offsets, int32_t weighted_route_input);
 int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld,
                const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t grad_ld,
                int32_t n_experts, int64_t d_in, int64_t d_out,

@@ -64,6 +64,12 @@ def test_workspace_queries(lib):
         lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 0)
     # weight grad: counters + bounded partial slots
     assert lib.cvmm_bwd_w_workspace_bytes(65536, 64, 1024, 128, N.BF16, 1) > 64 * 8 * 4
+    # room for the scaled route rows of a weighted route-input selection
+    base = lib.cvmm_bwd_w_workspace_bytes(65536, 64, 128, 1024, N.BF16, 1)
+    assert lib.cvmm_bwd_w_workspace_bytes_ex(65536, 64, 128, 1024, N.BF16, 1, 0) == base
+    assert lib.cvmm_bwd_w_workspace_bytes_ex(65536, 64, 128, 1024, N.BF16, 1, 1) >= base + 65536 * 128 * 2
+    assert lib.cvmm_bwd_w_workspace_bytes_ex(65536, 64, 128, 1024, N.F32, 1, 1) == \
+        lib.cvmm_bwd_w_workspace_bytes(65536, 64, 128, 1024, N.F32, 1)
 
 
 def test_invalid_arguments_fail_before_launch(lib):
