@@ -19,6 +19,7 @@ F32, F16, BF16 = 0, 1, 2            # cvmm.py:36-44 dtype ids
 FLAG_ATOMIC_REDUCE = 1
 FLAG_COUNTERS_ZEROED = 2
 FLAG_COUNTS_READY = 16
+FLAG_ACCUMULATE = 32
 CAST_T_INTERLEAVED = 1
 CAST_N_INTERLEAVED = 2
 TUNE_PANEL_TILES_PER_WG = 1

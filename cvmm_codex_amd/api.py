@@ -60,8 +60,12 @@ def _env_on(name: str, default: str = "0") -> bool:
 # test compares against, test_cvmm_correctness.py:73-86).
 cvmm_expert_offsets_call = None
 cvmm_use_triton_expert_offsets = not _env_on("CVMM_DISABLE_TRITON_EXPERT_OFFSETS")
-# Accepted for compatibility; the HIP backward never materialises more than one
-# route-ordered [R, d_in] buffer, so top-k chunking is not needed.
+# Top-k columns per slice of the low-memory grad-input (cvmm.py:62, :80-84,
+# :1228-1338): a token-input unweighted top-k sum that goes through the
+# [R, d_in] route buffer runs over slices of this many top-k columns, each
+# with a buffer of T * chunk rows, summed in fp32 and rounded once (the bits
+# of the one-call sum).  0 (the default): all at once, falling back to slices
+# when that workspace does not fit in memory.  Read when cvmm() is called.
 cvmm_lowmem_chunk_size = int(os.environ.get("CVMM_LOWMEM_CHUNK_SIZE", "0"))
 # Sum the top-k terms (weighted forward combine, token-input grad_x) with fp32
 # atomics into token rows instead of a route-ordered buffer + ordered row sum.
@@ -576,7 +580,11 @@ def _fast_path(op: torch.dtype, d_in: int, d_out: int) -> bool:
 
 
 def _flags() -> int:
-    return N.FLAG_ATOMIC_REDUCE if cvmm_atomic_reduce else 0
+    """ABI flags in the low 32 bits; bits 32..47: the low-memory slice width."""
+    f = N.FLAG_ATOMIC_REDUCE if cvmm_atomic_reduce else 0
+    if cvmm_lowmem_chunk_size > 0:
+        f |= min(int(cvmm_lowmem_chunk_size), 0xffff) << 32
+    return f
 
 
 def _cast_keys(keys: torch.Tensor, op: torch.dtype, plan: _CopyPlan):

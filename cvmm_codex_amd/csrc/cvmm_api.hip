@@ -928,12 +928,13 @@ size_t cvmm_bwd_x_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d
                                   int64_t top_k, int32_t grad_x_dtype, int32_t op_dtype, int32_t need_grad_rw,
                                   int32_t flags) {
   Carver c(nullptr);
-  const bool dense = reduce_needed(weighted, token_input, top_k) && !weighted &&
-                     !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
+  const bool reduce = reduce_needed(weighted, token_input, top_k) ||
+                      ((flags & CVMM_FLAG_ACCUMULATE) && token_input && !weighted);
+  const bool dense = reduce && !weighted && !(flags & (CVMM_FLAG_ATOMIC_REDUCE | CVMM_FLAG_ACCUMULATE)) &&
                      use_dense_topk(op_dtype, grad_x_rows, n_experts, d_out, d_in, top_k);
   if (dense) carve_dense(c, grad_x_rows, n_experts, d_out, d_in, n_routes, op_dtype);
   if (!has_offsets) c.take((size_t)n_experts * 8);
-  if (reduce_needed(weighted, token_input, top_k) && !dense) {
+  if (reduce && !dense) {
     if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
       c.take((size_t)grad_x_rows * d_in * 4);
     } else {
@@ -965,7 +966,16 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
   if (grad_rw && !weighted) return fail(CVMM_ERR_INVALID, "cvmm_bwd_x: grad_rw needs reduction_weight");
   if (grad_rw && (!x || x_ld < d_in)) return fail(CVMM_ERR_INVALID, "cvmm_bwd_x: grad_rw needs x");
   if (weighted && n_routes % top_k != 0) return fail(CVMM_ERR_INVALID, "cvmm_bwd_x: R not a multiple of top_k");
-  const bool reduce = reduce_needed(weighted, token_input, top_k);
+  // CVMM_FLAG_ACCUMULATE: grad_x is an fp32 running sum; the route rows are
+  // rounded to x_dtype, the dtype the final gradient will be stored in (a
+  // slice of one top-k column still adds its rows to the sum)
+  const bool accumulate = (flags & CVMM_FLAG_ACCUMULATE) != 0;
+  const bool reduce = reduce_needed(weighted, token_input, top_k) || (accumulate && token_input && !weighted);
+  if (accumulate && !(reduce && !weighted && grad_x && grad_x_dtype == kF32 && !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
+                      (x_dtype == kBF16 || x_dtype == kF16) && d_in % 8 == 0 && top_k <= 64))
+    return fail(CVMM_ERR_UNSUPPORTED,
+                "cvmm_bwd_x: CVMM_FLAG_ACCUMULATE takes a token-input unweighted top-k sum (top_k <= 64, d_in %% 8 "
+                "== 0) into fp32 grad_x, with x_dtype bf16 or f16 the dtype of its rows");
   if (grad_x) {
     const int64_t want = reduce ? n_routes / top_k : n_routes;
     if (grad_x_rows != want)
@@ -973,8 +983,8 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
                   (long long)want);
   }
   const size_t need = cvmm_bwd_x_workspace_bytes(n_routes, n_experts, d_in, d_out, grad_x_rows, offsets != nullptr,
-                                                 weighted, token_input, top_k, grad_x_dtype, op_dtype,
-                                                 grad_rw != nullptr, flags);
+                                                 weighted, token_input, top_k, accumulate ? x_dtype : grad_x_dtype,
+                                                 op_dtype, grad_rw != nullptr, flags);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(CVMM_ERR_WORKSPACE, "cvmm_bwd_x: workspace too small (%zu < %zu)", workspace_bytes, need);
   if (n_routes == 0 || (!grad_x && !grad_rw)) return CVMM_OK;
@@ -986,7 +996,7 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
 
   hipStream_t s = (hipStream_t)stream;
   Carver c(workspace);
-  const bool dense = reduce && !weighted && !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
+  const bool dense = reduce && !weighted && !(flags & (CVMM_FLAG_ATOMIC_REDUCE | CVMM_FLAG_ACCUMULATE)) &&
                      use_dense_topk(op_dtype, grad_x_rows, n_experts, d_out, d_in, top_k);
   DenseWs dws{};
   if (dense) dws = carve_dense(c, grad_x_rows, n_experts, d_out, d_in, n_routes, op_dtype);
@@ -1050,7 +1060,7 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
       else p.val_dtype = grad_x_dtype;
     } else {
       // row q = sorted route q; the combine gathers each token's routes
-      const int32_t bdt = weighted ? op_dtype : grad_x_dtype;
+      const int32_t bdt = weighted ? op_dtype : accumulate ? x_dtype : grad_x_dtype;
       route_buf = c.take((size_t)n_routes * d_in * dtype_size(bdt));
       int32_t* inv_ws = (int32_t*)c.take((size_t)n_routes * 4);
       inv = route_pos;
@@ -1091,10 +1101,10 @@ int cvmm_bwd_x(const void* grad, int32_t grad_dtype, int64_t grad_rows, int64_t 
                                         grad_x_dtype, grad_x_ld, s); }),
                        "cvmm_bwd_x(cast)");
     } else {
-      const int32_t bdt = weighted ? op_dtype : grad_x_dtype;
+      const int32_t bdt = weighted ? op_dtype : accumulate ? x_dtype : grad_x_dtype;
       r = check_launch(timed_combine(s, [&] { return launch_combine_rows(route_buf, bdt, d_in, inv, rp, offs + (n_experts - 1), weighted ? rw : nullptr, rw_dtype, op_dtype,
                                            grad_x_rows, top_k, d_in, weighted ? op_dtype : -1, grad_x, grad_x_dtype,
-                                           grad_x_ld, s); }),
+                                           grad_x_ld, s, accumulate); }),
                        "cvmm_bwd_x(combine)");
     }
     if (r) return r;

@@ -271,7 +271,7 @@ hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_l
                                const int64_t* rp, const int64_t* rows_end, const void* w, int32_t w_dtype,
                                int32_t w_round, int64_t n_tokens,
                                int64_t k, int64_t n, int32_t mid_dtype, void* out, int32_t out_dtype, int64_t out_ld,
-                               hipStream_t stream);
+                               hipStream_t stream, bool accumulate = false);
 hipError_t launch_invert_rows(const int64_t* rp, int64_t n_routes, int32_t* inv, hipStream_t stream);
 // out[t][n] = rnd(rnd(acc[t][n], mid_dtype), out_dtype)
 hipError_t launch_cast_rows(const float* acc, int64_t acc_ld, int64_t rows, int64_t n, int32_t mid_dtype,

@@ -207,7 +207,7 @@ __global__ __launch_bounds__(256) void combine_rows_wave_kernel(
     const BufT* __restrict__ buf, int64_t buf_ld, const int32_t* __restrict__ inv, const int64_t* __restrict__ rp,
     int64_t n_routes, const int64_t* __restrict__ rows_end, const void* __restrict__ w, int32_t w_dtype,
     int32_t w_round, int64_t k, int64_t n, int32_t mid_dtype, void* __restrict__ out, int32_t out_dtype,
-    int64_t out_ld, int64_t n_tokens) {
+    int64_t out_ld, int64_t n_tokens, int32_t accumulate) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= n_tokens) return;
@@ -235,6 +235,13 @@ __global__ __launch_bounds__(256) void combine_rows_wave_kernel(
       in[pc] = cb + pc * 512 + lane * 8 < n;
 #pragma unroll
       for (int q = 0; q < 8; ++q) acc[pc][q] = 0.f;
+      if (accumulate && in[pc]) {  // out: the fp32 running sum
+        const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(out) + t * out_ld + cb +
+                                                            pc * 512 + lane * 8);
+        const float4 a = src[0], b = src[1];
+        acc[pc][0] = a.x; acc[pc][1] = a.y; acc[pc][2] = a.z; acc[pc][3] = a.w;
+        acc[pc][4] = b.x; acc[pc][5] = b.y; acc[pc][6] = b.z; acc[pc][7] = b.w;
+      }
     }
     for (int64_t j0 = 0; j0 < k; j0 += RB) {
       uint4 v[RB][NP];
@@ -303,12 +310,14 @@ hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_l
                                const int64_t* rp, const int64_t* rows_end, const void* w, int32_t w_dtype,
                                int32_t w_round, int64_t n_tokens,
                                int64_t k, int64_t n, int32_t mid_dtype, void* out, int32_t out_dtype, int64_t out_ld,
-                               hipStream_t stream) {
+                               hipStream_t stream, bool accumulate) {
   if (n_tokens <= 0 || n <= 0) return hipSuccess;
   if (n_tokens > 0x7fffffffll || (n + 2047) / 2048 > 65535) return hipErrorInvalidValue;
   if ((inv == nullptr) != (rp == nullptr)) return hipErrorInvalidValue;
   const bool wave_ok = (buf_dtype == kBF16 || buf_dtype == kF16) && k <= 64 && n % 8 == 0 &&
                        vec_ok(buf, buf_dtype, buf_ld) && vec_ok(out, out_dtype, out_ld);
+  // a running sum: fp32 rows, added to unrounded, by the wave kernel only
+  if (accumulate && !(wave_ok && out_dtype == kF32 && mid_dtype < 0)) return hipErrorInvalidValue;
   if (wave_ok) {
     const dim3 grid((unsigned)((n_tokens + 3) / 4));
     // whole 2048-column rows per batch where rows are that wide; 1024 columns
@@ -316,7 +325,8 @@ hipError_t launch_combine_rows(const void* buf, int32_t buf_dtype, int64_t buf_l
     const bool wide = n >= 2048;
 #define CVMM_COMBINE(T, NP)                                                                                      \
   hipLaunchKernelGGL((combine_rows_wave_kernel<T, NP>), grid, dim3(256), 0, stream, (const T*)buf, buf_ld, inv, \
-                     rp, n_tokens * k, rows_end, w, w_dtype, w_round, k, n, mid_dtype, out, out_dtype, out_ld, n_tokens)
+                     rp, n_tokens * k, rows_end, w, w_dtype, w_round, k, n, mid_dtype, out, out_dtype, out_ld, n_tokens, \
+                     accumulate ? 1 : 0)
     if (buf_dtype == kBF16) {
       if (wide) CVMM_COMBINE(bf16_t, 4);
       else CVMM_COMBINE(bf16_t, 2);

@@ -425,6 +425,45 @@ Tensor gelu_backward(const Tensor& grad, const Tensor& pre, int64_t stream) {
 // ---------------------------------------------------------------------------
 // backward (cvmm.py:1552-1755): (grad_x, grad_keys, grad_reduction_weight)
 // ---------------------------------------------------------------------------
+// Host-side flags above the ABI's 32 bits: bits 32..47 carry the low-memory
+// grad-input's top-k columns per slice (cvmm_lowmem_chunk_size; 0: all).
+int64_t lowmem_chunk_of(int64_t flags) { return (flags >> 32) & 0xffff; }
+
+// The token gradient of a token-input unweighted top-k sum taken over slices
+// of `chunk` top-k columns (cvmm_grouped_backward_lowmem, cvmm.py:1228-1338):
+// each slice of the selection is sorted on its own, its routes' rows go
+// through a route buffer of T * chunk rows (not T * top_k), and are added in
+// route order to an fp32 running sum (CVMM_FLAG_ACCUMULATE) that is rounded
+// once at the end -- the bits of the one-call sum.  g: [T * top_k, d_out]
+// route rows; perm: the selection's out_index; s32: its sorted ids.
+Tensor grad_x_by_slices(const Tensor& g, const Tensor& kv, const Tensor& s32, const Tensor& perm, int64_t T,
+                        int64_t k, int64_t E, int64_t d_in, int64_t d_out, int64_t chunk, at::ScalarType x_type,
+                        int32_t od, int64_t flags, int64_t stream) {
+  Tensor ids = at::empty({T * k}, s32.options());
+  ids.index_put_({perm}, s32);  // the id of route t * k + j
+  ids = ids.view({T, k});
+  Tensor gv = g.reshape({T, k, d_out});
+  Tensor acc = at::zeros({T, d_in}, g.options().dtype(at::kFloat));
+  const int32_t aflags = (int32_t)flags | CVMM_FLAG_ACCUMULATE;
+  for (int64_t cs = 0; cs < k; cs += chunk) {
+    const int64_t c = std::min(chunk, k - cs), Rc = T * c;
+    Tensor ids_c = ids.narrow(1, cs, c).contiguous();
+    const std::vector<Tensor> srt = sort_routes(ids_c, E, c, stream, std::nullopt);  // ssel, perm, tok, off, pos
+    Tensor g_c = gv.narrow(1, cs, c).reshape({Rc, d_out}).contiguous();
+    const size_t ws_bytes = cvmm_bwd_x_workspace_bytes(Rc, (int32_t)E, d_in, d_out, T, 1, 0, 1, c, dtype_id(x_type),
+                                                       od, 0, aflags);
+    OptT ws;
+    if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(g, at::kByte));
+    check(cvmm_bwd_x(ptr(g_c), dtype_id(g_c.scalar_type()), Rc, d_out, ptr(kv), dtype_id(kv.scalar_type()),
+                     (int32_t)E, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2), tptr<int32_t>(srt[0]),
+                     tptr<int64_t>(srt[2]), tptr<int64_t>(srt[1]), Rc, tptr<int64_t>(srt[3]),
+                     tptr<int32_t>(srt[4]), nullptr, 0, c, nullptr, dtype_id(x_type), 0, 0, od, ptr(acc),
+                     dtype_id(at::kFloat), T, d_in, nullptr, 0, aflags, ptr(ws), ws_bytes, (void*)stream),
+          "cvmm_bwd_x(slice)");
+  }
+  return acc.to(x_type);
+}
+
 std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const Tensor& x, const Tensor& keys,
                                       const OptT& keys_x, bool keys_x_is_t, const Tensor& sel, const Tensor& sel_index,
                                       const OptT& out_index, const Tensor& offsets, const OptT& route_pos,
@@ -486,11 +525,40 @@ std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const
     if (need_grad_x) gx = at::empty(xr.sizes(), opts(x, x.scalar_type()));
     if (need_grad_rw) grad_rw = at::empty(rw->sizes(), opts(*rw, rw->scalar_type()));
     const int64_t gx_rows = gx.has_value() ? gx->size(0) : xr.size(0);
+    // a token-input unweighted top-k sum on the route buffer can run over
+    // slices of its top-k columns: when cvmm_lowmem_chunk_size asks for it,
+    // or when the one-call workspace does not fit (halving the slice until
+    // it does), as the reference falls back on torch.OutOfMemoryError
+    const bool sliceable = need_grad_x && !rw.has_value() && oi.has_value() && k > 1 && k <= 64 &&
+                           !(flags & CVMM_FLAG_ATOMIC_REDUCE) && d_in % 8 == 0 &&
+                           (x.scalar_type() == at::kBFloat16 || x.scalar_type() == at::kHalf) &&
+                           cvmm_topk_dense(gx_rows, (int32_t)E, d_out, d_in, k, od) == 0;
+    auto by_slices = [&](int64_t chunk) {
+      return grad_x_by_slices(g, kv, s32, *oi, gx_rows, k, E, d_in, d_out, chunk, x.scalar_type(), od, flags, stream)
+          .view(x.sizes());
+    };
+    const int64_t chunk = lowmem_chunk_of(flags);
+    if (sliceable && chunk > 0 && chunk < k) {
+      gx.reset();
+      return {by_slices(chunk), grad_w, grad_rw};
+    }
     const size_t ws_bytes = cvmm_bwd_x_workspace_bytes(R, (int32_t)E, d_in, d_out, gx_rows, 1, rw.has_value() ? 1 : 0,
                                                        oi.has_value() ? 1 : 0, k, dtype_id(x.scalar_type()), od,
                                                        need_grad_rw ? 1 : 0, (int32_t)flags);
     OptT ws;
-    if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(x, at::kByte));
+    try {
+      if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(x, at::kByte));
+    } catch (const c10::OutOfMemoryError&) {
+      if (!sliceable) throw;
+      gx.reset();
+      for (int64_t c = k / 2;; c /= 2) {
+        try {
+          return {by_slices(c), grad_w, grad_rw};
+        } catch (const c10::OutOfMemoryError&) {
+          if (c <= 1) throw;
+        }
+      }
+    }
     check(cvmm_bwd_x(ptr(g), dtype_id(g.scalar_type()), g.size(0), g.stride(0), ptr(kv),
                      dtype_id(kv.scalar_type()), (int32_t)E, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2),
                      tptr<int32_t>(s32), tptr<int64_t>(si), tptr<int64_t>(oi), R, tptr<int64_t>(offsets),

@@ -50,6 +50,12 @@ extern "C" {
 #define CVMM_FLAG_COUNTS_READY 16 /* cvmm_sort_routes_cast_keys_ex: the workspace already holds the
                                      count matrix of these ids for n_experts, written by
                                      cvmm_copy_ids_count (see there) */
+#define CVMM_FLAG_ACCUMULATE 32 /* cvmm_bwd_x, token-input unweighted top-k sum: grad_x is an fp32
+                                   running sum; this call's sums (each route's row rounded to
+                                   x_dtype, as it would be stored) are added to it in route order,
+                                   unrounded.  Calls over consecutive slices of a selection's
+                                   top-k columns, then one rounding to x_dtype, give the bits of
+                                   one call over all of them (the low-memory grad-input). */
 
 /* kernel classes for the timing hooks */
 #define CVMM_KC_SORT 1        /* histogram + scan + scatter of cvmm_sort_routes */
@@ -345,7 +351,11 @@ int cvmm_gelu_backward(const void* grad, int32_t grad_dtype, int64_t grad_ld, co
  * top-k sum's flags as for cvmm_fwd (here K = d_out, N = d_in; the reduce
  * GEMM is not taken for a weighted call that asks for grad_rw).  With
  * grad_rw and d_out > 128, 16-bit x with 8-byte aligned rows (x pointer and
- * x_ld) keeps the DMA-staged kernel; other x takes the slower tiled one. */
+ * x_ld) keeps the DMA-staged kernel; other x takes the slower tiled one.
+ * CVMM_FLAG_ACCUMULATE (the low-memory grad-input over slices of the top-k
+ * columns, cvmm.py:1228-1338): grad_x fp32 holds a running sum that the
+ * call adds to; x may be NULL but x_dtype names the rows' dtype; the
+ * workspace query takes that dtype as grad_x_dtype. */
 size_t cvmm_bwd_x_workspace_bytes(int64_t n_routes, int32_t n_experts, int64_t d_in, int64_t d_out,
                                   int64_t grad_x_rows, int32_t has_offsets, int32_t weighted, int32_t token_input,
                                   int64_t top_k, int32_t grad_x_dtype, int32_t op_dtype, int32_t need_grad_rw,
