@@ -1215,7 +1215,9 @@ int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, con
                           wgrad_scales_rows(op_dtype, d_in) && align_up(c.used, 256) + rows_bytes <= workspace_bytes;
   if (scale_rows) {
     void* xs = c.take(rows_bytes);
-    int r = check_launch(timed(CVMM_KC_WGRAD, s, [&] {
+    // timed with the row work (combine class): the weight-gradient class
+    // times the GEMM alone, one launch per call
+    int r = check_launch(timed_combine(s, [&] {
       return launch_scale_rows(x, x_dtype, x_ld, true, rw, rw_dtype, op_dtype, x_rows, top_k, d_in, op_dtype, xs,
                                s);
     }), "cvmm_bwd_w(scale)");

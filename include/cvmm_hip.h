@@ -64,7 +64,9 @@ extern "C" {
 #define CVMM_KC_GEMM_FWD 8    /* routed GEMM of cvmm_fwd */
 #define CVMM_KC_GEMM_BWDX 16  /* routed GEMM of cvmm_bwd_x */
 #define CVMM_KC_WGRAD 32      /* weight-gradient kernel of cvmm_bwd_w */
-#define CVMM_KC_COMBINE 64    /* top-k row combine / fp32 cast / gate-grad sum */
+#define CVMM_KC_COMBINE 64    /* row work: top-k row combine / fp32 cast / gate-grad sum / dense
+                                 top-k slot table and row scaling / weighted rows of the weight
+                                 gradient */
 #define CVMM_KC_FILL 128      /* zero fills */
 #define CVMM_KC_ROUTE 512     /* router (softmax, top-k, histogram) + its scatter; router backward */
 
