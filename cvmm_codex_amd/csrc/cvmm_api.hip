@@ -38,6 +38,7 @@ static bool nt_eligible(const GemmParams& p, int32_t op) {
 }
 
 hipError_t launch_routed_gemm(const GemmParams& p, int32_t op, hipStream_t s) {
+  if (small_gemm_eligible(p, op)) return launch_routed_small(p, s);
   if (nt_eligible(p, op)) return op == kBF16 ? launch_routed_gemm_nt_bf16(p, s) : launch_routed_gemm_nt_f16(p, s);
   if (p.act != 0) return hipErrorInvalidValue;  // the activation epilogue exists in the ring kernel only
   if (op == kBF16) return launch_routed_gemm_bf16(p, s);
@@ -57,6 +58,7 @@ static bool wgrad_fast_eligible(const WgradParams& p, int32_t op) {
 }
 
 hipError_t launch_wgrad(const WgradParams& p, int32_t op, hipStream_t s) {
+  if (small_wgrad_eligible(p, op)) return launch_wgrad_small(p, s);
   if (wgrad_fast_eligible(p, op)) return op == kBF16 ? launch_wgrad_v3_bf16(p, s) : launch_wgrad_v3_f16(p, s);
   if (op == kBF16) return launch_wgrad_bf16(p, s);
   if (op == kF16) return launch_wgrad_f16(p, s);

@@ -130,6 +130,13 @@ struct WgradParams {
   int32_t tile_choice;     // 16-bit fast path tile: kWgTile*
 };
 
+// Small fp32 problems (cvmm_small.hip): 16 x 64 routed-product tiles and
+// 64 x 64 weight-gradient blocks, plain FMAs.
+bool small_gemm_eligible(const GemmParams& p, int32_t op);
+hipError_t launch_routed_small(const GemmParams& p, hipStream_t stream);
+bool small_wgrad_eligible(const WgradParams& p, int32_t op);
+hipError_t launch_wgrad_small(const WgradParams& p, hipStream_t stream);
+
 // Weight-gradient workgroup orders.  The hardware places workgroup i on XCD
 // i % 8; each XCD has its own L2.
 //   chunk-major:  the tiles of one route chunk adjacent, contiguous ranges of

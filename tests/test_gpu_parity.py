@@ -901,3 +901,20 @@ def test_config_ff_projections(name, reduce_mode):
     got = U.run_hip(p.x, p.keys, p.sel, p.weights, p.grad_out, p.route_input, p.amp)
     exp = U.run_oracle(p.x, p.keys, p.sel, p.weights, p.grad_out, p.route_input, p.amp, compute=np.float32)
     U.compare(got, exp, 2e-2)
+
+
+@pytest.mark.parametrize("route_input", [False, True])
+@pytest.mark.parametrize("D,H", [(600, 72), (64, 130), (200, 8)])
+def test_small_fp32_problems(D, H, route_input):
+    """fp32 problems small enough for the 16 x 64 routed-product tiles and
+    the per-expert 64 x 64 weight-gradient blocks (cvmm_small.hip): K over
+    several rounds of 256 with a ragged tail (600), ragged output columns,
+    both weight orientations (forward n-contiguous, grad-input k-contiguous),
+    an expert with more than 128 routes (weight-gradient rounds) and
+    out-of-range ids, against the oracle at the fp32 tolerance."""
+    x, keys, sel, w, go = _rand_case(31 + D + H, 2, 96, D, H, 5, 4, False, route_input, x_dt=torch.float32)
+    sel[0, :40, 0] = 7       # out of range for 5 experts: left out, their rows zero
+    go = go.float()
+    got = U.run_hip(x, keys, sel, w, go, route_input, False)
+    exp = U.run_oracle(x, keys, sel, w, go, route_input, False)
+    U.compare(got, exp, 1e-4)
