@@ -96,24 +96,26 @@ def time_steps(runner: Runner, steps: int, warmup: int):
 def time_phases(runner: Runner, iters: int):
     """GPU time of the phases of a step, from HIP events on torch's stream
     between them: selector preparation, forward (which runs the selector's
-    sort), backward.  The iterations run back to back with no synchronisation
-    (the host stays ahead of the GPU), so the events time the GPU's work, not
-    host submission; call it after warm-up steps."""
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(iters)]
-    for ev in evs:
+    sort), backward.  The iterations run back to back with no synchronisation,
+    so where the host stays ahead of the GPU the events time the GPU's work,
+    not host submission (in a host-bound step, as at the tiny fp32 shape, they
+    also hold the GPU's waits for the host); call it after warm-up steps.
+    # one event per phase boundary: an iteration's end is the next one's start
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3 * iters + 1)]
+    ev[0].record()
+    for i in range(iters):
         runner.zero()
-        ev[0].record()
         s = runner.prepare()
-        ev[1].record()
+        ev[3 * i + 1].record()
         y = runner.forward(s)
-        ev[2].record()
+        ev[3 * i + 2].record()
         runner.backward(y)
-        ev[3].record()
+        ev[3 * i + 3].record()
         runner.n_steps += 1
     torch.cuda.synchronize()
     acc = np.zeros(3)
-    for ev in evs:
-        acc += [ev[i].elapsed_time(ev[i + 1]) for i in range(3)]
+    for i in range(iters):
+        acc += [ev[3 * i + j].elapsed_time(ev[3 * i + j + 1]) for j in range(3)]
     return dict(zip(("prepare", "fwd", "bwd"), (acc / iters).tolist()))
 
 
@@ -556,7 +558,7 @@ def kernel_class(name: str):
         return role
     base = name.split("<")[0].split("(")[0].split()[-1] if name else ""
     if base.startswith("cvmm::"):
-        for key, cls in (("topk_gemm", "dense_topk"), ("topk_slot_table", "dense_prep"),
+        for key, cls in (("routed_small", "gemm"), ("topk_gemm", "dense_topk"), ("topk_slot_table", "dense_prep"),
                          ("scale_rows", "dense_prep"), ("copy_rows_op", "dense_prep"),
                          ("combine_rows", "combine"), ("sort_", "sort"), ("cast_keys", "cast"),
                          ("copy_ids", "sort"), ("sum_partials", "dgate"), ("fill_zero", "fill"), ("gelu", "gelu"),

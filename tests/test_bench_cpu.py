@@ -17,6 +17,8 @@ import bench as B
     ("void cvmm::sort_scatter_cast_kernel<int, bf16>(cvmm::ScatterArgs<int>)", "sort"),
     ("void cvmm::copy_ids_count_kernel<long>(long const*, long)", "sort"),
     ("void cvmm::combine_rows_wave_kernel<bf16>(int)", "combine"),
+    ("void cvmm::routed_small_kernel<4>(cvmm::GemmParams)", "gemm"),
+    ("void cvmm::route_topk_hist_kernel<float, 16, 8>(float const*)", "router"),
 ])
 def test_kernel_classes(name, cls):
     assert B.kernel_class(name) == cls
