@@ -116,6 +116,24 @@ def test_dense_topk_duplicate_experts(dense):
         U.compare(got, U.run_oracle(x, keys, sel, w, go, route_input, True), 2e-2)
 
 
+@pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True)])
+def test_dense_topk_heavy_repeats(dense, weighted, route_input):
+    """Repeats up to the whole top-k: some tokens send all 64 routes to one
+    expert, others 32 + 32 to two, others a mix, in a tile beside tokens with
+    no repeats -- the tile runs up to 64 passes over the experts, each pass
+    taking every token's next route on the expert from the next-route links."""
+    T, K, E = 300, 64, 40
+    x, keys, sel, w, go = _case(41, 1, T, 64, 72, E, K, weighted, route_input, dup=True)
+    sel[0, 0, :] = 5                          # 64 routes on one expert
+    sel[0, 1, :32] = 7
+    sel[0, 1, 32:] = 9                        # 32 + 32
+    g = torch.Generator().manual_seed(42)
+    sel[0, 2:40] = torch.randint(0, 3, (38, K), generator=g)   # many repeats over three experts
+    sel[0, 280, ::2] = 11                     # every other route, in the tile's second half
+    got = U.run_hip(x, keys, sel, w, go, route_input, True)
+    U.compare(got, U.run_oracle(x, keys, sel, w, go, route_input, True), 2e-2)
+
+
 def test_dense_topk_invalid_ids_contribute_nothing(dense):
     E = 8
     for weighted, route_input in ((False, False), (True, True)):
