@@ -99,7 +99,7 @@ def time_phases(runner: Runner, iters: int):
     sort), backward.  The iterations run back to back with no synchronisation,
     so where the host stays ahead of the GPU the events time the GPU's work,
     not host submission (in a host-bound step, as at the tiny fp32 shape, they
-    also hold the GPU's waits for the host); call it after warm-up steps.
+    also hold the GPU's waits for the host); call it after warm-up steps."""
     # one event per phase boundary: an iteration's end is the next one's start
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3 * iters + 1)]
     ev[0].record()
