@@ -93,6 +93,53 @@ def time_steps(runner: Runner, steps: int, warmup: int):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
+def grads_of(runner: Runner):
+    out = [runner.x.grad, runner.keys.grad]
+    if runner.w is not None:
+        out.append(runner.w.grad)
+    return [g.detach().clone() for g in out]
+
+
+def time_steps_graph(runner: Runner, steps: int, warmup: int):
+    """Steps as replays of one HIP graph captured from a step (selector,
+    forward, backward: every launch of the step, re-run on each replay), for
+    steps whose host submission takes longer than their kernels.  Returns
+    the ms per replay and whether a replay's gradients equal an eager
+    step's bit for bit."""
+    runner.step()
+    torch.cuda.synchronize()
+    eager = grads_of(runner)
+    # warm-up on the capture's side stream, then capture with the gradients
+    # unset, so the backward allocates them from the graph's pool
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            runner.step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    runner.zero()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        s = runner.prepare()
+        y = runner.forward(s)
+        runner.backward(y)
+    for _ in range(max(warmup, 1)):
+        graph.replay()
+    torch.cuda.synchronize()
+    same = all(torch.equal(a, b) for a, b in zip(grads_of(runner), eager))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    same = same and all(torch.equal(a, b) for a, b in zip(grads_of(runner), eager))  # after the timed replays
+    runner.n_steps += max(warmup, 1) + steps  # replays (the eager steps count themselves)
+    del graph
+    runner.zero()
+    return ms, same
+
+
 def time_phases(runner: Runner, iters: int):
     """GPU time of the phases of a step, from HIP events on torch's stream
     between them: selector preparation, forward (which runs the selector's
@@ -674,6 +721,11 @@ def summarize(dirpath: str, copy_dir=None) -> str:
                   f"MFMA frac {rf['mfma_frac']:.4f}, HBM frac {rf['hbm_frac']:.4f}",
                   f"- kernel us per launch: " + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in
                                                           bench["kernel_ms_per_launch"].items())]
+        cfg = bench.get("config", {})
+        if cfg.get("launch") == "hip_graph":
+            lines.append(f"- steps timed as HIP graph replays of one captured step (selector, forward, backward; "
+                         f"eager step {cfg['eager_ms_per_step'] * 1e3:.1f} us on the same box, host-bound); "
+                         f"replay gradients bit-identical to an eager step's: {cfg['graph_bit_identical']}")
         if "breakdown_ms" in bench:
             lines.append("- step breakdown (GPU time): " + ", ".join(
                 f"{k} {v * 1e3:.1f} us" for k, v in bench["breakdown_ms"].items()) +
@@ -801,6 +853,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(W.PROJECTIONS))
     ap.add_argument("--kernel-iters", type=int, default=100)
+    ap.add_argument("--graph", action="store_true",
+                    help="time the K steps as replays of one HIP graph captured from a step (for a "
+                         "host-bound step, as at the tiny fp32 shape); phases and kernels stay eager")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["fwd", "bwd_w", "bwd_x", "cast_keys", "copy"], default=None,
                     help="launch only this phase --steps times, or the copy calibration (rocprofv3 runs)")
@@ -890,6 +945,15 @@ def main():
     log("kernel ms/launch " + json.dumps({k: round(v["avg_ms"], 5) for k, v in kt.items()}))
     ms = time_steps(runner, args.steps, args.warmup)
     log(f"step {ms:.4f} ms")
+    launch = {"launch": "eager"}
+    if args.graph:
+        eager_ms = ms
+        ms, same = time_steps_graph(runner, args.steps, args.warmup)
+        log(f"graph replay {ms:.4f} ms per step (eager {eager_ms:.4f}), gradients bit-identical: {same}")
+        if not same:
+            raise SystemExit("bench: graph replay gradients differ from an eager step's")
+        launch = {"launch": "hip_graph", "eager_ms_per_step": round(eager_ms, 5),
+                  "graph_bit_identical": same}
     dtype = "bf16" if proj.amp else "fp32"
     bound = BOUND[proj.name]
     # dominant kernel: the GEMM class with the most device time per step
@@ -916,7 +980,7 @@ def main():
         "config": {"workload": proj.name, "routes": proj.routes, "d_in": proj.keys.shape[1],
                    "d_out": proj.keys.shape[2], "n_experts": proj.keys.shape[0],
                    "top_k": proj.sel.shape[-1], "weighted": proj.weights is not None,
-                   "step": "sel+fwd+bwd", "gflop_per_step": round(proj.flops / 1e9, 3)},
+                   "step": "sel+fwd+bwd", "gflop_per_step": round(proj.flops / 1e9, 3), **launch},
         "step_roofline": step_roof,
         "breakdown_ms": {k: round(v, 5) for k, v in breakdown(phases, kt).items()},
         "kernel_ms_per_launch": {k: round(v["avg_ms"], 5) for k, v in kt.items()},

@@ -37,7 +37,7 @@ struct RouteMeta {
 // ceil(count_e / BM) consecutive tiles.  Wave 0 scans the offsets 64 experts at
 // a time; returns false (uniformly) when `tile` is past the last tile.
 template <int BM>
-__device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& m) {
+__device__ bool gemm_schedule_tile(const GemmParams& p, int64_t tile, RouteMeta<BM>& m) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -130,11 +130,15 @@ __device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& 
     if (lane == 0 && m.expert < 0) m.row0 = carry;  // past the last tile: the tile count
   }
   __syncthreads();
-  if (m.expert < 0) return false;
+  return m.expert >= 0;
+}
+
+// The route metadata of every row of the tile gemm_schedule_tile found.
+template <int BM>
+__device__ void gemm_route_meta(const GemmParams& p, RouteMeta<BM>& m) {
+  const int tid = threadIdx.x;
   const int64_t row0 = m.row0;
   const int32_t rows = m.rows;
-
-  // ---- per-row route metadata -------------------------------------------------
   for (int r = tid; r < BM; r += kGemmThreads) {
     int64_t ar = -1, orow = -1, widx = -1, dgr = -1;
     float wv = 1.f;
@@ -161,7 +165,13 @@ __device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& 
     m.dgrow[r] = dgr;
   }
   __syncthreads();
+}
 
+// Both: the tile, then its rows' route metadata.
+template <int BM>
+__device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& m) {
+  if (!gemm_schedule_tile<BM>(p, tile, m)) return false;
+  gemm_route_meta<BM>(p, m);
   return true;
 }
 

@@ -553,9 +553,13 @@ void set_sort_chunk(int64_t routes) { g_sort_chunk.store(routes); }
 int64_t sort_chunk_size(int64_t n_routes, int32_t n_experts) {
   const int64_t knob = g_sort_chunk.load();
   if (knob > 0) return (knob + kSortThreads - 1) / kSortThreads * kSortThreads;
-  // >= kSortMinChunk routes; (E + 1) * n_chunks <= 64K
+  // >= kSortMinChunk routes; (E + 1) * n_chunks <= 64K.  A sort of fewer than
+  // 8 such chunks takes 8 chunks of at least one round (256 routes): its
+  // launch is latency-bound, and a chunk's waves go through their routes in
+  // rounds of 64.
   int64_t c = (n_routes * (int64_t)(n_experts + 1) + 65535) / 65536;
-  if (c < kSortMinChunk) c = kSortMinChunk;
+  if (c < kSortMinChunk) c = n_routes < 8 * kSortMinChunk ? std::max<int64_t>((n_routes + 7) / 8, kSortThreads)
+                                                          : kSortMinChunk;
   return (c + kSortThreads - 1) / kSortThreads * kSortThreads;
 }
 

@@ -38,6 +38,8 @@ fi
 # ffn: the bench line times the fused and the composed stack; the trace and
 # the counter runs take the fused stack (the bench line's value) alone
 if [ "$W" = ffn ]; then ARGS="--ffn --ffn-variant fused"; LINE="--ffn"; else ARGS="--workload $W"; LINE=$ARGS; fi
+# the tiny fp32 step is host-bound: its steps are timed as HIP graph replays
+if [ "$W" = tiny_fp32 ]; then ARGS="$ARGS --graph"; LINE="$LINE --graph"; fi
 step "bench line"
 timeout -k 10 300 python3 bench.py $LINE --no-cpu-baseline > "$OUT/bench.json" 2> "$OUT/bench.err" || exit $?
 step "kernel trace"
