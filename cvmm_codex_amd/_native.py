@@ -20,6 +20,7 @@ FLAG_ATOMIC_REDUCE = 1
 FLAG_COUNTERS_ZEROED = 2
 FLAG_COUNTS_READY = 16
 FLAG_ACCUMULATE = 32
+FLAG_ROWS_SCALED = 64
 CAST_T_INTERLEAVED = 1
 CAST_N_INTERLEAVED = 2
 TUNE_PANEL_TILES_PER_WG = 1
@@ -74,6 +75,15 @@ _SIGS = {
         _P, _P, _P, _I64,                     # sorted_sel, sel_index, out_index, R
         _P, _P, _P, _I32, _I64,               # offsets, route_pos, rw, rw dtype, reduce_k
         _I32, _P, _I32, _I64, _I64,           # op, out, out dtype, out rows, out ld
+        _I32, _P, _SZ, _P]),                  # flags, ws, ws bytes, stream
+    "cvmm_fwd_keep_scaled": (ctypes.c_int, [
+        _P, _I32, _I64, _I64,                 # x, dtype, rows, ld
+        _P, _I32, _I32, _I64, _I64,           # keys, dtype, E, d_in, d_out
+        _I64, _I64, _I64,                     # key strides
+        _P, _P, _P, _I64,                     # sorted_sel, sel_index, out_index, R
+        _P, _P, _P, _I32, _I64,               # offsets, route_pos, rw, rw dtype, reduce_k
+        _I32, _P, _I32, _I64, _I64,           # op, out, out dtype, out rows, out ld
+        _P, _P,                               # scaled rows, int32 written flag
         _I32, _P, _SZ, _P]),                  # flags, ws, ws bytes, stream
     "cvmm_fwd_gelu": (ctypes.c_int, [
         _P, _I32, _I64, _I64,                 # x, dtype, rows, ld

@@ -272,7 +272,8 @@ int run_dense_topk(const DenseWs& w, const void* src, int32_t src_dtype, int64_t
                    int64_t n_routes, int64_t n_tokens, int64_t top_k, int32_t n_experts, const void* keys,
                    int32_t keys_dtype, int64_t d_in, int64_t d_out, int64_t k_se, int64_t k_si, int64_t k_sj,
                    bool fwd, const void* rw, int32_t rw_dtype, int32_t w_round, int32_t op_dtype, void* out,
-                   int32_t out_dtype, int64_t out_ld, uint32_t gemm_class, const char* what, hipStream_t s) {
+                   int32_t out_dtype, int64_t out_ld, uint32_t gemm_class, const char* what, hipStream_t s,
+                   void* scaled_rows = nullptr) {
   const int64_t K = fwd ? d_in : d_out, N = fwd ? d_out : d_in;
   const int64_t esz = (int64_t)dtype_size(op_dtype);
   // B_e[k][n] = b[e * b_se + n * b_sn + k]: keys[e][k][n] for the forward,
@@ -304,12 +305,14 @@ int run_dense_topk(const DenseWs& w, const void* src, int32_t src_dtype, int64_t
   const void* A = src;
   int64_t a_ld = src_ld;
   if (rw != nullptr) {
+    // (into the caller's buffer when it keeps them: [n_routes][K])
+    void* dst = scaled_rows != nullptr ? scaled_rows : w.src;
     int r = check_launch(timed_combine(s, [&] {
       return launch_scale_rows(src, src_dtype, src_ld, src_per_route, rw, rw_dtype, w_round, n_routes, top_k, K,
-                               op_dtype, w.src, s);
+                               op_dtype, dst, s);
     }), what);
     if (r) return r;
-    A = w.src;
+    A = dst;
     a_ld = K;
   } else if (!(src_dtype == op_dtype && src_per_route && aligned16(src) && (src_ld * esz) % 16 == 0 &&
                 topk_gemm_a_fits(n_routes, src_ld, K))) {
@@ -363,7 +366,7 @@ extern "C" {
 
 const char* cvmm_last_error(void) { return g_err.c_str(); }
 
-int cvmm_abi_version(void) { return 12; }
+int cvmm_abi_version(void) { return 13; }
 
 int cvmm_timing_enable(uint32_t class_mask) {
   std::lock_guard<std::mutex> lk(g_timing_mu);
@@ -766,7 +769,9 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
                     int64_t n_routes, const int64_t* offsets, const int32_t* route_pos, const void* rw,
                     int32_t rw_dtype, int64_t reduce_k, int32_t op_dtype, void* out, int32_t out_dtype,
                     int64_t out_rows, int64_t out_ld, void* pre_act, int32_t flags, void* workspace,
-                    size_t workspace_bytes, void* stream) {
+                    size_t workspace_bytes, void* stream, void* scaled_rows = nullptr,
+                    int32_t* scaled_written = nullptr) {
+  if (scaled_written != nullptr) *scaled_written = 0;
   if (!valid_dtype(x_dtype) || !valid_dtype(keys_dtype) || !valid_dtype(op_dtype) || !valid_dtype(out_dtype) ||
       (rw && !valid_dtype(rw_dtype)))
     return fail(CVMM_ERR_INVALID, "cvmm_fwd: invalid dtype id");
@@ -843,11 +848,16 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
   }
   if (dense) {
     // high fan-out: one GEMM over expert slots of the x rows (scaled by
-    // rnd_out(w)), no route buffer
-    return run_dense_topk(dws, x, x_dtype, x_ld, out_index == nullptr, sorted_sel, route_pos, rp, offs, n_routes,
-                          out_rows, reduce_k, n_experts, keys, keys_dtype, d_in, d_out, k_se, k_si, k_sj, true, rw,
-                          rw_dtype, out_dtype, op_dtype, out, out_dtype, out_ld, CVMM_KC_GEMM_FWD,
-                          "cvmm_fwd(dense)", s);
+    // rnd_out(w)), no route buffer.  Route input with out == op dtype: the
+    // scaled rows are those the weight gradient scales, kept when asked for.
+    const bool keep = scaled_rows != nullptr && scaled_written != nullptr && out_index == nullptr &&
+                      x_rows == n_routes && out_dtype == op_dtype && (op_dtype == kBF16 || op_dtype == kF16);
+    const int r = run_dense_topk(dws, x, x_dtype, x_ld, out_index == nullptr, sorted_sel, route_pos, rp, offs,
+                                 n_routes, out_rows, reduce_k, n_experts, keys, keys_dtype, d_in, d_out, k_se, k_si,
+                                 k_sj, true, rw, rw_dtype, out_dtype, op_dtype, out, out_dtype, out_ld,
+                                 CVMM_KC_GEMM_FWD, "cvmm_fwd(dense)", s, keep ? scaled_rows : nullptr);
+    if (r == 0 && keep) *scaled_written = 1;
+    return r;
   }
   if (flags & CVMM_FLAG_ATOMIC_REDUCE) {
     // fused combine: y rounded to the output dtype, times rnd_out(w), fp32 atomics per token row
@@ -895,6 +905,21 @@ int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const
   return fwd_core(x, x_dtype, x_rows, x_ld, keys, keys_dtype, n_experts, d_in, d_out, k_se, k_si, k_sj, sorted_sel,
                   sel_index, out_index, n_routes, offsets, route_pos, rw, rw_dtype, reduce_k, op_dtype, out,
                   out_dtype, out_rows, out_ld, nullptr, flags, workspace, workspace_bytes, stream);
+}
+
+int cvmm_fwd_keep_scaled(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const void* keys,
+                         int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out, int64_t k_se,
+                         int64_t k_si, int64_t k_sj, const int32_t* sorted_sel, const int64_t* sel_index,
+                         const int64_t* out_index, int64_t n_routes, const int64_t* offsets,
+                         const int32_t* route_pos, const void* rw, int32_t rw_dtype, int64_t reduce_k,
+                         int32_t op_dtype, void* out, int32_t out_dtype, int64_t out_rows, int64_t out_ld,
+                         void* scaled_rows, int32_t* scaled_written, int32_t flags, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  if (scaled_written == nullptr) return fail(CVMM_ERR_INVALID, "cvmm_fwd_keep_scaled: scaled_written NULL");
+  return fwd_core(x, x_dtype, x_rows, x_ld, keys, keys_dtype, n_experts, d_in, d_out, k_se, k_si, k_sj, sorted_sel,
+                  sel_index, out_index, n_routes, offsets, route_pos, rw, rw_dtype, reduce_k, op_dtype, out,
+                  out_dtype, out_rows, out_ld, nullptr, flags, workspace, workspace_bytes, stream, scaled_rows,
+                  scaled_written);
 }
 
 int cvmm_fwd_gelu(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, const void* keys,
@@ -1181,6 +1206,13 @@ int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, con
     return fail(CVMM_ERR_UNSUPPORTED, "cvmm_bwd_w: x/grad storage must be fp32 or the op dtype");
   if (op_dtype == kF32 && (x_dtype != kF32 || grad_dtype != kF32))
     return fail(CVMM_ERR_UNSUPPORTED, "cvmm_bwd_w: fp32 op needs fp32 x and grad");
+  // x already scaled by the routes' weights (the rows cvmm_fwd_keep_scaled
+  // kept): a weighted selection with route input, rows in the 16-bit op dtype
+  const bool rows_scaled = (flags & CVMM_FLAG_ROWS_SCALED) != 0;
+  if (rows_scaled && !(weighted && out_index == nullptr && x_dtype == op_dtype &&
+                       (op_dtype == kBF16 || op_dtype == kF16) && x_rows == n_routes))
+    return fail(CVMM_ERR_INVALID, "cvmm_bwd_w: CVMM_FLAG_ROWS_SCALED needs a weighted selection with route input "
+                                  "and x in the 16-bit op dtype, one row per route");
 
   hipStream_t s = (hipStream_t)stream;
   WgradParams p{};
@@ -1213,9 +1245,11 @@ int cvmm_bwd_w(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld, con
   // (the weight moves from the d_out-wide gradient slices of every dW tile to
   // one pass over the d_in-wide route rows).
   const size_t rows_bytes = (size_t)x_rows * d_in * dtype_size(op_dtype);
-  const bool scale_rows = weighted && out_index == nullptr && x_rows <= n_routes && n_routes > 0 &&
+  const bool scale_rows = !rows_scaled && weighted && out_index == nullptr && x_rows <= n_routes && n_routes > 0 &&
                           wgrad_scales_rows(op_dtype, d_in) && align_up(c.used, 256) + rows_bytes <= workspace_bytes;
-  if (scale_rows) {
+  if (rows_scaled) {
+    rw = nullptr;  // (the selection stays weighted: one gradient row per token)
+  } else if (scale_rows) {
     void* xs = c.take(rows_bytes);
     // timed with the row work (combine class): the weight-gradient class
     // times the GEMM alone, one launch per call

@@ -308,9 +308,13 @@ std::tuple<OptT, OptT> cast_keys(const Tensor& keys, int64_t op_id, bool want_t,
 // (a [E, d_in, d_out] copy, or an interleaved copy already viewed so).
 Tensor copy_view(const Tensor& copy, bool is_t) { return is_t ? copy.transpose(1, 2) : copy; }
 
+// `scaled` (not NULL): a weighted route-input call whose top-k sum the
+// library takes as the dense GEMM keeps its scaled route rows there for the
+// weight gradient (cvmm_fwd_keep_scaled); left undefined otherwise.
 Tensor cvmm_forward_impl(const Tensor& x, const Tensor& keys, const OptT& keys_op, bool keys_op_is_t, const Tensor& sel,
                const Tensor& sel_index, const OptT& out_index, const Tensor& offsets, const OptT& route_pos,
-               const OptT& rw, int64_t op_id, int64_t out_id, int64_t flags, int64_t stream) {
+               const OptT& rw, int64_t op_id, int64_t out_id, int64_t flags, int64_t stream,
+               Tensor* scaled = nullptr) {
   require_device(x, "x");
   require_device(keys, "keys");
   require_device(sel, "sel");
@@ -353,6 +357,21 @@ Tensor cvmm_forward_impl(const Tensor& x, const Tensor& keys, const OptT& keys_o
                                                    rw.has_value() ? 1 : 0, (int32_t)flags);
   OptT ws;
   if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(x, at::kByte));
+  if (scaled != nullptr && rwf.has_value() && !oi.has_value() && xf.size(0) == R && outd == od &&
+      (op == at::kBFloat16 || op == at::kHalf) && !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
+      cvmm_topk_dense(out_rows, (int32_t)E, d_in, d_out, k, od) == 1) {
+    Tensor xs = at::empty({R, d_in}, opts(x, op));
+    int32_t written = 0;
+    check(cvmm_fwd_keep_scaled(ptr(xf), dtype_id(xf.scalar_type()), xf.size(0), xf.stride(0), ptr(kv),
+                               dtype_id(kv.scalar_type()), (int32_t)E, d_in, d_out, kv.stride(0), kv.stride(1),
+                               kv.stride(2), tptr<int32_t>(s32), tptr<int64_t>(si), nullptr, R,
+                               tptr<int64_t>(offsets), tptr<int32_t>(route_pos), ptr(rwf),
+                               dtype_id(rwf->scalar_type()), k, od, ptr(out), outd, out_rows, d_out, ptr(xs),
+                               &written, (int32_t)flags, ptr(ws), ws_bytes, (void*)stream),
+          "cvmm_fwd_keep_scaled");
+    if (written) *scaled = xs;
+    return out;
+  }
   check(cvmm_fwd(ptr(xf), dtype_id(xf.scalar_type()), xf.size(0), xf.stride(0), ptr(kv),
                  dtype_id(kv.scalar_type()), (int32_t)E, d_in, d_out, kv.stride(0), kv.stride(1), kv.stride(2),
                  tptr<int32_t>(s32), tptr<int64_t>(si), tptr<int64_t>(oi), R, tptr<int64_t>(offsets),
@@ -468,7 +487,8 @@ std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const
                                       const OptT& keys_x, bool keys_x_is_t, const Tensor& sel, const Tensor& sel_index,
                                       const OptT& out_index, const Tensor& offsets, const OptT& route_pos,
                                       const OptT& rw, int64_t top_k, int64_t op_id, bool need_grad_x,
-                                      bool need_grad_keys, bool need_grad_rw, int64_t flags, int64_t stream) {
+                                      bool need_grad_keys, bool need_grad_rw, int64_t flags, int64_t stream,
+                                      const OptT& scaled_x = std::nullopt) {
   const auto op = dtype_of(op_id);
   const int64_t E = keys.size(0), d_in = keys.size(1), d_out = keys.size(2);
   const int64_t k = rw.has_value() ? rw->size(-1) : top_k;
@@ -486,11 +506,15 @@ std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const
   OptT grad_x, grad_w, grad_rw;
 
   if (need_grad_keys) {
-    Tensor xs = rows_of(fast && x.scalar_type() != op ? x.to(op) : storage_for(x, op), d_in);
+    // the route rows the forward scaled (cvmm_fwd_keep_scaled), or x
+    const bool pre_scaled = scaled_x.has_value();
+    Tensor xs = pre_scaled ? *scaled_x
+                           : rows_of(fast && x.scalar_type() != op ? x.to(op) : storage_for(x, op), d_in);
     grad_w = at::empty(keys.sizes(), opts(keys, keys.scalar_type()));
     // a weighted route-input selection gets room for its scaled route rows
-    const size_t ws_bytes =
-        cvmm_bwd_w_workspace_bytes_ex(R, (int32_t)E, d_in, d_out, od, 1, rw.has_value() && !oi.has_value() ? 1 : 0);
+    // (none needed when the forward kept them)
+    const size_t ws_bytes = cvmm_bwd_w_workspace_bytes_ex(R, (int32_t)E, d_in, d_out, od, 1,
+                                                          rw.has_value() && !oi.has_value() && !pre_scaled ? 1 : 0);
     const size_t ctr_bytes = cvmm_bwd_w_counter_bytes(R, (int32_t)E, d_in, d_out, od);
     Tensor ws;
     bool zeroed;
@@ -507,7 +531,8 @@ std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const
       s.clean = ctr_bytes;  // partial tiles follow the counter region
       ws = s.buf;
     }
-    const int32_t wflags = (int32_t)flags | (zeroed ? CVMM_FLAG_COUNTERS_ZEROED : 0);
+    const int32_t wflags = (int32_t)flags | (zeroed ? CVMM_FLAG_COUNTERS_ZEROED : 0) |
+                           (pre_scaled ? CVMM_FLAG_ROWS_SCALED : 0);
     check(cvmm_bwd_w(ptr(xs), dtype_id(xs.scalar_type()), xs.size(0), xs.stride(0), ptr(g),
                      dtype_id(g.scalar_type()), g.size(0), g.stride(0), (int32_t)E, d_in, d_out, tptr<int32_t>(s32),
                      tptr<int64_t>(si), tptr<int64_t>(oi), R, tptr<int64_t>(offsets), ptr(rwf), rwd, k, od,
@@ -596,15 +621,18 @@ struct CvmmFunction : public torch::autograd::Function<CvmmFunction> {
                         const std::vector<int64_t>& out_shape) {
     const bool need_x = x.requires_grad(), need_keys = keys.requires_grad();
     const bool need_rw = rw.has_value() && rw->requires_grad();
-    ctx->save_for_backward({x, keys, opt_or_undef(rw), sel, sel_index, opt_or_undef(out_index), offsets,
-                            opt_or_undef(route_pos), need_x || need_rw ? opt_or_undef(keys_x) : Tensor()});
     ctx->saved_data["keys_x_is_t"] = keys_x_is_t;
     ctx->saved_data["top_k"] = top_k;
     ctx->saved_data["op_id"] = op_id;
     ctx->saved_data["flags"] = flags;
     ctx->saved_data["need"] = (int64_t)((need_x ? 1 : 0) | (need_keys ? 2 : 0) | (need_rw ? 4 : 0));
+    // a weight gradient that needs the weight-scaled route rows the forward's
+    // dense top-k sum makes keeps them (one pass over the route rows saved)
+    Tensor scaled;
     Tensor out = cvmm_forward_impl(x, keys, keys_op, keys_op_is_t, sel, sel_index, out_index, offsets, route_pos,
-                                   rw, op_id, -1, flags, current_stream(x));
+                                   rw, op_id, -1, flags, current_stream(x), need_keys ? &scaled : nullptr);
+    ctx->save_for_backward({x, keys, opt_or_undef(rw), sel, sel_index, opt_or_undef(out_index), offsets,
+                            opt_or_undef(route_pos), need_x || need_rw ? opt_or_undef(keys_x) : Tensor(), scaled});
     // not a view in autograd's sense (its base is no input and is never seen)
     return at::_unsafe_view(out, out_shape);
   }
@@ -618,12 +646,30 @@ struct CvmmFunction : public torch::autograd::Function<CvmmFunction> {
         grads[0], x, v[1], undef_or_opt(v[8]), ctx->saved_data["keys_x_is_t"].toBool(), v[3], v[4],
         undef_or_opt(v[5]), v[6], undef_or_opt(v[7]), undef_or_opt(v[2]), ctx->saved_data["top_k"].toInt(),
         ctx->saved_data["op_id"].toInt(), (need & 1) != 0, (need & 2) != 0, (need & 4) != 0,
-        ctx->saved_data["flags"].toInt(), current_stream(x));
+        ctx->saved_data["flags"].toInt(), current_stream(x), undef_or_opt(v[9]));
     // one entry per forward argument
     return {opt_or_undef(gx), opt_or_undef(gw), opt_or_undef(grw), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(),
             Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
   }
 };
+
+// The Python-facing forward and backward (torch.compile's ops): no kept rows.
+Tensor forward_py(const Tensor& x, const Tensor& keys, const OptT& keys_op, bool keys_op_is_t, const Tensor& sel,
+                  const Tensor& sel_index, const OptT& out_index, const Tensor& offsets, const OptT& route_pos,
+                  const OptT& rw, int64_t op_id, int64_t out_id, int64_t flags, int64_t stream) {
+  return cvmm_forward_impl(x, keys, keys_op, keys_op_is_t, sel, sel_index, out_index, offsets, route_pos, rw, op_id,
+                           out_id, flags, stream);
+}
+
+std::tuple<OptT, OptT, OptT> backward_py(const Tensor& grad_output, const Tensor& x, const Tensor& keys,
+                                         const OptT& keys_x, bool keys_x_is_t, const Tensor& sel,
+                                         const Tensor& sel_index, const OptT& out_index, const Tensor& offsets,
+                                         const OptT& route_pos, const OptT& rw, int64_t top_k, int64_t op_id,
+                                         bool need_grad_x, bool need_grad_keys, bool need_grad_rw, int64_t flags,
+                                         int64_t stream) {
+  return cvmm_backward_impl(grad_output, x, keys, keys_x, keys_x_is_t, sel, sel_index, out_index, offsets, route_pos,
+                            rw, top_k, op_id, need_grad_x, need_grad_keys, need_grad_rw, flags, stream);
+}
 
 Tensor cvmm_apply(const Tensor& x, const Tensor& keys, const OptT& rw, const Tensor& sel, const Tensor& sel_index,
                   const OptT& out_index, const Tensor& offsets, const OptT& route_pos, const OptT& keys_op,
@@ -650,10 +696,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("stream"), py::arg("counted_ws") = py::none());
   m.def("cast_keys", &cast_keys, py::arg("keys"), py::arg("op_id"), py::arg("want_t"), py::arg("want_n"),
         py::arg("layout"), py::arg("stream"));
-  m.def("forward", &cvmm_forward_impl);
+  m.def("forward", &forward_py);
   m.def("forward_gelu", &forward_gelu);
   m.def("gelu_backward", &gelu_backward, py::arg("grad"), py::arg("pre_act"), py::arg("stream"));
-  m.def("backward", &cvmm_backward_impl);
+  m.def("backward", &backward_py);
   m.def("cvmm_apply", &cvmm_apply);
   // operand rules, exposed for tests
   m.def("storage_for", [](const Tensor& t, int64_t op_id) { return storage_for(t, dtype_of(op_id)); });

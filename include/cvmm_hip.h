@@ -56,6 +56,11 @@ extern "C" {
                                    unrounded.  Calls over consecutive slices of a selection's
                                    top-k columns, then one rounding to x_dtype, give the bits of
                                    one call over all of them (the low-memory grad-input). */
+#define CVMM_FLAG_ROWS_SCALED 64 /* cvmm_bwd_w, weighted selection with route input: x holds the
+                                    route rows already scaled, x'_r = rnd_op(rnd_op(w_r) *
+                                    rnd_op(x_r)), as cvmm_fwd_keep_scaled keeps them (op dtype,
+                                    one row per route); reduction_weight is still passed (the
+                                    gradient rows stay one per token) but not applied again */
 
 /* kernel classes for the timing hooks */
 #define CVMM_KC_SORT 1        /* histogram + scan + scatter of cvmm_sort_routes */
@@ -313,6 +318,27 @@ int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld,
              const int64_t* offsets, const int32_t* route_pos, const void* reduction_weight, int32_t rw_dtype,
              int64_t reduce_k, int32_t op_dtype, void* out, int32_t out_dtype, int64_t out_rows, int64_t out_ld,
              int32_t flags, void* workspace, size_t workspace_bytes, void* stream);
+
+/* cvmm_fwd that keeps the scaled route rows of a weighted top-k sum for the
+ * backward.  When the call takes the sum as the dense GEMM (cvmm_topk_dense)
+ * over route input (out_index NULL, x_rows == n_routes) with a 16-bit op and
+ * out_dtype == op_dtype, the GEMM's operand rows x'_r = rnd_op(rnd_op(w_r) *
+ * rnd_op(x_r)) -- bit for bit the rows cvmm_bwd_w would scale -- are written
+ * to scaled_rows ([n_routes][d_in], op dtype, row stride d_in) instead of the
+ * workspace, and *scaled_written is set to 1; otherwise nothing is written
+ * there and *scaled_written is 0.  cvmm_bwd_w with CVMM_FLAG_ROWS_SCALED then
+ * takes them as x, without its own scaling pass.  Same workspace as cvmm_fwd.
+ * No counterpart in the reference (which scales inside its kernels): it saves
+ * the weight gradient a read and a write of the route rows. */
+int cvmm_fwd_keep_scaled(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld,
+                         const void* keys, int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out,
+                         int64_t k_se, int64_t k_si, int64_t k_sj,
+                         const int32_t* sorted_sel, const int64_t* sel_index, const int64_t* out_index,
+                         int64_t n_routes, const int64_t* offsets, const int32_t* route_pos,
+                         const void* reduction_weight, int32_t rw_dtype, int64_t reduce_k, int32_t op_dtype,
+                         void* out, int32_t out_dtype, int64_t out_rows, int64_t out_ld, void* scaled_rows,
+                         int32_t* scaled_written, int32_t flags, void* workspace, size_t workspace_bytes,
+                         void* stream);
 
 /* cvmm_fwd followed by the GELU (erf form), for the up projection of the
  * reference's MoE callers (no counterpart in cvmm.py: its callers write

@@ -298,3 +298,71 @@ def test_dense_topk_rows_not_16_byte_aligned(dense):
     torch.cuda.synchronize()
     exp = U.run_oracle(big[..., 1:].reshape(1, T, K, D).contiguous(), keys, sel, w, go, True, True, need_w=False)
     assert U.norm_rel(U.to_np(y), exp["out"]) <= 2e-2
+
+
+def test_kept_scaled_rows_give_the_weight_gradient_bits(dense):
+    """cvmm_fwd_keep_scaled: the dense weighted forward over route input keeps
+    its operand rows x'_r = rnd(rnd(w_r) * x_r) (equal bit for bit to the same
+    product in torch), its output is cvmm_fwd's, and cvmm_bwd_w given those
+    rows with CVMM_FLAG_ROWS_SCALED writes the bits of its own scaling pass.
+    Off the dense path nothing is kept."""
+    import ctypes
+    lib = N.lib()
+    B, T, D, H, E, K = 2, 96, 64, 128, 32, 16
+    x, keys, sel, w, go = _case(41, B, T, D, H, E, K, True, True)
+    x, keys, w, go = x.cuda(), keys.cuda(), w.cuda(), go.cuda()
+    s = C.cvmm_prepare_sel2(sel.cuda(), w, route_input=True)
+    s._resolve(E)
+    R, Tn = B * T * K, B * T
+    offs = C._offsets_for(s.sel, E)
+    rp = s.out_index if s.out_index is not None else s.sel_index
+    rpos = C._route_pos(rp, R)
+    assert s.out_index is None and rpos is not None
+    xr = x.reshape(R, D).contiguous()
+    wf = w.reshape(-1).contiguous()
+    st = N.stream_of(x.device)
+    bf = N.BF16
+
+    def fwd(keep):
+        out = torch.empty(Tn, H, dtype=torch.bfloat16, device="cuda")
+        ws_b = lib.cvmm_fwd_workspace_bytes(R, E, D, H, Tn, bf, bf, 1, 1, 0)
+        ws = torch.full((ws_b,), 0x5A, dtype=torch.uint8, device="cuda")
+        args = [N.ptr(xr), bf, R, D, N.ptr(keys), N.F32, E, D, H, keys.stride(0), keys.stride(1), keys.stride(2),
+                N.ptr(s.sel), N.ptr(s.sel_index), None, R, N.ptr(offs), N.ptr(rpos), N.ptr(wf), N.F32, K, bf,
+                N.ptr(out), bf, Tn, H]
+        if not keep:
+            N.check(lib.cvmm_fwd(*args, 0, N.ptr(ws), ws_b, st), "cvmm_fwd")
+            return out, None, None
+        xs = torch.full((R, D), 7.0, dtype=torch.bfloat16, device="cuda")
+        written = ctypes.c_int32(-1)
+        N.check(lib.cvmm_fwd_keep_scaled(*args, N.ptr(xs), ctypes.addressof(written), 0, N.ptr(ws), ws_b, st),
+                "cvmm_fwd_keep_scaled")
+        return out, xs, written.value
+
+    def bwd_w(xin, flags, room):
+        dw = torch.empty(E, D, H, dtype=torch.float32, device="cuda")
+        ws_b = lib.cvmm_bwd_w_workspace_bytes_ex(R, E, D, H, bf, 1, 1 if room else 0)
+        ws = torch.zeros(ws_b, dtype=torch.uint8, device="cuda")
+        N.check(lib.cvmm_bwd_w(N.ptr(xin), bf, R, D, N.ptr(go), bf, Tn, H, E, D, H, N.ptr(s.sel),
+                               N.ptr(s.sel_index), None, R, N.ptr(offs), N.ptr(wf), N.F32, K, bf, N.ptr(dw), N.F32,
+                               dw.stride(0), dw.stride(1), dw.stride(2), flags, N.ptr(ws), ws_b, st), "cvmm_bwd_w")
+        return dw
+
+    out_plain, _, _ = fwd(False)
+    out_keep, xs, written = fwd(True)
+    torch.cuda.synchronize()
+    assert written == 1
+    assert torch.equal(out_keep, out_plain)
+    ref = (wf.to(torch.bfloat16).float()[:, None] * xr.float()).to(torch.bfloat16)
+    assert torch.equal(xs, ref)
+    dw_scaled_here = bwd_w(xr, 0, True)
+    dw_kept = bwd_w(xs, N.FLAG_ROWS_SCALED, False)
+    torch.cuda.synchronize()
+    assert torch.equal(dw_kept, dw_scaled_here)
+
+    # the route-buffer path keeps nothing
+    assert lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 1) == 0
+    _, xs2, written2 = fwd(True)
+    torch.cuda.synchronize()
+    assert written2 == 0
+    assert bool((xs2 == 7.0).all())

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.cvmm_abi_version() == 12
+    assert lib.cvmm_abi_version() == 13
 
 
 def test_workspace_queries(lib):
@@ -99,6 +99,27 @@ def test_invalid_arguments_fail_before_launch(lib):
     wargs = [None, 0, 8, 16, None, 0, 4, 16, 8, 128, 8, 1, None, None, None, 8, None, None, ctypes.c_void_p(16),
              0, 4, 0, None, 0, 2, 8, 0, None, 0, None]
     assert lib.cvmm_fwd(*wargs) == 3
+
+
+def test_kept_scaled_rows_arguments_fail_before_launch(lib):
+    """cvmm_fwd_keep_scaled needs its written flag (cleared on any error);
+    cvmm_bwd_w takes CVMM_FLAG_ROWS_SCALED only for a weighted route-input
+    selection whose x is in the 16-bit op dtype."""
+    fake = ctypes.c_void_p(256)
+    args = [None, 7, 1, 16, None, 0, 4, 16, 8, 128, 8, 1, None, None, None, 1, None, None, None, 0, 1,
+            2, None, 2, 1, 8]
+    assert lib.cvmm_fwd_keep_scaled(*args, None, None, 0, None, 0, None) == 1
+    written = ctypes.c_int32(5)
+    assert lib.cvmm_fwd_keep_scaled(*args, None, ctypes.addressof(written), 0, None, 0, None) == 1
+    assert written.value == 0 and b"dtype" in lib.cvmm_last_error()
+
+    def bwd_w(x_dtype, out_index, rw, flags):
+        return lib.cvmm_bwd_w(fake, x_dtype, 8, 16, fake, N.BF16, 2, 8, 4, 16, 8, fake, fake, out_index, 8, fake,
+                              rw, N.F32, 4, N.BF16, fake, N.F32, 128, 8, 1, flags, fake, 1 << 30, None)
+    assert bwd_w(N.BF16, fake, fake, N.FLAG_ROWS_SCALED) == 1          # token input
+    assert b"ROWS_SCALED" in lib.cvmm_last_error()
+    assert bwd_w(N.BF16, None, None, N.FLAG_ROWS_SCALED) == 1          # unweighted
+    assert bwd_w(N.F32, None, fake, N.FLAG_ROWS_SCALED) == 1           # rows not in the op dtype
 
 
 def test_missing_library_raises(monkeypatch, tmp_path):
