@@ -23,6 +23,7 @@ hipError_t launch_wgrad_f32(const WgradParams& p, hipStream_t stream);
 hipError_t launch_routed_gemm_nt_bf16(const GemmParams& p, hipStream_t stream);
 hipError_t launch_routed_gemm_nt_f16(const GemmParams& p, hipStream_t stream);
 bool routed_gemm_ring_applies(const GemmParams& p, int32_t op);
+bool routed_gemm_panel_applies(const GemmParams& p, int32_t op);
 
 // Fast path (DMA-staged, 16-bit k-contiguous operands) when eligible, else the
 // general kernel (any storage type / stride / width).
@@ -35,6 +36,12 @@ static bool nt_eligible(const GemmParams& p, int32_t op) {
   if (!common) return false;
   if (p.b_sk == 1) return p.b_sn % 8 == 0;
   return p.b_sn == 1 && p.b_sk % 8 == 0 && p.N % 8 == 0 && routed_gemm_ring_applies(p, op);
+}
+
+// Whether launch_routed_gemm runs the small-K (panel) kernel for p: the only
+// kernel that writes xs_out.
+static bool routed_gemm_is_panel(const GemmParams& p, int32_t op) {
+  return !small_gemm_eligible(p, op) && nt_eligible(p, op) && routed_gemm_panel_applies(p, op);
 }
 
 hipError_t launch_routed_gemm(const GemmParams& p, int32_t op, hipStream_t s) {
@@ -885,8 +892,19 @@ static int fwd_core(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld
   }
   p.epi = kEpiStore; p.out = ybuf; p.out_dtype = out_dtype; p.out_ld = d_out; p.out_rows = n_routes;
   p.o_idx = nullptr;
+  // route input kept for the weight gradient: the small-K kernel writes the
+  // scaled rows from its activation fragments (the rows cvmm_bwd_w scales)
+  const bool keep = scaled_rows != nullptr && scaled_written != nullptr && out_index == nullptr &&
+                    x_rows == n_routes && out_dtype == op_dtype && (op_dtype == kBF16 || op_dtype == kF16) &&
+                    routed_gemm_is_panel(p, op_dtype);
+  if (keep) {
+    p.xs_out = scaled_rows;
+    p.xs_w = rw;
+    p.xs_w_dtype = rw_dtype;
+  }
   r = check_launch(timed(CVMM_KC_GEMM_FWD, s, [&] { return launch_routed_gemm(p, op_dtype, s); }), "cvmm_fwd(gemm)");
   if (r) return r;
+  if (keep) *scaled_written = 1;
   return check_launch(timed_combine(s, [&] { return launch_combine_rows(ybuf, out_dtype, d_out, inv, rp, offs + (n_experts - 1), rw, rw_dtype, out_dtype, out_rows, reduce_k, d_out,
                                           out_dtype, out, out_dtype, out_ld, s); }),
                       "cvmm_fwd(combine)");

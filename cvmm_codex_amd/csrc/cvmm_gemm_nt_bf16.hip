@@ -9,4 +9,6 @@ hipError_t launch_routed_gemm_nt_bf16(const GemmParams& p, hipStream_t stream) {
 // Whether the fast-path dispatch runs the ring kernel for these parameters
 // (the only kernel with the activation epilogue); same rules for f16.
 bool routed_gemm_ring_applies(const GemmParams& p, int32_t op) { return ring_eligible(p, op); }
+
+bool routed_gemm_panel_applies(const GemmParams& p, int32_t op) { return panel_eligible(p, op); }
 }  // namespace cvmm

@@ -346,6 +346,34 @@ __global__ __launch_bounds__(kGemmThreads, (PanelCfg<KP, BN, WM>::OCC)) void rou
   issue_fence();
   if (T > 1) issue(1, ring1);
   issue_fence();
+  // The activation rows scaled by their routing weights (xs_out), from the
+  // fragments in registers: rnd_op(rnd_op(w) * a), each row once (row block j
+  // of the tile by group j % G of its min(groups, 4) workgroups).  Issued
+  // after the first weight DMAs, so the fragment loads' wait leaves those in
+  // flight; the extra stores only make the tile waits below stricter.
+  if (p.xs_out != nullptr) {
+    const int64_t grp = id % n_groups;
+    const int64_t G = n_groups < 4 ? n_groups : 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = wm * 64 + j * 16 + fr;
+      const int64_t ar = meta.arow[m], wi = meta.widx[m];
+      if (grp != j % G || ar < 0 || wi < 0) continue;
+      const float sc = round_to(load_as_f32(p.xs_w, p.xs_w_dtype, wi), DTypeOf<OpT>::value);
+#pragma unroll
+      for (int ks = 0; ks < Cfg::KS; ++ks) {
+        const int k = (ks * 4 + fq) * 8;
+        if (k >= p.K) continue;
+        Chunk16 in, o;
+        in.u = af[j][ks];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          reinterpret_cast<OpT*>(&o)[i] = from_f32<OpT>(sc * to_f32(reinterpret_cast<const OpT*>(&in)[i]));
+        *reinterpret_cast<uint4*>(static_cast<OpT*>(p.xs_out) + ar * p.K + k) = o.u;
+      }
+    }
+  }
+  issue_fence();
   // three statically named buffers: every LDS access names its buffer, so the
   // compiler can tell the in-flight DMA targets from the buffer being read
   for (int t = 0; t < T; t += 3) {

@@ -84,6 +84,12 @@ struct GemmParams {
   // whose expert id is outside [0, E), sorted past offsets[E - 1]; done by the
   // workgroups past the last m-tile (direct per-route stores only)
   int32_t zero_unrouted;
+  // small-K kernel only (routed_gemm_is_panel): also write every tile row's
+  // activation row scaled by its routing weight, xs_out[arow][k] =
+  // rnd_op(rnd_op(xs_w[widx]) * a[arow][k]) ([a_rows][K], op dtype); NULL: no
+  int32_t xs_w_dtype;
+  void* xs_out;
+  const void* xs_w;
 };
 constexpr int32_t kTokenMajorMaxExperts = 256;
 

@@ -308,9 +308,10 @@ std::tuple<OptT, OptT> cast_keys(const Tensor& keys, int64_t op_id, bool want_t,
 // (a [E, d_in, d_out] copy, or an interleaved copy already viewed so).
 Tensor copy_view(const Tensor& copy, bool is_t) { return is_t ? copy.transpose(1, 2) : copy; }
 
-// `scaled` (not NULL): a weighted route-input call whose top-k sum the
-// library takes as the dense GEMM keeps its scaled route rows there for the
-// weight gradient (cvmm_fwd_keep_scaled); left undefined otherwise.
+// `scaled` (not NULL): a weighted route-input call keeps its scaled route
+// rows there for the weight gradient where the library makes them anyway
+// (cvmm_fwd_keep_scaled: the dense top-k sum, or the small-K routed product's
+// activation fragments); left undefined otherwise.
 Tensor cvmm_forward_impl(const Tensor& x, const Tensor& keys, const OptT& keys_op, bool keys_op_is_t, const Tensor& sel,
                const Tensor& sel_index, const OptT& out_index, const Tensor& offsets, const OptT& route_pos,
                const OptT& rw, int64_t op_id, int64_t out_id, int64_t flags, int64_t stream,
@@ -359,7 +360,8 @@ Tensor cvmm_forward_impl(const Tensor& x, const Tensor& keys, const OptT& keys_o
   if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, opts(x, at::kByte));
   if (scaled != nullptr && rwf.has_value() && !oi.has_value() && xf.size(0) == R && outd == od &&
       (op == at::kBFloat16 || op == at::kHalf) && !(flags & CVMM_FLAG_ATOMIC_REDUCE) &&
-      cvmm_topk_dense(out_rows, (int32_t)E, d_in, d_out, k, od) == 1) {
+      (cvmm_topk_dense(out_rows, (int32_t)E, d_in, d_out, k, od) == 1 || d_in <= 128)) {
+    // (the dense sum, or a small-K routed product: the two that keep them)
     Tensor xs = at::empty({R, d_in}, opts(x, op));
     int32_t written = 0;
     check(cvmm_fwd_keep_scaled(ptr(xf), dtype_id(xf.scalar_type()), xf.size(0), xf.stride(0), ptr(kv),

@@ -320,16 +320,19 @@ int cvmm_fwd(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld,
              int32_t flags, void* workspace, size_t workspace_bytes, void* stream);
 
 /* cvmm_fwd that keeps the scaled route rows of a weighted top-k sum for the
- * backward.  When the call takes the sum as the dense GEMM (cvmm_topk_dense)
- * over route input (out_index NULL, x_rows == n_routes) with a 16-bit op and
- * out_dtype == op_dtype, the GEMM's operand rows x'_r = rnd_op(rnd_op(w_r) *
- * rnd_op(x_r)) -- bit for bit the rows cvmm_bwd_w would scale -- are written
- * to scaled_rows ([n_routes][d_in], op dtype, row stride d_in) instead of the
- * workspace, and *scaled_written is set to 1; otherwise nothing is written
- * there and *scaled_written is 0.  cvmm_bwd_w with CVMM_FLAG_ROWS_SCALED then
- * takes them as x, without its own scaling pass.  Same workspace as cvmm_fwd.
- * No counterpart in the reference (which scales inside its kernels): it saves
- * the weight gradient a read and a write of the route rows. */
+ * backward.  For route input (out_index NULL, x_rows == n_routes) with a
+ * 16-bit op and out_dtype == op_dtype, where the call makes them anyway --
+ * the dense GEMM's operand rows (cvmm_topk_dense), or the activation
+ * fragments of the small-K routed product (d_in <= 128, 16-byte aligned
+ * op-dtype rows and keys) -- the rows x'_r = rnd_op(rnd_op(w_r) * rnd_op(x_r)),
+ * bit for bit the rows cvmm_bwd_w would scale, are written to scaled_rows
+ * ([n_routes][d_in], op dtype, row stride d_in) and *scaled_written is set to
+ * 1; otherwise nothing is written there and *scaled_written is 0.  Rows of
+ * routes whose expert id is outside [0, E) may be left unwritten (no product
+ * reads them).  cvmm_bwd_w with CVMM_FLAG_ROWS_SCALED then takes them as x,
+ * without its own scaling pass.  Same workspace as cvmm_fwd.  No counterpart
+ * in the reference (which scales inside its kernels): it saves the weight
+ * gradient a read and a write of the route rows. */
 int cvmm_fwd_keep_scaled(const void* x, int32_t x_dtype, int64_t x_rows, int64_t x_ld,
                          const void* keys, int32_t keys_dtype, int32_t n_experts, int64_t d_in, int64_t d_out,
                          int64_t k_se, int64_t k_si, int64_t k_sj,

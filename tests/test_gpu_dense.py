@@ -300,16 +300,21 @@ def test_dense_topk_rows_not_16_byte_aligned(dense):
     assert U.norm_rel(U.to_np(y), exp["out"]) <= 2e-2
 
 
-def test_kept_scaled_rows_give_the_weight_gradient_bits(dense):
-    """cvmm_fwd_keep_scaled: the dense weighted forward over route input keeps
-    its operand rows x'_r = rnd(rnd(w_r) * x_r) (equal bit for bit to the same
-    product in torch), its output is cvmm_fwd's, and cvmm_bwd_w given those
-    rows with CVMM_FLAG_ROWS_SCALED writes the bits of its own scaling pass.
-    Off the dense path nothing is kept."""
+@pytest.mark.parametrize("mode,D,kept", [
+    (2, 64, True),      # dense top-k sum: its operand rows
+    (1, 64, True),      # route buffer, small-K product: its activation fragments
+    (1, 256, False),    # route buffer, long-K product: nothing kept
+])
+def test_kept_scaled_rows_give_the_weight_gradient_bits(mode, D, kept):
+    """cvmm_fwd_keep_scaled: a weighted forward over route input keeps the
+    rows x'_r = rnd(rnd(w_r) * x_r) where it makes them (equal bit for bit to
+    the same product in torch), its output is cvmm_fwd's, and cvmm_bwd_w given
+    those rows with CVMM_FLAG_ROWS_SCALED writes the bits of its own scaling
+    pass.  Where the product makes no such rows nothing is written."""
     import ctypes
     lib = N.lib()
-    B, T, D, H, E, K = 2, 96, 64, 128, 32, 16
-    x, keys, sel, w, go = _case(41, B, T, D, H, E, K, True, True)
+    B, T, H, E, K = 2, 96, 128, 32, 16
+    x, keys, sel, w, go = _case(41 + D, B, T, D, H, E, K, True, True)
     x, keys, w, go = x.cuda(), keys.cuda(), w.cuda(), go.cuda()
     s = C.cvmm_prepare_sel2(sel.cuda(), w, route_input=True)
     s._resolve(E)
@@ -320,14 +325,17 @@ def test_kept_scaled_rows_give_the_weight_gradient_bits(dense):
     assert s.out_index is None and rpos is not None
     xr = x.reshape(R, D).contiguous()
     wf = w.reshape(-1).contiguous()
+    # the long-K product reads a [E][d_out][d_in] copy: keys as the op-dtype
+    # per-expert layout the fast kernels take (k contiguous)
+    kt = keys.to(torch.bfloat16).transpose(1, 2).contiguous()
     st = N.stream_of(x.device)
     bf = N.BF16
 
     def fwd(keep):
         out = torch.empty(Tn, H, dtype=torch.bfloat16, device="cuda")
         ws_b = lib.cvmm_fwd_workspace_bytes(R, E, D, H, Tn, bf, bf, 1, 1, 0)
-        ws = torch.full((ws_b,), 0x5A, dtype=torch.uint8, device="cuda")
-        args = [N.ptr(xr), bf, R, D, N.ptr(keys), N.F32, E, D, H, keys.stride(0), keys.stride(1), keys.stride(2),
+        ws = torch.full((max(ws_b, 1),), 0x5A, dtype=torch.uint8, device="cuda")
+        args = [N.ptr(xr), bf, R, D, N.ptr(kt), bf, E, D, H, kt.stride(0), 1, kt.stride(1),
                 N.ptr(s.sel), N.ptr(s.sel_index), None, R, N.ptr(offs), N.ptr(rpos), N.ptr(wf), N.F32, K, bf,
                 N.ptr(out), bf, Tn, H]
         if not keep:
@@ -348,21 +356,21 @@ def test_kept_scaled_rows_give_the_weight_gradient_bits(dense):
                                dw.stride(0), dw.stride(1), dw.stride(2), flags, N.ptr(ws), ws_b, st), "cvmm_bwd_w")
         return dw
 
-    out_plain, _, _ = fwd(False)
-    out_keep, xs, written = fwd(True)
-    torch.cuda.synchronize()
-    assert written == 1
+    assert lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, mode) == 0
+    try:
+        out_plain, _, _ = fwd(False)
+        out_keep, xs, written = fwd(True)
+        torch.cuda.synchronize()
+    finally:
+        lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 0)
     assert torch.equal(out_keep, out_plain)
+    if not kept:
+        assert written == 0 and bool((xs == 7.0).all())
+        return
+    assert written == 1
     ref = (wf.to(torch.bfloat16).float()[:, None] * xr.float()).to(torch.bfloat16)
     assert torch.equal(xs, ref)
     dw_scaled_here = bwd_w(xr, 0, True)
     dw_kept = bwd_w(xs, N.FLAG_ROWS_SCALED, False)
     torch.cuda.synchronize()
     assert torch.equal(dw_kept, dw_scaled_here)
-
-    # the route-buffer path keeps nothing
-    assert lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 1) == 0
-    _, xs2, written2 = fwd(True)
-    torch.cuda.synchronize()
-    assert written2 == 0
-    assert bool((xs2 == 7.0).all())
