@@ -40,7 +40,9 @@ inline CastArgs<OutT> make_cast_args(const void* keys, int64_t se, int64_t si, i
 // unit column stride, 16-byte aligned rows, d_in and d_out multiples of 64:
 // read as float4 rows (16 threads per 256-byte row), written to kn as 8-byte
 // pieces of the same rows and, through a padded fp32 LDS tile, to kt as
-// 16-byte pieces of its rows (8 consecutive d_in values per thread).  RNE,
+// 16-byte pieces of its rows (8 consecutive d_in values per thread); a tile
+// with kn alone goes 8 values per thread, one 16-byte store each (the
+// 8-byte stores cost the SwitchHead value projection's cast ~9 us).  RNE,
 // the rounding of the reference's in-register cast (cvmm.py:198-204).
 // LDS of one cast block: the fp32 tile, 64 rows of up to 128 columns plus
 // one padding column (the launches that cast provide it).
@@ -52,6 +54,26 @@ __device__ __forceinline__ void cast_tile_vec(const CastArgs<OutT>& a, int64_t e
   float(*tile)[65] = reinterpret_cast<float(*)[65]>(lds);
   const int64_t i0 = ti * 64, j0 = tj * 64;
   const int t = threadIdx.x;
+  if (a.kt == nullptr) {
+    // kn only: 8 consecutive values of a row per thread, one 16-byte store
+    const int c8 = (t & 7) * 8;
+    float4 v[2][2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float* src = a.keys + e * a.se + (i0 + (t >> 3) + 32 * q) * a.si + j0 + c8;
+      v[q][0] = *reinterpret_cast<const float4*>(src);
+      v[q][1] = *reinterpret_cast<const float4*>(src + 4);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      union { uint4 u; OutT h[8]; } pk;
+      const float f[8] = {v[q][0].x, v[q][0].y, v[q][0].z, v[q][0].w, v[q][1].x, v[q][1].y, v[q][1].z, v[q][1].w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) pk.h[k] = from_f32<OutT>(f[k]);
+      *reinterpret_cast<uint4*>(a.kn + e * a.n_se + (i0 + (t >> 3) + 32 * q) * a.n_sr + j0 + c8) = pk.u;
+    }
+    return;
+  }
   const int c4 = (t & 15) * 4;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
