@@ -379,10 +379,13 @@ def cpu_baseline(proj: W.Projection, cap_s: float = 120.0):
 
 
 def load_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of a kernel class from its profile.sh counters
+    (profiles/traffic_<class>_<workload>.json), None where none were taken."""
     path = os.path.join(ROOT, "profiles", f"traffic_{kernel}_{workload}.json")
     if os.path.exists(path):
         with open(path) as f:
-            return json.load(f).get("bytes_per_launch")
+            d = json.load(f)
+        return d.get("bytes_per_launch") if isinstance(d, dict) else None
     return None
 
 

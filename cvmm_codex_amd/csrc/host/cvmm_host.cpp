@@ -10,6 +10,7 @@
 // (cvmm.py:1796-1803), cvmm_triton (cvmm.py:814-867) with the weighted combine
 // (cvmm.py:1543-1545), and CVMM.backward's products (cvmm.py:1552-1755).
 #include <torch/extension.h>
+#include <c10/hip/HIPGuard.h>
 #include <c10/hip/HIPStream.h>
 
 #include <map>
@@ -111,17 +112,42 @@ at::TensorOptions opts(const Tensor& like, at::ScalarType dt) {
 // so they can share it.
 struct Scratch {
   Tensor buf;
-  size_t clean = 0;  // length of the prefix known to be zero
+  size_t clean = 0;       // length of the prefix known to be zero
+  bool captured = false;  // a HIP graph capture recorded kernels that use buf
 };
 std::mutex g_mu;
 std::map<std::pair<int, int64_t>, Scratch> g_sort_ws, g_wgrad_ws;
+// Kept buffers replaced by larger ones after a graph capture used them: the
+// graph's replays still read and write them, so they stay allocated until the
+// process ends instead of going back to the allocator.
+std::vector<Tensor> g_retired;
+
+bool stream_capturing(int64_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing((hipStream_t)(uintptr_t)stream, &st) == hipSuccess &&
+         st == hipStreamCaptureStatusActive;
+}
+
+// The kept scratch of `s` with at least `bytes`, (re)allocated -- and zeroed
+// when `zero` -- on `stream` itself, the stream the kernels that use it run on.
+// Call with g_mu held.
+Tensor& kept_scratch(Scratch& s, const Tensor& like, int64_t stream, size_t bytes, bool zero) {
+  if (!s.buf.defined() || (size_t)s.buf.numel() < bytes) {
+    if (s.buf.defined() && s.captured) g_retired.push_back(s.buf);
+    c10::hip::HIPStreamGuard guard(
+        c10::hip::getStreamFromExternal((hipStream_t)(uintptr_t)stream, like.get_device()));
+    const int64_t n = (int64_t)std::max<size_t>(bytes, 1);
+    s.buf = zero ? at::zeros({n}, opts(like, at::kByte)) : at::empty({n}, opts(like, at::kByte));
+    s.clean = zero ? (size_t)n : 0;
+    s.captured = false;
+  }
+  if (stream_capturing(stream)) s.captured = true;
+  return s.buf;
+}
 
 Tensor sort_workspace(const Tensor& like, int64_t stream, size_t bytes) {
   std::lock_guard<std::mutex> lk(g_mu);
-  Scratch& s = g_sort_ws[{(int)like.get_device(), stream}];
-  if (!s.buf.defined() || (size_t)s.buf.numel() < bytes)
-    s.buf = at::empty({(int64_t)std::max<size_t>(bytes, 1)}, opts(like, at::kByte));
-  return s.buf;
+  return kept_scratch(g_sort_ws[{(int)like.get_device(), stream}], like, stream, bytes, false);
 }
 
 // ---------------------------------------------------------------------------
@@ -525,10 +551,7 @@ std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const
       // kernel; a kept workspace is zeroed once (when allocated)
       std::lock_guard<std::mutex> lk(g_mu);
       Scratch& s = g_wgrad_ws[{(int)x.get_device(), stream}];
-      if (!s.buf.defined() || (size_t)s.buf.numel() < ws_bytes) {
-        s.buf = at::zeros({(int64_t)std::max<size_t>(ws_bytes, 1)}, opts(x, at::kByte));
-        s.clean = (size_t)s.buf.numel();
-      }
+      kept_scratch(s, x, stream, ws_bytes, true);
       zeroed = ctr_bytes <= s.clean;
       s.clean = ctr_bytes;  // partial tiles follow the counter region
       ws = s.buf;

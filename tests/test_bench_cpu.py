@@ -64,3 +64,26 @@ def test_step_fabric_bytes(tmp_path):
     assert f["fabric_bytes_per_step"] == int(((200 * 2 + 50) * 10 + (10 * 2 + 30) * 20) * 1024 / 10)
     assert f["steps_traced"] == 10
     assert f["covered"] == pytest.approx(1900 / 2000)
+
+
+def test_committed_traffic_records_are_records():
+    """Every profiles/traffic_*.json that bench.py reads holds bytes per launch
+    (a class whose kernels the counters could not attribute gets no file)."""
+    import glob
+    import json
+    files = glob.glob(os.path.join(B.ROOT, "profiles", "traffic_*.json"))
+    assert files
+    for f in files:
+        with open(f) as fh:
+            d = json.load(fh)
+        assert isinstance(d, dict), f
+        key = "fabric_bytes_per_step" if os.path.basename(f).startswith("traffic_step_") else "bytes_per_launch"
+        assert d.get(key, 0) > 0, f
+
+
+def test_missing_or_empty_traffic_reads_as_none(tmp_path, monkeypatch):
+    monkeypatch.setattr(B, "ROOT", str(tmp_path))
+    os.makedirs(tmp_path / "profiles")
+    assert B.load_traffic("gemm_fwd", "nothing") is None
+    (tmp_path / "profiles" / "traffic_gemm_fwd_empty.json").write_text("null")
+    assert B.load_traffic("gemm_fwd", "empty") is None
