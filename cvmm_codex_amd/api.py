@@ -456,8 +456,12 @@ def cvmm_prepare_sel2(sel: Union[torch.Tensor, CVMMSel], w: Optional[torch.Tenso
                                      w)
         if route_input:
             route_index = sel.out_index if sel.out_index is not None else sel.sel_index
-            return CVMMSel(sel.raw_sel, sel.sel, route_index, None, w)
-        return CVMMSel(sel.raw_sel, sel.sel, sel.sel_index, sel.out_index, w)
+            out = CVMMSel(None, sel.sel, route_index, None, w)
+        else:
+            out = CVMMSel(None, sel.sel, sel.sel_index, sel.out_index, w)
+        # raw_sel as the parent holds it: its int32 copy is made if it is read
+        out._raw_sel, out._raw_src = sel._raw_sel, sel._raw_src
+        return out
 
     n_per_batch = sel.shape[-1]
     if not sel.is_cuda:
@@ -503,6 +507,9 @@ class _RouteTopK(torch.autograd.Function):
         ctx.save_for_backward(logits, sel)
         ctx.top_k, ctx.renormalize = top_k, renormalize
         ctx.mark_non_differentiable(sel, ssel, perm, tok, offsets, route_pos)
+        # no zero tensors for the six id outputs (autograd would fill one per
+        # output before every backward): their gradients arrive as None
+        ctx.set_materialize_grads(False)
         return w, sel, ssel, perm, tok, offsets, route_pos
 
     @staticmethod
