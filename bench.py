@@ -878,7 +878,7 @@ def main():
                          "wgrad), or of the whole step (step)")
     ap.add_argument("--tune", action="append", default=[], metavar="KNOB=VALUE",
                     help="set a library tuning knob (panel_tiles_per_wg, wgrad_order, wgrad_tile, gemm_order, "
-                         "dense_topk, sort_chunk, ring_tile) before running")
+                         "dense_topk, sort_chunk, ring_tile, wgrad_chunk) before running")
     args = ap.parse_args()
 
     if args.summarize:
@@ -899,7 +899,7 @@ def main():
     knobs = {"panel_tiles_per_wg": N.TUNE_PANEL_TILES_PER_WG, "wgrad_order": N.TUNE_WGRAD_ORDER,
              "gemm_order": N.TUNE_GEMM_ORDER,
              "wgrad_tile": N.TUNE_WGRAD_TILE, "dense_topk": N.TUNE_DENSE_TOPK,
-             "sort_chunk": N.TUNE_SORT_CHUNK, "ring_tile": N.TUNE_RING_TILE}
+             "sort_chunk": N.TUNE_SORT_CHUNK, "ring_tile": N.TUNE_RING_TILE, "wgrad_chunk": N.TUNE_WGRAD_CHUNK}
     for kv in args.tune:
         name, _, value = kv.partition("=")
         if name not in knobs:

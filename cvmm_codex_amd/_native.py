@@ -30,6 +30,7 @@ TUNE_WGRAD_TILE = 5
 TUNE_DENSE_TOPK = 6
 TUNE_SORT_CHUNK = 7
 TUNE_RING_TILE = 8
+TUNE_WGRAD_CHUNK = 9
 
 # kernel classes of the timing hooks (include/cvmm_hip.h CVMM_KC_*)
 KC_SORT, KC_OFFSETS, KC_CAST_KEYS, KC_GEMM_FWD, KC_GEMM_BWDX, KC_WGRAD, KC_COMBINE, KC_FILL, KC_ROUTE = (

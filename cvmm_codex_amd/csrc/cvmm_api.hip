@@ -77,13 +77,25 @@ hipError_t launch_wgrad(const WgradParams& p, int32_t op, hipStream_t s) {
 // launch_routed_gemm_op: 256x64 tiles for N <= 64, else 128x128).
 int routed_gemm_bm(int64_t N) { return N <= 64 ? 256 : 128; }
 
+// routes per weight-gradient chunk (CVMM_TUNE_WGRAD_CHUNK; 0: built in)
+static std::atomic<int64_t> g_wgrad_chunk{0};
+
 void wgrad_geometry(int64_t M, int64_t N, int64_t n_routes, int32_t n_experts, int32_t op_dtype, int64_t* split,
                     int64_t* grid_chunks, int64_t* max_slots, int64_t* tiles_mn) {
   const int64_t bk = op_dtype == kF32 ? 32 : 64;
-  // chunk = max(1024, 2 * mean routes per expert): balanced loads stay one
-  // chunk per expert; an expert above twice the mean is split.
-  int64_t s = n_experts > 0 ? (2 * n_routes + n_experts - 1) / n_experts : n_routes;
-  if (s < 1024) s = 1024;
+  // chunk = max(1024, 6 * mean routes per expert): an expert is split only
+  // when it holds over six times the mean.  Every split adds an fp32 partial
+  // of the expert's dW per chunk, written and read back; measured on the FFN
+  // stack (Zipf-skewed, up to 16x the mean on one expert) the weight gradient
+  // takes 670 / 570 / 516 / 534 / 644 / 710 us per launch at 2 / 4 / 6 / 8 /
+  // 12 / 16 x the mean (unsplit experts beyond that become the last
+  // workgroups to finish); balanced configs do not split at any of them.
+  const int64_t knob = g_wgrad_chunk.load();
+  int64_t s = knob;
+  if (s <= 0) {
+    s = n_experts > 0 ? (6 * n_routes + n_experts - 1) / n_experts : n_routes;
+    if (s < 1024) s = 1024;
+  }
   s = (s + bk - 1) / bk * bk;
   *split = s;
   *grid_chunks = (n_routes + s - 1) / s + n_experts;
@@ -410,6 +422,11 @@ int cvmm_tuning_set(int32_t knob, int64_t value) {
   if (knob == CVMM_TUNE_WGRAD_ORDER) {
     if (value < 0 || value > 3) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: weight-gradient order must be 0 .. 3");
     g_wgrad_order.store((int32_t)value);
+    return CVMM_OK;
+  }
+  if (knob == CVMM_TUNE_WGRAD_CHUNK) {
+    if (value < 0 || value > (1ll << 30)) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: weight-gradient chunk out of range");
+    g_wgrad_chunk.store(value);
     return CVMM_OK;
   }
   if (knob == CVMM_TUNE_WGRAD_TILE) {

@@ -112,9 +112,15 @@ int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launche
  *     Built in: the cost model of cvmm_topk_dense.
  *   CVMM_TUNE_SORT_CHUNK: routes per chunk of the selector sort (a multiple
  *     of 256; larger chunks, fewer scatter workgroups).  Built in: >= 1024,
- *     and the count matrix (chunks x (E + 1)) at most 64K entries.  A chunk
- *     that makes the sort's workspace exceed 1 MiB fails
+ *     and the count matrix (chunks x (E + 1)) at most 64K entries; a sort of
+ *     fewer than 8192 routes takes 8 chunks of at least 256.  A chunk that
+ *     makes the sort's workspace exceed 1 MiB fails
  *     cvmm_sort_routes_noalloc.
+ *   CVMM_TUNE_WGRAD_CHUNK: routes per chunk of the weight gradient's split
+ *     reduction (rounded up to the kernel's 32- or 64-route slices; an
+ *     expert with more routes is split into chunks whose fp32 partials are
+ *     summed in chunk order).  Built in: max(1024, 6 x the mean routes per
+ *     expert).  Workspace queries depend on it: query after setting it.
  *   CVMM_TUNE_RING_TILE: m-tile height of the long-K routed GEMM (K > 128)
  *     with 128-column tiles: 1 = 128 rows, 2 = 160 rows.  Built in: 160 rows
  *     unless the estimated dispatch rounds times the tile height come out
@@ -127,6 +133,7 @@ int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launche
 #define CVMM_TUNE_DENSE_TOPK 6
 #define CVMM_TUNE_SORT_CHUNK 7
 #define CVMM_TUNE_RING_TILE 8
+#define CVMM_TUNE_WGRAD_CHUNK 9
 int cvmm_tuning_set(int32_t knob, int64_t value);
 
 /* Whether a top-k sum -- out[t] = sum over the top_k routes (t, j) of

@@ -566,8 +566,19 @@ def _rand_case(seed, B, T, D, H, E, K, weighted=False, route_input=False, x_dt=t
     return x, keys, sel, w, go
 
 
+@pytest.fixture
+def small_wgrad_chunks():
+    """Weight-gradient chunks of 1024 routes, so that the hot expert of these
+    cases (~6000 routes) is split into several chunks."""
+    from cvmm_codex_amd import _native as N
+    lib = N.lib()
+    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_CHUNK, 1024) == 0
+    yield
+    lib.cvmm_tuning_set(N.TUNE_WGRAD_CHUNK, 0)
+
+
 @pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True), (True, False), (False, True)])
-def test_hot_expert_split_reduction(weighted, route_input, reduce_mode):
+def test_hot_expert_split_reduction(weighted, route_input, reduce_mode, small_wgrad_chunks):
     """One expert holds ~70% of the routes: its weight gradient is split into
     several route chunks reduced in a fixed order."""
     x, keys, sel, w, go = _rand_case(11, 4, 512, 128, 96, 8, 4, weighted, route_input, skew=0.7)
@@ -576,7 +587,27 @@ def test_hot_expert_split_reduction(weighted, route_input, reduce_mode):
     U.compare(got, exp, 2e-2)
 
 
-def test_weight_grad_is_deterministic():
+def test_hot_expert_unsplit_and_split_agree():
+    """The same hot-expert case under the built-in chunk (not split at ~6000
+    routes) and under 1024-route chunks (split, partials summed in chunk
+    order): both against the oracle, and within a few fp32 roundings of each
+    other."""
+    from cvmm_codex_amd import _native as N
+    lib = N.lib()
+    x, keys, sel, w, go = _rand_case(13, 4, 512, 128, 96, 8, 4, True, True, skew=0.7)
+    one = U.run_hip(x, keys, sel, w, go, True, True)
+    try:
+        assert lib.cvmm_tuning_set(N.TUNE_WGRAD_CHUNK, 1024) == 0
+        split = U.run_hip(x, keys, sel, w, go, True, True)
+    finally:
+        lib.cvmm_tuning_set(N.TUNE_WGRAD_CHUNK, 0)
+    exp = U.run_oracle(x, keys, sel, w, go, True, True)
+    U.compare(one, exp, 2e-2)
+    U.compare(split, exp, 2e-2)
+    assert U.norm_rel(U.to_np(one["keys_grad"]), U.to_np(split["keys_grad"])) <= 1e-5
+
+
+def test_weight_grad_is_deterministic(small_wgrad_chunks):
     x, keys, sel, w, go = _rand_case(12, 4, 512, 128, 96, 8, 4, True, True, skew=0.7)
     a = U.run_hip(x, keys, sel, w, go, True, True)
     b = U.run_hip(x, keys, sel, w, go, True, True)
@@ -589,7 +620,7 @@ def test_weight_grad_is_deterministic():
     (False, False, 512, 384, torch.bfloat16), (True, True, 384, 512, torch.bfloat16),
     (True, False, 512, 256, torch.float16),
 ])
-def test_weight_grad_order_and_tile_do_not_change_bits(weighted, route_input, D, H, amp):
+def test_weight_grad_order_and_tile_do_not_change_bits(weighted, route_input, D, H, amp, small_wgrad_chunks):
     """Every workgroup order and dW tile of the weight-gradient kernel sums
     each element over the same 32-route slices and the same split chunks in
     the same order: identical bits, hot expert (split into chunks) included.

@@ -147,6 +147,10 @@ def test_tuning_knob_rejects_bad_values(lib):
     assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 3) != 0
     assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 2) == 0
     assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 0) == 0
+    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_CHUNK, -1) != 0
+    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_CHUNK, 1 << 31) != 0
+    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_CHUNK, 2048) == 0
+    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_CHUNK, 0) == 0
     assert lib.cvmm_tuning_set(4, 32) != 0               # the retired reduce-GEMM threshold knob
 
 
