@@ -109,14 +109,14 @@ void wgrad_geometry(int64_t M, int64_t N, int64_t n_routes, int32_t n_experts, i
 int32_t wgrad_auto_tile(int64_t M, int64_t N, int64_t grid_chunks) {
   if (M < 256 || N < 256) return kWgTileBase;
   const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
-  return grid_chunks * tiles >= 4 * 256 ? kWgTile256x256 : kWgTileBase;
+  return grid_chunks * tiles >= 4 * 256 ? kWgTile256x256W8 : kWgTileBase;
 }
 
 // fp32 partial elements of one slot: the M x N rounding of the tile the
 // launch may take, at most (base or any coarser fast-path tile)
 int64_t wgrad_partial_elems(int64_t M, int64_t N) {
   int64_t best = 0;
-  for (int32_t c = kWgTileBase; c <= kWgTile256x256; ++c) {
+  for (int32_t c = kWgTileBase; c <= kWgTile256x256W8; ++c) {
     int bm, bn;
     wgrad_fast_tile(M, N, c, &bm, &bn);
     const int64_t e = ((M + bm - 1) / bm * bm) * ((N + bn - 1) / bn * bn);
@@ -415,7 +415,7 @@ int cvmm_tuning_set(int32_t knob, int64_t value) {
     return CVMM_OK;
   }
   if (knob == CVMM_TUNE_RING_TILE) {
-    if (value < 0 || value > 2) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: long-K tile choice must be 0, 1 or 2");
+    if (value < 0 || value > 3) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: long-K tile choice must be 0 to 3");
     g_ring_tile.store((int32_t)value);
     return CVMM_OK;
   }
@@ -430,7 +430,7 @@ int cvmm_tuning_set(int32_t knob, int64_t value) {
     return CVMM_OK;
   }
   if (knob == CVMM_TUNE_WGRAD_TILE) {
-    if (value < 0 || value > 4) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: weight-gradient tile must be 0 .. 4");
+    if (value < 0 || value > 5) return fail(CVMM_ERR_INVALID, "cvmm_tuning_set: weight-gradient tile must be 0 .. 5");
     g_wgrad_tile.store((int32_t)value);
     return CVMM_OK;
   }

@@ -133,13 +133,14 @@ __device__ bool gemm_schedule_tile(const GemmParams& p, int64_t tile, RouteMeta<
   return m.expert >= 0;
 }
 
-// The route metadata of every row of the tile gemm_schedule_tile found.
-template <int BM>
+// The route metadata of every row of the tile gemm_schedule_tile found (NT:
+// the workgroup's thread count).
+template <int BM, int NT = kGemmThreads>
 __device__ void gemm_route_meta(const GemmParams& p, RouteMeta<BM>& m) {
   const int tid = threadIdx.x;
   const int64_t row0 = m.row0;
   const int32_t rows = m.rows;
-  for (int r = tid; r < BM; r += kGemmThreads) {
+  for (int r = tid; r < BM; r += NT) {
     int64_t ar = -1, orow = -1, widx = -1, dgr = -1;
     float wv = 1.f;
     if (r < rows) {
@@ -168,10 +169,10 @@ __device__ void gemm_route_meta(const GemmParams& p, RouteMeta<BM>& m) {
 }
 
 // Both: the tile, then its rows' route metadata.
-template <int BM>
+template <int BM, int NT = kGemmThreads>
 __device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& m) {
   if (!gemm_schedule_tile<BM>(p, tile, m)) return false;
-  gemm_route_meta<BM>(p, m);
+  gemm_route_meta<BM, NT>(p, m);
   return true;
 }
 
@@ -185,7 +186,7 @@ __device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& 
 // n_surplus launched takes every n_surplus-th such route; a launch of
 // ceil(R / BM) + min(E, R) m-tiles has at least one surplus m-tile whenever
 // such routes exist.
-template <int BM>
+template <int BM, int NT = kGemmThreads>
 __device__ void zero_unrouted_cols(const GemmParams& p, const RouteMeta<BM>& m, int64_t tile, int64_t m_tiles,
                                    int64_t c0, int64_t c1, int64_t dg_tile) {
   const bool zero_out = p.zero_unrouted && p.out != nullptr;
@@ -204,7 +205,7 @@ __device__ void zero_unrouted_cols(const GemmParams& p, const RouteMeta<BM>& m, 
     if (!zero_out) continue;
     const int64_t oi = p.o_idx != nullptr ? p.o_idx[q] / p.o_div : q;
     if (oi < 0 || oi >= p.out_rows) continue;
-    for (int64_t c = c0 + threadIdx.x; c < c1; c += kGemmThreads) {
+    for (int64_t c = c0 + threadIdx.x; c < c1; c += NT) {
       store_from_f32(p.out, p.out_dtype, oi * p.out_ld + c, 0.f);
       if (p.act != 0 && p.aux != nullptr) store_from_f32(p.aux, p.out_dtype, oi * p.out_ld + c, 0.f);
     }

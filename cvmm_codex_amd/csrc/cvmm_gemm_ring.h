@@ -1,7 +1,9 @@
 // Routed GEMM with a DMA ring for a long inner dimension (K > 128, 16-bit
-// k-contiguous operands): the ff_up forward (K = d_in = 1024, N = 128), the
-// ff_down input gradient (K = 1024, N = 128) and the SwitchHead V forward /
-// O input gradient (K = 2048, N = 64).
+// operands): the ff_up forward (K = d_in = 1024, N = 128), the ff_down input
+// gradient (K = 1024, N = 128), the SwitchHead V forward / O input gradient
+// (K = 2048, N = 64) and both FFN-stack projections (K = 2048 / 512, N = 512
+// / 2048).  A workgroup is four waves (one 128- or 160-row tile of 128
+// columns, or 256 x 64) or eight (256 x 256).
 //
 // The k loop streams slices (BK = 64 or 32 values of k for every A row and B
 // row of the tile) through a ring of STAGES LDS buffers, STAGES - 1 of them
@@ -40,7 +42,7 @@
 
 namespace cvmm {
 
-template <int BM, int BN, int STAGES, int BK_>
+template <int BM, int BN, int STAGES, int BK_, int NW = 4>
 struct RingCfg {
   static constexpr int BK = BK_;                       // 16-bit values per k slice
   static constexpr int ROWB = BK * 2;                  // bytes per LDS row
@@ -50,13 +52,14 @@ struct RingCfg {
   static constexpr int A_BYTES = BM * ROWB;
   static constexpr int B_BYTES = BN * ROWB;
   static constexpr int SLICE_BYTES = A_BYTES + B_BYTES;
-  static constexpr int D = SLICE_BYTES / 4096;         // DMA instructions per wave per slice
-  static constexpr int DA = A_BYTES / 4096;            // ... of which for A
-  static constexpr int WN = BN / 64, WM = 4 / WN;      // wave grid: 64 columns per wave
-  static constexpr int WROWS = BM / WM;                // rows per wave: 64, or 80 (160-row tiles)
+  static constexpr int NT = NW * 64;                   // threads per workgroup
+  static constexpr int D = SLICE_BYTES / (NW * 1024);  // DMA instructions per wave per slice
+  static constexpr int WN = BN / 64, WM = NW / WN;     // wave grid: 64 columns per wave
+  static constexpr int WROWS = BM / WM;                // rows per wave: 64, 80 or 128
   static constexpr int MB = WROWS / 16;                // 16-row MFMA blocks per wave
-  static_assert(WM * WN == 4 && WM * WROWS == BM && WROWS % 16 == 0, "4 waves of whole 16-row blocks");
-  static_assert(SLICE_BYTES % 4096 == 0, "whole DMA instructions per wave");
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  static_assert(WM * WN == NW && WM * WROWS == BM && WROWS % 16 == 0, "waves of whole 16-row blocks");
+  static_assert(SLICE_BYTES % (NW * 1024) == 0, "whole DMA instructions per wave");
   static_assert(STAGES >= 2 && STAGES <= 5, "ring depth");
   static_assert((STAGES - 2) * D < 64, "vmcnt range");
 };
@@ -98,15 +101,15 @@ __device__ __forceinline__ void lds_wait_tied_tr(lds_u32x2 (&x)[4][2], lds_u32x4
 // operand (the weight gradient's transposed reads).  One weight copy then
 // serves both products of a step.
 template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int Role, int BK, bool DG = false,
-          bool BNC = false>
-__global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(const GemmParams p) {
-  using Cfg = RingCfg<BM, BN, STAGES, BK>;
+          bool BNC = false, int NW = 4>
+__global__ __launch_bounds__(NW * 64, OCC) void routed_gemm_ring_kernel(const GemmParams p) {
+  using Cfg = RingCfg<BM, BN, STAGES, BK, NW>;
   constexpr int MB = Cfg::MB, WR = Cfg::WROWS;
   constexpr int ROWB_B = BNC ? BN * 2 : Cfg::ROWB;  // bytes per LDS row of a B slice
   constexpr int CPR_B = ROWB_B / 16;
   constexpr int A_INSTS = Cfg::A_BYTES / 1024;     // DMA instructions of a slice's A rows
   static_assert(Cfg::A_BYTES % 1024 == 0, "A and B rows in separate DMA instructions");
-  static_assert(!BNC || CPR_B == 8 || CPR_B == 16, "128- or 256-byte B rows");
+  static_assert(!BNC || CPR_B == 8 || CPR_B == 16 || CPR_B == 32, "128- to 512-byte B rows");
   static_assert(!RA || Cfg::KSS == 1, "read-ahead keeps one k step per slice");
   __shared__ __attribute__((aligned(1024))) char ring[STAGES * Cfg::SLICE_BYTES];
   __shared__ RouteMeta<BM> meta;
@@ -120,8 +123,8 @@ __global__ __launch_bounds__(kGemmThreads, OCC) void routed_gemm_ring_kernel(con
   const int64_t ntile = id % n_ntiles;
   const int64_t n0 = ntile * BN;
 
-  if (!gemm_schedule<BM>(p, tile, meta)) {
-    zero_unrouted_cols<BM>(p, meta, tile, gridDim.x / n_ntiles, n0, n0 + BN, ntile);
+  if (!gemm_schedule<BM, Cfg::NT>(p, tile, meta)) {
+    zero_unrouted_cols<BM, Cfg::NT>(p, meta, tile, gridDim.x / n_ntiles, n0, n0 + BN, ntile);
     return;
   }
   const int32_t expert = meta.expert;
@@ -498,7 +501,7 @@ inline bool ring_eligible(const GemmParams& p, int32_t op) {
          (reinterpret_cast<uintptr_t>(p.out) % 16) == 0 && ((size_t)p.out_ld * esz) % 16 == 0;
 }
 
-template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int BK, bool BNC>
+template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int BK, bool BNC, int NW>
 hipError_t launch_routed_gemm_ring_b(const GemmParams& p_in, hipStream_t stream) {
   GemmParams p = p_in;
   p.token_major = resolve_token_major(p);
@@ -509,22 +512,24 @@ hipError_t launch_routed_gemm_ring_b(const GemmParams& p_in, hipStream_t stream)
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
   // the routing-weight gradient only ever comes with the grad-input product
   if (p.role == 0 && p.dg == nullptr)
-    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 0, BK, false, BNC>),
-                       dim3((unsigned)grid), dim3(kGemmThreads), 0, stream, p);
+    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 0, BK, false, BNC, NW>),
+                       dim3((unsigned)grid), dim3(NW * 64), 0, stream, p);
   else if (p.dg == nullptr)
-    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1, BK, false, BNC>),
-                       dim3((unsigned)grid), dim3(kGemmThreads), 0, stream, p);
+    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1, BK, false, BNC, NW>),
+                       dim3((unsigned)grid), dim3(NW * 64), 0, stream, p);
+  else if constexpr (BN <= 128)  // the routing-weight gradient's partials are per 64 or 128 columns
+    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1, BK, true, BNC, NW>),
+                       dim3((unsigned)grid), dim3(NW * 64), 0, stream, p);
   else
-    hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1, BK, true, BNC>),
-                       dim3((unsigned)grid), dim3(kGemmThreads), 0, stream, p);
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
 // k-contiguous weights ([n][k] rows), or n-contiguous ones (BNC, b_sn == 1)
-template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int BK>
+template <typename OpT, typename OutT, int BM, int BN, int STAGES, int OCC, bool RA, int BK, int NW = 4>
 hipError_t launch_routed_gemm_ring_t(const GemmParams& p, hipStream_t stream) {
-  if (p.b_sk == 1) return launch_routed_gemm_ring_b<OpT, OutT, BM, BN, STAGES, OCC, RA, BK, false>(p, stream);
-  return launch_routed_gemm_ring_b<OpT, OutT, BM, BN, STAGES, OCC, RA, BK, true>(p, stream);
+  if (p.b_sk == 1) return launch_routed_gemm_ring_b<OpT, OutT, BM, BN, STAGES, OCC, RA, BK, false, NW>(p, stream);
+  return launch_routed_gemm_ring_b<OpT, OutT, BM, BN, STAGES, OCC, RA, BK, true, NW>(p, stream);
 }
 
 // 128 x 128 tiles: two 32 KB slices of 64 k (128-byte rows: each gathered A
@@ -554,10 +559,29 @@ inline bool ring_tall_tiles(const GemmParams& p) {
   return 20 * 160 * rounds(160) <= 21 * 128 * rounds(128);
 }
 
+// 256 x 256 tiles of eight waves (2 x 4 waves of 128 x 64; two 64 KB slices
+// + metadata = 137 KB, one workgroup per CU): each gathered A row piece
+// serves twice the columns of a 128-column tile.  At the FFN stack (K =
+// 2048 / 512, N = 512 / 2048, ~4.5-18 dispatch rounds) the forward went 508
+// -> 452 us and the grad-input without the routing-weight gradient 548 ->
+// 476 us per launch.  Four waves of 128 x 128 (the same tile), 320 x 128,
+// 256 x 128 and 128 x 256 of eight waves, and 32-k slices in a 4-slice ring
+// all measured slower or no faster.  Taken where N is a multiple of 256 and
+// the grid fills at least two rounds of 256 CUs (tile count estimated as R /
+// 256 + E / 2), and never with the routing-weight gradient (its partials are
+// per 128 columns).
+inline bool ring_wide_tiles(const GemmParams& p) {
+  if (p.dg != nullptr || p.N % 256 != 0 || p.ring_tile == 1 || p.ring_tile == 2) return false;
+  if (p.ring_tile == 3) return true;
+  const int64_t tiles = ((p.n_routes + 255) / 256 + p.n_experts / 2) * (p.N / 256);
+  return tiles >= 2 * 256;
+}
+
 template <typename OpT, typename OutT>
 hipError_t launch_routed_gemm_ring_out(const GemmParams& p, hipStream_t stream) {
   if (p.N <= 64) return launch_routed_gemm_ring_t<OpT, OutT, 256, 64, 3, 2, true, 32>(p, stream);
-  if (p.ring_tile == 2 || (p.ring_tile == 0 && ring_tall_tiles(p)))
+  if (ring_wide_tiles(p)) return launch_routed_gemm_ring_t<OpT, OutT, 256, 256, 2, 1, false, 64, 8>(p, stream);
+  if (p.ring_tile == 2 || ((p.ring_tile == 0 || p.ring_tile == 3) && ring_tall_tiles(p)))
     return launch_routed_gemm_ring_t<OpT, OutT, 160, 128, 2, 2, false, 64>(p, stream);
   return launch_routed_gemm_ring_t<OpT, OutT, 128, 128, 2, 2, false, 64>(p, stream);
 }

@@ -167,20 +167,21 @@ __host__ __device__ inline void wgrad_tile(int64_t M, int64_t N, int* bm, int* b
 // 128 x 128: 256 x 128, 128 x 256 or 256 x 256 (fewer bytes gathered per
 // flop; four waves of up to 128 x 128, one workgroup per CU).
 constexpr int32_t kWgTileBase = 0, kWgTile256x128 = 1, kWgTile128x256 = 2, kWgTile256x256 = 3;
+constexpr int32_t kWgTile256x256W8 = 4;  // 256 x 256 of eight waves
 __host__ __device__ inline void wgrad_fast_tile(int64_t M, int64_t N, int32_t choice, int* bm, int* bn) {
   wgrad_tile(M, N, bm, bn);
   if (*bm != 128 || *bn != 128) return;
   if (choice == kWgTile256x128) *bm = 256;
   else if (choice == kWgTile128x256) *bn = 256;
-  else if (choice == kWgTile256x256) { *bm = 256; *bn = 256; }
+  else if (choice == kWgTile256x256 || choice == kWgTile256x256W8) { *bm = 256; *bn = 256; }
 }
 // tiles_mn counts base tiles (the finest: one counter each, enough for any
 // coarser tile); partials are sized for the largest rounding of M x N.
 void wgrad_geometry(int64_t M, int64_t N, int64_t n_routes, int32_t n_experts, int32_t op_dtype,
                     int64_t* split, int64_t* grid_chunks, int64_t* max_slots, int64_t* tiles_mn);
 int64_t wgrad_partial_elems(int64_t M, int64_t N);
-// built-in tile choice (no knob): 256 x 256 where M, N >= 256 and the grid
-// holds >= 4 workgroups per CU, else the base tile
+// built-in tile choice (no knob): 256 x 256 of eight waves where M, N >= 256
+// and the grid holds >= 4 tiles per CU, else the base tile
 int32_t wgrad_auto_tile(int64_t M, int64_t N, int64_t grid_chunks);
 
 // ---------------------------------------------------------------------------

@@ -27,9 +27,11 @@
 //    stores dW.
 //  * Tiles: 128 x 128 (and 256 x 64 / 64 x 256 on a narrow side) at two
 //    workgroups per CU, each wave 64 x 64; or, for wide dW, 256 x 256 (or
-//    256 x 128 / 128 x 256) at one workgroup per CU, each wave up to 128 x 128
-//    with its accumulators in AGPRs.  Every tile sums each dW element over
-//    the same slices in the same order, so the tile choice never changes bits.
+//    256 x 128 / 128 x 256) at one workgroup per CU, each of four waves up to
+//    128 x 128 with its accumulators in AGPRs, or 256 x 256 of eight waves
+//    of 128 x 64 (two waves per SIMD: the FFN stack's launch 514 -> 485 us).
+//    Every tile sums each dW element over the same slices in the same
+//    order, so the tile choice never changes bits.
 // Workgroup orders (WgradParams::order): tile-major by default; chunk-major
 // and chunk-per-XCD for tuning.
 // LDS rows are swizzled at 16-byte granularity so that a transposed read's
@@ -67,7 +69,7 @@ struct Wg3Cfg {
   using TA = RouteSlice<BM>;                   // x rows: dW rows m0 .. m0 + BM
   using TB = RouteSlice<BN>;                   // dY rows: dW columns n0 .. n0 + BN
   static constexpr int NW = WM * WN, NT = NW * 64;
-  static_assert(NW == 4, "4 waves");
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   static constexpr int JM = BM / WM / 16, IN = BN / WN / 16;
   static constexpr int OCC = JM * IN <= 16 ? 2 : 1;  // workgroups per CU
   static_assert(JM * WM * 16 == BM && IN * WN * 16 == BN && JM >= 1 && IN >= 1, "wave grid");
@@ -134,7 +136,7 @@ __host__ __device__ inline bool wgrad_dw_vec(const WgradParams& p) {
 }
 
 template <typename OpT, int BM, int BN, int WM, int WN, int STAGES, bool WEIGHTED>
-__global__ __launch_bounds__(256, (BM / WM / 16) * (BN / WN / 16) <= 16 ? 2 : 1) void wgrad_v3_kernel(
+__global__ __launch_bounds__(WM * WN * 64, (BM / WM / 16) * (BN / WN / 16) <= 16 ? 2 : 1) void wgrad_v3_kernel(
     const WgradParams p) {
   using Cfg = Wg3Cfg<BM, BN, WM, WN, STAGES, WEIGHTED>;
   constexpr int JM = Cfg::JM, IN = Cfg::IN;
@@ -480,6 +482,8 @@ template <typename OpT>
 hipError_t launch_wgrad_v3_op(const WgradParams& p, hipStream_t stream) {
   int bm, bn;
   wgrad_fast_tile(p.M, p.N, wgrad_dw_vec(p) ? p.tile_choice : kWgTileBase, &bm, &bn);
+  if (bm == 256 && bn == 256 && wgrad_dw_vec(p) && p.tile_choice == kWgTile256x256W8)
+    return launch_wgrad_v3_t<OpT, 256, 256, 2, 4, 4>(p, stream);
   if (bm == 256 && bn == 256) return launch_wgrad_v3_t<OpT, 256, 256, 2, 2, 4>(p, stream);
   if (bm == 256 && bn == 128) return launch_wgrad_v3_t<OpT, 256, 128, 2, 2, 4>(p, stream);
   if (bm == 128 && bn == 256) return launch_wgrad_v3_t<OpT, 128, 256, 2, 2, 4>(p, stream);

@@ -99,8 +99,9 @@ int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launche
  *     Built in: 3 for the 16-bit kernel's 128 x 128 dW tile, else 2.
  *   CVMM_TUNE_WGRAD_TILE: dW tile of the 16-bit weight-gradient kernel where
  *     its base tile is 128 x 128 and dW is contiguous aligned fp32: 1 = 128 x
- *     128, 2 = 256 x 128, 3 = 128 x 256, 4 = 256 x 256.  Built in: 256 x 256
- *     when d_in, d_out >= 256 and the grid holds >= 4 workgroups per CU.
+ *     128, 2 = 256 x 128, 3 = 128 x 256, 4 = 256 x 256 of four waves, 5 =
+ *     256 x 256 of eight waves.  Built in: 256 x 256 of eight waves when
+ *     d_in, d_out >= 256 and the grid holds >= 4 tiles per CU.
  *   CVMM_TUNE_GEMM_ORDER: m-tile order of the routed GEMMs (forward, grad
  *     input), 1 = expert-major, 2 = token-major (tile j of every expert next
  *     to each other; up to 256 experts).  Built in: token-major for the
@@ -121,11 +122,14 @@ int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launche
  *     expert with more routes is split into chunks whose fp32 partials are
  *     summed in chunk order).  Built in: max(1024, 6 x the mean routes per
  *     expert).  Workspace queries depend on it: query after setting it.
- *   CVMM_TUNE_RING_TILE: m-tile height of the long-K routed GEMM (K > 128)
- *     with 128-column tiles: 1 = 128 rows, 2 = 160 rows.  Built in: 160 rows
+ *   CVMM_TUNE_RING_TILE: tile of the long-K routed GEMM (K > 128, N > 64):
+ *     1 = 128 x 128, 2 = 160 x 128, 3 = 256 x 256 of eight waves where N is
+ *     a multiple of 256 and no routing-weight gradient is taken (elsewhere
+ *     the built-in height).  Built in: 256 x 256 where it applies and the
+ *     grid fills two rounds of 256 CUs (the FFN stack); else 160 rows
  *     unless the estimated dispatch rounds times the tile height come out
  *     more than 5 % higher (the ff_up forward: one round of ~442 tiles
- *     instead of 544 tiles on 512 slots).  Both give the same bits. */
+ *     instead of 544 tiles on 512 slots).  All give the same bits. */
 #define CVMM_TUNE_PANEL_TILES_PER_WG 1
 #define CVMM_TUNE_WGRAD_ORDER 2
 #define CVMM_TUNE_GEMM_ORDER 3

@@ -633,7 +633,7 @@ def test_weight_grad_order_and_tile_do_not_change_bits(weighted, route_input, D,
     ref = None
     try:
         for order in (1, 2, 3):
-            for tile in (1, 2, 3, 4):
+            for tile in (1, 2, 3, 4, 5):
                 assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, order) == 0
                 assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, tile) == 0
                 got = U.run_hip(x, keys, sel, w, go, route_input, True, amp_dtype=amp)
@@ -694,27 +694,33 @@ def test_gemm_order_does_not_change_bits(weighted, route_input, skew):
     (True, True, 128, 256, 0.7),      # long-K weighted grad-input with the routing-weight gradient, hot expert
     (False, False, 384, 256, None),   # long-K forward, two n tiles
     (True, False, 256, 384, 0.0),     # both products long-K
+    (False, True, 512, 512, 0.5),     # both products 256 x 256 where chosen, hot expert
 ])
 def test_long_k_tile_height_does_not_change_bits(weighted, route_input, D, H, skew):
-    """128- and 160-row m-tiles of the long-K routed GEMM run every row's
-    k slices in the same order: identical bits, and the oracle's values."""
+    """128- and 160-row m-tiles of the long-K routed GEMM, and its eight-wave
+    256 x 256 tiles (where N is a multiple of 256 and no routing-weight
+    gradient is taken), run every row's k slices in the same order:
+    identical bits, and the oracle's values."""
     from cvmm_codex_amd import _native as N
     x, keys, sel, w, go = _rand_case(35, 4, 384, D, H, 12, 6, weighted, route_input, skew=skew)
     lib = N.lib()
+    runs = []
     try:
-        assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 1) == 0
-        a = U.run_hip(x, keys, sel, w, go, route_input, True)
-        assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 2) == 0
-        b = U.run_hip(x, keys, sel, w, go, route_input, True)
+        for t in (1, 2, 3):
+            assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, t) == 0
+            runs.append(U.run_hip(x, keys, sel, w, go, route_input, True))
     finally:
         lib.cvmm_tuning_set(N.TUNE_RING_TILE, 0)
-    for n in ("out", "x_grad", "keys_grad", "weights_grad"):
-        if a[n] is None:
-            assert b[n] is None
-        else:
-            assert torch.equal(a[n], b[n]), n
+    a = runs[0]
+    for t, b in zip((2, 3), runs[1:]):
+        for n in ("out", "x_grad", "keys_grad", "weights_grad"):
+            if a[n] is None:
+                assert b[n] is None
+            else:
+                assert torch.equal(a[n], b[n]), (t, n)
     exp = U.run_oracle(x, keys, sel, w, go, route_input, True)
-    U.compare(b, exp, 2e-2)
+    for b in runs[1:]:
+        U.compare(b, exp, 2e-2)
 
 
 @pytest.mark.parametrize("op", [torch.bfloat16, torch.float16])
@@ -726,6 +732,9 @@ def test_long_k_tile_height_does_not_change_bits(weighted, route_input, D, H, sk
     (64, 512, True, True, 0),       # grad-input 256 x 64 + routing-weight gradient (SwitchHead O)
     (512, 256, False, False, 1),    # both products long-K
     (200, 96, True, False, 0),      # d_in % 64 != 0: the last k slice part-filled
+    (512, 256, False, False, 3),    # both products 256 x 256, eight waves
+    (256, 512, False, True, 3),     # both 256 x 256, route input
+    (200, 512, True, False, 3),     # weighted forward 256 x 256 with a part-filled last k slice
 ])
 def test_long_k_reads_either_weight_orientation(D, H, weighted, route_input, tile, op):
     """The long-K routed GEMM reads the weights k-contiguous ([n][k] rows: the
@@ -778,15 +787,17 @@ def test_long_k_reads_either_weight_orientation(D, H, weighted, route_input, til
         assert U.norm_rel(U.to_np(grw).reshape(exp["weights_grad"].shape), exp["weights_grad"]) <= 2e-2
 
 
-def test_long_k_gelu_epilogue_tile_height_does_not_change_bits():
-    """The GELU epilogue of the long-K forward at both tile heights."""
+@pytest.mark.parametrize("H", [128, 512])
+def test_long_k_gelu_epilogue_tile_height_does_not_change_bits(H):
+    """The GELU epilogue of the long-K forward at every tile shape (256 x 256
+    where H is a multiple of 256)."""
     from cvmm_codex_amd import _native as N
     import cvmm_codex_amd.api as C
-    x, keys, sel, _, go = _rand_case(36, 4, 384, 256, 128, 12, 6)
+    x, keys, sel, _, go = _rand_case(36, 4, 384, 256, H, 12, 6)
     lib = N.lib()
     outs = []
     try:
-        for t in (1, 2):
+        for t in (1, 2, 3):
             assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, t) == 0
             xd, kd = x.cuda().requires_grad_(True), keys.cuda().requires_grad_(True)
             with torch.autocast("cuda", dtype=torch.bfloat16):
@@ -796,8 +807,9 @@ def test_long_k_gelu_epilogue_tile_height_does_not_change_bits():
             outs.append((y.detach(), xd.grad, kd.grad))
     finally:
         lib.cvmm_tuning_set(N.TUNE_RING_TILE, 0)
-    for u, v in zip(*outs):
-        assert torch.equal(u, v)
+    for other in outs[1:]:
+        for u, v in zip(outs[0], other):
+            assert torch.equal(u, v)
 
 
 @pytest.mark.parametrize("weighted,route_input", [(False, False), (True, True), (True, False)])

@@ -138,13 +138,14 @@ def test_tuning_knob_rejects_bad_values(lib):
     assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, -1) != 0
     assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, 3) == 0
     assert lib.cvmm_tuning_set(N.TUNE_WGRAD_ORDER, 0) == 0
-    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 5) != 0
+    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 6) != 0
     assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, -1) != 0
-    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 4) == 0
+    assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 5) == 0
     assert lib.cvmm_tuning_set(N.TUNE_WGRAD_TILE, 0) == 0
     assert lib.cvmm_tuning_set(N.TUNE_GEMM_ORDER, 3) != 0
     assert lib.cvmm_tuning_set(N.TUNE_GEMM_ORDER, 0) == 0
-    assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 3) != 0
+    assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 4) != 0
+    assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 3) == 0
     assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 2) == 0
     assert lib.cvmm_tuning_set(N.TUNE_RING_TILE, 0) == 0
     assert lib.cvmm_tuning_set(N.TUNE_WGRAD_CHUNK, -1) != 0
