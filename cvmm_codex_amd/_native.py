@@ -21,6 +21,9 @@ FLAG_COUNTERS_ZEROED = 2
 FLAG_COUNTS_READY = 16
 FLAG_ACCUMULATE = 32
 FLAG_ROWS_SCALED = 64
+# host-only flag of the extension's backward (never passed to the C ABI):
+# the weight gradient on a second stream, concurrent with the grad-input
+HOST_OVERLAP_BACKWARD = 1 << 48
 CAST_T_INTERLEAVED = 1
 CAST_N_INTERLEAVED = 2
 TUNE_PANEL_TILES_PER_WG = 1

@@ -476,6 +476,56 @@ Tensor gelu_backward(const Tensor& grad, const Tensor& pre, int64_t stream) {
 // grad-input's top-k columns per slice (cvmm_lowmem_chunk_size; 0: all).
 int64_t lowmem_chunk_of(int64_t flags) { return (flags >> 32) & 0xffff; }
 
+// Host flag (bit 48, never passed to the C ABI): the backward's weight
+// gradient runs on a second stream of the device, concurrent with the
+// grad-input and its top-k sum, which it does not depend on.
+constexpr int64_t kHostOverlapBackward = int64_t(1) << 48;
+
+// The second stream: one torch pool stream per device (default priority),
+// and the fork / join events, created once; record-and-wait pairs under a
+// lock.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex g_side_mu;
+std::map<int, SideStream> g_side;
+
+SideStream& side_stream(int dev) {
+  SideStream& ss = g_side[dev];
+  if (ss.stream == nullptr) {
+    ss.stream = c10::hip::getStreamFromPool(false, (c10::DeviceIndex)dev).stream();
+    c10::hip::HIPGuard guard((c10::DeviceIndex)dev);
+    TORCH_CHECK(hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) == hipSuccess &&
+                    hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) == hipSuccess,
+                "cvmm: event creation failed");
+  }
+  return ss;
+}
+
+// Work enqueued on `main` so far -> the side stream of the device: returns it.
+hipStream_t fork_to_side(int dev, hipStream_t main) {
+  std::lock_guard<std::mutex> lk(g_side_mu);
+  SideStream& ss = side_stream(dev);
+  TORCH_CHECK(hipEventRecord(ss.fork, main) == hipSuccess && hipStreamWaitEvent(ss.stream, ss.fork, 0) == hipSuccess,
+              "cvmm: stream fork failed");
+  return ss.stream;
+}
+
+// Makes `main` wait for the side stream's work when it goes out of scope
+// (every return and exception path of the backward after a fork).
+struct SideJoin {
+  int dev = -1;
+  hipStream_t main = nullptr;
+  ~SideJoin() {
+    if (dev < 0) return;
+    std::lock_guard<std::mutex> lk(g_side_mu);
+    SideStream& ss = side_stream(dev);
+    hipEventRecord(ss.join, ss.stream);
+    hipStreamWaitEvent(main, ss.join, 0);
+  }
+};
+
 // The token gradient of a token-input unweighted top-k sum taken over slices
 // of `chunk` top-k columns (cvmm_grouped_backward_lowmem, cvmm.py:1228-1338):
 // each slice of the selection is sorted on its own, its routes' rows go
@@ -532,6 +582,8 @@ std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const
   const int32_t rwd = rwf.has_value() ? dtype_id(rwf->scalar_type()) : 0;
   const int32_t od = (int32_t)op_id;
   OptT grad_x, grad_w, grad_rw;
+  // joins the side stream back into `stream` on every way out below
+  SideJoin join;
 
   if (need_grad_keys) {
     // the route rows the forward scaled (cvmm_fwd_keep_scaled), or x
@@ -539,6 +591,15 @@ std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const
     Tensor xs = pre_scaled ? *scaled_x
                            : rows_of(fast && x.scalar_type() != op ? x.to(op) : storage_for(x, op), d_in);
     grad_w = at::empty(keys.sizes(), opts(keys, keys.scalar_type()));
+    // with a grad-input to run as well, the weight gradient goes to the side
+    // stream once its inputs are enqueued: its temporaries are freed to the
+    // caller's stream, whose next work waits for the join
+    int64_t wstream = stream;
+    if ((flags & kHostOverlapBackward) && (need_grad_x || need_grad_rw)) {
+      wstream = (int64_t)(uintptr_t)fork_to_side(x.get_device(), (hipStream_t)(uintptr_t)stream);
+      join.dev = x.get_device();
+      join.main = (hipStream_t)(uintptr_t)stream;
+    }
     // a weighted route-input selection gets room for its scaled route rows
     // (none needed when the forward kept them)
     const size_t ws_bytes = cvmm_bwd_w_workspace_bytes_ex(R, (int32_t)E, d_in, d_out, od, 1,
@@ -550,8 +611,8 @@ std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const
       // the tile counters at the start of the workspace are left zero by the
       // kernel; a kept workspace is zeroed once (when allocated)
       std::lock_guard<std::mutex> lk(g_mu);
-      Scratch& s = g_wgrad_ws[{(int)x.get_device(), stream}];
-      kept_scratch(s, x, stream, ws_bytes, true);
+      Scratch& s = g_wgrad_ws[{(int)x.get_device(), wstream}];
+      kept_scratch(s, x, wstream, ws_bytes, true);
       zeroed = ctr_bytes <= s.clean;
       s.clean = ctr_bytes;  // partial tiles follow the counter region
       ws = s.buf;
@@ -562,7 +623,7 @@ std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const
                      dtype_id(g.scalar_type()), g.size(0), g.stride(0), (int32_t)E, d_in, d_out, tptr<int32_t>(s32),
                      tptr<int64_t>(si), tptr<int64_t>(oi), R, tptr<int64_t>(offsets), ptr(rwf), rwd, k, od,
                      ptr(grad_w), dtype_id(grad_w->scalar_type()), grad_w->stride(0), grad_w->stride(1),
-                     grad_w->stride(2), wflags, ptr(ws), (size_t)ws.numel(), (void*)stream),
+                     grad_w->stride(2), wflags, ptr(ws), (size_t)ws.numel(), (void*)wstream),
           "cvmm_bwd_w");
   }
 

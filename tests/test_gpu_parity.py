@@ -961,3 +961,28 @@ def test_small_fp32_problems(D, H, route_input):
     got = U.run_hip(x, keys, sel, w, go, route_input, False)
     exp = U.run_oracle(x, keys, sel, w, go, route_input, False)
     U.compare(got, exp, 1e-4)
+
+
+@pytest.mark.parametrize("weighted,route_input,D,H,lowmem", [
+    (False, False, 256, 128, 0),    # token input: route-buffer grad-input + top-k sum
+    (True, True, 128, 256, 0),      # weighted route input: routing-weight gradient too
+    (True, False, 512, 256, 0),     # weighted token input, both products long-K
+    (False, False, 128, 256, 2),    # low-memory slices of the top-k sum (an early return)
+])
+def test_backward_on_two_streams_gives_the_same_bits(weighted, route_input, D, H, lowmem, monkeypatch):
+    """With cvmm_overlap_backward the weight gradient runs on a second stream,
+    forked from and joined back into the caller's stream: the same kernels,
+    so every gradient has the one-stream bits, on every return path."""
+    x, keys, sel, w, go = _rand_case(71 + D + H + lowmem, 2, 256, D, H, 16, 4, weighted, route_input, skew=0.5)
+    monkeypatch.setattr(C, "cvmm_lowmem_chunk_size", lowmem)
+    runs = []
+    for overlap in (False, True, True):
+        monkeypatch.setattr(C, "cvmm_overlap_backward", overlap)
+        runs.append(U.run_hip(x, keys, sel, w, go, route_input, True))
+    for r in runs[1:]:
+        for n in ("out", "x_grad", "keys_grad", "weights_grad"):
+            if runs[0][n] is None:
+                assert r[n] is None
+            else:
+                assert torch.equal(runs[0][n], r[n]), n
+    U.compare(runs[1], U.run_oracle(x, keys, sel, w, go, route_input, True), 2e-2)
