@@ -180,15 +180,16 @@ __device__ bool gemm_schedule(const GemmParams& p, int64_t tile, RouteMeta<BM>& 
 // leaving the tile count in m.row0), for the routes no tile covers -- expert
 // id outside [0, E), sorted at or past offsets[E - 1]: when the call asks
 // for it, zero the columns [c0, c1) of their output rows (and GELU
-// pre-activation rows); and zero their routing-weight gradient partial of
-// n tile `dg_tile` (>= 0 when the caller covers exactly that n tile), so the
-// partials need no fill before the launch.  Surplus m-tile j of the
+// pre-activation rows); and zero their routing-weight gradient partials
+// dg_tile .. dg_tile + dg_count - 1 (dg_tile >= 0 when the caller covers
+// exactly those partials' columns), so the partials need no fill before the
+// launch.  Surplus m-tile j of the
 // n_surplus launched takes every n_surplus-th such route; a launch of
 // ceil(R / BM) + min(E, R) m-tiles has at least one surplus m-tile whenever
 // such routes exist.
 template <int BM, int NT = kGemmThreads>
 __device__ void zero_unrouted_cols(const GemmParams& p, const RouteMeta<BM>& m, int64_t tile, int64_t m_tiles,
-                                   int64_t c0, int64_t c1, int64_t dg_tile) {
+                                   int64_t c0, int64_t c1, int64_t dg_tile, int dg_count = 1) {
   const bool zero_out = p.zero_unrouted && p.out != nullptr;
   const bool zero_dg = p.dg != nullptr && dg_tile >= 0;
   if (!zero_out && !zero_dg) return;
@@ -200,7 +201,8 @@ __device__ void zero_unrouted_cols(const GemmParams& p, const RouteMeta<BM>& m, 
   for (int64_t q = q0 + j; q < p.n_routes; q += n_surplus) {
     if (zero_dg && threadIdx.x == 0) {
       const int64_t wi = p.w_idx[q];
-      if (wi >= 0 && wi < p.n_routes) p.dg[wi * p.dg_ntiles + dg_tile] = 0.f;
+      if (wi >= 0 && wi < p.n_routes)
+        for (int t = 0; t < dg_count; ++t) p.dg[wi * p.dg_ntiles + dg_tile + t] = 0.f;
     }
     if (!zero_out) continue;
     const int64_t oi = p.o_idx != nullptr ? p.o_idx[q] / p.o_div : q;

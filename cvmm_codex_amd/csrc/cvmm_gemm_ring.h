@@ -124,7 +124,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void routed_gemm_ring_kernel(const Ge
   const int64_t n0 = ntile * BN;
 
   if (!gemm_schedule<BM, Cfg::NT>(p, tile, meta)) {
-    zero_unrouted_cols<BM, Cfg::NT>(p, meta, tile, gridDim.x / n_ntiles, n0, n0 + BN, ntile);
+    // the routing-weight gradient's partials: one per 128 columns (per tile
+    // where BN = 64)
+    constexpr int kDgPer = BN > 128 ? BN / 128 : 1;
+    zero_unrouted_cols<BM, Cfg::NT>(p, meta, tile, gridDim.x / n_ntiles, n0, n0 + BN, ntile * kDgPer, kDgPer);
     return;
   }
   const int32_t expert = meta.expert;
@@ -239,9 +242,13 @@ __global__ __launch_bounds__(NW * 64, OCC) void routed_gemm_ring_kernel(const Ge
   // DG (16-bit x with 8-byte aligned rows, ring_eligible): every x piece
   // this lane needs for the routing-weight gradient (MB rows x 4 blocks of 4
   // columns, 8 bytes each) is requested early, so the gathers' latency
-  // overlaps the last MFMAs (or at least the output stores)
-  uint2 xpre[MB][4];
+  // overlaps the last MFMAs (or at least the output stores).  Waves of 8 row
+  // blocks (256 x 256 tiles) have no registers for them: their sums load
+  // the pieces where they use them.
+  constexpr bool XPRE = MB <= 5;
+  uint2 xpre[XPRE ? MB : 1][4];
   auto load_x = [&]() {
+    if constexpr (!XPRE) return;
     const int64_t nw = n0 + wn * 64;
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
@@ -323,7 +330,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void routed_gemm_ring_kernel(const Ge
     }
     if constexpr (DG) {
       // the last slice: the x pieces take the place of its refill, which
-      // would only bring zeros from past K
+      // would only bring zeros from past K (a peeled slice either way)
       vm_wait<(STAGES - 2) * Cfg::D>();
       wg_barrier();
       load_x();
@@ -442,7 +449,11 @@ __global__ __launch_bounds__(NW * 64, OCC) void routed_gemm_ring_kernel(const Ge
         for (int i = 0; i < 4; ++i) {
           if (nwave + i * 16 + 4 * fq >= p.N) continue;
           union { uint2 u; bf16_t b[4]; f16_t h[4]; } c;
-          c.u = xpre[j][i];
+          if constexpr (XPRE)
+            c.u = xpre[j][i];
+          else
+            c.u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.dg_x) + xr * p.dg_x_ld +
+                                                  nwave + i * 16 + 4 * fq);
 #pragma unroll
           for (int q = 0; q < 4; ++q)
             sum += round_to(acc[i][j][q], p.dg_val_dtype) * (xbf ? (float)c.b[q] : (float)c.h[q]);
@@ -461,6 +472,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void routed_gemm_ring_kernel(const Ge
     } else {
       // every wave is past its last LDS read of the ring (the DMA drained
       // above): the ring's first bytes take the per-wave partials
+      // partials per 128 columns: the tile's two waves of each 128-column
+      // piece in wn order (one piece for BN = 128, two for 256 x 256 tiles)
+      constexpr int WPP = 2, DGP = Cfg::WN / WPP;
       float* red = reinterpret_cast<float*>(ring);
       wg_barrier();
       if (fq == 0) {
@@ -468,14 +482,14 @@ __global__ __launch_bounds__(NW * 64, OCC) void routed_gemm_ring_kernel(const Ge
         for (int j = 0; j < MB; ++j) red[wn * BM + wm * WR + j * 16 + fr] = part[j];
       }
       __syncthreads();
-      if (wn == 0 && fq == 0) {
+      if (wn % WPP == 0 && fq == 0) {
 #pragma unroll
         for (int j = 0; j < MB; ++j) {
           const int m = wm * WR + j * 16 + fr;
-          float sum = red[m];
+          float sum = red[wn * BM + m];
 #pragma unroll
-          for (int w = 1; w < Cfg::WN; ++w) sum += red[w * BM + m];
-          if (meta.widx[m] >= 0) p.dg[meta.widx[m] * p.dg_ntiles + ntile] = sum;
+          for (int w = 1; w < WPP; ++w) sum += red[(wn + w) * BM + m];
+          if (meta.widx[m] >= 0) p.dg[meta.widx[m] * p.dg_ntiles + ntile * DGP + wn / WPP] = sum;
         }
       }
     }
@@ -517,11 +531,9 @@ hipError_t launch_routed_gemm_ring_b(const GemmParams& p_in, hipStream_t stream)
   else if (p.dg == nullptr)
     hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1, BK, false, BNC, NW>),
                        dim3((unsigned)grid), dim3(NW * 64), 0, stream, p);
-  else if constexpr (BN <= 128)  // the routing-weight gradient's partials are per 64 or 128 columns
+  else
     hipLaunchKernelGGL((routed_gemm_ring_kernel<OpT, OutT, BM, BN, STAGES, OCC, RA, 1, BK, true, BNC, NW>),
                        dim3((unsigned)grid), dim3(NW * 64), 0, stream, p);
-  else
-    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
@@ -568,10 +580,10 @@ inline bool ring_tall_tiles(const GemmParams& p) {
 // 256 x 128 and 128 x 256 of eight waves, and 32-k slices in a 4-slice ring
 // all measured slower or no faster.  Taken where N is a multiple of 256 and
 // the grid fills at least two rounds of 256 CUs (tile count estimated as R /
-// 256 + E / 2), and never with the routing-weight gradient (its partials are
-// per 128 columns).
+// 256 + E / 2).  With the routing-weight gradient each 128-column half of
+// the tile writes its own partial, summed as a 128-column tile sums it.
 inline bool ring_wide_tiles(const GemmParams& p) {
-  if (p.dg != nullptr || p.N % 256 != 0 || p.ring_tile == 1 || p.ring_tile == 2) return false;
+  if (p.N % 256 != 0 || p.ring_tile == 1 || p.ring_tile == 2) return false;
   if (p.ring_tile == 3) return true;
   const int64_t tiles = ((p.n_routes + 255) / 256 + p.n_experts / 2) * (p.N / 256);
   return tiles >= 2 * 256;

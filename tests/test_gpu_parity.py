@@ -445,15 +445,16 @@ def test_invalid_ids_contribute_nothing(weighted, route_input):
 
 
 @pytest.mark.parametrize("D,H,amp,ring_tile", [(128, 256, True, 1), (1024, 320, True, 1), (1024, 320, True, 2),
-                                               (64, 256, True, 0), (256, 64, True, 0), (48, 96, True, 0),
-                                               (96, 80, False, 0)])
+                                               (512, 320, True, 3), (64, 256, True, 0), (256, 64, True, 0),
+                                               (48, 96, True, 0), (96, 80, False, 0)])
 def test_weight_grad_partials_need_no_filled_workspace(D, H, amp, ring_tile):
     """Through the C ABI, weighted route-input grad-input with grad_rw: the
     per-(route, n tile) partials are written by the GEMM itself (covered
     routes by their tile, routes with out-of-range expert ids as zeros by the
     surplus workgroups), so a workspace of 0xFF bytes (NaN as fp32) gives the
     same bits as a zeroed one.  Shapes: the long-K ring kernel (128- and
-    160-row tiles, and its 256 x 64 tile for N <= 64), the short-K tiled
+    160-row tiles, its 256 x 256 tile with two partials per n tile, and its
+    256 x 64 tile for N <= 64), the short-K tiled
     kernel (128 x 128 and 256 x 64) and the general kernel (fp32 op)."""
     from cvmm_codex_amd import _native as N
     E, K, T = 8, 4, 192
@@ -695,12 +696,13 @@ def test_gemm_order_does_not_change_bits(weighted, route_input, skew):
     (False, False, 384, 256, None),   # long-K forward, two n tiles
     (True, False, 256, 384, 0.0),     # both products long-K
     (False, True, 512, 512, 0.5),     # both products 256 x 256 where chosen, hot expert
+    (True, False, 256, 512, 0.5),     # 256 x 256 grad-input with the routing-weight gradient
 ])
 def test_long_k_tile_height_does_not_change_bits(weighted, route_input, D, H, skew):
     """128- and 160-row m-tiles of the long-K routed GEMM, and its eight-wave
-    256 x 256 tiles (where N is a multiple of 256 and no routing-weight
-    gradient is taken), run every row's k slices in the same order:
-    identical bits, and the oracle's values."""
+    256 x 256 tiles (where N is a multiple of 256; with the routing-weight
+    gradient one partial per 128-column half), run every row's k slices in
+    the same order: identical bits, and the oracle's values."""
     from cvmm_codex_amd import _native as N
     x, keys, sel, w, go = _rand_case(35, 4, 384, D, H, 12, 6, weighted, route_input, skew=skew)
     lib = N.lib()
@@ -735,6 +737,7 @@ def test_long_k_tile_height_does_not_change_bits(weighted, route_input, D, H, sk
     (512, 256, False, False, 3),    # both products 256 x 256, eight waves
     (256, 512, False, True, 3),     # both 256 x 256, route input
     (200, 512, True, False, 3),     # weighted forward 256 x 256 with a part-filled last k slice
+    (512, 256, True, True, 3),      # grad-input 256 x 256 + routing-weight gradient
 ])
 def test_long_k_reads_either_weight_orientation(D, H, weighted, route_input, tile, op):
     """The long-K routed GEMM reads the weights k-contiguous ([n][k] rows: the
