@@ -330,7 +330,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void routed_gemm_ring_kernel(const Ge
     }
     if constexpr (DG) {
       // the last slice: the x pieces take the place of its refill, which
-      // would only bring zeros from past K (a peeled slice either way)
+      // would only bring zeros from past K (8-block waves, which load their
+      // pieces in the sums, peel it all the same)
       vm_wait<(STAGES - 2) * Cfg::D>();
       wg_barrier();
       load_x();
@@ -470,10 +471,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void routed_gemm_ring_kernel(const Ge
         if (fq == 0 && meta.widx[m] >= 0) p.dg[meta.widx[m] * p.dg_ntiles + ntile] = part[j];
       }
     } else {
-      // every wave is past its last LDS read of the ring (the DMA drained
-      // above): the ring's first bytes take the per-wave partials
-      // partials per 128 columns: the tile's two waves of each 128-column
-      // piece in wn order (one piece for BN = 128, two for 256 x 256 tiles)
+      // one partial per 128 columns: the two waves of each 128-column piece
+      // summed in wn order (one piece for BN = 128, two for 256 x 256
+      // tiles).  Every wave is past its last LDS read of the ring (the DMA
+      // drained above): the ring's first bytes take the per-wave partials.
       constexpr int WPP = 2, DGP = Cfg::WN / WPP;
       float* red = reinterpret_cast<float*>(ring);
       wg_barrier();

@@ -582,18 +582,22 @@ std::tuple<OptT, OptT, OptT> cvmm_backward_impl(const Tensor& grad_output, const
   const int32_t rwd = rwf.has_value() ? dtype_id(rwf->scalar_type()) : 0;
   const int32_t od = (int32_t)op_id;
   OptT grad_x, grad_w, grad_rw;
-  // joins the side stream back into `stream` on every way out below
+  // the weight gradient's x rows: declared before the join below, so that
+  // a temporary (x converted to the op dtype) outlives the side stream's use
+  Tensor xs;
+  // joins the side stream back into `stream` on every way out below (and,
+  // destroyed before the tensors declared above, before they are freed)
   SideJoin join;
 
   if (need_grad_keys) {
     // the route rows the forward scaled (cvmm_fwd_keep_scaled), or x
     const bool pre_scaled = scaled_x.has_value();
-    Tensor xs = pre_scaled ? *scaled_x
-                           : rows_of(fast && x.scalar_type() != op ? x.to(op) : storage_for(x, op), d_in);
+    xs = pre_scaled ? *scaled_x : rows_of(fast && x.scalar_type() != op ? x.to(op) : storage_for(x, op), d_in);
     grad_w = at::empty(keys.sizes(), opts(keys, keys.scalar_type()));
     // with a grad-input to run as well, the weight gradient goes to the side
-    // stream once its inputs are enqueued: its temporaries are freed to the
-    // caller's stream, whose next work waits for the join
+    // stream once its inputs are enqueued; its inputs (g, xs and the routing
+    // tensors, all declared before `join`) are freed to the caller's stream
+    // only after the join, so no later work there reuses them too early
     int64_t wstream = stream;
     if ((flags & kHostOverlapBackward) && (need_grad_x || need_grad_rw)) {
       wstream = (int64_t)(uintptr_t)fork_to_side(x.get_device(), (hipStream_t)(uintptr_t)stream);

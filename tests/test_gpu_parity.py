@@ -966,17 +966,20 @@ def test_small_fp32_problems(D, H, route_input):
     U.compare(got, exp, 1e-4)
 
 
-@pytest.mark.parametrize("weighted,route_input,D,H,lowmem", [
-    (False, False, 256, 128, 0),    # token input: route-buffer grad-input + top-k sum
-    (True, True, 128, 256, 0),      # weighted route input: routing-weight gradient too
-    (True, False, 512, 256, 0),     # weighted token input, both products long-K
-    (False, False, 128, 256, 2),    # low-memory slices of the top-k sum (an early return)
+@pytest.mark.parametrize("weighted,route_input,D,H,lowmem,x_dt", [
+    (False, False, 256, 128, 0, torch.bfloat16),   # token input: route-buffer grad-input + top-k sum
+    (True, True, 128, 256, 0, torch.bfloat16),     # weighted route input: routing-weight gradient too
+    (True, False, 512, 256, 0, torch.bfloat16),    # weighted token input, both products long-K
+    (False, False, 128, 256, 2, torch.bfloat16),   # low-memory slices of the top-k sum (an early return)
+    (False, False, 256, 256, 0, torch.float32),    # fp32 x under bf16 autocast: converted x rows
 ])
-def test_backward_on_two_streams_gives_the_same_bits(weighted, route_input, D, H, lowmem, monkeypatch):
+def test_backward_on_two_streams_gives_the_same_bits(weighted, route_input, D, H, lowmem, x_dt, monkeypatch):
     """With cvmm_overlap_backward the weight gradient runs on a second stream,
     forked from and joined back into the caller's stream: the same kernels,
-    so every gradient has the one-stream bits, on every return path."""
-    x, keys, sel, w, go = _rand_case(71 + D + H + lowmem, 2, 256, D, H, 16, 4, weighted, route_input, skew=0.5)
+    so every gradient has the one-stream bits, on every return path (x in
+    another dtype: the converted rows live until the join)."""
+    x, keys, sel, w, go = _rand_case(71 + D + H + lowmem, 2, 256, D, H, 16, 4, weighted, route_input, skew=0.5,
+                                     x_dt=x_dt)
     monkeypatch.setattr(C, "cvmm_lowmem_chunk_size", lowmem)
     runs = []
     for overlap in (False, True, True):
