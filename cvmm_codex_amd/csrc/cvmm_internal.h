@@ -165,7 +165,8 @@ __host__ __device__ inline void wgrad_tile(int64_t M, int64_t N, int* bm, int* b
 }
 // The 16-bit fast path may take a coarser tile where the base tile is
 // 128 x 128: 256 x 128, 128 x 256 or 256 x 256 (fewer bytes gathered per
-// flop; four waves of up to 128 x 128, one workgroup per CU).
+// flop; four waves of up to 128 x 128, or 256 x 256 as eight waves of 128 x
+// 64; one workgroup per CU).
 constexpr int32_t kWgTileBase = 0, kWgTile256x128 = 1, kWgTile128x256 = 2, kWgTile256x256 = 3;
 constexpr int32_t kWgTile256x256W8 = 4;  // 256 x 256 of eight waves
 __host__ __device__ inline void wgrad_fast_tile(int64_t M, int64_t N, int32_t choice, int* bm, int* bn) {

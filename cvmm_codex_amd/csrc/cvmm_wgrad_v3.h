@@ -60,10 +60,11 @@ struct RouteSlice {
 };
 
 // A BM x BN tile on a WM x WN grid of waves; each wave owns JM x IN blocks of
-// 16 x 16 (x columns x dY columns).  Up to 16 blocks per wave (64 accumulator
-// registers) run two workgroups per CU with 80 KB of LDS each; more blocks
-// run one workgroup per CU -- one wave per SIMD, whose 512 registers hold the
-// accumulators in AGPRs -- with all 160 KB.
+// 16 x 16 (x columns x dY columns).  Four waves of up to 16 blocks (64
+// accumulator registers) run two workgroups per CU with 80 KB of LDS each;
+// four waves of more blocks run one workgroup per CU -- one wave per SIMD,
+// whose 512 registers hold the accumulators in AGPRs -- with all 160 KB;
+// eight waves (two per SIMD, 256 registers each) run one workgroup per CU.
 template <int BM, int BN, int WM, int WN, int STAGES, bool WEIGHTED>
 struct Wg3Cfg {
   using TA = RouteSlice<BM>;                   // x rows: dW rows m0 .. m0 + BM
