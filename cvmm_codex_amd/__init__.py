@@ -9,6 +9,7 @@ from .api import (  # noqa: F401
     create_kernels,
     cvmm,
     cvmm_expert_offsets,
+    cvmm_gate_logits,
     cvmm_gelu,
     cvmm_prepare_sel,
     cvmm_prepare_sel2,

@@ -562,6 +562,75 @@ def cvmm_route_topk(logits: torch.Tensor, k: int, renormalize: bool = True):
     return w.view(*lead, k), sel, CVMMSel._deferred(sel, routing, False, None)
 
 
+def _gate_grad_chunks(n_tokens: int, d_in: int, n_experts: int) -> int:
+    """Token chunks of the gate gradient's product: enough [E x D] output
+    tiles to fill the GPU (a single [D x T] @ [T x E] product has D*E/8192
+    tiles of 128 x 64: 32 at the FFN stack's 2048 x 128), each chunk at least
+    1024 tokens; 1 when the tokens do not split evenly."""
+    c = 1
+    while c < 16 and (d_in * n_experts // 8192) * c * 2 <= 512 and n_tokens % (2 * c) == 0 \
+            and n_tokens // (2 * c) >= 1024:
+        c *= 2
+    return c
+
+
+class _GateLogits(torch.autograd.Function):
+    """logits = x @ gate as autocast computes it (both operands in the op
+    dtype, that dtype out; benchmark_ffn_moe.py:91), whose gate gradient
+    x^T @ dlogits -- a long-K product with few output tiles -- runs over token
+    chunks as one batched product with fp32 partials, summed in chunk order
+    and rounded to the op dtype as the single product's output is."""
+
+    @staticmethod
+    def forward(ctx, x, gate, op):
+        xb, gb = x.to(op), gate.to(op)
+        ctx.save_for_backward(xb, gb)
+        ctx.dtypes = (x.dtype, gate.dtype)
+        return xb @ gb
+
+    @staticmethod
+    def backward(ctx, g):
+        xb, gb = ctx.saved_tensors
+        x_dtype, gate_dtype = ctx.dtypes
+        D, E = gb.shape
+        g2 = g.to(xb.dtype).reshape(-1, E).contiguous()
+        x2 = xb.reshape(-1, D)
+        dx = dgate = None
+        if ctx.needs_input_grad[0]:
+            dx = (g2 @ gb.t().contiguous()).to(x_dtype).view(xb.shape)
+        if ctx.needs_input_grad[1]:
+            T = x2.shape[0]
+            c = _gate_grad_chunks(T, D, E)
+            if c == 1:
+                dgate = (x2.t() @ g2).to(gate_dtype)
+            else:
+                a = g2.view(c, T // c, E).transpose(1, 2).contiguous()   # [c, E, T / c]
+                b = x2.contiguous().view(c, T // c, D)                     # [c, T / c, D]
+                part = torch.bmm(a, b) if a.dtype == torch.float32 else \
+                    torch.bmm(a, b, out_dtype=torch.float32)              # [c, E, D] fp32
+                dgate = part.sum(0).t().to(xb.dtype).to(gate_dtype)
+        return dx, dgate, None
+
+
+def cvmm_gate_logits(x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+    """The router's projection of the reference's MoE callers, ``logits = x @
+    gate`` (benchmark_ffn_moe.py:91), in the autocast dtype where autocast is
+    on (else the promoted dtype): the same forward, input gradient and rounding
+    points, with the gate gradient taken over token chunks (one batched
+    product instead of a single long-K one whose few output tiles leave most
+    CUs idle).  x ``[..., D]``, gate ``[D, E]``; returns ``[..., E]``."""
+    _require_device(x, "x")
+    _require_device(gate, "gate")
+    if gate.dim() != 2 or x.shape[-1] != gate.shape[0]:
+        raise ValueError(f"cvmm_gate_logits: x {tuple(x.shape)} and gate {tuple(gate.shape)} do not multiply")
+    if torch.is_autocast_enabled("cuda"):
+        op = torch.get_autocast_dtype("cuda")
+    else:
+        op = torch.result_type(x, gate)
+    with torch.autocast("cuda", enabled=False):
+        return _GateLogits.apply(x, gate, op)
+
+
 # ----------------------------------------------------------------------------
 # launch helpers
 # ----------------------------------------------------------------------------

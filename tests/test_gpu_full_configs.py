@@ -234,8 +234,9 @@ def test_c5_ffn_stack_full_size_sampled():
 
 def test_c5_fused_stack_full_size_every_token_and_expert():
     """The path the C5 bench line times, workloads.ffn_forward_fused (the
-    native router cvmm_route_topk and the up projection with its GELU in the
-    GEMM epilogue, cvmm_gelu), at full size.  The router's choice is checked
+    router projection cvmm_gate_logits, the native router cvmm_route_topk and
+    the up projection with its GELU in the GEMM epilogue, cvmm_gelu), at full
+    size.  The router's choice is checked
     to be a top-k of the softmax in probability order; then, with that
     routing, the whole stack is restated in float32 on the GPU (the torch
     path of oracle/torch_cpu_path.py, torch autograd for the gradients,

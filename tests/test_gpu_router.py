@@ -149,3 +149,40 @@ def test_ffn_stack_with_fused_router_matches_torch_router():
                       "down_grad": down.grad}
     exp = {n: to_np(v) for n, v in res[False].items()}
     compare(res[True], exp, 2e-2, names=tuple(exp))
+
+
+@pytest.mark.parametrize("T,D,E,amp", [
+    (16384, 2048, 128, True),    # the FFN stack's router projection: 16 token chunks
+    (4096, 512, 64, True),       # 4 chunks
+    (1000, 64, 16, True),        # one product (too few tokens to split)
+    (2048, 256, 32, False),      # fp32, no autocast
+])
+def test_gate_logits_against_the_torch_projection(T, D, E, amp):
+    """cvmm_gate_logits(x, gate) is the callers' ``x @ gate``
+    (benchmark_ffn_moe.py:91) under autocast: the same logits bit for bit,
+    the same input gradient, and the gate gradient -- summed over token
+    chunks in fp32 -- within the op dtype's rounding of torch's, and against
+    float64."""
+    g = torch.Generator().manual_seed(T + D + E)
+    xd = torch.randn(T, D, generator=g).to(torch.bfloat16 if amp else torch.float32).cuda()
+    gate = (torch.randn(D, E, generator=g) / D ** 0.5).cuda()
+    dl = torch.randn(T, E, generator=g).cuda()
+    outs = []
+    for fn in (lambda a, b: a @ b, C.cvmm_gate_logits):
+        x = xd.clone().requires_grad_(True)
+        gt = gate.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=amp):
+            y = fn(x, gt)
+        y.backward(dl.to(y.dtype))
+        torch.cuda.synchronize()
+        outs.append((y.detach(), x.grad, gt.grad))
+    (y0, dx0, dg0), (y1, dx1, dg1) = outs
+    assert y1.dtype == y0.dtype and dg1.dtype == dg0.dtype and dx1.dtype == dx0.dtype
+    assert torch.equal(y1, y0)
+    tol = 2e-2 if amp else 1e-4
+    assert norm_rel(to_np(dx1), to_np(dx0)) <= tol
+    assert norm_rel(to_np(dg1), to_np(dg0)) <= tol
+    # float64 restatement of the gate gradient with the op-dtype operands
+    xo = xd.double().cpu()
+    dlo = dl.to(y0.dtype).double().cpu()
+    assert norm_rel(to_np(dg1), (xo.t() @ dlo).numpy()) <= tol

@@ -164,12 +164,13 @@ def ffn_forward(s: FFNStack, cvmm_mod, x, gate, w_up, w_down):
 
 
 def ffn_forward_fused(s: FFNStack, cvmm_mod, x, gate, w_up, w_down):
-    """ffn_forward with the library's fused router (cvmm_route_topk) and
-    up projection + GELU (cvmm_gelu) in place of the torch lines."""
+    """ffn_forward with the library's router projection (cvmm_gate_logits),
+    fused router (cvmm_route_topk) and up projection + GELU (cvmm_gelu) in
+    place of the torch lines."""
     B, T, D = x.shape
     E, _, H = w_up.shape
     with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
-        logits = x @ gate + s.bias
+        logits = cvmm_mod.cvmm_gate_logits(x, gate) + s.bias
         weights, _, sel_up = cvmm_mod.cvmm_route_topk(logits, s.k, True)
         hidden = cvmm_mod.cvmm_gelu(x, sel_up, w_up)
         sel_down = cvmm_mod.cvmm_prepare_sel2(sel_up, weights, route_input=True)
