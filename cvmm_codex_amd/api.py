@@ -604,11 +604,13 @@ class _GateLogits(torch.autograd.Function):
             if c == 1:
                 dgate = (x2.t() @ g2).to(gate_dtype)
             else:
-                a = g2.view(c, T // c, E).transpose(1, 2).contiguous()   # [c, E, T / c]
-                b = x2.contiguous().view(c, T // c, D)                     # [c, T / c, D]
+                # x's chunks as the transposed left operand (no copy); the
+                # right operand stays contiguous
+                a = x2.contiguous().view(c, T // c, D).transpose(1, 2)   # [c, D, T / c]
+                b = g2.view(c, T // c, E)                                  # [c, T / c, E]
                 part = torch.bmm(a, b) if a.dtype == torch.float32 else \
-                    torch.bmm(a, b, out_dtype=torch.float32)              # [c, E, D] fp32
-                dgate = part.sum(0).t().to(xb.dtype).to(gate_dtype)
+                    torch.bmm(a, b, out_dtype=torch.float32)              # [c, D, E] fp32
+                dgate = part.sum(0).to(xb.dtype).to(gate_dtype)
         return dx, dgate, None
 
 
