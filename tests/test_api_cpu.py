@@ -141,3 +141,24 @@ def test_shape_log_is_on_by_default():
     if "CVMM_LOG_SHAPES" in os.environ:
         pytest.skip("CVMM_LOG_SHAPES set in the environment")
     assert C.cvmm_log_shapes is True
+
+
+def test_gate_gradient_chunks():
+    """The gate gradient's token chunks (cvmm_gate_logits): powers of two,
+    each at least 1024 tokens, until the [E x D] output tiles of the batched
+    product fill the GPU (512 tiles of 128 x 64); one product where the
+    tokens do not split evenly or are too few."""
+    assert C._gate_grad_chunks(16384, 2048, 128) == 16     # the FFN stack: 32 tiles x 16
+    assert C._gate_grad_chunks(4096, 512, 64) == 4         # 1024 tokens per chunk
+    assert C._gate_grad_chunks(1000, 64, 16) == 1          # too few tokens
+    assert C._gate_grad_chunks(16383, 2048, 128) == 1      # odd token count
+    assert C._gate_grad_chunks(65536, 4096, 1024) == 1     # 512 tiles already
+    for T, D, E in ((16384, 2048, 128), (8192, 1024, 64), (2048, 256, 32)):
+        c = C._gate_grad_chunks(T, D, E)
+        assert T % c == 0 and (c == 1 or T // c >= 1024)
+
+
+def test_gate_logits_has_no_cpu_path():
+    """cvmm_gate_logits, like the products, takes device tensors only."""
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        C.cvmm_gate_logits(torch.randn(4, 8), torch.randn(8, 3))
