@@ -124,8 +124,9 @@ int cvmm_timing_result(uint32_t kernel_class, double* total_ms, int64_t* launche
  *     expert).  Workspace queries depend on it: query after setting it.
  *   CVMM_TUNE_RING_TILE: tile of the long-K routed GEMM (K > 128, N > 64):
  *     1 = 128 x 128, 2 = 160 x 128, 3 = 256 x 256 of eight waves where N is
- *     a multiple of 256 (elsewhere the built-in height).  Built in: 256 x 256 where it applies and the
- *     grid fills two rounds of 256 CUs (the FFN stack); else 160 rows
+ *     a multiple of 256 (elsewhere the built-in height).  Built in: 256 x
+ *     256 where it applies and the grid fills two rounds of 256 CUs (the
+ *     FFN stack); else 160 rows
  *     unless the estimated dispatch rounds times the tile height come out
  *     more than 5 % higher (the ff_up forward: one round of ~442 tiles
  *     instead of 544 tiles on 512 slots).  All give the same bits. */
