@@ -92,3 +92,13 @@ def test_random_case_with_dense_top_k_sums_matches_the_oracle(case):
         _check(case)
     finally:
         lib.cvmm_tuning_set(N.TUNE_DENSE_TOPK, 0)
+
+
+@pytest.mark.parametrize("case", [c for c in _cases() if c[7] or not c[8]], ids=_case_id)
+def test_random_case_with_atomic_top_k_sums_matches_the_oracle(case, monkeypatch):
+    """The cases that sum over top-k (a weighted forward, or the input
+    gradient of a token-input selection) with those sums taken by fp32
+    atomics (CVMM_ATOMIC_REDUCE)."""
+    import cvmm_codex_amd.api as C
+    monkeypatch.setattr(C, "cvmm_atomic_reduce", True)
+    _check(case)
