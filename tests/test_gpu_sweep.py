@@ -102,3 +102,22 @@ def test_random_case_with_atomic_top_k_sums_matches_the_oracle(case, monkeypatch
     import cvmm_codex_amd.api as C
     monkeypatch.setattr(C, "cvmm_atomic_reduce", True)
     _check(case)
+
+
+@pytest.mark.parametrize("case", _cases(), ids=_case_id)
+def test_random_case_with_the_backward_on_two_streams_matches_the_oracle(case, monkeypatch):
+    """Every case with the weight gradient on a second stream beside the
+    input gradient (CVMM_OVERLAP_BACKWARD)."""
+    import cvmm_codex_amd.api as C
+    monkeypatch.setattr(C, "cvmm_overlap_backward", True)
+    _check(case)
+
+
+@pytest.mark.parametrize("case", [c for c in _cases() if not c[7] and not c[8] and c[6] >= 4], ids=_case_id)
+def test_random_case_with_low_memory_slices_matches_the_oracle(case, monkeypatch):
+    """Token-input unweighted cases with top-k >= 4 with the input gradient's
+    top-k sum taken over slices of two top-k columns at a time
+    (CVMM_LOWMEM_CHUNK_SIZE=2)."""
+    import cvmm_codex_amd.api as C
+    monkeypatch.setattr(C, "cvmm_lowmem_chunk_size", 2)
+    _check(case)
