@@ -153,3 +153,29 @@ def test_random_case_tile_and_order_knobs_keep_the_bits(case):
             lib.cvmm_tuning_set(code, 0)
         for n in stable:
             assert torch.equal(got[n], base[n]), (knob, value, n)
+
+
+def _foreign_prepare(sd, wd, route_input=False):
+    """A selector built by the caller with torch ops, the way the reference's
+    pure-torch preparation builds it (cvmm.py:1786-1803): an unstable sort,
+    no inverse permutation or offsets attached."""
+    import cvmm_codex_amd.api as C
+    fsel = sd.flatten().to(torch.int32)
+    ssel, sel_index = fsel.sort()
+    if route_input:
+        return C.CVMMSel(fsel.view_as(sd), ssel.view_as(sd), sel_index, None, wd)
+    return C.CVMMSel(fsel.view_as(sd), ssel.view_as(sd), sel_index // sd.shape[-1], sel_index, wd)
+
+
+@pytest.mark.parametrize("case", _cases(), ids=_case_id)
+def test_random_case_with_a_caller_built_selector_matches_the_oracle(case):
+    x, keys, sel, w, go = _make(case)
+    route_input, mode = case[8], case[9]
+    _, amp_dt, tol = _MODES[mode]
+    amp = amp_dt is not None
+    print(f"sweep case {case}", flush=True)
+    got = U.run_hip(x, keys, sel, w, go, route_input, amp, amp_dtype=amp_dt or torch.bfloat16,
+                    prepare=_foreign_prepare)
+    exp = U.run_oracle(x, keys, sel, w, go, route_input, amp,
+                       amp_dtype="float16" if amp_dt == torch.float16 else "bfloat16")
+    U.compare(got, exp, tol)
