@@ -41,6 +41,21 @@ CASES = [  # T, E, k, renormalize, logits dtype
 ]
 
 
+def _random_cases(n=16, seed=77):
+    """Seeded draws within the router's limits (1..1024 experts, top-k up
+    to 64 and at most the expert count)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        E = int(rng.integers(1, 1025))
+        k = int(rng.integers(1, min(E, 64) + 1))
+        out.append((int(rng.integers(1, 5000)), E, k, bool(rng.integers(0, 2)), str(rng.choice(list(DT)))))
+    return out
+
+
+CASES = CASES + _random_cases()
+
+
 def _logits(T, E, dt, seed):
     g = torch.Generator().manual_seed(seed)
     # a Zipf-like bias makes some experts hot, as in the C5 routing
