@@ -101,6 +101,34 @@ def test_cvmm_gelu_matches_composition_and_oracle(T, k, E, d_in, d_out, route_in
     assert n == (0 if fused else 1)
 
 
+def _random_cases(n=16, seed=5):
+    """Seeded draws: widths around the long-K switch (K > 128) and odd ones,
+    route or token input, bf16 autocast or fp32."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    widths = (8, 24, 33, 64, 96, 128, 136, 200, 256, 384, 520, 1024)
+    out = []
+    while len(out) < n:
+        T, k = int(rng.integers(1, 1000)), int(rng.integers(1, 9))
+        E = int(rng.choice((1, 3, 8, 16, 64)))
+        d_in, d_out = (int(rng.choice(widths)) for _ in range(2))
+        if T * k * d_in * d_out > 2e8:
+            continue
+        out.append((T, k, E, d_in, d_out, bool(rng.integers(0, 2)), bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("T,k,E,d_in,d_out,route_input,amp", _random_cases())
+def test_cvmm_gelu_random_shapes(T, k, E, d_in, d_out, route_input, amp):
+    x, keys, sel, gy = _case(T, k, E, d_in, d_out, route_input, seed=3 * T + d_out,
+                             x_dtype=torch.bfloat16 if amp else torch.float32)
+    got = _run(C.cvmm_gelu, x, keys, sel, gy, route_input, amp)
+    ref = _run(lambda a, s, w: F.gelu(C.cvmm(a, s, w)), x, keys, sel, gy, route_input, amp)
+    tol = 2e-2 if amp else 1e-4
+    compare(got, {n: to_np(v) for n, v in ref.items()}, tol)
+    compare(got, _oracle(x, keys, sel, gy, route_input, amp), tol)
+
+
 def test_cvmm_gelu_weighted_selection_is_the_composition():
     x, keys, sel, _ = _case(100, 3, 8, 256, 64, True, seed=3)
     g = torch.Generator().manual_seed(4)
