@@ -179,3 +179,24 @@ def test_random_case_with_a_caller_built_selector_matches_the_oracle(case):
     exp = U.run_oracle(x, keys, sel, w, go, route_input, amp,
                        amp_dtype="float16" if amp_dt == torch.float16 else "bfloat16")
     U.compare(got, exp, tol)
+
+
+def _large_cases(n=6, seed=99):
+    """Larger draws (~29000-32768 routes, 256 <-> 1024 wide, 32 or 64
+    experts): the forward (N = 1024) or the grad-input (N = 1024) has
+    (routes / 256 + experts / 2) x 4 >= 512 tiles, where the built-in choice
+    takes the eight-wave 256 x 256 long-K tiles."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        T, K = int(rng.integers(7200, 8193)), 4
+        E = int(rng.choice((32, 64)))
+        D, H = ((256, 1024), (1024, 256))[len(out) % 2]
+        out.append((200 + len(out), 1, T, D, H, E, K, bool(rng.integers(0, 2)), bool(rng.integers(0, 2)),
+                    str(rng.choice(["bf16", "fp16"])), None))
+    return out
+
+
+@pytest.mark.parametrize("case", _large_cases(), ids=_case_id)
+def test_large_random_case_matches_the_oracle(case):
+    _check(case)
